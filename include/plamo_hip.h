@@ -1,0 +1,239 @@
+/*
+ * plamo_hip.h -- C ABI of the MI355X (gfx950) PLaMo-3 0.8B token loop.
+ *
+ * This is the drop-in boundary for the hot path of mikuteto-dev/plamo3-0.8b-runtime:
+ * the Swift `Runtime` / `Batch` / `Sampler` / `decodeBatch` surface
+ * (Sources/Plamo/Runtime.swift, Batch.swift, Sampler.swift, BatchDecode.swift) whose
+ * Metal dispatches (Kernels.metal, Batch.metal) are replaced by hand-written HIP
+ * kernels.  Plain pointers and sizes only; no C++ or torch types cross it.
+ *
+ * Conventions
+ *   - Every function that can fail returns PLAMO_OK (0) or a PLAMO_E* code and, when
+ *     `err` is non-NULL, writes a NUL-terminated message of at most `errlen` bytes.
+ *     Message substrings the reference's callers match are kept verbatim.
+ *   - Validation happens before any state changes (Runtime.swift:328-330): a failed
+ *     call leaves position, logits and KV exactly as they were.
+ *   - A handle is not re-entrant: one HIP stream per handle, every call returns after
+ *     its GPU work completed (the reference commits and waits per call).
+ *   - Token IDs are int32.  The greedy argmax of an all-NaN logits row is 0xffffffff in
+ *     the reference (Kernels.metal:713-728); it is returned as the int32 -1.
+ */
+#ifndef PLAMO_HIP_H
+#define PLAMO_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PLAMO_OK 0
+#define PLAMO_EINVAL 1  /* invalid argument, token, length or context exhausted */
+#define PLAMO_EIO 2     /* file missing or unreadable */
+#define PLAMO_EFORMAT 3 /* malformed safetensors / .p12 / config */
+#define PLAMO_EDEVICE 4 /* HIP runtime or kernel failure */
+#define PLAMO_ESTATE 5  /* call not valid in the current state */
+
+typedef struct plamo_runtime plamo_runtime;
+typedef struct plamo_batch plamo_batch;
+
+typedef struct plamo_stats {
+    int64_t position;         /* Runtime.position (Runtime.swift:154) */
+    double gpu_seconds;       /* Runtime.gpuSeconds (Runtime.swift:155,463) */
+    int64_t device_bytes;     /* all device memory held by the handle */
+    int64_t weight_bytes;     /* Weights.gpuBytes (Runtime.swift:25) */
+    int64_t linear_bytes;     /* bytes of the 16x4 projections + LM head read per decode step */
+    int32_t context;          /* Runtime.context (Runtime.swift:147) */
+    int32_t packed;           /* 1 when the .p12 archive is used (Runtime.swift:148) */
+    int32_t last_output_rows; /* Runtime.lastOutputRows (Runtime.swift:153) */
+    int32_t local_capacity;   /* ring slots of a sliding-window layer */
+} plamo_stats;
+
+/* ---- Runtime (Runtime.swift:128-553) ------------------------------------------- */
+
+/* Runtime.init(directory:context:packed:) (Runtime.swift:164-286): validates
+ * config.json (Runtime.swift:180-190), model.safetensors (Runtime.swift:33-101) or
+ * model.p12 (Packed.swift:12-91), config-mlx.json RoPE frequencies (Runtime.swift:268-274),
+ * uploads the weights to HBM and allocates the ring/global KV.  `source_sha256` is the
+ * value the .p12 header must carry (Packed.swift:35); NULL selects the reference's
+ * pinned checksum of the original model. */
+int plamo_open(const char* directory, int32_t context, int32_t packed, const char* source_sha256,
+               plamo_runtime** out, char* err, size_t errlen);
+void plamo_close(plamo_runtime* rt);
+
+/* Runtime.reset() (Runtime.swift:319); also clears the sampler history. */
+void plamo_reset(plamo_runtime* rt);
+
+/* Runtime.forward(_:output:) (Runtime.swift:321-467): 1..min(context,16) tokens at the
+ * current position.  With output, `*next` receives the selected next token: the greedy
+ * argmax, or Sampler.select when sampling controls are set (plamo_set_sampling).
+ * Error "Invalid tokens or context exhausted" (Runtime.swift:330). */
+int plamo_forward(plamo_runtime* rt, const int32_t* tokens, int32_t count, int32_t output,
+                  int32_t* next, char* err, size_t errlen);
+
+/* Runtime.prefill(_:) (Runtime.swift:469-483): any prompt length up to the context.
+ * Processed in large MFMA chunks with the reference's 16-token chunk RoPE coordinates.
+ * Error "Input exceeds context" (Runtime.swift:474). */
+int plamo_prefill(plamo_runtime* rt, const int32_t* tokens, int32_t count, int32_t* next,
+                  char* err, size_t errlen);
+
+/* Runtime.logits(into:slot:) (Runtime.swift:547-552): BF16 logits widened to 107520
+ * floats.  `bf16` variant copies the raw bits (Runtime.logitValues bit patterns). */
+int plamo_logits(plamo_runtime* rt, int32_t slot, float* values, char* err, size_t errlen);
+int plamo_logits_bf16(plamo_runtime* rt, int32_t slot, uint16_t* bits, char* err, size_t errlen);
+
+/* Final normalised hidden state of the last output row (Runtime.normalized, used by the
+ * batch equivalence test BatchMapTests.swift:22-24). 1536 floats. */
+int plamo_hidden(plamo_runtime* rt, float* values, char* err, size_t errlen);
+
+/* Runtime.predictions() (Runtime.swift:522-525). */
+int plamo_predictions(plamo_runtime* rt, int32_t* out, int32_t capacity, int32_t* count);
+
+int plamo_get_stats(plamo_runtime* rt, plamo_stats* out);
+
+/* Copies the ring/global KV of `layer` (BF16 bits, [capacity][128] each) to host memory.
+ * Mirrors the layer.keys / layer.values buffers the reference tests read
+ * (BatchMapTests.swift:25-29).  `capacity` receives the slot count. */
+int plamo_kv(plamo_runtime* rt, int32_t layer, uint16_t* keys, uint16_t* values, int32_t* capacity,
+             char* err, size_t errlen);
+
+/* ---- On-GPU sampling controls (Sampler.swift:9-70, Main.swift:235-244) ------------- */
+
+/* Enables Sampler.select semantics for every subsequent output: FP32 repetition penalty
+ * (divide if positive else multiply), presence, frequency x count, no-repeat-n-gram ban,
+ * then the first strict maximum with default 0.  All run on the GPU over the full
+ * vocabulary.  penalty 1, presence 0, frequency 0, ngram <= 1 restores pure greedy. */
+int plamo_set_sampling(plamo_runtime* rt, float repetition_penalty, float frequency_penalty,
+                       float presence_penalty, int32_t no_repeat_ngram);
+/* `generated.append(id)` of Main.swift:280: adds to the history the controls see
+ * (generated tokens only, Main.swift:237-238).  Cleared by plamo_reset. */
+int plamo_sampler_observe(plamo_runtime* rt, int32_t id);
+
+/* The token loop of Main.swift:235-288 driven on the device: prefill `prompt`, then up to
+ * `max_tokens` emitted tokens, stopping on token 1 or 16 (Main.swift:279).  Each decode
+ * step is one replay of a captured hipGraph; the next token is fed back on the device.
+ * `out_ids` (capacity max_tokens) receives the emitted tokens, `*stop_reason` 1 for
+ * "stop", 0 for the length limit. */
+int plamo_generate(plamo_runtime* rt, const int32_t* prompt, int32_t count, int32_t max_tokens,
+                   int32_t* out_ids, int32_t* out_count, int32_t* stop_reason, char* err,
+                   size_t errlen);
+
+/* Device-timed decode microbenchmark: replays the captured decode step `steps` times
+ * back to back (token fed back on the device) from the current state, returning the
+ * average GPU milliseconds per step measured with HIP events on the handle's stream.
+ * Leaves the runtime advanced by `steps` positions. */
+int plamo_bench_decode(plamo_runtime* rt, int32_t steps, double* ms_per_step, char* err,
+                       size_t errlen);
+
+/* ---- Batch of up to four sequences (Batch.swift:4-187) ------------------------------ */
+
+/* Batch(_ scalar:) (Batch.swift:33-78): shares the runtime's weights, owns 4 KV slices.
+ * Requires context below 8192 ("Batch requires dense greedy inference with context below
+ * 8192"). */
+int plamo_batch_open(plamo_runtime* rt, plamo_batch** out, char* err, size_t errlen);
+void plamo_batch_close(plamo_batch* b);
+
+/* Batch.prefill (Batch.swift:80-107): `count` prompts (1..4) laid out back to back in
+ * `tokens` with `lengths[i]` tokens each; `next[i]` receives each lane's prediction. */
+int plamo_batch_prefill(plamo_batch* b, const int32_t* tokens, const int32_t* lengths, int32_t count,
+                        int32_t* next, char* err, size_t errlen);
+
+/* Batch.step (Batch.swift:109-180): tokens[i] < 0 marks an inactive lane (Swift nil).
+ * All active lanes run in one decode step that reads every weight once.  `next` receives
+ * predictions for every lane (Batch.predictions). */
+int plamo_batch_step(plamo_batch* b, const int32_t* tokens, int32_t count, int32_t* next, char* err,
+                     size_t errlen);
+void plamo_batch_reset(plamo_batch* b);
+
+/* Lane state read-back for the batch == scalar invariant (BatchMapTests.swift:21-31). */
+int plamo_batch_logits_bf16(plamo_batch* b, int32_t lane, uint16_t* bits, char* err, size_t errlen);
+int plamo_batch_hidden(plamo_batch* b, int32_t lane, float* values, char* err, size_t errlen);
+int plamo_batch_kv(plamo_batch* b, int32_t lane, int32_t layer, uint16_t* keys, uint16_t* values,
+                   int32_t* capacity, char* err, size_t errlen);
+int plamo_batch_positions(plamo_batch* b, int32_t* out, int32_t capacity, int32_t* count);
+
+/* ---- Lane scheduler (BatchDecode.swift:8-47) --------------------------------------- */
+
+/* step: receives `count` tokens (<0 = nil) and writes `count` predictions; returns 0 to
+ * continue, non-zero to abort.  emit(lane, id), finish(lane, ids, n, reason) likewise. */
+typedef int (*plamo_step_fn)(void* user, const int32_t* tokens, int32_t count, int32_t* next);
+typedef int (*plamo_emit_fn)(void* user, int32_t lane, int32_t id);
+typedef int (*plamo_finish_fn)(void* user, int32_t lane, const int32_t* ids, int32_t n, int32_t reason);
+
+#define PLAMO_REASON_STOP 1
+#define PLAMO_REASON_LENGTH 2
+
+/* decodeBatch(_:limits:step:emit:finish:stopOnTruncation:) (BatchDecode.swift:8-37).
+ * Pure host logic.  Outputs: `ids` is [count][ids_stride], `lengths[count]`,
+ * `reasons[count]`; `*lanes` receives the number of lanes reported (last+1). */
+int plamo_decode_batch(const int32_t* initial, const int32_t* limits, int32_t count, plamo_step_fn step,
+                       plamo_emit_fn emit, plamo_finish_fn finish, void* user, int32_t stop_on_truncation,
+                       int32_t* ids, int32_t ids_stride, int32_t* lengths, int32_t* reasons, int32_t* lanes,
+                       char* err, size_t errlen);
+
+/* Batch.generate (BatchDecode.swift:40-47): prefill + decodeBatch over the GPU batch. */
+int plamo_batch_generate(plamo_batch* b, const int32_t* tokens, const int32_t* lengths, const int32_t* limits,
+                         int32_t count, int32_t stop_on_truncation, int32_t* ids, int32_t ids_stride,
+                         int32_t* out_lengths, int32_t* reasons, int32_t* lanes, char* err, size_t errlen);
+
+/* ---- Weight formats (Runtime.swift:23-111, Packed.swift, scripts/pack_weights.py) ---- */
+
+typedef struct plamo_pack_report {
+    int64_t original_linear_bytes; /* pack_weights.py:140 */
+    int64_t packed_linear_bytes;
+    int64_t archive_bytes;
+    int64_t compressed_blocks;
+    int64_t blocks;
+} plamo_pack_report;
+
+/* scripts/pack_weights.py main (pack_weights.py:89-142): writes `output` (.p12) from a
+ * BF16 safetensors file, skipping the input embedding; every block is verified to
+ * round-trip bit-exactly.  Written atomically (.part + rename). */
+int plamo_pack(const char* safetensors, const char* output, const char* source_sha256,
+               plamo_pack_report* report, char* err, size_t errlen);
+
+/* Weights(path:).tensor(name, shape) validation (Runtime.swift:33-101) without a device. */
+int plamo_check_weights(const char* path, const char* name, const int64_t* shape, int32_t ndim, char* err,
+                        size_t errlen);
+
+/* Packed(path:).tensor(name, shape) validation (Packed.swift:12-91) without a device;
+ * `*is_packed` = 1 for a 2-D block-table tensor. */
+int plamo_check_packed(const char* path, const char* source_sha256, const char* name, const int64_t* shape,
+                       int32_t ndim, int32_t* is_packed, char* err, size_t errlen);
+
+/* ---- Kernel-level entry points (Metal kernel dispatch ABI, Kernels.metal) ----------
+ * Device pointers are passed as plain addresses; `stream` is a hipStream_t (NULL =
+ * default stream).  Used by the kernel parity tests and the GEMV microbenchmark. */
+
+/* `linear` (Kernels.metal:92-114) / `project{2,3,4}` (Batch.metal:171-221): y = W.x for
+ * `rows` activation rows.  `table` != 0 selects the .p12 decode (`w` = payload).  mode 0:
+ * y FP32 roundbf; mode 2: y BF16 bits (LM head).  n in {1536, 2048, 6144}. */
+int plamo_kernel_linear(uint64_t w, uint64_t table, uint64_t x, uint64_t y, int32_t n, int32_t m, int32_t rows,
+                        int32_t mode, uint64_t stream);
+
+/* `packed_bits` decode of `count` consecutive weights (Kernels.metal:23-44) into BF16 bits
+ * (PackedDecodeTests.swift:34-42). */
+int plamo_kernel_unpack(uint64_t payload, uint64_t table, uint64_t out, int64_t count, uint64_t stream);
+
+/* `argmax` (Kernels.metal:704-729): rows x n logits, FP32 (bf16 == 0) or BF16 bits. */
+int plamo_kernel_argmax(uint64_t x, uint64_t out, int32_t n, int32_t rows, int32_t bf16, uint64_t stream);
+
+/* `Sampler.select` on the GPU over FP32 logits (modified in place, like the Swift API):
+ * history of `hist` int32 ids; result written to `out` (device int32). */
+int plamo_kernel_select(uint64_t logits, int32_t n, uint64_t history, int32_t hist, float penalty,
+                        int32_t ngram, float frequency, float presence, uint64_t out, uint64_t stream);
+
+/* MFMA BF16 GEMM of the prefill path: Y[t][m] = roundbf(sum_k X[t][k] W[m][k]) with
+ * X BF16 [tokens][n], W plain BF16 or .p12 ([m][n]), Y FP32 or BF16 (out_bf16). */
+int plamo_kernel_gemm(uint64_t w, uint64_t table, uint64_t x, uint64_t y, int32_t n, int32_t m, int32_t tokens,
+                      int32_t out_bf16, uint64_t stream);
+
+/* Library build identification (gfx arch, HIP version). */
+const char* plamo_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

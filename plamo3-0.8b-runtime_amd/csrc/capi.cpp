@@ -1,0 +1,495 @@
+// extern "C" boundary (include/plamo_hip.h).  No C++ exception crosses it.
+#include <cstdio>
+#include <cstring>
+#include <functional>
+
+#include "../../include/plamo_hip.h"
+#include "formats.h"
+#include "runtime.h"
+
+struct plamo_runtime {
+    plamo::RuntimeImpl impl;
+};
+struct plamo_batch {
+    std::unique_ptr<plamo::BatchImpl> impl;
+    plamo_runtime* rt;
+};
+
+namespace {
+void set_err(char* err, size_t len, const std::string& m) {
+    if (err && len) {
+        std::snprintf(err, len, "%s", m.c_str());
+    }
+}
+
+int guard(char* err, size_t len, const std::function<void()>& f) {
+    try {
+        f();
+        return PLAMO_OK;
+    } catch (const plamo::Error& e) {
+        set_err(err, len, e.what());
+        return e.code;
+    } catch (const std::bad_alloc&) {
+        set_err(err, len, "out of host memory");
+        return PLAMO_EDEVICE;
+    } catch (const std::exception& e) {
+        set_err(err, len, e.what());
+        return PLAMO_EFORMAT;
+    }
+}
+
+std::vector<std::vector<int32_t>> split_prompts(const int32_t* tokens, const int32_t* lengths, int32_t count) {
+    if (count < 1 || count > 4 || !tokens || !lengths) throw plamo::Error(plamo::E_INVAL, "Expected one to four valid prompts");
+    std::vector<std::vector<int32_t>> p;
+    size_t off = 0;
+    for (int i = 0; i < count; ++i) {
+        if (lengths[i] < 0) throw plamo::Error(plamo::E_INVAL, "Expected one to four valid prompts");
+        p.emplace_back(tokens + off, tokens + off + lengths[i]);
+        off += size_t(lengths[i]);
+    }
+    return p;
+}
+
+// decodeBatch (BatchDecode.swift:8-37)
+struct LaneOutput {
+    std::vector<int32_t> ids;
+    int reason = 0;
+};
+
+std::vector<LaneOutput> decode_batch(const std::vector<int32_t>& initial, const std::vector<int32_t>& limits,
+                                     const std::function<std::vector<int32_t>(const std::vector<int32_t>&)>& step,
+                                     const std::function<void(int, int)>& emit,
+                                     const std::function<void(int, const LaneOutput&)>& finish, bool stop_on_truncation) {
+    const int count = int(initial.size());
+    bool ok = count >= 1 && count <= 4 && int(limits.size()) == count;
+    for (int i = 0; ok && i < count; ++i) ok = initial[i] >= 0 && initial[i] < plamo::VOCAB && limits[i] >= 0 && limits[i] <= 8191;
+    if (!ok) throw plamo::Error(plamo::E_INVAL, "Invalid quad decode inputs");
+    std::vector<int32_t> next = initial;
+    std::vector<LaneOutput> out(count);
+    int last = count - 1;
+    auto pending = [&]() {
+        for (int i = 0; i <= last; ++i)
+            if (!out[i].reason) return true;
+        return false;
+    };
+    while (pending()) {
+        std::vector<int32_t> tokens(count, -1);
+        for (int lane = 0; lane < count; ++lane) {
+            if (lane > last) break;
+            if (out[lane].reason) continue;
+            if (int(out[lane].ids.size()) == limits[lane]) out[lane].reason = PLAMO_REASON_LENGTH;
+            else if (next[lane] == 1 || next[lane] == 16) out[lane].reason = PLAMO_REASON_STOP;
+            else {
+                out[lane].ids.push_back(next[lane]);
+                emit(lane, next[lane]);
+                if (int(out[lane].ids.size()) == limits[lane]) out[lane].reason = PLAMO_REASON_LENGTH;
+                else tokens[lane] = next[lane];
+            }
+            if (out[lane].reason) {
+                if (stop_on_truncation && out[lane].reason == PLAMO_REASON_LENGTH) last = std::min(last, lane);
+                finish(lane, out[lane]);
+            }
+        }
+        bool any = false;
+        for (int32_t t : tokens) any |= t >= 0;
+        if (!any) break;
+        next = step(tokens);
+        bool valid = int(next.size()) == count;
+        for (int i = 0; valid && i < count; ++i) valid = next[i] >= 0 && next[i] < plamo::VOCAB;
+        if (!valid) throw plamo::Error(plamo::E_INVAL, "Invalid quad predictions");
+    }
+    out.resize(size_t(last) + 1);
+    return out;
+}
+
+struct CallbackAbort {};
+
+void write_outputs(const std::vector<LaneOutput>& res, int32_t* ids, int32_t stride, int32_t* lengths, int32_t* reasons,
+                   int32_t* lanes) {
+    for (size_t i = 0; i < res.size(); ++i) {
+        const int n = int(res[i].ids.size());
+        if (n > stride) throw plamo::Error(plamo::E_INVAL, "output buffer too small");
+        if (ids) std::memcpy(ids + i * size_t(stride), res[i].ids.data(), size_t(n) * 4);
+        if (lengths) lengths[i] = n;
+        if (reasons) reasons[i] = res[i].reason;
+    }
+    if (lanes) *lanes = int32_t(res.size());
+}
+}  // namespace
+
+extern "C" {
+
+const char* plamo_version(void) {
+    static char text[96];
+    std::snprintf(text, sizeof(text), "plamo_hip 0.1 gfx950 HIP %d.%d.%d", HIP_VERSION_MAJOR, HIP_VERSION_MINOR,
+                  HIP_VERSION_PATCH);
+    return text;
+}
+
+int plamo_open(const char* directory, int32_t context, int32_t packed, const char* sha, plamo_runtime** out, char* err,
+               size_t errlen) {
+    return guard(err, errlen, [&] {
+        if (!out || !directory) throw plamo::Error(plamo::E_INVAL, "null argument");
+        *out = nullptr;
+        if (context < 1 || context > plamo::MAX_CONTEXT) throw plamo::Error(plamo::E_INVAL, "Context must be 1...32768");
+        auto rt = std::make_unique<plamo_runtime>();
+        auto& r = rt->impl;
+        r.context = context;
+        int dev = 0;
+        if (hipGetDeviceCount(&dev) != hipSuccess || dev < 1)
+            throw plamo::Error(plamo::E_DEVICE, "An MI355X (gfx950) HIP device is required");
+        PLAMO_HIP(hipStreamCreateWithFlags(&r.stream, hipStreamNonBlocking));
+        r.model = plamo::load_model(directory, context, packed != 0, sha ? sha : "", r.stream);
+        r.eng = std::make_unique<plamo::Engine>(r.model, context, 1, r.stream);
+        *out = rt.release();
+    });
+}
+
+void plamo_close(plamo_runtime* rt) { delete rt; }
+
+void plamo_reset(plamo_runtime* rt) {
+    if (rt) rt->impl.reset();
+}
+
+int plamo_forward(plamo_runtime* rt, const int32_t* tokens, int32_t count, int32_t output, int32_t* next, char* err,
+                  size_t errlen) {
+    return guard(err, errlen, [&] {
+        if (!rt || (!tokens && count)) throw plamo::Error(plamo::E_INVAL, "Invalid tokens or context exhausted");
+        const int n = rt->impl.forward(tokens, count, output != 0);
+        if (next) *next = n;
+    });
+}
+
+int plamo_prefill(plamo_runtime* rt, const int32_t* tokens, int32_t count, int32_t* next, char* err, size_t errlen) {
+    return guard(err, errlen, [&] {
+        if (!rt || (!tokens && count)) throw plamo::Error(plamo::E_INVAL, "Input exceeds context");
+        const int n = rt->impl.prefill(tokens, count);
+        if (next) *next = n;
+    });
+}
+
+int plamo_logits_bf16(plamo_runtime* rt, int32_t slot, uint16_t* bits, char* err, size_t errlen) {
+    return guard(err, errlen, [&] {
+        if (!rt || !bits || slot < 0 || slot >= std::max(1, rt->impl.last_output_rows))
+            throw plamo::Error(plamo::E_INVAL, "Invalid logits slot");
+        PLAMO_HIP(hipMemcpy(bits, rt->impl.eng->logits + size_t(slot) * plamo::VOCAB, plamo::VOCAB * 2,
+                            hipMemcpyDeviceToHost));
+    });
+}
+
+int plamo_logits(plamo_runtime* rt, int32_t slot, float* values, char* err, size_t errlen) {
+    std::vector<uint16_t> b(plamo::VOCAB);
+    int rc = plamo_logits_bf16(rt, slot, b.data(), err, errlen);
+    if (rc) return rc;
+    if (!values) return PLAMO_EINVAL;
+    for (int i = 0; i < plamo::VOCAB; ++i) values[i] = plamo::host_bf(b[i]);
+    return PLAMO_OK;
+}
+
+int plamo_hidden(plamo_runtime* rt, float* values, char* err, size_t errlen) {
+    return guard(err, errlen, [&] {
+        if (!rt || !values) throw plamo::Error(plamo::E_INVAL, "null argument");
+        PLAMO_HIP(hipMemcpy(values, rt->impl.eng->hidden, plamo::HIDDEN * 4, hipMemcpyDeviceToHost));
+    });
+}
+
+int plamo_predictions(plamo_runtime* rt, int32_t* out, int32_t capacity, int32_t* count) {
+    if (!rt) return PLAMO_EINVAL;
+    const int n = rt->impl.last_output_rows ? int(rt->impl.predictions.size()) : 0;
+    for (int i = 0; i < n && i < capacity; ++i) out[i] = rt->impl.predictions[i];
+    if (count) *count = n;
+    return PLAMO_OK;
+}
+
+int plamo_get_stats(plamo_runtime* rt, plamo_stats* s) {
+    if (!rt || !s) return PLAMO_EINVAL;
+    auto& r = rt->impl;
+    s->position = r.position;
+    s->gpu_seconds = r.gpu_seconds;
+    s->device_bytes = int64_t(r.model->arena.bytes() + r.eng->arena.bytes());
+    s->weight_bytes = r.model->weight_bytes;
+    s->linear_bytes = r.model->linear_bytes;
+    s->context = r.context;
+    s->packed = r.model->packed ? 1 : 0;
+    s->last_output_rows = r.last_output_rows;
+    s->local_capacity = r.eng->local_capacity;
+    return PLAMO_OK;
+}
+
+int plamo_kv(plamo_runtime* rt, int32_t layer, uint16_t* keys, uint16_t* values, int32_t* capacity, char* err,
+             size_t errlen) {
+    return guard(err, errlen, [&] {
+        if (!rt || layer < 0 || layer >= plamo::LAYERS) throw plamo::Error(plamo::E_INVAL, "Invalid layer");
+        auto& e = *rt->impl.eng;
+        const size_t n = size_t(e.capacity[layer]) * plamo::HEAD_DIM * 2;
+        if (keys) PLAMO_HIP(hipMemcpy(keys, e.keys[layer], n, hipMemcpyDeviceToHost));
+        if (values) PLAMO_HIP(hipMemcpy(values, e.values[layer], n, hipMemcpyDeviceToHost));
+        if (capacity) *capacity = e.capacity[layer];
+    });
+}
+
+int plamo_set_sampling(plamo_runtime* rt, float penalty, float frequency, float presence, int32_t ngram) {
+    if (!rt) return PLAMO_EINVAL;
+    auto& r = rt->impl;
+    r.penalty = penalty;
+    r.frequency = frequency;
+    r.presence = presence;
+    r.ngram = ngram;
+    r.sampling = penalty != 1.0f || frequency != 0.0f || presence != 0.0f || ngram > 1;
+    return PLAMO_OK;
+}
+
+int plamo_sampler_observe(plamo_runtime* rt, int32_t id) {
+    if (!rt) return PLAMO_EINVAL;
+    rt->impl.history.push_back(id);
+    return PLAMO_OK;
+}
+
+int plamo_generate(plamo_runtime* rt, const int32_t* prompt, int32_t count, int32_t max_tokens, int32_t* out_ids,
+                   int32_t* out_count, int32_t* stop_reason, char* err, size_t errlen) {
+    return guard(err, errlen, [&] {
+        if (!rt || !prompt) throw plamo::Error(plamo::E_INVAL, "null argument");
+        int reason = 0;
+        auto ids = rt->impl.generate(prompt, count, max_tokens, &reason);
+        if (out_ids && !ids.empty()) std::memcpy(out_ids, ids.data(), ids.size() * 4);
+        if (out_count) *out_count = int32_t(ids.size());
+        if (stop_reason) *stop_reason = reason == 1 ? 1 : 0;
+        if (reason == 3) throw plamo::Error(plamo::E_INVAL, "Invalid tokens or context exhausted");
+    });
+}
+
+int plamo_bench_decode(plamo_runtime* rt, int32_t steps, double* ms, char* err, size_t errlen) {
+    return guard(err, errlen, [&] {
+        if (!rt) throw plamo::Error(plamo::E_INVAL, "null argument");
+        const double v = rt->impl.bench_decode(steps);
+        if (ms) *ms = v;
+    });
+}
+
+// ---------------------------------------------------------------------------- batch
+int plamo_batch_open(plamo_runtime* rt, plamo_batch** out, char* err, size_t errlen) {
+    return guard(err, errlen, [&] {
+        if (!rt || !out) throw plamo::Error(plamo::E_INVAL, "null argument");
+        auto b = std::make_unique<plamo_batch>();
+        b->rt = rt;
+        b->impl = std::make_unique<plamo::BatchImpl>(&rt->impl);
+        *out = b.release();
+    });
+}
+
+void plamo_batch_close(plamo_batch* b) { delete b; }
+
+int plamo_batch_prefill(plamo_batch* b, const int32_t* tokens, const int32_t* lengths, int32_t count, int32_t* next,
+                        char* err, size_t errlen) {
+    return guard(err, errlen, [&] {
+        if (!b) throw plamo::Error(plamo::E_INVAL, "null argument");
+        auto res = b->impl->prefill(split_prompts(tokens, lengths, count));
+        if (next) std::memcpy(next, res.data(), res.size() * 4);
+    });
+}
+
+int plamo_batch_step(plamo_batch* b, const int32_t* tokens, int32_t count, int32_t* next, char* err, size_t errlen) {
+    return guard(err, errlen, [&] {
+        if (!b || !tokens || count < 0) throw plamo::Error(plamo::E_INVAL, "Invalid quad step or context exhausted");
+        auto res = b->impl->step(std::vector<int32_t>(tokens, tokens + count));
+        if (next) std::memcpy(next, res.data(), res.size() * 4);
+    });
+}
+
+void plamo_batch_reset(plamo_batch* b) {
+    if (b) b->impl->reset();
+}
+
+int plamo_batch_logits_bf16(plamo_batch* b, int32_t lane, uint16_t* bits, char* err, size_t errlen) {
+    return guard(err, errlen, [&] {
+        if (!b || !bits || lane < 0 || lane >= plamo::ROWS) throw plamo::Error(plamo::E_INVAL, "Invalid lane");
+        PLAMO_HIP(hipMemcpy(bits, b->impl->lane_logits + size_t(lane) * plamo::VOCAB, plamo::VOCAB * 2,
+                            hipMemcpyDeviceToHost));
+    });
+}
+
+int plamo_batch_hidden(plamo_batch* b, int32_t lane, float* values, char* err, size_t errlen) {
+    return guard(err, errlen, [&] {
+        if (!b || !values || lane < 0 || lane >= plamo::ROWS) throw plamo::Error(plamo::E_INVAL, "Invalid lane");
+        PLAMO_HIP(hipMemcpy(values, b->impl->lane_hidden + size_t(lane) * plamo::HIDDEN, plamo::HIDDEN * 4,
+                            hipMemcpyDeviceToHost));
+    });
+}
+
+int plamo_batch_kv(plamo_batch* b, int32_t lane, int32_t layer, uint16_t* keys, uint16_t* values, int32_t* capacity,
+                   char* err, size_t errlen) {
+    return guard(err, errlen, [&] {
+        if (!b || lane < 0 || lane >= plamo::ROWS || layer < 0 || layer >= plamo::LAYERS)
+            throw plamo::Error(plamo::E_INVAL, "Invalid lane or layer");
+        auto& e = *b->impl->eng;
+        const size_t n = size_t(e.capacity[layer]) * plamo::HEAD_DIM;
+        if (keys) PLAMO_HIP(hipMemcpy(keys, e.keys[layer] + size_t(lane) * n, n * 2, hipMemcpyDeviceToHost));
+        if (values) PLAMO_HIP(hipMemcpy(values, e.values[layer] + size_t(lane) * n, n * 2, hipMemcpyDeviceToHost));
+        if (capacity) *capacity = e.capacity[layer];
+    });
+}
+
+int plamo_batch_positions(plamo_batch* b, int32_t* out, int32_t capacity, int32_t* count) {
+    if (!b) return PLAMO_EINVAL;
+    const auto& p = b->impl->positions;
+    for (size_t i = 0; i < p.size() && int32_t(i) < capacity; ++i) out[i] = int32_t(p[i]);
+    if (count) *count = int32_t(p.size());
+    return PLAMO_OK;
+}
+
+int plamo_decode_batch(const int32_t* initial, const int32_t* limits, int32_t count, plamo_step_fn step,
+                       plamo_emit_fn emit, plamo_finish_fn finish, void* user, int32_t stop_on_truncation, int32_t* ids,
+                       int32_t ids_stride, int32_t* lengths, int32_t* reasons, int32_t* lanes, char* err,
+                       size_t errlen) {
+    return guard(err, errlen, [&] {
+        if (!initial || !limits || !step || count < 1 || count > 4)
+            throw plamo::Error(plamo::E_INVAL, "Invalid quad decode inputs");
+        auto res = decode_batch(
+            std::vector<int32_t>(initial, initial + count), std::vector<int32_t>(limits, limits + count),
+            [&](const std::vector<int32_t>& t) {
+                std::vector<int32_t> next(size_t(count), -1);
+                if (step(user, t.data(), count, next.data()) != 0)
+                    throw plamo::Error(plamo::E_STATE, "step callback aborted");
+                return next;
+            },
+            [&](int lane, int id) {
+                if (emit && emit(user, lane, id) != 0) throw plamo::Error(plamo::E_STATE, "emit callback aborted");
+            },
+            [&](int lane, const LaneOutput& o) {
+                if (finish && finish(user, lane, o.ids.data(), int32_t(o.ids.size()), o.reason) != 0)
+                    throw plamo::Error(plamo::E_STATE, "finish callback aborted");
+            },
+            stop_on_truncation != 0);
+        write_outputs(res, ids, ids_stride, lengths, reasons, lanes);
+    });
+}
+
+int plamo_batch_generate(plamo_batch* b, const int32_t* tokens, const int32_t* lengths, const int32_t* limits,
+                         int32_t count, int32_t stop_on_truncation, int32_t* ids, int32_t ids_stride,
+                         int32_t* out_lengths, int32_t* reasons, int32_t* lanes, char* err, size_t errlen) {
+    return guard(err, errlen, [&] {
+        if (!b || !limits) throw plamo::Error(plamo::E_INVAL, "Quad output budget exceeds context");
+        auto prompts = split_prompts(tokens, lengths, count);
+        // Batch.generate (BatchDecode.swift:40-47)
+        for (int i = 0; i < count; ++i)
+            if (limits[i] < 0 || limits[i] > 8191 || int64_t(prompts[i].size()) + limits[i] > b->rt->impl.context)
+                throw plamo::Error(plamo::E_INVAL, "Quad output budget exceeds context");
+        try {
+            auto first = b->impl->prefill(prompts);
+            auto res = decode_batch(
+                first, std::vector<int32_t>(limits, limits + count),
+                [&](const std::vector<int32_t>& t) { return b->impl->step(t); }, [](int, int) {},
+                [](int, const LaneOutput&) {}, stop_on_truncation != 0);
+            write_outputs(res, ids, ids_stride, out_lengths, reasons, lanes);
+        } catch (...) {
+            b->impl->reset();
+            throw;
+        }
+    });
+}
+
+// ------------------------------------------------------------------- weight formats
+int plamo_pack(const char* src, const char* out, const char* sha, plamo_pack_report* report, char* err, size_t errlen) {
+    return guard(err, errlen, [&] {
+        if (!src || !out) throw plamo::Error(plamo::E_INVAL, "null argument");
+        auto r = plamo::pack_archive(src, out, sha ? sha : "");
+        if (report) {
+            report->original_linear_bytes = r.original_linear_bytes;
+            report->packed_linear_bytes = r.packed_linear_bytes;
+            report->archive_bytes = r.archive_bytes;
+            report->compressed_blocks = r.compressed_blocks;
+            report->blocks = r.blocks;
+        }
+    });
+}
+
+int plamo_check_weights(const char* path, const char* name, const int64_t* shape, int32_t ndim, char* err, size_t errlen) {
+    return guard(err, errlen, [&] {
+        plamo::SafeTensors st(path ? path : "");
+        if (name) st.tensor(name, std::vector<int64_t>(shape, shape + ndim));
+    });
+}
+
+int plamo_check_packed(const char* path, const char* sha, const char* name, const int64_t* shape, int32_t ndim,
+                       int32_t* is_packed, char* err, size_t errlen) {
+    return guard(err, errlen, [&] {
+        plamo::PackedArchive pk(path ? path : "", sha ? sha : "");
+        if (name) {
+            auto t = pk.tensor(name, std::vector<int64_t>(shape, shape + ndim));
+            if (is_packed) *is_packed = t.blocked ? 1 : 0;
+        }
+    });
+}
+
+// ------------------------------------------------------------------- kernel entries
+int plamo_kernel_linear(uint64_t w, uint64_t table, uint64_t x, uint64_t y, int32_t n, int32_t m, int32_t rows,
+                        int32_t mode, uint64_t stream) {
+    return guard(nullptr, 0, [&] {
+        if (rows < 1 || rows > plamo::ROWS || m < 4 || (n != 1536 && n != 2048 && n != 6144) ||
+            m % (n >= 6144 ? 2 : 4) != 0 || (mode != 0 && mode != 2))
+            throw plamo::Error(plamo::E_INVAL, "unsupported linear shape");
+        plamo::GemvParams g{};
+        g.w = reinterpret_cast<const uint16_t*>(w);
+        g.table = reinterpret_cast<const uint32_t*>(table);
+        g.m = m;
+        g.rows = rows;
+        g.in = reinterpret_cast<const float*>(x);
+        g.out = reinterpret_cast<float*>(y);
+        g.out16 = reinterpret_cast<uint16_t*>(y);
+        const int groups = m / (n >= 6144 ? 2 : 4);
+        const int blocks = std::max(1, std::min(4096, (groups + 3) / 4));
+        plamo::launch_gemv(n, table != 0, rows == 1 ? 1 : plamo::ROWS, plamo::PRO_PLAIN,
+                           mode == 2 ? plamo::EPI_BF16 : plamo::EPI_ROUND, g, blocks,
+                           reinterpret_cast<hipStream_t>(stream));
+        PLAMO_HIP(hipGetLastError());
+    });
+}
+
+int plamo_kernel_unpack(uint64_t payload, uint64_t table, uint64_t out, int64_t count, uint64_t stream) {
+    return guard(nullptr, 0, [&] {
+        plamo::launch_unpack(reinterpret_cast<const uint8_t*>(payload), reinterpret_cast<const uint32_t*>(table),
+                             reinterpret_cast<uint16_t*>(out), count, reinterpret_cast<hipStream_t>(stream));
+        PLAMO_HIP(hipGetLastError());
+    });
+}
+
+int plamo_kernel_argmax(uint64_t x, uint64_t out, int32_t n, int32_t rows, int32_t bf16, uint64_t stream) {
+    return guard(nullptr, 0, [&] {
+        if (n < 1 || rows < 1) throw plamo::Error(plamo::E_INVAL, "bad argmax shape");
+        plamo::launch_argmax(reinterpret_cast<const void*>(x), reinterpret_cast<uint32_t*>(out), n, rows, bf16 != 0,
+                             reinterpret_cast<hipStream_t>(stream));
+        PLAMO_HIP(hipGetLastError());
+    });
+}
+
+int plamo_kernel_select(uint64_t logits, int32_t n, uint64_t history, int32_t hist, float penalty, int32_t ngram,
+                        float frequency, float presence, uint64_t out, uint64_t stream) {
+    return guard(nullptr, 0, [&] {
+        if (n < 1 || hist < 0) throw plamo::Error(plamo::E_INVAL, "bad select shape");
+        plamo::launch_select(reinterpret_cast<float*>(logits), n, reinterpret_cast<const int32_t*>(history), hist,
+                             penalty, ngram, frequency, presence, reinterpret_cast<int32_t*>(out),
+                             reinterpret_cast<hipStream_t>(stream));
+        PLAMO_HIP(hipGetLastError());
+    });
+}
+
+int plamo_kernel_gemm(uint64_t w, uint64_t table, uint64_t x, uint64_t y, int32_t n, int32_t m, int32_t tokens,
+                      int32_t out_bf16, uint64_t stream) {
+    return guard(nullptr, 0, [&] {
+        if (n % 128 != 0 || m < 1 || tokens < 1) throw plamo::Error(plamo::E_INVAL, "bad GEMM shape");
+        plamo::GemmParams g{};
+        g.w = reinterpret_cast<const uint16_t*>(w);
+        g.table = reinterpret_cast<const uint32_t*>(table);
+        g.x = reinterpret_cast<const uint16_t*>(x);
+        g.y = reinterpret_cast<float*>(y);
+        g.y16 = reinterpret_cast<uint16_t*>(y);
+        g.m = m;
+        g.k = n;
+        g.tokens = tokens;
+        plamo::launch_gemm(table != 0, out_bf16 ? plamo::GEMM_BF16 : plamo::GEMM_F32, g,
+                           reinterpret_cast<hipStream_t>(stream));
+        PLAMO_HIP(hipGetLastError());
+    });
+}
+
+}  // extern "C"

@@ -1,0 +1,80 @@
+// Device helpers shared by the gfx950 kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace plamo {
+namespace dev {
+
+constexpr float SCALE = 0.08838834764831845f;  // 1/sqrt(128) (Kernels.metal:372)
+constexpr float NEG_INF = -__builtin_inff();
+
+// BF16 <-> FP32 exactly as Kernels.metal:5-10: integer round-to-nearest-even on the FP32
+// bit pattern with wrap-around and no NaN special case.
+__device__ __forceinline__ float bf(uint32_t h) { return __uint_as_float(h << 16); }
+__device__ __forceinline__ uint32_t bits(float x) {
+    const uint32_t u = __float_as_uint(x);
+    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+__device__ __forceinline__ float roundbf(float x) { return bf(bits(x)); }
+__device__ __forceinline__ float lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// Butterfly reductions over the 64-lane wavefront; every lane ends with the same bits.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+// Reduction over aligned groups of 16 lanes.
+__device__ __forceinline__ float group16_sum(float v) {
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// a.b over 8 BF16 pairs packed in two uint4, accumulated in element order.
+__device__ __forceinline__ float dot8(const uint4 w, const uint4 x, float acc) {
+    acc = fmaf(lo(w.x), lo(x.x), acc);
+    acc = fmaf(hi(w.x), hi(x.x), acc);
+    acc = fmaf(lo(w.y), lo(x.y), acc);
+    acc = fmaf(hi(w.y), hi(x.y), acc);
+    acc = fmaf(lo(w.z), lo(x.z), acc);
+    acc = fmaf(hi(w.z), hi(x.z), acc);
+    acc = fmaf(lo(w.w), lo(x.w), acc);
+    acc = fmaf(hi(w.w), hi(x.w), acc);
+    return acc;
+}
+
+// .p12 decode of the 8 weights a lane owns inside a 128-weight block
+// (Kernels.metal:23-44): sm = 8 sign/mantissa bytes, nib = 8 exponent codes.
+__device__ __forceinline__ uint32_t p12_word(uint32_t s, uint32_t code, uint32_t minimum) {
+    const uint32_t e = code == 15u ? 0u : minimum + code;
+    return (s & 127u) | ((s & 128u) << 8) | (e << 7);
+}
+__device__ __forceinline__ uint4 p12_decode8(uint2 sm, uint32_t nib, uint32_t tag) {
+    const uint32_t m = tag + 107u;
+    uint4 r;
+    r.x = p12_word(sm.x & 255u, nib & 15u, m) | (p12_word((sm.x >> 8) & 255u, (nib >> 4) & 15u, m) << 16);
+    r.y = p12_word((sm.x >> 16) & 255u, (nib >> 8) & 15u, m) | (p12_word(sm.x >> 24, (nib >> 12) & 15u, m) << 16);
+    r.z = p12_word(sm.y & 255u, (nib >> 16) & 15u, m) | (p12_word((sm.y >> 8) & 255u, (nib >> 20) & 15u, m) << 16);
+    r.w = p12_word((sm.y >> 16) & 255u, (nib >> 24) & 15u, m) | (p12_word(sm.y >> 24, nib >> 28, m) << 16);
+    return r;
+}
+
+// Rotate-half RoPE of the pair (a = x[d], b = x[d+64]) (Kernels.metal:261-274):
+// out[d] = roundbf(roundbf(a*c) + roundbf(-b*s)), out[d+64] = roundbf(roundbf(b*c) + roundbf(a*s)).
+__device__ __forceinline__ void rope_pair(float a, float b, float2 cs, float& ra, float& rb) {
+    ra = roundbf(roundbf(a * cs.x) + roundbf(-b * cs.y));
+    rb = roundbf(roundbf(b * cs.x) + roundbf(a * cs.y));
+}
+
+}  // namespace dev
+}  // namespace plamo

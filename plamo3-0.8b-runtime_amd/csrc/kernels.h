@@ -1,0 +1,106 @@
+// Kernel parameter blocks and host-side launchers (defined in the .hip files).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace plamo {
+
+constexpr int ROWS = 4;       // activation rows of one decode step (Batch lanes)
+constexpr int KEYS_PER_PART = 64;  // keys per split-K decode attention partition
+constexpr int HEAD_BLOCKS = 1024;  // workgroups of the LM-head GEMV (argmax partials)
+
+// Per-step state kept in device memory so one captured graph replays every step.
+struct StepState {
+    uint32_t rows;            // active rows (1..4)
+    uint32_t stopped;         // device loop finished: every kernel returns at once
+    uint32_t loop;            // device-driven loop: feed `next` back as `token`, advance pos
+    uint32_t stop_enabled;    // loop stops on token 1 or 16 (Main.swift:279)
+    uint32_t max_tokens;      // loop: emitted-token limit
+    uint32_t produced;        // loop: tokens emitted so far
+    uint32_t reason;          // loop: 1 stop, 2 length, 3 invalid token
+    uint32_t sampling;        // Sampler.select controls active
+    float penalty, frequency, presence;
+    int32_t ngram;
+    uint32_t lane[ROWS];      // KV slice of each row
+    uint32_t pos[ROWS];       // absolute position of each row's input token
+    int32_t token[ROWS];      // input token of each row
+    uint32_t next[ROWS];      // selected next token of each row
+    uint32_t hist_len[ROWS];  // generated-history length (sampler)
+    uint32_t counted[ROWS];   // history entries already folded into the counts
+};
+
+// Buffers the decode kernels share.
+struct DecodeBuffers {
+    StepState* state;
+    int32_t* out_ids;         // loop: emitted tokens
+    int32_t* history;         // [ROWS][hist_cap]
+    uint32_t hist_cap;
+    int32_t* counts;          // [ROWS][VOCAB]
+    uint32_t* banned;         // [ROWS][VOCAB/32]
+    float* head_v;            // [ROWS][HEAD_BLOCKS] argmax partials
+    uint32_t* head_i;
+    uint32_t* tickets;        // [1] LM-head ticket, zero between launches
+};
+
+enum Prologue { PRO_PLAIN = 0, PRO_EMBED = 1, PRO_RESID = 2 };
+enum Epilogue { EPI_ROUND = 0, EPI_SWIGLU = 1, EPI_LOGITS = 2, EPI_BF16 = 3 };
+
+struct GemvParams {
+    const uint16_t* w;        // plain BF16 [m][n] or .p12 payload
+    const uint32_t* table;    // .p12 block table (packed only)
+    int m;                    // weight rows
+    int rows;                 // activation rows when no StepState is given
+    const StepState* state;   // may be null (kernel-level entry points)
+    // prologue
+    const float* in;          // PLAIN: [rows][n]; RESID: projection output [rows][1536]
+    const float* resid_in;    // RESID: residual stream x
+    float* resid_out;         // EMBED/RESID: updated residual (written by block 0)
+    const uint16_t* g_post;   // RESID: post norm weight
+    float post_offset;
+    const uint16_t* g_next;   // EMBED/RESID: following norm weight (+1.0)
+    const uint16_t* embed;    // EMBED: embedding table [VOCAB][1536]
+    float* hidden;            // optional: normalised rows (final hidden)
+    // epilogue
+    float* out;               // ROUND/SWIGLU: FP32 [rows][m or m/2]
+    uint16_t* out16;          // LOGITS/BF16: [rows][m]
+    DecodeBuffers bufs;       // LOGITS: sampler + argmax partials + state update
+};
+
+struct AttnParams {
+    const StepState* state;   // decode: rows from the step state; null for prefill
+    uint32_t p0;              // prefill: position of token 0 (16-token RoPE groups start here)
+    uint32_t tokens;          // prefill: rows
+    uint32_t lane;            // prefill: KV slice
+    uint16_t* out16;          // prefill: BF16 output [tokens][2048]
+    const float* qkv;         // [rows][2304] (BF16-valued FP32)
+    const uint16_t* q_norm;   // [128]
+    const uint16_t* k_norm;
+    uint16_t* keys;           // [lanes][capacity][128]
+    uint16_t* values;
+    uint32_t capacity;
+    const float2* local_rope; // [2064][64] (cos, sin)
+    const float2* global_rope;// [context][64]
+    float* part_m;            // [ROWS][parts][16]
+    float* part_l;
+    float* part_o;            // [ROWS][parts][16][128]
+    uint32_t parts;           // grid.x
+    uint32_t* tickets;        // [rows], zero between launches
+    float* out;               // decode: FP32 [rows][2048]
+};
+
+// decode.hip
+void launch_gemv(int n, bool packed, int maxr, Prologue pro, Epilogue epi, const GemvParams& p, int blocks,
+                 hipStream_t s);
+void launch_attention(bool full, const AttnParams& p, int rows, hipStream_t s);
+void launch_step_begin(const DecodeBuffers& b, hipStream_t s);
+void launch_argmax(const void* x, uint32_t* out, int n, int rows, bool bf16, hipStream_t s);
+void launch_select(float* logits, int n, const int32_t* history, int hist, float penalty, int ngram, float frequency,
+                   float presence, int32_t* out, hipStream_t s);
+void launch_unpack(const uint8_t* payload, const uint32_t* table, uint16_t* out, int64_t count, hipStream_t s);
+void launch_fill_u32(uint32_t* p, uint32_t value, size_t count, hipStream_t s);
+
+// prefill.hip
+struct PrefillParams;
+}  // namespace plamo

@@ -1,0 +1,47 @@
+// Parameter blocks of the prefill kernels (prefill.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace plamo {
+
+enum GemmEpilogue { GEMM_F32 = 0, GEMM_BF16 = 1, GEMM_SWIGLU = 2 };
+
+struct GemmParams {
+    const uint16_t* w;      // plain BF16 [m][k] or .p12 payload
+    const uint32_t* table;  // .p12 block table
+    const uint16_t* x;      // BF16 [tokens][k]
+    float* y;               // F32: [tokens][m]
+    uint16_t* y16;          // BF16: [tokens][m]; SWIGLU: [tokens][6144]
+    int m, k, tokens;
+};
+
+struct RowsNormParams {
+    const int32_t* tokens_in;  // embedding mode when set
+    const uint16_t* embed;
+    const float* in;           // residual mode: projection output [T][1536]
+    const uint16_t* g_post;
+    float post_offset;
+    float* x;                  // residual stream [T][1536] (updated in place)
+    const uint16_t* g_next;
+    uint16_t* xn;              // next-norm output BF16 [T][1536] (optional)
+};
+
+struct KvWriteParams {
+    const float* qkv;          // [T][2304]
+    const uint16_t* k_norm;
+    uint16_t* keys;            // lane slice [capacity][128]
+    uint16_t* values;
+    uint32_t capacity, p0;
+    int tokens;
+    int full;
+    const float2* global_rope;
+};
+
+void launch_gemm(bool packed, GemmEpilogue epi, const GemmParams& p, hipStream_t s);
+void launch_rows_norm(const RowsNormParams& p, int tokens, hipStream_t s);
+void launch_kv_write(const KvWriteParams& p, hipStream_t s);
+
+}  // namespace plamo

@@ -1,0 +1,815 @@
+// Host runtime: model upload, KV management, decode step graph, prefill, batch lanes.
+#include "runtime.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstdlib>
+#include <fstream>
+#include <sstream>
+
+#include "formats.h"
+#include "json.h"
+
+namespace plamo {
+
+// ------------------------------------------------------------------------------ arena
+DeviceArena::~DeviceArena() {
+    for (void* p : ptrs_) (void)hipFree(p);
+}
+
+void* DeviceArena::alloc(size_t bytes) {
+    void* p = nullptr;
+    const size_t n = std::max<size_t>(256, (bytes + 255) / 256 * 256);
+    PLAMO_HIP(hipMalloc(&p, n));
+    ptrs_.push_back(p);
+    bytes_ += n;
+    return p;
+}
+
+// ------------------------------------------------------------------------- model load
+namespace {
+std::string read_text(const std::string& path) {
+    std::ifstream f(path, std::ios::binary);
+    if (!f) throw Error(E_IO, "Cannot read " + path);
+    std::stringstream ss;
+    ss << f.rdbuf();
+    return ss.str();
+}
+
+// Runtime.swift:180-190
+void validate_config(const std::string& dir) {
+    const std::string msg = "Only the original BF16 PLaMo 3 Translate 0.8B configuration is supported";
+    json::Value c;
+    try {
+        c = json::parse(read_text(dir + "/config.json"));
+    } catch (const Error&) {
+        throw;
+    } catch (const std::exception&) {
+        throw Error(E_FORMAT, msg);
+    }
+    const std::pair<const char*, int64_t> ints[] = {
+        {"hidden_size", 1536}, {"num_hidden_layers", 16}, {"num_attention_heads", 16}, {"num_key_value_heads", 1},
+        {"head_dim", 128}, {"intermediate_size", 6144}, {"vocab_size", 107520}, {"window_size", 2048},
+        {"sliding_window_pattern", 8}};
+    for (auto& kv : ints) {
+        const json::Value* v = c.get(kv.first);
+        if (!v || v->kind != json::Value::Number || v->num != double(kv.second)) throw Error(E_FORMAT, msg);
+    }
+    auto is_false = [&](const char* k) {
+        const json::Value* v = c.get(k);
+        return v && v->kind == json::Value::Bool && !v->b;
+    };
+    auto is_str = [&](const char* k, const char* s) {
+        const json::Value* v = c.get(k);
+        return v && v->kind == json::Value::String && v->str == s;
+    };
+    auto is_num = [&](const char* k, double d) {
+        const json::Value* v = c.get(k);
+        return v && v->kind == json::Value::Number && v->num == d;
+    };
+    if (!is_false("tie_word_embeddings") || !is_false("scale_embedding") || !is_str("model_type", "plamo3") ||
+        !is_str("dtype", "bfloat16") || !is_num("rope_theta", 1000000.0) || !is_num("rope_local_theta", 10000.0) ||
+        !is_num("rope_scaling_factor", 256.0) || !is_num("rms_norm_eps", 1e-6))
+        throw Error(E_FORMAT, msg);
+}
+
+// config-mlx.json plamo_rope_inv_freq (Runtime.swift:268-274)
+void read_frequencies(const std::string& dir, std::vector<double>& local, std::vector<double>& full) {
+    const std::string msg = "Missing source-exact RoPE frequencies in config-mlx.json";
+    json::Value c;
+    try {
+        c = json::parse(read_text(dir + "/config-mlx.json"));
+    } catch (const std::exception&) {
+        throw Error(E_FORMAT, msg);
+    }
+    const json::Value* f = c.get("plamo_rope_inv_freq");
+    const json::Value* l = f ? f->get("local") : nullptr;
+    const json::Value* g = f ? f->get("full") : nullptr;
+    if (!l || !g || l->kind != json::Value::Array || g->kind != json::Value::Array || l->arr.size() != 64 ||
+        g->arr.size() != 64)
+        throw Error(E_FORMAT, msg);
+    for (int i = 0; i < 64; ++i) {
+        if (l->arr[i].kind != json::Value::Number || g->arr[i].kind != json::Value::Number) throw Error(E_FORMAT, msg);
+        const double a = l->arr[i].num, b = g->arr[i].num;
+        if (!std::isfinite(a) || !std::isfinite(b) || a <= 0 || b <= 0) throw Error(E_FORMAT, msg);
+        local.push_back(a);
+        full.push_back(b);
+    }
+}
+
+// Local table: (bits(cos), bits(sin)) of float(pos)*f (Kernels.metal:212-219).  Global
+// factors: roundbf(roundbf(cos(angle))*1.5545177444479562f) (Kernels.metal:264-267).  cos
+// and sin of the FP32 angle are evaluated in double precision and rounded to FP32.
+std::vector<float2> rope_table(const std::vector<double>& freqs, int rows, bool global) {
+    std::vector<float2> t(size_t(rows) * 64);
+    const float mscale = 1.5545177444479562f;
+    for (int p = 0; p < rows; ++p)
+        for (int d = 0; d < 64; ++d) {
+            const float angle = float(p) * float(freqs[d]);
+            float c = host_bf(host_bits(float(std::cos(double(angle)))));
+            float s = host_bf(host_bits(float(std::sin(double(angle)))));
+            if (global) {
+                c = host_bf(host_bits(c * mscale));
+                s = host_bf(host_bits(s * mscale));
+            }
+            t[size_t(p) * 64 + d] = make_float2(c, s);
+        }
+    return t;
+}
+
+template <class T>
+T* upload(DeviceArena& a, const void* src, size_t bytes) {
+    T* p = static_cast<T*>(a.alloc(bytes));
+    PLAMO_HIP(hipMemcpy(p, src, bytes, hipMemcpyHostToDevice));
+    return p;
+}
+}  // namespace
+
+std::shared_ptr<Model> load_model(const std::string& dir, int context, bool packed, const std::string& sha,
+                                  hipStream_t) {
+    validate_config(dir);
+    SafeTensors st(dir + "/model.safetensors");
+    std::unique_ptr<PackedArchive> pk;
+    if (packed) pk = std::make_unique<PackedArchive>(dir + "/model.p12", sha);
+    std::vector<double> flocal, ffull;
+    // Tensor validation in the order of Runtime.swift:233-250 before any device work.
+    struct Req { std::string name; std::vector<int64_t> shape; };
+    std::vector<Req> reqs = {{"lm_head.weight", {VOCAB, HIDDEN}}, {"model.norm.weight", {HIDDEN}}};
+    for (int i = 0; i < LAYERS; ++i) {
+        const std::string p = "model.layers.layers." + std::to_string(i) + ".";
+        reqs.push_back({p + "pre_mixer_norm.weight", {HIDDEN}});
+        reqs.push_back({p + "post_mixer_norm.weight", {HIDDEN}});
+        reqs.push_back({p + "pre_mlp_norm.weight", {HIDDEN}});
+        reqs.push_back({p + "post_mlp_norm.weight", {HIDDEN}});
+        reqs.push_back({p + "mixer.qkv_proj.weight", {QKV, HIDDEN}});
+        reqs.push_back({p + "mixer.o_proj.weight", {HIDDEN, ATTN}});
+        reqs.push_back({p + "mixer.q_norm.weight", {HEAD_DIM}});
+        reqs.push_back({p + "mixer.k_norm.weight", {HEAD_DIM}});
+        reqs.push_back({p + "mlp.gate_up_proj.weight", {2 * INTER, HIDDEN}});
+        reqs.push_back({p + "mlp.down_proj.weight", {HIDDEN, INTER}});
+    }
+    std::vector<TensorView> views;
+    std::vector<PackedTensor> ptens;
+    for (auto& r : reqs) {
+        views.push_back(st.tensor(r.name, r.shape));
+        if (pk) ptens.push_back(pk->tensor(r.name, r.shape));
+    }
+    read_frequencies(dir, flocal, ffull);
+
+    auto m = std::make_shared<Model>();
+    m->packed = packed;
+    DeviceArena& a = m->arena;
+    const uint8_t* payload = nullptr;
+    if (pk) payload = upload<uint8_t>(a, pk->payload(), pk->payload_bytes());
+    size_t idx = 0;
+    auto linear = [&](int64_t rows, int64_t cols) {
+        Linear L;
+        if (pk) {
+            const PackedTensor& t = ptens[idx];
+            L.w = reinterpret_cast<const uint16_t*>(payload + t.data_offset);
+            L.table = reinterpret_cast<const uint32_t*>(payload + t.table_offset);
+            L.bytes = int64_t(t.data_bytes + t.blocks * 4);
+        } else {
+            L.w = upload<uint16_t>(a, views[idx].data, views[idx].bytes);
+            L.bytes = rows * cols * 2;
+        }
+        ++idx;
+        m->linear_bytes += L.bytes;
+        return L;
+    };
+    auto vec = [&]() {
+        const uint16_t* p;
+        if (pk) p = reinterpret_cast<const uint16_t*>(payload + ptens[idx].data_offset);
+        else p = upload<uint16_t>(a, views[idx].data, views[idx].bytes);
+        ++idx;
+        return p;
+    };
+    m->head = linear(VOCAB, HIDDEN);
+    m->final_norm = vec();
+    for (int i = 0; i < LAYERS; ++i) {
+        LayerWeights& L = m->layers[i];
+        L.pre = vec();
+        L.post = vec();
+        L.pre_mlp = vec();
+        L.post_mlp = vec();
+        L.qkv = linear(QKV, HIDDEN);
+        L.o = linear(HIDDEN, ATTN);
+        L.q_norm = vec();
+        L.k_norm = vec();
+        L.up = linear(2 * INTER, HIDDEN);
+        L.down = linear(HIDDEN, INTER);
+    }
+    // The input embedding moves to HBM so the gather runs inside the decode graph.
+    m->embed = upload<uint16_t>(a, st.embedding().data, st.embedding().bytes);
+    auto lt = rope_table(flocal, LOCAL_ROPE_ROWS, false);
+    auto gt = rope_table(ffull, context, true);
+    m->local_rope = upload<float2>(a, lt.data(), lt.size() * sizeof(float2));
+    m->global_rope = upload<float2>(a, gt.data(), gt.size() * sizeof(float2));
+    m->weight_bytes = int64_t(a.bytes());
+    return m;
+}
+
+// ----------------------------------------------------------------------------- engine
+Engine::Engine(std::shared_ptr<Model> mdl, int ctx, int nl, hipStream_t s)
+    : model(std::move(mdl)), context(ctx), lanes(nl), stream(s) {
+    const char* ng = std::getenv("PLAMO_NO_GRAPH");
+    use_graph = !(ng && ng[0] == '1');
+    const int parts_max = (context + KEYS_PER_PART - 1) / KEYS_PER_PART;
+    // Prefill chunk: up to 2048 tokens, bounded so the split-K partials stay under 1 GiB.
+    const size_t part_bytes = size_t(HEADS) * (HEAD_DIM + 2) * 4;
+    size_t c = (size_t(1) << 30) / (size_t(parts_max) * part_bytes);
+    c = std::max<size_t>(CHUNK, std::min<size_t>(2048, c / CHUNK * CHUNK));
+    chunk = int(std::min<size_t>(c, size_t((context + CHUNK - 1) / CHUNK * CHUNK)));
+    // Ring = window + one prefill chunk (the reference's rule with its 16-token chunk,
+    // Runtime.swift:240): the chunk's keys and the 2047 before it are resident at once.
+    local_capacity = std::min(context, WINDOW + chunk);
+    for (int l = 0; l < LAYERS; ++l) {
+        capacity[l] = is_global_layer(l) ? context : local_capacity;
+        const size_t n = size_t(lanes) * capacity[l] * HEAD_DIM;
+        keys[l] = arena.alloc_n<uint16_t>(n);
+        values[l] = arena.alloc_n<uint16_t>(n);
+        PLAMO_HIP(hipMemsetAsync(keys[l], 0, n * 2, stream));
+        PLAMO_HIP(hipMemsetAsync(values[l], 0, n * 2, stream));
+    }
+    qkv = arena.alloc_n<float>(ROWS * QKV);
+    att = arena.alloc_n<float>(ROWS * ATTN);
+    proj = arena.alloc_n<float>(ROWS * HIDDEN);
+    x0 = arena.alloc_n<float>(ROWS * HIDDEN);
+    x1 = arena.alloc_n<float>(ROWS * HIDDEN);
+    act = arena.alloc_n<float>(ROWS * INTER);
+    hidden = arena.alloc_n<float>(ROWS * HIDDEN);
+    resid_scratch = arena.alloc_n<float>(ROWS * HIDDEN);
+    logits = arena.alloc_n<uint16_t>(size_t(ROWS) * VOCAB);
+    state = arena.alloc_n<StepState>(1);
+    PLAMO_HIP(hipHostMalloc(reinterpret_cast<void**>(&host_state), sizeof(StepState), hipHostMallocDefault));
+    std::memset(host_state, 0, sizeof(StepState));
+    host_state->penalty = 1.0f;
+    PLAMO_HIP(hipMemsetAsync(state, 0, sizeof(StepState), stream));
+    bufs.state = state;
+    bufs.out_ids = arena.alloc_n<int32_t>(size_t(context) + 1);
+    bufs.hist_cap = uint32_t(context);
+    bufs.history = arena.alloc_n<int32_t>(size_t(ROWS) * context);
+    bufs.counts = arena.alloc_n<int32_t>(size_t(ROWS) * VOCAB);
+    bufs.banned = arena.alloc_n<uint32_t>(size_t(ROWS) * (VOCAB / 32));
+    bufs.head_v = arena.alloc_n<float>(size_t(ROWS) * HEAD_BLOCKS);
+    bufs.head_i = arena.alloc_n<uint32_t>(size_t(ROWS) * HEAD_BLOCKS);
+    bufs.tickets = arena.alloc_n<uint32_t>(1);
+    PLAMO_HIP(hipMemsetAsync(bufs.tickets, 0, 4, stream));
+    PLAMO_HIP(hipMemsetAsync(bufs.counts, 0, size_t(ROWS) * VOCAB * 4, stream));
+    PLAMO_HIP(hipMemsetAsync(bufs.banned, 0, size_t(ROWS) * (VOCAB / 32) * 4, stream));
+    decode_parts_local = uint32_t((std::min(context, WINDOW) + KEYS_PER_PART - 1) / KEYS_PER_PART);
+    decode_parts_global = uint32_t(parts_max);
+    part_rows_cap = size_t(std::max(chunk, ROWS)) * parts_max;
+    part_m = arena.alloc_n<float>(part_rows_cap * HEADS);
+    part_l = arena.alloc_n<float>(part_rows_cap * HEADS);
+    part_o = arena.alloc_n<float>(part_rows_cap * HEADS * HEAD_DIM);
+    attn_tickets = arena.alloc_n<uint32_t>(size_t(std::max(chunk, ROWS)));
+    PLAMO_HIP(hipMemsetAsync(attn_tickets, 0, size_t(std::max(chunk, ROWS)) * 4, stream));
+    p_x = arena.alloc_n<float>(size_t(chunk) * HIDDEN);
+    p_qkv = arena.alloc_n<float>(size_t(chunk) * QKV);
+    p_proj = arena.alloc_n<float>(size_t(chunk) * HIDDEN);
+    p_xn = arena.alloc_n<uint16_t>(size_t(chunk) * HIDDEN);
+    p_att = arena.alloc_n<uint16_t>(size_t(chunk) * ATTN);
+    p_act = arena.alloc_n<uint16_t>(size_t(chunk) * INTER);
+    p_tokens = arena.alloc_n<int32_t>(size_t(chunk));
+    PLAMO_HIP(hipEventCreate(&ev0));
+    PLAMO_HIP(hipEventCreate(&ev1));
+    PLAMO_HIP(hipStreamSynchronize(stream));
+}
+
+Engine::~Engine() {
+    if (graph) (void)hipGraphExecDestroy(graph);
+    (void)hipEventDestroy(ev0);
+    (void)hipEventDestroy(ev1);
+    if (host_state) (void)hipHostFree(host_state);
+}
+
+void Engine::zero_sampler() {
+    PLAMO_HIP(hipMemsetAsync(bufs.counts, 0, size_t(ROWS) * VOCAB * 4, stream));
+}
+
+void Engine::enqueue_head(const float* in, const float* resid_in) {
+    const Model& m = *model;
+    const int maxr = lanes == 1 ? 1 : ROWS;
+    GemvParams g{};
+    g.state = state;
+    g.m = VOCAB;
+    g.w = m.head.w;
+    g.table = m.head.table;
+    g.in = in;
+    g.resid_in = resid_in;
+    g.resid_out = resid_scratch;
+    g.g_post = m.layers[LAYERS - 1].post_mlp;
+    g.post_offset = post_mlp_offset();
+    g.g_next = m.final_norm;
+    g.hidden = hidden;
+    g.out16 = logits;
+    g.bufs = bufs;
+    launch_gemv(HIDDEN, m.packed, maxr, PRO_RESID, EPI_LOGITS, g, HEAD_BLOCKS, stream);
+}
+
+// One decode step (Runtime.swift:376-458 for one token per row; Batch.swift:147-165).
+void Engine::enqueue_step(bool head) {
+    const Model& m = *model;
+    const bool pk = m.packed;
+    const int maxr = lanes == 1 ? 1 : ROWS;
+    launch_step_begin(bufs, stream);
+    for (int l = 0; l < LAYERS; ++l) {
+        const LayerWeights& L = m.layers[l];
+        const bool full = is_global_layer(l);
+        GemvParams g{};
+        g.state = state;
+        // QKV with the (embedding or post-MLP residual) + pre-attention norm prologue
+        g.m = QKV;
+        g.w = L.qkv.w;
+        g.table = L.qkv.table;
+        g.resid_out = x0;
+        g.g_next = L.pre;
+        g.out = qkv;
+        if (l == 0) {
+            g.embed = m.embed;
+            launch_gemv(HIDDEN, pk, maxr, PRO_EMBED, EPI_ROUND, g, QKV / 16, stream);
+        } else {
+            g.in = proj;
+            g.resid_in = x1;
+            g.g_post = m.layers[l - 1].post_mlp;
+            g.post_offset = post_mlp_offset();
+            launch_gemv(HIDDEN, pk, maxr, PRO_RESID, EPI_ROUND, g, QKV / 16, stream);
+        }
+        AttnParams a{};
+        a.state = state;
+        a.qkv = qkv;
+        a.q_norm = L.q_norm;
+        a.k_norm = L.k_norm;
+        a.keys = keys[l];
+        a.values = values[l];
+        a.capacity = uint32_t(capacity[l]);
+        a.local_rope = m.local_rope;
+        a.global_rope = m.global_rope;
+        a.part_m = part_m;
+        a.part_l = part_l;
+        a.part_o = part_o;
+        a.parts = full ? decode_parts_global : decode_parts_local;
+        a.tickets = attn_tickets;
+        a.out = att;
+        launch_attention(full, a, ROWS, stream);
+        GemvParams o{};
+        o.state = state;
+        o.m = HIDDEN;
+        o.w = L.o.w;
+        o.table = L.o.table;
+        o.in = att;
+        o.out = proj;
+        launch_gemv(ATTN, pk, maxr, PRO_PLAIN, EPI_ROUND, o, HIDDEN / 16, stream);
+        GemvParams u{};
+        u.state = state;
+        u.m = 2 * INTER;
+        u.w = L.up.w;
+        u.table = L.up.table;
+        u.in = proj;
+        u.resid_in = x0;
+        u.resid_out = x1;
+        u.g_post = L.post;
+        u.post_offset = POST_MIXER_OFFSET;
+        u.g_next = L.pre_mlp;
+        u.out = act;
+        launch_gemv(HIDDEN, pk, maxr, PRO_RESID, EPI_SWIGLU, u, 2 * INTER / 16, stream);
+        GemvParams d{};
+        d.state = state;
+        d.m = HIDDEN;
+        d.w = L.down.w;
+        d.table = L.down.table;
+        d.in = act;
+        d.out = proj;
+        launch_gemv(INTER, pk, maxr, PRO_PLAIN, EPI_ROUND, d, HIDDEN / 8, stream);
+    }
+    if (head) enqueue_head(proj, x1);
+}
+
+void Engine::run_step() {
+    if (!use_graph) {
+        enqueue_step();
+        return;
+    }
+    if (!graph) {
+        hipGraph_t g = nullptr;
+        PLAMO_HIP(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal));
+        try {
+            enqueue_step();
+        } catch (...) {
+            (void)hipStreamEndCapture(stream, &g);
+            if (g) (void)hipGraphDestroy(g);
+            throw;
+        }
+        PLAMO_HIP(hipStreamEndCapture(stream, &g));
+        PLAMO_HIP(hipGraphInstantiate(&graph, g, nullptr, nullptr, 0));
+        PLAMO_HIP(hipGraphDestroy(g));
+    }
+    PLAMO_HIP(hipGraphLaunch(graph, stream));
+}
+
+// A prefill chunk of n tokens at p0 for one lane: every layer as MFMA GEMMs, K/V written
+// for the chunk, then attention of each token over its visible keys.
+void Engine::enqueue_prefill_chunk(int n, int p0, int lane, bool last_chunk, bool output) {
+    const Model& m = *model;
+    const bool pk = m.packed;
+    RowsNormParams rn{};
+    rn.tokens_in = p_tokens;
+    rn.embed = m.embed;
+    rn.x = p_x;
+    rn.g_next = m.layers[0].pre;
+    rn.xn = p_xn;
+    launch_rows_norm(rn, n, stream);
+    for (int l = 0; l < LAYERS; ++l) {
+        const LayerWeights& L = m.layers[l];
+        const bool full = is_global_layer(l);
+        GemmParams q{};
+        q.w = L.qkv.w; q.table = L.qkv.table; q.x = p_xn; q.y = p_qkv; q.m = QKV; q.k = HIDDEN; q.tokens = n;
+        launch_gemm(pk, GEMM_F32, q, stream);
+        KvWriteParams kw{};
+        kw.qkv = p_qkv;
+        kw.k_norm = L.k_norm;
+        kw.keys = keys[l] + size_t(lane) * capacity[l] * HEAD_DIM;
+        kw.values = values[l] + size_t(lane) * capacity[l] * HEAD_DIM;
+        kw.capacity = uint32_t(capacity[l]);
+        kw.p0 = uint32_t(p0);
+        kw.tokens = n;
+        kw.full = full;
+        kw.global_rope = m.global_rope;
+        launch_kv_write(kw, stream);
+        AttnParams a{};
+        a.p0 = uint32_t(p0);
+        a.tokens = uint32_t(n);
+        a.lane = uint32_t(lane);
+        a.out16 = p_att;
+        a.qkv = p_qkv;
+        a.q_norm = L.q_norm;
+        a.k_norm = L.k_norm;
+        a.keys = keys[l];
+        a.values = values[l];
+        a.capacity = uint32_t(capacity[l]);
+        a.local_rope = m.local_rope;
+        a.global_rope = m.global_rope;
+        a.part_m = part_m;
+        a.part_l = part_l;
+        a.part_o = part_o;
+        const int last = p0 + n;  // keys visible to the last token
+        const int visible = full ? last : std::min(last, WINDOW);
+        a.parts = uint32_t((visible + KEYS_PER_PART - 1) / KEYS_PER_PART);
+        a.tickets = attn_tickets;
+        launch_attention(full, a, n, stream);
+        GemmParams o{};
+        o.w = L.o.w; o.table = L.o.table; o.x = p_att; o.y = p_proj; o.m = HIDDEN; o.k = ATTN; o.tokens = n;
+        launch_gemm(pk, GEMM_F32, o, stream);
+        RowsNormParams r1{};
+        r1.in = p_proj; r1.g_post = L.post; r1.post_offset = POST_MIXER_OFFSET; r1.x = p_x; r1.g_next = L.pre_mlp;
+        r1.xn = p_xn;
+        launch_rows_norm(r1, n, stream);
+        GemmParams u{};
+        u.w = L.up.w; u.table = L.up.table; u.x = p_xn; u.y16 = p_act; u.m = 2 * INTER; u.k = HIDDEN; u.tokens = n;
+        launch_gemm(pk, GEMM_SWIGLU, u, stream);
+        GemmParams d{};
+        d.w = L.down.w; d.table = L.down.table; d.x = p_act; d.y = p_proj; d.m = HIDDEN; d.k = INTER; d.tokens = n;
+        launch_gemm(pk, GEMM_F32, d, stream);
+        if (l + 1 < LAYERS) {
+            RowsNormParams r2{};
+            r2.in = p_proj; r2.g_post = L.post_mlp; r2.post_offset = post_mlp_offset(); r2.x = p_x;
+            r2.g_next = m.layers[l + 1].pre; r2.xn = p_xn;
+            launch_rows_norm(r2, n, stream);
+        }
+    }
+    if (last_chunk && output) {
+        launch_step_begin(bufs, stream);
+        enqueue_head(p_proj + size_t(n - 1) * HIDDEN, p_x + size_t(n - 1) * HIDDEN);
+    }
+}
+
+void Engine::prefill(const int32_t* tokens, int n, int p0, int lane, bool output) {
+    for (int c0 = 0; c0 < n; c0 += chunk) {
+        const int cn = std::min(chunk, n - c0);
+        PLAMO_HIP(hipMemcpyAsync(p_tokens, tokens + c0, size_t(cn) * 4, hipMemcpyHostToDevice, stream));
+        enqueue_prefill_chunk(cn, p0 + c0, lane, c0 + cn == n, output);
+    }
+}
+
+// ---------------------------------------------------------------------------- runtime
+RuntimeImpl::~RuntimeImpl() {
+    eng.reset();
+    model.reset();
+    if (stream) (void)hipStreamDestroy(stream);
+}
+
+void RuntimeImpl::reset() {
+    position = 0;
+    gpu_seconds = 0;
+    last_output_rows = 0;
+    history.clear();
+    uploaded = 0;
+    counts_dirty = true;
+}
+
+void RuntimeImpl::begin_timing() { PLAMO_HIP(hipEventRecord(eng->ev0, stream)); }
+
+void RuntimeImpl::end_timing() {
+    PLAMO_HIP(hipEventRecord(eng->ev1, stream));
+    PLAMO_HIP(hipEventSynchronize(eng->ev1));
+    float ms = 0;
+    PLAMO_HIP(hipEventElapsedTime(&ms, eng->ev0, eng->ev1));
+    gpu_seconds += ms / 1000.0;
+}
+
+// Uploads the generated history not yet on the device and the sampler settings.
+void RuntimeImpl::sync_sampler(Engine& e, int row) {
+    StepState& hs = *e.host_state;
+    hs.sampling = sampling ? 1 : 0;
+    hs.penalty = penalty;
+    hs.frequency = frequency;
+    hs.presence = presence;
+    hs.ngram = ngram;
+    if (counts_dirty) {
+        e.zero_sampler();
+        hs.counted[row] = 0;
+        counts_dirty = false;
+    }
+    if (!sampling) {
+        hs.hist_len[row] = uint32_t(std::min<size_t>(history.size(), e.bufs.hist_cap));
+        return;
+    }
+    const size_t n = std::min<size_t>(history.size(), e.bufs.hist_cap);
+    if (uploaded < n) {
+        PLAMO_HIP(hipMemcpyAsync(e.bufs.history + size_t(row) * e.bufs.hist_cap + uploaded, history.data() + uploaded,
+                                 (n - uploaded) * 4, hipMemcpyHostToDevice, stream));
+        uploaded = n;
+    }
+    hs.hist_len[row] = uint32_t(n);
+}
+
+int RuntimeImpl::forward(const int32_t* tokens, int n, bool output) {
+    // Runtime.swift:328-330: validate before touching any state.
+    const int limit = std::min(context, CHUNK);
+    bool ok = n > 0 && n <= limit && position + n <= context;
+    for (int i = 0; ok && i < n; ++i) ok = tokens[i] >= 0 && tokens[i] < VOCAB;
+    if (!ok) throw Error(E_INVAL, "Invalid tokens or context exhausted");
+    Engine& e = *eng;
+    StepState& hs = *e.host_state;
+    hs.rows = 1;
+    hs.lane[0] = 0;
+    hs.pos[0] = uint32_t(position);
+    hs.token[0] = tokens[0];
+    hs.loop = 0;
+    hs.stopped = 0;
+    sync_sampler(e, 0);
+    PLAMO_HIP(hipMemcpyAsync(e.state, &hs, sizeof(StepState), hipMemcpyHostToDevice, stream));
+    begin_timing();
+    if (n == 1 && output) {
+        e.run_step();
+    } else if (n == 1) {
+        // no head: the reference leaves logits untouched without output (Runtime.swift:453-458)
+        e.enqueue_step(false);
+    } else {
+        e.prefill(tokens, n, int(position), 0, output);
+    }
+    end_timing();
+    PLAMO_HIP(hipMemcpyAsync(&hs, e.state, sizeof(StepState), hipMemcpyDeviceToHost, stream));
+    PLAMO_HIP(hipStreamSynchronize(stream));
+    PLAMO_HIP(hipGetLastError());
+    position += n;
+    last_output_rows = output ? 1 : 0;
+    if (!output) return -1;
+    const int next = int32_t(hs.next[0]);
+    predictions.assign(1, next);
+    return next;
+}
+
+int RuntimeImpl::prefill(const int32_t* tokens, int n) {
+    // Runtime.swift:474
+    bool ok = n > 0 && position + n <= context;
+    for (int i = 0; ok && i < n; ++i) ok = tokens[i] >= 0 && tokens[i] < VOCAB;
+    if (!ok) throw Error(E_INVAL, "Input exceeds context");
+    if (n == 1) return forward(tokens, 1, true);
+    Engine& e = *eng;
+    StepState& hs = *e.host_state;
+    hs.rows = 1;
+    hs.lane[0] = 0;
+    hs.pos[0] = uint32_t(position);
+    hs.loop = 0;
+    hs.stopped = 0;
+    sync_sampler(e, 0);
+    PLAMO_HIP(hipMemcpyAsync(e.state, &hs, sizeof(StepState), hipMemcpyHostToDevice, stream));
+    begin_timing();
+    e.prefill(tokens, n, int(position), 0, true);
+    end_timing();
+    PLAMO_HIP(hipMemcpyAsync(&hs, e.state, sizeof(StepState), hipMemcpyDeviceToHost, stream));
+    PLAMO_HIP(hipStreamSynchronize(stream));
+    PLAMO_HIP(hipGetLastError());
+    position += n;
+    last_output_rows = 1;
+    const int next = int32_t(hs.next[0]);
+    predictions.assign(1, next);
+    return next;
+}
+
+// ------------------------------------------------------------------------------ batch
+BatchImpl::BatchImpl(RuntimeImpl* r) : rt(r) {
+    if (rt->context < 1 || rt->context >= 8192)
+        throw Error(E_INVAL, "Batch requires dense greedy inference with context below 8192");  // Batch.swift:34-36
+    eng = std::make_unique<Engine>(rt->model, rt->context, ROWS, rt->stream);
+    lane_logits = eng->arena.alloc_n<uint16_t>(size_t(ROWS) * VOCAB);
+    lane_hidden = eng->arena.alloc_n<float>(size_t(ROWS) * HIDDEN);
+    for (auto& v : lane_next) v = 0;
+}
+
+BatchImpl::~BatchImpl() { eng.reset(); }
+
+void BatchImpl::reset() {
+    ready = false;
+    positions.clear();
+    gpu_seconds = 0;
+}
+
+std::vector<int32_t> BatchImpl::prefill(const std::vector<std::vector<int32_t>>& prompts) {
+    // Batch.swift:81-83
+    bool ok = prompts.size() >= 1 && prompts.size() <= 4;
+    for (auto& p : prompts) {
+        ok = ok && !p.empty() && int(p.size()) <= rt->context;
+        for (int32_t t : p) ok = ok && t >= 0 && t < VOCAB;
+    }
+    if (!ok) throw Error(E_INVAL, "Expected one to four valid prompts");
+    ready = false;
+    gpu_seconds = 0;
+    Engine& e = *eng;
+    hipStream_t s = e.stream;
+    StepState& hs = *e.host_state;
+    for (size_t lane = 0; lane < prompts.size(); ++lane) {
+        const auto& p = prompts[lane];
+        std::memset(&hs, 0, sizeof(StepState));
+        hs.rows = 1;
+        hs.lane[0] = uint32_t(lane);
+        hs.pos[0] = 0;
+        hs.token[0] = p[0];
+        hs.penalty = 1.0f;
+        PLAMO_HIP(hipMemcpyAsync(e.state, &hs, sizeof(StepState), hipMemcpyHostToDevice, s));
+        PLAMO_HIP(hipEventRecord(e.ev0, s));
+        if (p.size() == 1) e.run_step();
+        else e.prefill(p.data(), int(p.size()), 0, int(lane), true);
+        PLAMO_HIP(hipEventRecord(e.ev1, s));
+        PLAMO_HIP(hipMemcpyAsync(lane_logits + lane * VOCAB, e.logits, VOCAB * 2, hipMemcpyDeviceToDevice, s));
+        PLAMO_HIP(hipMemcpyAsync(lane_hidden + lane * HIDDEN, e.hidden, HIDDEN * 4, hipMemcpyDeviceToDevice, s));
+        PLAMO_HIP(hipMemcpyAsync(&hs, e.state, sizeof(StepState), hipMemcpyDeviceToHost, s));
+        PLAMO_HIP(hipStreamSynchronize(s));
+        PLAMO_HIP(hipGetLastError());
+        float ms = 0;
+        PLAMO_HIP(hipEventElapsedTime(&ms, e.ev0, e.ev1));
+        gpu_seconds += ms / 1000.0;
+        lane_next[lane] = int32_t(hs.next[0]);
+    }
+    positions.assign(prompts.size(), 0);
+    for (size_t i = 0; i < prompts.size(); ++i) positions[i] = int64_t(prompts[i].size());
+    ready = true;
+    return std::vector<int32_t>(lane_next, lane_next + prompts.size());
+}
+
+std::vector<int32_t> BatchImpl::step(const std::vector<int32_t>& tokens) {
+    // Batch.swift:110-112
+    bool ok = ready && tokens.size() == positions.size();
+    bool any = false;
+    for (size_t i = 0; ok && i < tokens.size(); ++i) {
+        if (tokens[i] < 0) continue;
+        any = true;
+        ok = tokens[i] < VOCAB && positions[i] < rt->context;
+    }
+    if (!ok || !any) throw Error(E_INVAL, "Invalid quad step or context exhausted");
+    Engine& e = *eng;
+    hipStream_t s = e.stream;
+    StepState& hs = *e.host_state;
+    std::memset(&hs, 0, sizeof(StepState));
+    hs.penalty = 1.0f;
+    std::vector<int> active;
+    for (size_t i = 0; i < tokens.size(); ++i)
+        if (tokens[i] >= 0) {
+            const int q = int(active.size());
+            hs.lane[q] = uint32_t(i);
+            hs.pos[q] = uint32_t(positions[i]);
+            hs.token[q] = tokens[i];
+            active.push_back(int(i));
+        }
+    hs.rows = uint32_t(active.size());
+    PLAMO_HIP(hipMemcpyAsync(e.state, &hs, sizeof(StepState), hipMemcpyHostToDevice, s));
+    PLAMO_HIP(hipEventRecord(e.ev0, s));
+    e.run_step();
+    PLAMO_HIP(hipEventRecord(e.ev1, s));
+    // Packed query rows are temporary; persistent outputs stay indexed by lane (Batch.swift:167-173).
+    for (size_t q = 0; q < active.size(); ++q) {
+        const int lane = active[q];
+        PLAMO_HIP(hipMemcpyAsync(lane_logits + size_t(lane) * VOCAB, e.logits + q * VOCAB, VOCAB * 2,
+                                 hipMemcpyDeviceToDevice, s));
+        PLAMO_HIP(hipMemcpyAsync(lane_hidden + size_t(lane) * HIDDEN, e.hidden + q * HIDDEN, HIDDEN * 4,
+                                 hipMemcpyDeviceToDevice, s));
+    }
+    PLAMO_HIP(hipMemcpyAsync(&hs, e.state, sizeof(StepState), hipMemcpyDeviceToHost, s));
+    const hipError_t sync = hipStreamSynchronize(s);
+    if (sync != hipSuccess) {
+        ready = false;
+        throw Error(E_DEVICE, std::string("Quad execution failed: ") + hipGetErrorString(sync));
+    }
+    float ms = 0;
+    PLAMO_HIP(hipEventElapsedTime(&ms, e.ev0, e.ev1));
+    gpu_seconds += ms / 1000.0;
+    for (size_t q = 0; q < active.size(); ++q) {
+        lane_next[active[q]] = int32_t(hs.next[q]);
+        positions[active[q]] += 1;
+    }
+    return std::vector<int32_t>(lane_next, lane_next + positions.size());
+}
+
+}  // namespace plamo
+
+namespace plamo {
+
+// The token loop of Main.swift:235-288 with the next token fed back on the device.
+std::vector<int32_t> RuntimeImpl::generate(const int32_t* prompt, int n, int max_tokens, int* reason) {
+    if (n <= 0 || max_tokens < 0 || int64_t(n) + max_tokens > context)
+        throw Error(E_INVAL, "Input plus output limit exceeds context");  // Main.swift:168-169
+    for (int i = 0; i < n; ++i)
+        if (prompt[i] < 0 || prompt[i] >= VOCAB) throw Error(E_INVAL, "Input exceeds context");
+    reset();
+    const int first = prefill(prompt, n);
+    *reason = 0;
+    if (max_tokens == 0) return {};
+    Engine& e = *eng;
+    StepState& hs = *e.host_state;
+    hs.rows = 1;
+    hs.lane[0] = 0;
+    hs.pos[0] = uint32_t(position);
+    hs.token[0] = first;
+    hs.loop = 1;
+    hs.stop_enabled = 1;
+    hs.max_tokens = uint32_t(max_tokens);
+    hs.produced = 0;
+    hs.reason = 0;
+    hs.stopped = 0;
+    sync_sampler(e, 0);
+    PLAMO_HIP(hipMemcpyAsync(e.state, &hs, sizeof(StepState), hipMemcpyHostToDevice, stream));
+    begin_timing();
+    int launched = 0;
+    while (launched < max_tokens) {
+        const int batch = std::min(16, max_tokens - launched);
+        for (int k = 0; k < batch; ++k) e.run_step();
+        launched += batch;
+        PLAMO_HIP(hipMemcpyAsync(&hs, e.state, sizeof(StepState), hipMemcpyDeviceToHost, stream));
+        PLAMO_HIP(hipStreamSynchronize(stream));
+        if (hs.stopped) break;
+    }
+    end_timing();
+    PLAMO_HIP(hipGetLastError());
+    std::vector<int32_t> out(hs.produced);
+    if (hs.produced)
+        PLAMO_HIP(hipMemcpy(out.data(), e.bufs.out_ids, size_t(hs.produced) * 4, hipMemcpyDeviceToHost));
+    position = hs.pos[0];
+    *reason = int(hs.reason);
+    hs.loop = 0;
+    if (sampling) {
+        history.insert(history.end(), out.begin(), out.end());
+        uploaded = history.size();
+    }
+    last_output_rows = 1;
+    predictions.assign(1, int32_t(hs.next[0]));
+    return out;
+}
+
+// Back-to-back replays of the decode graph, timed with HIP events on the handle's stream.
+double RuntimeImpl::bench_decode(int steps) {
+    if (steps <= 0 || position + steps > context) throw Error(E_INVAL, "Invalid tokens or context exhausted");
+    Engine& e = *eng;
+    StepState& hs = *e.host_state;
+    hs.rows = 1;
+    hs.lane[0] = 0;
+    hs.pos[0] = uint32_t(position);
+    hs.token[0] = predictions.empty() || predictions[0] < 0 || predictions[0] >= VOCAB ? 1000 : predictions[0];
+    hs.loop = 1;
+    hs.stop_enabled = 0;
+    hs.max_tokens = uint32_t(steps + 1);
+    hs.produced = 0;
+    hs.reason = 0;
+    hs.stopped = 0;
+    sync_sampler(e, 0);
+    PLAMO_HIP(hipMemcpyAsync(e.state, &hs, sizeof(StepState), hipMemcpyHostToDevice, stream));
+    e.run_step();  // capture outside the timed region
+    PLAMO_HIP(hipStreamSynchronize(stream));
+    PLAMO_HIP(hipEventRecord(e.ev0, stream));
+    for (int k = 1; k < steps; ++k) e.run_step();
+    PLAMO_HIP(hipEventRecord(e.ev1, stream));
+    PLAMO_HIP(hipEventSynchronize(e.ev1));
+    float ms = 0;
+    PLAMO_HIP(hipEventElapsedTime(&ms, e.ev0, e.ev1));
+    PLAMO_HIP(hipMemcpyAsync(&hs, e.state, sizeof(StepState), hipMemcpyDeviceToHost, stream));
+    PLAMO_HIP(hipStreamSynchronize(stream));
+    PLAMO_HIP(hipGetLastError());
+    position = hs.pos[0];
+    hs.loop = 0;
+    last_output_rows = 1;
+    predictions.assign(1, int32_t(hs.next[0]));
+    return steps > 1 ? double(ms) / (steps - 1) : 0.0;
+}
+
+}  // namespace plamo

@@ -1,0 +1,146 @@
+// Host runtime: the MI355X counterparts of Runtime, Batch and Weights
+// (Sources/Plamo/Runtime.swift:128-553, Batch.swift:4-187).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "common.h"
+#include "kernels.h"
+#include "prefill.h"
+
+namespace plamo {
+
+// Device memory owned by one object; freed together.
+class DeviceArena {
+  public:
+    ~DeviceArena();
+    void* alloc(size_t bytes);
+    template <class T>
+    T* alloc_n(size_t n) { return static_cast<T*>(alloc(n * sizeof(T))); }
+    size_t bytes() const { return bytes_; }
+
+  private:
+    std::vector<void*> ptrs_;
+    size_t bytes_ = 0;
+};
+
+struct Linear {
+    const uint16_t* w = nullptr;    // plain BF16 rows or .p12 payload
+    const uint32_t* table = nullptr;
+    int64_t bytes = 0;              // bytes a full GEMV pass reads (payload + table)
+};
+
+struct LayerWeights {
+    Linear qkv, o, up, down;
+    const uint16_t *pre = nullptr, *post = nullptr, *pre_mlp = nullptr, *post_mlp = nullptr;
+    const uint16_t *q_norm = nullptr, *k_norm = nullptr;
+};
+
+// Weights in HBM plus the RoPE tables; shared by a Runtime and its Batch.
+struct Model {
+    bool packed = false;
+    LayerWeights layers[LAYERS];
+    Linear head;
+    const uint16_t* final_norm = nullptr;
+    const uint16_t* embed = nullptr;
+    float2* local_rope = nullptr;   // [2064][64]
+    float2* global_rope = nullptr;  // [context][64]
+    int64_t weight_bytes = 0, linear_bytes = 0;
+    DeviceArena arena;
+};
+
+// KV, scratch, step state and the captured decode graph for `lanes` sequences.
+class Engine {
+  public:
+    Engine(std::shared_ptr<Model> model, int context, int lanes, hipStream_t stream);
+    ~Engine();
+
+    std::shared_ptr<Model> model;
+    int context, lanes, chunk, local_capacity;
+    hipStream_t stream;
+    DeviceArena arena;
+    uint16_t *keys[LAYERS], *values[LAYERS];
+    int capacity[LAYERS];
+    // decode scratch (ROWS rows)
+    float *qkv, *att, *proj, *x0, *x1, *act, *hidden, *resid_scratch;
+    uint16_t* logits;
+    StepState* state;        // device
+    StepState* host_state;   // pinned mirror
+    DecodeBuffers bufs;
+    float *part_m, *part_l, *part_o;
+    uint32_t* attn_tickets;
+    uint32_t decode_parts_local, decode_parts_global;
+    // prefill scratch (chunk rows)
+    float *p_x, *p_qkv, *p_proj;
+    uint16_t *p_xn, *p_att, *p_act;
+    int32_t* p_tokens;
+    size_t part_rows_cap;    // rows x parts the partial buffers hold
+    // graph
+    hipGraphExec_t graph = nullptr;
+    bool use_graph = true;
+    hipEvent_t ev0, ev1;
+
+    void enqueue_step(bool head = true);    // one decode step for state->rows rows
+    void run_step();                        // graph replay (or direct launches)
+    // prefill of `n` tokens of one lane at position p0 (n > 1); head on the last token.
+    void prefill(const int32_t* tokens, int n, int p0, int lane, bool output);
+    void zero_sampler();
+
+  private:
+    void enqueue_prefill_chunk(int n, int p0, int lane, bool last_chunk, bool output);
+    void enqueue_head(const float* in, const float* resid_in);
+};
+
+std::shared_ptr<Model> load_model(const std::string& dir, int context, bool packed, const std::string& sha,
+                                  hipStream_t stream);
+
+struct RuntimeImpl {
+    std::shared_ptr<Model> model;
+    std::unique_ptr<Engine> eng;
+    hipStream_t stream = nullptr;
+    int context = 0;
+    int64_t position = 0;
+    int last_output_rows = 0;
+    double gpu_seconds = 0;
+    std::vector<int32_t> predictions;
+    // sampler
+    bool sampling = false;
+    float penalty = 1, frequency = 0, presence = 0;
+    int ngram = 0;
+    std::vector<int32_t> history;   // generated ids (Main.swift:236-238)
+    size_t uploaded = 0;            // history entries already on the device
+    bool counts_dirty = true;
+
+    ~RuntimeImpl();
+    void reset();
+    int forward(const int32_t* tokens, int n, bool output);
+    int prefill(const int32_t* tokens, int n);
+    void begin_timing();
+    void end_timing();
+    void sync_sampler(Engine& e, int row);
+    std::vector<int32_t> generate(const int32_t* prompt, int n, int max_tokens, int* reason);
+    double bench_decode(int steps);
+};
+
+struct BatchImpl {
+    RuntimeImpl* rt;
+    std::unique_ptr<Engine> eng;
+    std::vector<int64_t> positions;
+    bool ready = false;
+    double gpu_seconds = 0;
+    uint16_t* lane_logits;   // [4][VOCAB]
+    float* lane_hidden;      // [4][1536]
+    int32_t lane_next[ROWS];
+
+    explicit BatchImpl(RuntimeImpl* rt);
+    ~BatchImpl();
+    std::vector<int32_t> prefill(const std::vector<std::vector<int32_t>>& prompts);
+    std::vector<int32_t> step(const std::vector<int32_t>& tokens);
+    void reset();
+};
+
+}  // namespace plamo

@@ -1,0 +1,268 @@
+"""Python mirror of the reference's Swift surface over the HIP C ABI.
+
+Names, argument meaning and error behaviour follow the reference:
+
+* ``Runtime``      -- ``Runtime`` (Sources/Plamo/Runtime.swift:128-553): ``forward``,
+                      ``prefill``, ``reset``, ``logits``, ``logit_values``, ``predictions``,
+                      ``position``, ``gpu_seconds``.
+* ``Batch``        -- ``Batch`` (Sources/Plamo/Batch.swift:4-187) and ``Batch.generate``
+                      (BatchDecode.swift:40-47).
+* ``decode_batch`` -- ``decodeBatch`` (BatchDecode.swift:8-37), native implementation.
+* ``pack``         -- ``scripts/pack_weights.py`` through the native packer.
+
+Every call goes to ``lib/libplamo_hip.so``; there is no CPU fallback.
+"""
+import ctypes
+
+import numpy as np
+
+from . import native
+from .native import PlamoError, VOCAB, HIDDEN, pack
+
+REASONS = {1: "stop", 2: "length"}
+
+
+def _u16_to_f32(bits):
+    return (bits.astype(np.uint32) << 16).view(np.float32)
+
+
+class Runtime:
+    """Runtime(directory:context:packed:) (Runtime.swift:164)."""
+
+    def __init__(self, directory, context, packed=False, source_sha256=None):
+        lib = native.load()
+        h = ctypes.c_void_p()
+        native.call(lib.plamo_open, str(directory).encode(), int(context), 1 if packed else 0,
+                    source_sha256.encode() if source_sha256 else None, ctypes.byref(h))
+        self._h = h
+        self._lib = lib
+
+    def close(self):
+        if getattr(self, "_h", None):
+            self._lib.plamo_close(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def reset(self):
+        self._lib.plamo_reset(self._h)
+
+    def forward(self, tokens, output=True):
+        """Runtime.forward(_:output:) (Runtime.swift:321-467) -> next token (-1 without output)."""
+        tokens = [int(t) for t in tokens]
+        nxt = ctypes.c_int32(-1)
+        native.call(self._lib.plamo_forward, self._h, native.i32(tokens), len(tokens), 1 if output else 0,
+                    ctypes.byref(nxt))
+        return nxt.value
+
+    def prefill(self, tokens):
+        """Runtime.prefill(_:) (Runtime.swift:469-483)."""
+        tokens = [int(t) for t in tokens]
+        nxt = ctypes.c_int32(-1)
+        native.call(self._lib.plamo_prefill, self._h, native.i32(tokens), len(tokens), ctypes.byref(nxt))
+        return nxt.value
+
+    def logit_bits(self, slot=0):
+        out = np.empty(VOCAB, dtype=np.uint16)
+        native.call(self._lib.plamo_logits_bf16, self._h, int(slot), out.ctypes.data_as(native.c_u16p))
+        return out
+
+    def logits(self, slot=0):
+        """Runtime.logits(into:slot:) (Runtime.swift:547-552)."""
+        return _u16_to_f32(self.logit_bits(slot))
+
+    logit_values = logits
+
+    def hidden(self):
+        out = np.empty(HIDDEN, dtype=np.float32)
+        native.call(self._lib.plamo_hidden, self._h, out.ctypes.data_as(native.c_f32p))
+        return out
+
+    def predictions(self):
+        buf = (ctypes.c_int32 * 4)()
+        n = ctypes.c_int32()
+        self._lib.plamo_predictions(self._h, buf, 4, ctypes.byref(n))
+        return [buf[i] for i in range(n.value)]
+
+    def stats(self):
+        s = native.Stats()
+        self._lib.plamo_get_stats(self._h, ctypes.byref(s))
+        return {k: getattr(s, k) for k, _ in native.Stats._fields_}
+
+    @property
+    def position(self):
+        return self.stats()["position"]
+
+    @property
+    def gpu_seconds(self):
+        return self.stats()["gpu_seconds"]
+
+    @property
+    def context(self):
+        return self.stats()["context"]
+
+    def kv(self, layer):
+        """Layer KV (BF16 bits [capacity][128]) as the reference tests read layer.keys/values."""
+        cap = ctypes.c_int32()
+        native.call(self._lib.plamo_kv, self._h, int(layer), None, None, ctypes.byref(cap))
+        k = np.empty((cap.value, 128), dtype=np.uint16)
+        v = np.empty((cap.value, 128), dtype=np.uint16)
+        native.call(self._lib.plamo_kv, self._h, int(layer), k.ctypes.data_as(native.c_u16p),
+                    v.ctypes.data_as(native.c_u16p), ctypes.byref(cap))
+        return k, v
+
+    def set_sampling(self, repetition_penalty=1.0, frequency_penalty=0.0, presence_penalty=0.0,
+                     no_repeat_ngram=0):
+        """Options --repetition-penalty/--frequency-penalty/--no-repeat-ngram (Main.swift:236-244)."""
+        self._lib.plamo_set_sampling(self._h, float(repetition_penalty), float(frequency_penalty),
+                                     float(presence_penalty), int(no_repeat_ngram))
+
+    def observe(self, token):
+        """generated.append(token) (Main.swift:280): history the sampling controls see."""
+        self._lib.plamo_sampler_observe(self._h, int(token))
+
+    def generate(self, prompt, max_tokens):
+        """Device-driven token loop of Main.swift:235-288 -> (ids, 'stop' | None)."""
+        prompt = [int(t) for t in prompt]
+        out = (ctypes.c_int32 * max(1, max_tokens))()
+        n, reason = ctypes.c_int32(), ctypes.c_int32()
+        native.call(self._lib.plamo_generate, self._h, native.i32(prompt), len(prompt), int(max_tokens), out,
+                    ctypes.byref(n), ctypes.byref(reason))
+        return [out[i] for i in range(n.value)], ("stop" if reason.value == 1 else None)
+
+    def bench_decode(self, steps):
+        ms = ctypes.c_double()
+        native.call(self._lib.plamo_bench_decode, self._h, int(steps), ctypes.byref(ms))
+        return ms.value
+
+
+class Batch:
+    """Batch(_ scalar:) (Batch.swift:33-78)."""
+
+    def __init__(self, runtime):
+        h = ctypes.c_void_p()
+        native.call(runtime._lib.plamo_batch_open, runtime._h, ctypes.byref(h))
+        self._h, self._lib, self.runtime = h, runtime._lib, runtime
+
+    def close(self):
+        if getattr(self, "_h", None):
+            self._lib.plamo_batch_close(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def prefill(self, prompts):
+        """Batch.prefill (Batch.swift:80-107)."""
+        flat = [int(t) for p in prompts for t in p]
+        nxt = (ctypes.c_int32 * 4)()
+        native.call(self._lib.plamo_batch_prefill, self._h, native.i32(flat),
+                    native.i32([len(p) for p in prompts]), len(prompts), nxt)
+        return [nxt[i] for i in range(len(prompts))]
+
+    def step(self, tokens):
+        """Batch.step (Batch.swift:109-180): None marks an inactive lane."""
+        t = [-1 if x is None else int(x) for x in tokens]
+        nxt = (ctypes.c_int32 * 4)()
+        native.call(self._lib.plamo_batch_step, self._h, native.i32(t), len(t), nxt)
+        return [nxt[i] for i in range(len(t))]
+
+    def reset(self):
+        self._lib.plamo_batch_reset(self._h)
+
+    def positions(self):
+        buf, n = (ctypes.c_int32 * 4)(), ctypes.c_int32()
+        self._lib.plamo_batch_positions(self._h, buf, 4, ctypes.byref(n))
+        return [buf[i] for i in range(n.value)]
+
+    def logit_bits(self, lane):
+        out = np.empty(VOCAB, dtype=np.uint16)
+        native.call(self._lib.plamo_batch_logits_bf16, self._h, int(lane), out.ctypes.data_as(native.c_u16p))
+        return out
+
+    def hidden(self, lane):
+        out = np.empty(HIDDEN, dtype=np.float32)
+        native.call(self._lib.plamo_batch_hidden, self._h, int(lane), out.ctypes.data_as(native.c_f32p))
+        return out
+
+    def kv(self, lane, layer):
+        cap = ctypes.c_int32()
+        native.call(self._lib.plamo_batch_kv, self._h, int(lane), int(layer), None, None, ctypes.byref(cap))
+        k = np.empty((cap.value, 128), dtype=np.uint16)
+        v = np.empty((cap.value, 128), dtype=np.uint16)
+        native.call(self._lib.plamo_batch_kv, self._h, int(lane), int(layer), k.ctypes.data_as(native.c_u16p),
+                    v.ctypes.data_as(native.c_u16p), ctypes.byref(cap))
+        return k, v
+
+    def generate(self, prompts, limits, stop_on_truncation=False):
+        """Batch.generate (BatchDecode.swift:40-47) -> [(ids, reason)]."""
+        stride = max(1, max(limits))
+        ids = (ctypes.c_int32 * (4 * stride))()
+        lengths, reasons, lanes = (ctypes.c_int32 * 4)(), (ctypes.c_int32 * 4)(), ctypes.c_int32()
+        flat = [int(t) for p in prompts for t in p]
+        native.call(self._lib.plamo_batch_generate, self._h, native.i32(flat), native.i32([len(p) for p in prompts]),
+                    native.i32(list(limits)), len(prompts), 1 if stop_on_truncation else 0, ids, stride, lengths,
+                    reasons, ctypes.byref(lanes))
+        return [([ids[i * stride + k] for k in range(lengths[i])], REASONS[reasons[i]]) for i in range(lanes.value)]
+
+
+def decode_batch(initial, limits, step, emit=None, finish=None, stop_on_truncation=False):
+    """decodeBatch (BatchDecode.swift:8-37) through the native scheduler -> [(ids, reason)]."""
+    lib = native.load()
+    count = len(initial)
+    failure = []
+
+    def _step(_, tokens, n, out):
+        try:
+            res = step([None if tokens[i] < 0 else tokens[i] for i in range(n)])
+            for i in range(n):
+                out[i] = int(res[i]) if i < len(res) else -1
+            return 0
+        except Exception as e:  # surfaced after the call returns
+            failure.append(e)
+            return 1
+
+    def _emit(_, lane, token):
+        try:
+            if emit:
+                emit(lane, token)
+            return 0
+        except Exception as e:
+            failure.append(e)
+            return 1
+
+    def _finish(_, lane, ids, n, reason):
+        try:
+            if finish:
+                finish(lane, ([ids[i] for i in range(n)], REASONS[reason]))
+            return 0
+        except Exception as e:
+            failure.append(e)
+            return 1
+
+    cb = (native.STEP_FN(_step), native.EMIT_FN(_emit), native.FINISH_FN(_finish))
+    stride = max(1, max(limits)) if limits else 1
+    ids = (ctypes.c_int32 * (4 * stride))()
+    lengths, reasons, lanes = (ctypes.c_int32 * 4)(), (ctypes.c_int32 * 4)(), ctypes.c_int32()
+    err = ctypes.create_string_buffer(512)
+    rc = lib.plamo_decode_batch(native.i32(list(initial)), native.i32(list(limits)), count, cb[0], cb[1], cb[2], None,
+                                1 if stop_on_truncation else 0, ids, stride, lengths, reasons, ctypes.byref(lanes),
+                                err, 512)
+    if failure:
+        raise failure[0]
+    if rc != 0:
+        raise PlamoError(rc, err.value.decode())
+    return [([ids[i * stride + k] for k in range(lengths[i])], REASONS[reasons[i]]) for i in range(lanes.value)]

@@ -1,0 +1,148 @@
+"""ctypes binding of lib/libplamo_hip.so (include/plamo_hip.h).
+
+The library is the product: there is no Python or CPU fallback.  ``load()`` raises when the
+shared library has not been built (``make -C plamo3-0.8b-runtime_amd``).
+"""
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(os.path.dirname(_HERE), "lib", "libplamo_hip.so")
+HEADER_PATH = os.path.join(os.path.dirname(os.path.dirname(_HERE)), "include", "plamo_hip.h")
+
+VOCAB, HIDDEN = 107520, 1536
+c_i32p = ctypes.POINTER(ctypes.c_int32)
+c_u16p = ctypes.POINTER(ctypes.c_uint16)
+c_f32p = ctypes.POINTER(ctypes.c_float)
+
+
+class Stats(ctypes.Structure):
+    _fields_ = [("position", ctypes.c_int64), ("gpu_seconds", ctypes.c_double),
+                ("device_bytes", ctypes.c_int64), ("weight_bytes", ctypes.c_int64),
+                ("linear_bytes", ctypes.c_int64), ("context", ctypes.c_int32),
+                ("packed", ctypes.c_int32), ("last_output_rows", ctypes.c_int32),
+                ("local_capacity", ctypes.c_int32)]
+
+
+class PackReport(ctypes.Structure):
+    _fields_ = [("original_linear_bytes", ctypes.c_int64), ("packed_linear_bytes", ctypes.c_int64),
+                ("archive_bytes", ctypes.c_int64), ("compressed_blocks", ctypes.c_int64),
+                ("blocks", ctypes.c_int64)]
+
+
+STEP_FN = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_void_p, c_i32p, ctypes.c_int32, c_i32p)
+EMIT_FN = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32)
+FINISH_FN = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_void_p, ctypes.c_int32, c_i32p, ctypes.c_int32, ctypes.c_int32)
+
+_SIGNATURES = {
+    "plamo_open": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_char_p,
+                                  ctypes.POINTER(ctypes.c_void_p), ctypes.c_char_p, ctypes.c_size_t]),
+    "plamo_close": (None, [ctypes.c_void_p]),
+    "plamo_reset": (None, [ctypes.c_void_p]),
+    "plamo_forward": (ctypes.c_int, [ctypes.c_void_p, c_i32p, ctypes.c_int32, ctypes.c_int32, c_i32p,
+                                     ctypes.c_char_p, ctypes.c_size_t]),
+    "plamo_prefill": (ctypes.c_int, [ctypes.c_void_p, c_i32p, ctypes.c_int32, c_i32p, ctypes.c_char_p,
+                                     ctypes.c_size_t]),
+    "plamo_logits": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, c_f32p, ctypes.c_char_p, ctypes.c_size_t]),
+    "plamo_logits_bf16": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, c_u16p, ctypes.c_char_p,
+                                         ctypes.c_size_t]),
+    "plamo_hidden": (ctypes.c_int, [ctypes.c_void_p, c_f32p, ctypes.c_char_p, ctypes.c_size_t]),
+    "plamo_predictions": (ctypes.c_int, [ctypes.c_void_p, c_i32p, ctypes.c_int32, c_i32p]),
+    "plamo_get_stats": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(Stats)]),
+    "plamo_kv": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, c_u16p, c_u16p, c_i32p, ctypes.c_char_p,
+                                ctypes.c_size_t]),
+    "plamo_set_sampling": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_float, ctypes.c_float, ctypes.c_float,
+                                          ctypes.c_int32]),
+    "plamo_sampler_observe": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32]),
+    "plamo_generate": (ctypes.c_int, [ctypes.c_void_p, c_i32p, ctypes.c_int32, ctypes.c_int32, c_i32p, c_i32p,
+                                      c_i32p, ctypes.c_char_p, ctypes.c_size_t]),
+    "plamo_bench_decode": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, ctypes.POINTER(ctypes.c_double),
+                                          ctypes.c_char_p, ctypes.c_size_t]),
+    "plamo_batch_open": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p), ctypes.c_char_p,
+                                        ctypes.c_size_t]),
+    "plamo_batch_close": (None, [ctypes.c_void_p]),
+    "plamo_batch_prefill": (ctypes.c_int, [ctypes.c_void_p, c_i32p, c_i32p, ctypes.c_int32, c_i32p,
+                                           ctypes.c_char_p, ctypes.c_size_t]),
+    "plamo_batch_step": (ctypes.c_int, [ctypes.c_void_p, c_i32p, ctypes.c_int32, c_i32p, ctypes.c_char_p,
+                                        ctypes.c_size_t]),
+    "plamo_batch_reset": (None, [ctypes.c_void_p]),
+    "plamo_batch_logits_bf16": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, c_u16p, ctypes.c_char_p,
+                                               ctypes.c_size_t]),
+    "plamo_batch_hidden": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, c_f32p, ctypes.c_char_p,
+                                          ctypes.c_size_t]),
+    "plamo_batch_kv": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, c_u16p, c_u16p, c_i32p,
+                                      ctypes.c_char_p, ctypes.c_size_t]),
+    "plamo_batch_positions": (ctypes.c_int, [ctypes.c_void_p, c_i32p, ctypes.c_int32, c_i32p]),
+    "plamo_decode_batch": (ctypes.c_int, [c_i32p, c_i32p, ctypes.c_int32, STEP_FN, EMIT_FN, FINISH_FN,
+                                          ctypes.c_void_p, ctypes.c_int32, c_i32p, ctypes.c_int32, c_i32p, c_i32p,
+                                          c_i32p, ctypes.c_char_p, ctypes.c_size_t]),
+    "plamo_batch_generate": (ctypes.c_int, [ctypes.c_void_p, c_i32p, c_i32p, c_i32p, ctypes.c_int32,
+                                            ctypes.c_int32, c_i32p, ctypes.c_int32, c_i32p, c_i32p, c_i32p,
+                                            ctypes.c_char_p, ctypes.c_size_t]),
+    "plamo_pack": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(PackReport),
+                                  ctypes.c_char_p, ctypes.c_size_t]),
+    "plamo_check_weights": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(ctypes.c_int64),
+                                           ctypes.c_int32, ctypes.c_char_p, ctypes.c_size_t]),
+    "plamo_check_packed": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p,
+                                          ctypes.POINTER(ctypes.c_int64), ctypes.c_int32, c_i32p, ctypes.c_char_p,
+                                          ctypes.c_size_t]),
+    "plamo_kernel_linear": (ctypes.c_int, [ctypes.c_uint64] * 4 + [ctypes.c_int32] * 4 + [ctypes.c_uint64]),
+    "plamo_kernel_unpack": (ctypes.c_int, [ctypes.c_uint64] * 3 + [ctypes.c_int64, ctypes.c_uint64]),
+    "plamo_kernel_argmax": (ctypes.c_int, [ctypes.c_uint64] * 2 + [ctypes.c_int32] * 3 + [ctypes.c_uint64]),
+    "plamo_kernel_select": (ctypes.c_int, [ctypes.c_uint64, ctypes.c_int32, ctypes.c_uint64, ctypes.c_int32,
+                                           ctypes.c_float, ctypes.c_int32, ctypes.c_float, ctypes.c_float,
+                                           ctypes.c_uint64, ctypes.c_uint64]),
+    "plamo_kernel_gemm": (ctypes.c_int, [ctypes.c_uint64] * 4 + [ctypes.c_int32] * 4 + [ctypes.c_uint64]),
+    "plamo_version": (ctypes.c_char_p, []),
+}
+
+_lib = None
+
+
+class PlamoError(RuntimeError):
+    def __init__(self, code, message):
+        super().__init__(message)
+        self.code = code
+
+
+def load():
+    """Load the HIP library (raises if it is missing: the product has no fallback)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"libplamo_hip.so not built: {LIB_PATH} (run make -C plamo3-0.8b-runtime_amd)")
+        lib = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+    return _lib
+
+
+def declared_symbols():
+    """Function names declared in include/plamo_hip.h."""
+    import re
+    text = open(HEADER_PATH).read()
+    return sorted(set(re.findall(r"\b(plamo_[a-z0-9_]+)\s*\(", text)) - {"plamo_step_fn", "plamo_emit_fn",
+                                                                         "plamo_finish_fn"})
+
+
+def call(fn, *args):
+    err = ctypes.create_string_buffer(512)
+    rc = fn(*args, err, 512)
+    if rc != 0:
+        raise PlamoError(rc, err.value.decode(errors="replace"))
+
+
+def i32(values):
+    arr = (ctypes.c_int32 * max(1, len(values)))(*values)
+    return arr
+
+
+def pack(source, output, source_sha256=None):
+    """scripts/pack_weights.py (pack_weights.py:89-142) through the native packer."""
+    rep = PackReport()
+    call(load().plamo_pack, source.encode(), output.encode(),
+         source_sha256.encode() if source_sha256 else None, ctypes.byref(rep))
+    return {k: getattr(rep, k) for k, _ in PackReport._fields_}

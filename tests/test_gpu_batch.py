@@ -1,0 +1,95 @@
+"""batch4: every lane's state is bit-equal to scalar decode of the same prompt
+(BatchMapTests.swift:6-73), for every subset of active lanes."""
+import numpy as np
+import pytest
+
+import plamo_hip
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def engines(model_dir):
+    d, sha = model_dir
+    rt = plamo_hip.Runtime(d, 160)
+    b = plamo_hip.Batch(rt)
+    yield rt, b
+    b.close()
+    rt.close()
+
+
+def prompts_for(lengths):
+    return [[1] + [1000 + k * 17 for k in range(1, n)] for n in lengths]
+
+
+def scalar_state(rt, prompt, steps):
+    rt.reset()
+    nxt = rt.prefill(prompt)
+    for _ in range(steps):
+        nxt = rt.forward([nxt])
+    kv = [rt.kv(l) for l in range(16)]
+    return nxt, rt.logit_bits().copy(), rt.hidden().copy(), kv
+
+
+@pytest.mark.parametrize("lengths", [[63, 3, 7, 5], [3, 63], [1, 4, 2], [2]])
+def test_batch_step_equals_scalar(engines, lengths):
+    rt, b = engines
+    prompts = prompts_for(lengths)
+    steps = 2
+    expected = [scalar_state(rt, p, steps) for p in prompts]
+    tokens = b.prefill(prompts)
+    for _ in range(steps):
+        tokens = b.step(tokens)
+    for lane, p in enumerate(prompts):
+        nxt, logits, hidden, kv = expected[lane]
+        assert tokens[lane] == nxt
+        assert np.array_equal(b.logit_bits(lane), logits)
+        assert np.array_equal(b.hidden(lane).view(np.uint32), hidden.view(np.uint32))
+        n = len(p) + steps
+        for layer in range(16):
+            k, v = b.kv(lane, layer)
+            assert np.array_equal(k[:n], kv[layer][0][:n]) and np.array_equal(v[:n], kv[layer][1][:n]), layer
+
+
+def test_lane_subsets(engines):
+    # masks 1..15 of active lanes: inactive lanes keep their state untouched
+    rt, b = engines
+    prompts = prompts_for([9, 5, 12, 3])
+    for mask in range(1, 16):
+        first = b.prefill(prompts)
+        tokens = [first[i] if mask >> i & 1 else None for i in range(4)]
+        out = b.step(tokens)
+        for lane in range(4):
+            if mask >> lane & 1:
+                nxt, logits, _, _ = scalar_state(rt, prompts[lane], 1)
+                assert out[lane] == nxt, (mask, lane)
+            else:
+                assert out[lane] == first[lane]
+        assert b.positions() == [len(p) + (mask >> i & 1) for i, p in enumerate(prompts)]
+
+
+def test_generate_matches_sequential(engines):
+    rt, b = engines
+    prompts = prompts_for([20, 14, 9, 30])
+    limits = [12, 5, 12, 8]
+    got = b.generate(prompts, limits)
+    for lane, (ids, reason) in enumerate(got):
+        rt.reset()
+        want, r = rt.generate(prompts[lane], limits[lane])
+        assert ids == want
+        assert reason == ("stop" if r == "stop" else "length")
+
+
+def test_batch_validation(engines, model_dir):
+    rt, b = engines
+    with pytest.raises(plamo_hip.PlamoError, match="Expected one to four valid prompts"):
+        b.prefill([])
+    b.reset()
+    with pytest.raises(plamo_hip.PlamoError, match="Invalid quad step"):
+        b.step([5])
+    big = plamo_hip.Runtime(model_dir[0], 8192)
+    try:
+        with pytest.raises(plamo_hip.PlamoError, match="below 8192"):
+            plamo_hip.Batch(big)
+    finally:
+        big.close()
