@@ -44,7 +44,7 @@ def gemv_microbench(torch, native, repeats=50):
         w = rng.standard_normal((m, n), dtype=np.float32) * np.float32(0.02)
         u = w.view(np.uint32)
         bits = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
-        entries, payload = pack_tensor(native, bits)
+        payload, entries = native.pack_tensor(bits)
         x = torch.randn(n, device="cuda").to(torch.bfloat16).float()
         wd = torch.from_numpy(bits.view(np.int16)).cuda()
         pd = torch.from_numpy(payload).cuda()
@@ -67,36 +67,6 @@ def gemv_microbench(torch, native, repeats=50):
                          "hbm_frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 3)}
         out[name] = res
     return out
-
-
-def pack_tensor(native, bits):
-    """Packs one BF16 matrix with the native packer via a temporary safetensors file."""
-    import hashlib
-    import struct
-    import tempfile
-    import numpy as np
-    with tempfile.TemporaryDirectory() as d:
-        emb = np.zeros((107520, 1536), np.uint16)
-        hdr = {"model.embed_tokens.weight": {"dtype": "BF16", "shape": [107520, 1536],
-                                             "data_offsets": [0, emb.nbytes]},
-               "w.weight": {"dtype": "BF16", "shape": list(bits.shape),
-                            "data_offsets": [emb.nbytes, emb.nbytes + bits.nbytes]}}
-        js = json.dumps(hdr).encode()
-        js += b" " * ((-(8 + len(js))) % 8)
-        src = os.path.join(d, "w.safetensors")
-        with open(src, "wb") as f:
-            f.write(struct.pack("<Q", len(js)) + js + emb.tobytes() + bits.tobytes())
-        sha = hashlib.sha256(open(src, "rb").read()).hexdigest()
-        out = os.path.join(d, "w.p12")
-        native.pack(src, out, sha)
-        with open(out, "rb") as f:
-            n = struct.unpack("<Q", f.read(8))[0]
-            h = json.loads(f.read(n))
-            payload = np.frombuffer(f.read(), dtype=np.uint8)
-        r = h["tensors"]["w.weight"]
-        entries = payload[r["offsets"][0]:r["offsets"][1]].view(np.uint32).copy()
-        data = payload[r["data"][0]:r["data"][1]].copy()
-        return entries, data
 
 
 def cpu_baseline(model_dir, prompt, decode_tokens):

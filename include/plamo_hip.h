@@ -193,6 +193,12 @@ typedef struct plamo_pack_report {
 int plamo_pack(const char* safetensors, const char* output, const char* source_sha256,
                plamo_pack_report* report, char* err, size_t errlen);
 
+/* pack_weights.py pack()/tag() (pack_weights.py:19-50,71-74) on one in-memory BF16 tensor of
+ * `count` values (count % 128 == 0): writes the payload (capacity `payload_cap` bytes; at most
+ * count*2) and count/128 tagged table entries; `*payload_bytes` receives the payload size. */
+int plamo_pack_tensor(const uint16_t* values, int64_t count, uint8_t* payload, int64_t payload_cap,
+                      uint32_t* table, int64_t* payload_bytes, char* err, size_t errlen);
+
 /* Weights(path:).tensor(name, shape) validation (Runtime.swift:33-101) without a device. */
 int plamo_check_weights(const char* path, const char* name, const int64_t* shape, int32_t ndim, char* err,
                         size_t errlen);
@@ -224,10 +230,12 @@ int plamo_kernel_argmax(uint64_t x, uint64_t out, int32_t n, int32_t rows, int32
 int plamo_kernel_select(uint64_t logits, int32_t n, uint64_t history, int32_t hist, float penalty,
                         int32_t ngram, float frequency, float presence, uint64_t out, uint64_t stream);
 
-/* MFMA BF16 GEMM of the prefill path: Y[t][m] = roundbf(sum_k X[t][k] W[m][k]) with
- * X BF16 [tokens][n], W plain BF16 or .p12 ([m][n]), Y FP32 or BF16 (out_bf16). */
+/* MFMA BF16 GEMM of the prefill path: Y[t][m] = sum_k X[t][k] W[m][k] with X BF16
+ * [tokens][n] and W plain BF16 or .p12 ([m][n]).  out_mode 0: Y FP32 BF16-rounded
+ * (`matrix` full == 0); 1: Y BF16 bits (full == 2); 2: Y raw FP32 (full == 1,
+ * Kernels.metal:196-197). */
 int plamo_kernel_gemm(uint64_t w, uint64_t table, uint64_t x, uint64_t y, int32_t n, int32_t m, int32_t tokens,
-                      int32_t out_bf16, uint64_t stream);
+                      int32_t out_mode, uint64_t stream);
 
 /* Library build identification (gfx arch, HIP version). */
 const char* plamo_version(void);

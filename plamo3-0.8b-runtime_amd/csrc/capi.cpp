@@ -403,6 +403,20 @@ int plamo_pack(const char* src, const char* out, const char* sha, plamo_pack_rep
     });
 }
 
+int plamo_pack_tensor(const uint16_t* values, int64_t count, uint8_t* payload, int64_t payload_cap, uint32_t* table,
+                      int64_t* payload_bytes, char* err, size_t errlen) {
+    return guard(err, errlen, [&] {
+        if (!values || !payload || !table || count <= 0 || count % 128 != 0)
+            throw plamo::Error(plamo::E_INVAL, "pack_tensor expects a multiple of 128 values");
+        std::vector<uint32_t> entries;
+        auto data = plamo::pack_blocks(values, size_t(count), entries, nullptr);
+        if (int64_t(data.size()) > payload_cap) throw plamo::Error(plamo::E_INVAL, "payload buffer too small");
+        std::memcpy(payload, data.data(), data.size());
+        std::memcpy(table, entries.data(), entries.size() * 4);
+        if (payload_bytes) *payload_bytes = int64_t(data.size());
+    });
+}
+
 int plamo_check_weights(const char* path, const char* name, const int64_t* shape, int32_t ndim, char* err, size_t errlen) {
     return guard(err, errlen, [&] {
         plamo::SafeTensors st(path ? path : "");
@@ -486,7 +500,9 @@ int plamo_kernel_gemm(uint64_t w, uint64_t table, uint64_t x, uint64_t y, int32_
         g.m = m;
         g.k = n;
         g.tokens = tokens;
-        plamo::launch_gemm(table != 0, out_bf16 ? plamo::GEMM_BF16 : plamo::GEMM_F32, g,
+        if (out_bf16 < 0 || out_bf16 > 2) throw plamo::Error(plamo::E_INVAL, "bad GEMM output mode");
+        const plamo::GemmEpilogue epi = out_bf16 == 1 ? plamo::GEMM_BF16 : out_bf16 == 2 ? plamo::GEMM_RAW : plamo::GEMM_F32;
+        plamo::launch_gemm(table != 0, epi, g,
                            reinterpret_cast<hipStream_t>(stream));
         PLAMO_HIP(hipGetLastError());
     });

@@ -233,7 +233,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvParams p) {
                         for (int k = 0; k < 2; ++k) {
                             const float gt = roundbf(acc[k][q]);
                             const float up = roundbf(acc[2 + k][q]);
-                            p.out[size_t(q) * INTER + 2 * g + k] = roundbf(roundbf(gt / (1.0f + expf(-gt))) * up);
+                            p.out[size_t(q) * INTER + 2 * g + k] = roundbf(roundbf(gt / (1.0f + exp_det(-gt))) * up);
                         }
         } else {  // EPI_LOGITS
 #pragma unroll
@@ -308,6 +308,7 @@ constexpr int KS = 129;  // padded LDS row of rotated keys
 
 template <bool FULL>
 __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
+#pragma clang fp contract(off)  // fixed rounding sequence, reproduced by the CPU oracle
     __shared__ float zs[17 * HEAD_DIM];
     __shared__ float qs[HEADS * HEAD_DIM];
     __shared__ float ks[KP * KS];
@@ -447,7 +448,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
             for (int hh = 0; hh < 4; ++hh) {
                 const float sc = valid ? s[hh] * SCALE : NEG_INF;
                 const float m = wave_max(sc);
-                const float e = valid ? expf(sc - m) : 0.f;
+                const float e = valid ? exp_det(sc - m) : 0.f;
                 const float l = wave_sum(e);
                 ps[(hb + hh) * KP + j] = e;
                 if (lane == 0) {
@@ -464,7 +465,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
             for (int j = 0; j < KP; ++j) {
                 const float v = bf(vs[j * HEAD_DIM + d]);
 #pragma unroll
-                for (int hh = 0; hh < 8; ++hh) o[hh] = fmaf(ps[(hb + hh) * KP + j], v, o[hh]);
+                for (int hh = 0; hh < 8; ++hh) o[hh] = o[hh] + ps[(hb + hh) * KP + j] * v;
             }
 #pragma unroll
             for (int hh = 0; hh < 8; ++hh) p.part_o[(pslot * HEADS + hb + hh) * HEAD_DIM + d] = o[hh];
@@ -488,7 +489,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
         for (uint32_t k = 0; k < nparts; ++k) M = fmaxf(M, __builtin_nontemporal_load(&p.part_m[(row0 + k) * HEADS + h]));
         float num = 0.f, den = 0.f;
         for (uint32_t k = 0; k < nparts; ++k) {
-            const float w = expf(__builtin_nontemporal_load(&p.part_m[(row0 + k) * HEADS + h]) - M);
+            const float w = exp_det(__builtin_nontemporal_load(&p.part_m[(row0 + k) * HEADS + h]) - M);
             den += __builtin_nontemporal_load(&p.part_l[(row0 + k) * HEADS + h]) * w;
             num += __builtin_nontemporal_load(&p.part_o[((row0 + k) * HEADS + h) * HEAD_DIM + d]) * w;
         }

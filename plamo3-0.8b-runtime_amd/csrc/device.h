@@ -69,6 +69,27 @@ __device__ __forceinline__ uint4 p12_decode8(uint2 sm, uint32_t nib, uint32_t ta
     return r;
 }
 
+// exp(x) with a fixed operation sequence the CPU oracle reproduces bit for bit:
+// Cody-Waite reduction x = k*ln2 + r (ln2 split in a 16-bit head, so k*LN2_HI is exact for
+// |k| <= 128), degree-7 Taylor polynomial of e^r in Horner form, then an exact 2^k scale.
+// Every product and sum is rounded separately (no contraction).  Accuracy: about 2 ulp.
+__device__ __forceinline__ float exp_det(float x) {
+#pragma clang fp contract(off)
+    if (!(x > -80.0f)) return 0.0f;  // no subnormal results; -inf maps to 0
+    if (x > 88.72283935546875f) return __builtin_inff();
+    const float k = rintf(x * 1.44269502162933349609375f);
+    const float r = (x - k * 0.693145751953125f) - k * 1.428606765330187e-06f;
+    float p = 1.98412698e-04f;                 // 1/7!
+    p = p * r + 1.38888889e-03f;               // 1/6!
+    p = p * r + 8.33333377e-03f;               // 1/5!
+    p = p * r + 4.16666679e-02f;               // 1/4!
+    p = p * r + 1.66666672e-01f;               // 1/3!
+    p = p * r + 0.5f;
+    p = p * r + 1.0f;
+    p = p * r + 1.0f;
+    return ldexpf(p, int(k));
+}
+
 // Rotate-half RoPE of the pair (a = x[d], b = x[d+64]) (Kernels.metal:261-274):
 // out[d] = roundbf(roundbf(a*c) + roundbf(-b*s)), out[d+64] = roundbf(roundbf(b*c) + roundbf(a*s)).
 __device__ __forceinline__ void rope_pair(float a, float b, float2 cs, float& ra, float& rb) {

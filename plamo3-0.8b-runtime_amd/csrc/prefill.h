@@ -7,7 +7,7 @@
 
 namespace plamo {
 
-enum GemmEpilogue { GEMM_F32 = 0, GEMM_BF16 = 1, GEMM_SWIGLU = 2 };
+enum GemmEpilogue { GEMM_F32 = 0, GEMM_BF16 = 1, GEMM_SWIGLU = 2, GEMM_RAW = 3 };
 
 struct GemmParams {
     const uint16_t* w;      // plain BF16 [m][k] or .p12 payload

@@ -108,7 +108,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmParams p) {
                 const int m = n0 + c * 32 + j;
                 const float g = roundbf(acc[c][r]);
                 const float u = roundbf(acc[c + 2][r]);
-                p.y16[size_t(t) * INTER + m] = uint16_t(bits(roundbf(g / (1.0f + expf(-g))) * u));
+                p.y16[size_t(t) * INTER + m] = uint16_t(bits(roundbf(g / (1.0f + exp_det(-g))) * u));
             }
         } else {
 #pragma unroll
@@ -116,6 +116,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmParams p) {
                 const int m = n0 + c * 32 + j;
                 if (m >= p.m) continue;
                 if constexpr (EPI == GEMM_F32) p.y[size_t(t) * p.m + m] = roundbf(acc[c][r]);
+                else if constexpr (EPI == GEMM_RAW) p.y[size_t(t) * p.m + m] = acc[c][r];
                 else p.y16[size_t(t) * p.m + m] = uint16_t(bits(acc[c][r]));
             }
         }
@@ -221,10 +222,12 @@ void launch_gemm(bool packed, GemmEpilogue epi, const GemmParams& p, hipStream_t
     if (packed) {
         if (epi == GEMM_F32) PLAMO_GEMM(true, GEMM_F32);
         else if (epi == GEMM_BF16) PLAMO_GEMM(true, GEMM_BF16);
+        else if (epi == GEMM_RAW) PLAMO_GEMM(true, GEMM_RAW);
         else PLAMO_GEMM(true, GEMM_SWIGLU);
     } else {
         if (epi == GEMM_F32) PLAMO_GEMM(false, GEMM_F32);
         else if (epi == GEMM_BF16) PLAMO_GEMM(false, GEMM_BF16);
+        else if (epi == GEMM_RAW) PLAMO_GEMM(false, GEMM_RAW);
         else PLAMO_GEMM(false, GEMM_SWIGLU);
     }
 #undef PLAMO_GEMM

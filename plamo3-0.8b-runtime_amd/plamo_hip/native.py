@@ -81,6 +81,9 @@ _SIGNATURES = {
                                             ctypes.c_char_p, ctypes.c_size_t]),
     "plamo_pack": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(PackReport),
                                   ctypes.c_char_p, ctypes.c_size_t]),
+    "plamo_pack_tensor": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64,
+                                         ctypes.c_void_p, ctypes.POINTER(ctypes.c_int64), ctypes.c_char_p,
+                                         ctypes.c_size_t]),
     "plamo_check_weights": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(ctypes.c_int64),
                                            ctypes.c_int32, ctypes.c_char_p, ctypes.c_size_t]),
     "plamo_check_packed": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p,
@@ -146,3 +149,15 @@ def pack(source, output, source_sha256=None):
     call(load().plamo_pack, source.encode(), output.encode(),
          source_sha256.encode() if source_sha256 else None, ctypes.byref(rep))
     return {k: getattr(rep, k) for k, _ in PackReport._fields_}
+
+
+def pack_tensor(bits):
+    """pack_weights.py pack()+tag() for one BF16 array -> (payload u8, table u32)."""
+    import numpy as np
+    bits = np.ascontiguousarray(bits, dtype=np.uint16).reshape(-1)
+    payload = np.empty(bits.size * 2, dtype=np.uint8)
+    table = np.empty(bits.size // 128, dtype=np.uint32)
+    n = ctypes.c_int64()
+    call(load().plamo_pack_tensor, bits.ctypes.data, bits.size, payload.ctypes.data, payload.size,
+         table.ctypes.data, ctypes.byref(n))
+    return payload[:n.value].copy(), table

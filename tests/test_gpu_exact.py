@@ -1,0 +1,84 @@
+"""Bit-exact decode: the GPU decode step equals the order-exact CPU restatement
+(oracle/exact.py) in every logit bit, hidden bit, KV bit and token.
+
+Config 1 in full: the 64-token prompt consumed through the decode step (Runtime.forward of
+one token, Runtime.swift:321-467), then 31 greedy steps -- 95 steps, plain BF16; a shorter
+run with the .p12 weights; and the sampling controls (Sampler.select over generated-only
+history, Main.swift:237-244) on the device against the restated select on exact logits.
+"""
+import numpy as np
+import pytest
+
+import plamo_hip
+from oracle import exact, sampler
+from oracle.bf16 import bf_np
+
+pytestmark = pytest.mark.gpu
+
+
+def run_pair(rt, ex, prompt, decode, check_kv=True):
+    nxt, ids = None, []
+    for pos in range(len(prompt) + decode):
+        t = prompt[pos] if pos < len(prompt) else nxt
+        if pos >= len(prompt):
+            ids.append(t)
+        got = rt.forward([t])
+        bits, hidden, want = ex.step(t, pos)
+        assert np.array_equal(rt.logit_bits(), bits), pos
+        assert np.array_equal(rt.hidden().view(np.uint32), hidden.view(np.uint32)), pos
+        assert got == want, pos
+        nxt = got
+        if pos % 16 == 15:
+            print(f"  bit-exact through step {pos}", flush=True)
+    if check_kv:
+        n = len(prompt) + decode
+        for layer in range(16):
+            k, v = rt.kv(layer)
+            assert np.array_equal(k[:n], ex.keys[layer][:n]) and np.array_equal(v[:n], ex.values[layer][:n]), layer
+    return ids
+
+
+def test_config1_decode_bit_exact(model_dir, oracle_weights, golden):
+    d, _ = model_dir
+    rt = plamo_hip.Runtime(d, 96)
+    ex = exact.ExactDecoder(oracle_weights, 96, rt.stats()["local_capacity"])
+    ids = run_pair(rt, ex, golden["config1"]["prompt"], 31)
+    assert len(ids) == 31
+    rt.close()
+
+
+def test_packed_decode_bit_exact(model_dir, oracle_weights, golden):
+    d, sha = model_dir
+    rt = plamo_hip.Runtime(d, 32, packed=True, source_sha256=sha)
+    ex = exact.ExactDecoder(oracle_weights, 32, rt.stats()["local_capacity"])
+    run_pair(rt, ex, golden["config1"]["prompt"][:6], 6)
+    rt.close()
+
+
+def test_sampling_controls_bit_exact(model_dir, oracle_weights, golden):
+    d, _ = model_dir
+    penalty, frequency, ngram = 1.1, 0.2, 4
+    rt = plamo_hip.Runtime(d, 64)
+    ex = exact.ExactDecoder(oracle_weights, 64, rt.stats()["local_capacity"])
+    prompt = golden["config1"]["prompt"][:8]
+    rt.set_sampling(penalty, frequency, 0.0, ngram)
+    for pos, t in enumerate(prompt[:-1]):
+        rt.forward([t])
+        ex.step(t, pos)
+    generated = []
+    nxt = rt.forward([prompt[-1]])
+    bits, _, _ = ex.step(prompt[-1], len(prompt) - 1)
+    assert nxt == sampler.select(bf_np(bits).copy(), generated, penalty, ngram, frequency)
+    pos = len(prompt)
+    for _ in range(20):
+        if nxt in (1, 16):
+            break
+        generated.append(nxt)
+        rt.observe(nxt)
+        t = nxt
+        nxt = rt.forward([t])
+        bits, _, _ = ex.step(t, pos)
+        pos += 1
+        assert np.array_equal(rt.logit_bits(), bits)
+        assert nxt == sampler.select(bf_np(bits).copy(), generated, penalty, ngram, frequency)
+    rt.close()
