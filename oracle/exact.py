@@ -13,7 +13,8 @@ correctly rounded IEEE FP32 operation, exactly as on the device):
   butterfly (offsets 32,16,8,4,2,1).
 * RMSNorm (`norm`, Kernels.metal:46-90): thread t of 256 sums squares of elements t+256k
   (k = 0..5); wave butterfly; then (w0+w1)+(w2+w3).  r = 1/sqrt(sum/n + 1e-6).
-* q/k norm (`qkv`, Kernels.metal:236-246): 16 lanes x 8 elements, 16-lane butterfly.
+* q/k norm (`qkv`, Kernels.metal:236-246): 16 lanes x 8 elements (the RoPE pairs d, d+64
+  of 4 consecutive d), 16-lane butterfly.
 * decode attention (Kernels.metal:440-562 split form): 64-key partitions; score = ordered
   sum over d of q*k; softmax statistics per partition with `exp_det`; P.V accumulated in key
   order without contraction; merge over partitions in order.
@@ -130,11 +131,13 @@ def norm_rows(x, w_bits, offset):
 
 
 def head_norm(v, w_bits):
-    """q/k RMSNorm over 128 (16 lanes x 8, 16-lane butterfly), +1 offset."""
+    """q/k RMSNorm over 128, +1 offset: lane `sub` of 16 sums the squares of dims
+    sub*4+j then 64+sub*4+j (j = 0..3) in that order; 16-lane XOR butterfly."""
+    v = v.astype(F)
+    lanes = np.concatenate([v[:64].reshape(16, 4), v[64:].reshape(16, 4)], axis=1)
     ss = np.zeros(16, F)
-    t = v.astype(F).reshape(16, 8)
     for j in range(8):
-        ss += t[:, j] * t[:, j]
+        ss += lanes[:, j] * lanes[:, j]
     tot = butterfly(ss[None, :])[0]
     r = F(1) / np.sqrt(F(tot / F(128)) + EPS)
     return roundbf_np(roundbf_np(v * r) * gain(w_bits, 1.0))

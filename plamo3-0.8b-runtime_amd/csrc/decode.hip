@@ -50,16 +50,22 @@ __device__ __forceinline__ void stage_rows(const GemvParams& p, int rows, uint16
             }
         } else {
             // z = roundbf(roundbf(p*r) * roundbf(bf(w)+offset)); x = roundbf(x + z)
-            // (Kernels.metal:59-72, full == 1)
-            float pv[MAXR][E];
+            // (Kernels.metal:59-72, full == 1).  Every independent load is issued first.
+            float pv[MAXR][E], rv[MAXR][E], gp[E];
+#pragma unroll
+            for (int k = 0; k < E; ++k) gp[k] = bf(p.g_post[tid + 256 * k]);
+#pragma unroll
+            for (int q = 0; q < MAXR; ++q)
+#pragma unroll
+                for (int k = 0; k < E; ++k) {
+                    pv[q][k] = (q < rows) ? p.in[q * HIDDEN + tid + 256 * k] : 0.f;
+                    rv[q][k] = (q < rows) ? p.resid_in[q * HIDDEN + tid + 256 * k] : 0.f;
+                }
 #pragma unroll
             for (int q = 0; q < MAXR; ++q) {
                 ss[q] = 0.f;
 #pragma unroll
-                for (int k = 0; k < E; ++k) {
-                    pv[q][k] = (q < rows) ? p.in[q * HIDDEN + tid + 256 * k] : 0.f;
-                    ss[q] += pv[q][k] * pv[q][k];
-                }
+                for (int k = 0; k < E; ++k) ss[q] += pv[q][k] * pv[q][k];
             }
 #pragma unroll
             for (int q = 0; q < MAXR; ++q) {
@@ -73,15 +79,17 @@ __device__ __forceinline__ void stage_rows(const GemvParams& p, int rows, uint16
                 const float r = 1.0f / sqrtf(total / float(HIDDEN) + 1e-6f);
 #pragma unroll
                 for (int k = 0; k < E; ++k) {
-                    const int i = tid + 256 * k;
-                    const float g = roundbf(bf(p.g_post[i]) + p.post_offset);
+                    const float g = roundbf(gp[k] + p.post_offset);
                     const float z = roundbf(roundbf(pv[q][k] * r) * g);
-                    xv[q][k] = (q < rows) ? roundbf(p.resid_in[q * HIDDEN + i] + z) : 0.f;
+                    xv[q][k] = (q < rows) ? roundbf(rv[q][k] + z) : 0.f;
                 }
             }
             __syncthreads();
         }
         // next norm with +1 offset (Kernels.metal:76-89)
+        float gn[E];
+#pragma unroll
+        for (int k = 0; k < E; ++k) gn[k] = roundbf(bf(p.g_next[tid + 256 * k]) + 1.0f);
 #pragma unroll
         for (int q = 0; q < MAXR; ++q) {
             ss[q] = 0.f;
@@ -99,8 +107,7 @@ __device__ __forceinline__ void stage_rows(const GemvParams& p, int rows, uint16
 #pragma unroll
             for (int k = 0; k < E; ++k) {
                 const int i = tid + 256 * k;
-                const float g = roundbf(bf(p.g_next[i]) + 1.0f);
-                const float xn = roundbf(roundbf(xv[q][k] * r) * g);
+                const float xn = roundbf(roundbf(xv[q][k] * r) * gn[k]);
                 xs[q * HIDDEN + i] = uint16_t(bits(xn));
                 if (blockIdx.x == 0) {
                     p.resid_out[q * HIDDEN + i] = xv[q][k];
@@ -136,14 +143,20 @@ __device__ __forceinline__ bool better(float v, uint32_t i, float bv, uint32_t b
     return v > bv || (v == bv && i < bi);  // Kernels.metal:716
 }
 
+struct Controls {
+    bool on;
+    int ngram;
+    float penalty, frequency, presence;
+};
+
 // Sampler.select adjustments of one logit (Sampler.swift:11-24), FP32, no contraction.
-__device__ __forceinline__ float sampled(float l, int32_t count, bool banned, const StepState* st) {
+__device__ __forceinline__ float sampled(float l, int32_t count, bool banned, const Controls& c) {
 #pragma clang fp contract(off)
     if (count > 0) {
-        if (st->penalty != 1.0f) l = l > 0.0f ? l / st->penalty : l * st->penalty;
-        if (st->presence != 0.0f) l = l - st->presence;
-        if (st->frequency != 0.0f) {
-            const float f = st->frequency * float(count);
+        if (c.penalty != 1.0f) l = l > 0.0f ? l / c.penalty : l * c.penalty;
+        if (c.presence != 0.0f) l = l - c.presence;
+        if (c.frequency != 0.0f) {
+            const float f = c.frequency * float(count);
             l = l - f;
         }
     }
@@ -159,12 +172,15 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvParams p) {
     __shared__ float red[MAXR * 4];
     __shared__ float cand_v[MAXR * 4];
     __shared__ uint32_t cand_i[MAXR * 4];
-    __shared__ int s_last;
 
     const StepState* st = p.state;
     if (st && st->stopped) return;
     const int rows = st ? int(st->rows) : p.rows;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    Controls ctl{false, 0, 1.0f, 0.0f, 0.0f};
+    if constexpr (EPI == EPI_LOGITS) {
+        if (st && st->sampling) ctl = Controls{true, st->ngram, st->penalty, st->frequency, st->presence};
+    }
 
     stage_rows<N, MAXR, PRO>(p, rows, xs, red);
     __syncthreads();
@@ -175,18 +191,39 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvParams p) {
 #pragma unroll
     for (int q = 0; q < MAXR; ++q) { best_v[q] = NEG_INF; best_i[q] = 0xffffffffu; }
 
-    for (int g = blockIdx.x * 4 + wave; g < groups; g += gridDim.x * 4) {
-        int wrow[U];
+    auto rows_of = [&](int g, int* wrow) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             if constexpr (EPI == EPI_SWIGLU) wrow[u] = (u < 2) ? 2 * g + u : INTER + 2 * g + (u - 2);
             else wrow[u] = g * U + u;
         }
-        uint4 w[U][IT];
+    };
+    // Software pipelined over the wave's row groups: the next group's weights are in flight
+    // while the current group is reduced and written.
+    const int stride = gridDim.x * 4;
+    int g = blockIdx.x * 4 + wave;
+    uint4 w[U][IT];
+    if (g < groups) {
+        int wrow[U];
+        rows_of(g, wrow);
 #pragma unroll
         for (int u = 0; u < U; ++u)
 #pragma unroll
             for (int it = 0; it < IT; ++it) w[u][it] = load_w<N, PACKED>(p, wrow[u], it, lane);
+    }
+    for (; g < groups; g += stride) {
+        int wrow[U];
+        rows_of(g, wrow);
+        uint4 wn[U][IT];
+        const int gn = g + stride;
+        if (gn < groups) {
+            int nrow[U];
+            rows_of(gn, nrow);
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+#pragma unroll
+                for (int it = 0; it < IT; ++it) wn[u][it] = load_w<N, PACKED>(p, nrow[u], it, lane);
+        }
         float acc[U][MAXR];
 #pragma unroll
         for (int u = 0; u < U; ++u)
@@ -244,21 +281,27 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvParams p) {
                     const uint32_t b = bits(acc[u][q]);
                     if (lane == 0) p.out16[size_t(q) * VOCAB + wrow[u]] = uint16_t(b);
                     float v = bf(b);
-                    if (st && st->sampling) {
+                    if (ctl.on) {
                         const uint32_t r = uint32_t(wrow[u]);
                         const int32_t c = p.bufs.counts[size_t(q) * VOCAB + r];
-                        const bool ban = st->ngram > 1 &&
+                        const bool ban = ctl.ngram > 1 &&
                                          ((p.bufs.banned[size_t(q) * (VOCAB / 32) + (r >> 5)] >> (r & 31)) & 1u);
-                        v = sampled(v, c, ban, st);
+                        v = sampled(v, c, ban, ctl);
                     }
                     if (better(v, uint32_t(wrow[u]), best_v[q], best_i[q])) { best_v[q] = v; best_i[q] = wrow[u]; }
                 }
             }
         }
+        if (gn < groups) {
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+#pragma unroll
+                for (int it = 0; it < IT; ++it) w[u][it] = wn[u][it];
+        }
     }
 
     if constexpr (EPI == EPI_LOGITS) {
-        // block partial -> ticket -> the last workgroup merges in block order
+        // block partial; head_merge_kernel reduces the partials of every block
         if (lane == 0)
 #pragma unroll
             for (int q = 0; q < MAXR; ++q) { cand_v[q * 4 + wave] = best_v[q]; cand_i[q * 4 + wave] = best_i[q]; }
@@ -272,48 +315,63 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvParams p) {
             p.bufs.head_v[q * HEAD_BLOCKS + blockIdx.x] = bv;
             p.bufs.head_i[q * HEAD_BLOCKS + blockIdx.x] = bi;
         }
-        __threadfence();
-        __syncthreads();
-        if (tid == 0) {
-            const uint32_t prev = atomicAdd(&p.bufs.tickets[0], 1u);
-            s_last = prev == gridDim.x - 1;
+    }
+}
+
+// First maximum over the LM-head block partials (Kernels.metal:704-729 semantics: ties to
+// the lowest index, NaN never wins, none -> 0xffffffff; Sampler.select defaults to 0), then
+// the device side of the token loop: feed the token back and advance the position.
+__global__ __launch_bounds__(256) void head_merge_kernel(DecodeBuffers b, int blocks) {
+    __shared__ float cv[ROWS * 4];
+    __shared__ uint32_t ci[ROWS * 4];
+    StepState* st = b.state;
+    if (st->stopped) return;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int rows = int(st->rows);
+    for (int q = 0; q < rows && q < ROWS; ++q) {
+        float bv = NEG_INF;
+        uint32_t bi = 0xffffffffu;
+        for (int k = tid; k < blocks; k += 256) {
+            const float v = b.head_v[q * HEAD_BLOCKS + k];
+            const uint32_t i = b.head_i[q * HEAD_BLOCKS + k];
+            if (better(v, i, bv, bi)) { bv = v; bi = i; }
         }
-        __syncthreads();
-        if (!s_last) return;
-        __threadfence();
-        if (tid < MAXR && tid < rows) {
-            const int q = tid;
-            float bv = NEG_INF;
-            uint32_t bi = 0xffffffffu;
-            for (int k = 0; k < int(gridDim.x); ++k) {
-                const float v = __builtin_nontemporal_load(&p.bufs.head_v[q * HEAD_BLOCKS + k]);
-                const uint32_t i = __builtin_nontemporal_load(&p.bufs.head_i[q * HEAD_BLOCKS + k]);
-                if (better(v, i, bv, bi)) { bv = v; bi = i; }
-            }
-            StepState* sw = p.bufs.state;
-            if (sw->sampling && bi == 0xffffffffu) bi = 0;  // Sampler.select default index (Sampler.swift:26)
-            sw->next[q] = bi;
-            if (sw->loop) {
-                sw->token[q] = int32_t(bi);
-                sw->pos[q] += 1;
-            }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            const float v = __shfl_xor(bv, o, 64);
+            const uint32_t i = __shfl_xor(bi, o, 64);
+            if (better(v, i, bv, bi)) { bv = v; bi = i; }
         }
-        if (tid == 0) p.bufs.tickets[0] = 0;
+        if (lane == 0) { cv[q * 4 + wave] = bv; ci[q * 4 + wave] = bi; }
+    }
+    __syncthreads();
+    if (tid < rows && tid < ROWS) {
+        const int q = tid;
+        float bv = cv[q * 4];
+        uint32_t bi = ci[q * 4];
+        for (int k = 1; k < 4; ++k)
+            if (better(cv[q * 4 + k], ci[q * 4 + k], bv, bi)) { bv = cv[q * 4 + k]; bi = ci[q * 4 + k]; }
+        if (st->sampling && bi == 0xffffffffu) bi = 0;  // Sampler.select default index (Sampler.swift:26)
+        st->next[q] = bi;
+        if (st->loop) {
+            st->token[q] = int32_t(bi);
+            st->pos[q] += 1;
+        }
     }
 }
 
 // ---------------------------------------------------------------------- decode attention
 constexpr int KP = KEYS_PER_PART;
-constexpr int KS = 129;  // padded LDS row of rotated keys
+constexpr int KS = 132;  // padded LDS row of rotated keys (16-byte aligned rows)
 
 template <bool FULL>
 __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
 #pragma clang fp contract(off)  // fixed rounding sequence, reproduced by the CPU oracle
-    __shared__ float zs[17 * HEAD_DIM];
-    __shared__ float qs[HEADS * HEAD_DIM];
-    __shared__ float ks[KP * KS];
+    __shared__ __align__(16) float qs[HEADS * HEAD_DIM];
+    __shared__ __align__(16) float ks[KP * KS];
     __shared__ __align__(16) uint16_t vs[KP * HEAD_DIM];
-    __shared__ float ps[HEADS * KP];
+    __shared__ __align__(16) float ps[HEADS * KP];
+    __shared__ __align__(16) float knew[HEAD_DIM];
     __shared__ int s_last;
 
     const StepState* st = p.state;
@@ -350,105 +408,137 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
     const size_t pslot = size_t(q) * p.parts + blockIdx.x;
 
     if (k0 < count) {
-        // q/k RMSNorm over 128 with +1 offset (Kernels.metal:236-246)
-        const float* x = p.qkv + size_t(q) * QKV;
-        for (int h = tid >> 4; h < 17; h += 16) {
-            const int sub = tid & 15;
-            float v[8];
-            float ss = 0.f;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                v[j] = x[h * HEAD_DIM + sub * 8 + j];
-                ss += v[j] * v[j];
-            }
-            ss = group16_sum(ss);
-            const float r = 1.0f / sqrtf(ss / 128.0f + 1e-6f);
-            const uint16_t* g = h < HEADS ? p.q_norm : p.k_norm;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int d = sub * 8 + j;
-                zs[h * HEAD_DIM + d] = roundbf(roundbf(v[j] * r) * roundbf(bf(g[d]) + 1.0f));
-            }
-        }
-        __syncthreads();
-        // RoPE of the queries: global at pos, local at pos-base (Kernels.metal:250-252)
-        const float2* qrope = FULL ? p.global_rope + size_t(pos) * 64 : p.local_rope + size_t(qcoord) * 64;
-        for (int e = tid; e < HEADS * 64; e += 256) {
-            const int h = e >> 6, d = e & 63;
-            float ra, rb;
-            rope_pair(zs[h * HEAD_DIM + d], zs[h * HEAD_DIM + d + 64], qrope[d], ra, rb);
-            qs[h * HEAD_DIM + d] = ra;
-            qs[h * HEAD_DIM + d + 64] = rb;
-        }
-        // Keys and values of this partition.  The newest key (relative index count-1) is
-        // produced here: stored normalised-unrotated (local) or rotated at pos (global),
-        // written to slot pos % capacity (Kernels.metal:253-257).
         const uint32_t newest = st ? count - 1 : 0xffffffffu;  // prefill keys are already cached
-        for (int e = tid; e < KP * 16; e += 256) {
-            const int j = e >> 4, c8 = e & 15;
-            const uint32_t r = k0 + j;
-            uint4 kv = make_uint4(0, 0, 0, 0), vv = make_uint4(0, 0, 0, 0);
-            if (r < count && r != newest) {
-                uint32_t phys = start + r;
-                phys = phys >= cap ? phys - cap : phys;  // visible keys (<= capacity) wrap at most once
-                kv = *reinterpret_cast<const uint4*>(K + size_t(phys) * HEAD_DIM + c8 * 8);
-                vv = *reinterpret_cast<const uint4*>(V + size_t(phys) * HEAD_DIM + c8 * 8);
+        const bool has_new = newest >= k0 && newest < k0 + KP;
+        const float* x = p.qkv + size_t(q) * QKV;
+        // ---- every independent global load first
+        const int hq = tid >> 4, sq = tid & 15;                 // q head, pair group (4 pairs)
+        const float4 qlo = *reinterpret_cast<const float4*>(x + hq * HEAD_DIM + sq * 4);
+        const float4 qhi = *reinterpret_cast<const float4*>(x + hq * HEAD_DIM + 64 + sq * 4);
+        const uint2 glo = *reinterpret_cast<const uint2*>(p.q_norm + sq * 4);
+        const uint2 ghi = *reinterpret_cast<const uint2*>(p.q_norm + 64 + sq * 4);
+        const uint4 qr = *reinterpret_cast<const uint4*>((FULL ? p.global_rope : p.local_rope) + size_t(qcoord) * 64 + sq * 4);
+        const int kj = tid >> 2, ksub = tid & 3;                // key, pair group (16 pairs)
+        const uint32_t kr = k0 + kj;
+        uint4 ka[2] = {make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)};
+        uint4 kb[2] = {make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)};
+        uint4 vv[4] = {make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)};
+        uint4 rr[4] = {make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)};
+        if (kr < count && kr != newest) {
+            uint32_t phys = start + kr;
+            phys = phys >= cap ? phys - cap : phys;  // visible keys (<= capacity) wrap at most once
+            const uint16_t* krow = K + size_t(phys) * HEAD_DIM;
+            ka[0] = *reinterpret_cast<const uint4*>(krow + ksub * 16);
+            ka[1] = *reinterpret_cast<const uint4*>(krow + ksub * 16 + 8);
+            kb[0] = *reinterpret_cast<const uint4*>(krow + 64 + ksub * 16);
+            kb[1] = *reinterpret_cast<const uint4*>(krow + 64 + ksub * 16 + 8);
+            const uint16_t* vrow = V + size_t(phys) * HEAD_DIM + ksub * 32;  // 32 of the 128 values
+#pragma unroll
+            for (int i = 0; i < 4; ++i) vv[i] = *reinterpret_cast<const uint4*>(vrow + 8 * i);
+        }
+        if (!FULL && kr < count) {
+            const uint4* rrow = reinterpret_cast<const uint4*>(p.local_rope + size_t(coff + kr) * 64 + ksub * 16);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) rr[i] = rrow[i];
+        }
+        // ---- queries: norm and RoPE in registers
+        {
+            float z[8];
+            head_norm8(qlo, qhi, glo, ghi, z);
+            const uint32_t c4[4] = {qr.x, qr.y, qr.z, qr.w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                float ra, rb;
+                rope_pair(z[j], z[4 + j], c4[j], ra, rb);
+                qs[hq * HEAD_DIM + sq * 4 + j] = ra;
+                qs[hq * HEAD_DIM + 64 + sq * 4 + j] = rb;
             }
-            float* kr = ks + j * KS + c8 * 8;
-            kr[0] = lo(kv.x); kr[1] = hi(kv.x); kr[2] = lo(kv.y); kr[3] = hi(kv.y);
-            kr[4] = lo(kv.z); kr[5] = hi(kv.z); kr[6] = lo(kv.w); kr[7] = hi(kv.w);
-            *reinterpret_cast<uint4*>(vs + j * HEAD_DIM + c8 * 8) = vv;
+        }
+        // ---- the newest key: k norm, RoPE at pos for global layers, KV write (Kernels.metal:253-257)
+        if (has_new && tid < 16) {
+            const float4 klo = *reinterpret_cast<const float4*>(x + ATTN + tid * 4);
+            const float4 khi = *reinterpret_cast<const float4*>(x + ATTN + 64 + tid * 4);
+            const uint2 gl = *reinterpret_cast<const uint2*>(p.k_norm + tid * 4);
+            const uint2 gh = *reinterpret_cast<const uint2*>(p.k_norm + 64 + tid * 4);
+            float z[8];
+            head_norm8(klo, khi, gl, gh, z);
+            const size_t slot = size_t(pos % cap) * HEAD_DIM;
+            if (FULL) {
+                const uint4 gr = *reinterpret_cast<const uint4*>(p.global_rope + size_t(pos) * 64 + tid * 4);
+                const uint32_t c4[4] = {gr.x, gr.y, gr.z, gr.w};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) rope_pair(z[j], z[4 + j], c4[j], z[j], z[4 + j]);
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                K[slot + tid * 4 + j] = uint16_t(bits(z[j]));
+                K[slot + 64 + tid * 4 + j] = uint16_t(bits(z[4 + j]));
+                knew[tid * 4 + j] = z[j];
+                knew[64 + tid * 4 + j] = z[4 + j];
+            }
+        }
+        if (has_new && tid >= 64 && tid < 192) {
+            const int d = tid - 64;
+            const uint32_t bv = bits(x[QKV - HEAD_DIM + d]);
+            V[size_t(pos % cap) * HEAD_DIM + d] = uint16_t(bv);
+            vs[int(newest - k0) * HEAD_DIM + d] = uint16_t(bv);
         }
         __syncthreads();
-        if (newest >= k0 && newest < k0 + KP) {
-            const int j = int(newest - k0);
-            const size_t slot = size_t(pos % cap) * HEAD_DIM;
-            if (tid < 64) {
-                const int d = tid;
-                float a = zs[16 * HEAD_DIM + d], b = zs[16 * HEAD_DIM + d + 64];
-                if (FULL) rope_pair(a, b, p.global_rope[size_t(pos) * 64 + d], a, b);
-                const uint32_t ba = bits(a), bb = bits(b);
-                K[slot + d] = uint16_t(ba);
-                K[slot + d + 64] = uint16_t(bb);
-                ks[j * KS + d] = bf(ba);
-                ks[j * KS + d + 64] = bf(bb);
-            } else if (tid < 192) {
-                const int d = tid - 64;
-                const uint32_t bv = bits(x[QKV - HEAD_DIM + d]);
-                V[slot + d] = uint16_t(bv);
-                vs[j * HEAD_DIM + d] = uint16_t(bv);
+        // ---- keys: (newest from LDS) rotate with coordinate coff + r, stage FP32 in LDS
+        {
+            float a[16], b[16];
+            const uint32_t aw[8] = {ka[0].x, ka[0].y, ka[0].z, ka[0].w, ka[1].x, ka[1].y, ka[1].z, ka[1].w};
+            const uint32_t bw[8] = {kb[0].x, kb[0].y, kb[0].z, kb[0].w, kb[1].x, kb[1].y, kb[1].z, kb[1].w};
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                a[2 * i] = lo(aw[i]); a[2 * i + 1] = hi(aw[i]);
+                b[2 * i] = lo(bw[i]); b[2 * i + 1] = hi(bw[i]);
             }
-            __syncthreads();
-        }
-        // Local keys are rotated with their chunk-relative coordinate r (Kernels.metal:283-284)
-        if (!FULL) {
-            for (int e = tid; e < KP * 64; e += 256) {
-                const int j = e >> 6, d = e & 63;
-                const uint32_t r = k0 + j;
-                if (r < count) {
-                    float ra, rb;
-                    rope_pair(ks[j * KS + d], ks[j * KS + d + 64], p.local_rope[size_t(coff + r) * 64 + d], ra, rb);
-                    ks[j * KS + d] = ra;
-                    ks[j * KS + d + 64] = rb;
-                }
+            if (kr == newest) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) { a[i] = knew[ksub * 16 + i]; b[i] = knew[64 + ksub * 16 + i]; }
             }
-            __syncthreads();
+            if (!FULL && kr < count) {
+                const uint32_t rw[16] = {rr[0].x, rr[0].y, rr[0].z, rr[0].w, rr[1].x, rr[1].y, rr[1].z, rr[1].w,
+                                         rr[2].x, rr[2].y, rr[2].z, rr[2].w, rr[3].x, rr[3].y, rr[3].z, rr[3].w};
+#pragma unroll
+                for (int i = 0; i < 16; ++i) rope_pair(a[i], b[i], rw[i], a[i], b[i]);
+            }
+            float* krow = ks + kj * KS;
+#pragma unroll
+            for (int i = 0; i < 16; i += 4) {
+                *reinterpret_cast<float4*>(krow + ksub * 16 + i) = make_float4(a[i], a[i + 1], a[i + 2], a[i + 3]);
+                *reinterpret_cast<float4*>(krow + 64 + ksub * 16 + i) = make_float4(b[i], b[i + 1], b[i + 2], b[i + 3]);
+            }
+            if (kr != newest) {  // the newest V row was staged before the barrier
+#pragma unroll
+                for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(vs + kj * HEAD_DIM + ksub * 32 + 8 * i) = vv[i];
+            }
         }
-        // scores for 4 heads per wave, one key per lane
+        __syncthreads();
+        // ---- scores for 4 heads per wave, one key per lane: ordered sum over d
         {
             const int j = lane, hb = wave * 4;
-            float s[4] = {0.f, 0.f, 0.f, 0.f};
-            for (int d = 0; d < HEAD_DIM; ++d) {
-                const float kd = ks[j * KS + d];
+            float sc[4] = {0.f, 0.f, 0.f, 0.f};
+            const float* krow = ks + j * KS;
+#pragma unroll 2
+            for (int d = 0; d < HEAD_DIM; d += 4) {
+                const float4 kd = *reinterpret_cast<const float4*>(krow + d);
 #pragma unroll
-                for (int hh = 0; hh < 4; ++hh) s[hh] = fmaf(qs[(hb + hh) * HEAD_DIM + d], kd, s[hh]);
+                for (int hh = 0; hh < 4; ++hh) {
+                    const float4 qd = *reinterpret_cast<const float4*>(qs + (hb + hh) * HEAD_DIM + d);
+                    sc[hh] = fmaf(qd.x, kd.x, sc[hh]);
+                    sc[hh] = fmaf(qd.y, kd.y, sc[hh]);
+                    sc[hh] = fmaf(qd.z, kd.z, sc[hh]);
+                    sc[hh] = fmaf(qd.w, kd.w, sc[hh]);
+                }
             }
             const bool valid = k0 + j < count;
 #pragma unroll
             for (int hh = 0; hh < 4; ++hh) {
-                const float sc = valid ? s[hh] * SCALE : NEG_INF;
-                const float m = wave_max(sc);
-                const float e = valid ? exp_det(sc - m) : 0.f;
+                const float s = valid ? sc[hh] * SCALE : NEG_INF;
+                const float m = wave_max(s);
+                const float e = valid ? exp_det(s - m) : 0.f;
                 const float l = wave_sum(e);
                 ps[(hb + hh) * KP + j] = e;
                 if (lane == 0) {
@@ -458,14 +548,22 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
             }
         }
         __syncthreads();
-        // unnormalised P.V for 8 heads x 1 dim per thread
+        // ---- unnormalised P.V for 8 heads x 1 dim per thread, keys in order
         {
             const int d = tid & 127, hb = (tid >> 7) * 8;
             float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-            for (int j = 0; j < KP; ++j) {
-                const float v = bf(vs[j * HEAD_DIM + d]);
+#pragma unroll 2
+            for (int j = 0; j < KP; j += 4) {
+                const float v0 = bf(vs[(j + 0) * HEAD_DIM + d]), v1 = bf(vs[(j + 1) * HEAD_DIM + d]);
+                const float v2 = bf(vs[(j + 2) * HEAD_DIM + d]), v3 = bf(vs[(j + 3) * HEAD_DIM + d]);
 #pragma unroll
-                for (int hh = 0; hh < 8; ++hh) o[hh] = o[hh] + ps[(hb + hh) * KP + j] * v;
+                for (int hh = 0; hh < 8; ++hh) {
+                    const float4 pp = *reinterpret_cast<const float4*>(ps + (hb + hh) * KP + j);
+                    o[hh] = o[hh] + pp.x * v0;
+                    o[hh] = o[hh] + pp.y * v1;
+                    o[hh] = o[hh] + pp.z * v2;
+                    o[hh] = o[hh] + pp.w * v3;
+                }
             }
 #pragma unroll
             for (int hh = 0; hh < 8; ++hh) p.part_o[(pslot * HEADS + hb + hh) * HEAD_DIM + d] = o[hh];
@@ -483,17 +581,41 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
     __threadfence();
     const uint32_t nparts = (count + KP - 1) / KP;
     const size_t row0 = size_t(q) * p.parts;
+    // per head: M = max_p m_p, w_p = exp(m_p - M), den = sum_p l_p w_p (partition order);
+    // the weights go to LDS (the key tile is free now), then each (h, d) sums o_p w_p.
+    float* wts = ks;                                   // [nparts][16], nparts <= KP*KS/16
+    __shared__ float den_s[HEADS];
+    const uint32_t np = nparts <= uint32_t(KP * KS / HEADS) ? nparts : uint32_t(KP * KS / HEADS);
+    if (tid < HEADS) {
+        const int h = tid;
+        float M = NEG_INF;
+#pragma unroll 4
+        for (uint32_t k = 0; k < nparts; ++k) M = fmaxf(M, p.part_m[(row0 + k) * HEADS + h]);
+        float den = 0.f;
+#pragma unroll 4
+        for (uint32_t k = 0; k < nparts; ++k) {
+            const float w = exp_det(p.part_m[(row0 + k) * HEADS + h] - M);
+            den = den + p.part_l[(row0 + k) * HEADS + h] * w;
+            if (k < np) wts[k * HEADS + h] = w;
+        }
+        den_s[h] = den;
+    }
+    __syncthreads();
     for (int e = tid; e < HEADS * HEAD_DIM; e += 256) {
         const int h = e >> 7, d = e & 127;
-        float M = NEG_INF;
-        for (uint32_t k = 0; k < nparts; ++k) M = fmaxf(M, __builtin_nontemporal_load(&p.part_m[(row0 + k) * HEADS + h]));
-        float num = 0.f, den = 0.f;
-        for (uint32_t k = 0; k < nparts; ++k) {
-            const float w = exp_det(__builtin_nontemporal_load(&p.part_m[(row0 + k) * HEADS + h]) - M);
-            den += __builtin_nontemporal_load(&p.part_l[(row0 + k) * HEADS + h]) * w;
-            num += __builtin_nontemporal_load(&p.part_o[((row0 + k) * HEADS + h) * HEAD_DIM + d]) * w;
+        float num = 0.f;
+        if (nparts == np) {
+#pragma unroll 4
+            for (uint32_t k = 0; k < nparts; ++k)
+                num = num + p.part_o[((row0 + k) * HEADS + h) * HEAD_DIM + d] * wts[k * HEADS + h];
+        } else {  // more partitions than the LDS table holds: recompute the weights
+            float M = NEG_INF;
+            for (uint32_t k = 0; k < nparts; ++k) M = fmaxf(M, p.part_m[(row0 + k) * HEADS + h]);
+            for (uint32_t k = 0; k < nparts; ++k)
+                num = num + p.part_o[((row0 + k) * HEADS + h) * HEAD_DIM + d] *
+                                exp_det(p.part_m[(row0 + k) * HEADS + h] - M);
         }
-        const float o = roundbf(num / den);
+        const float o = roundbf(num / den_s[h]);
         if (p.out16) p.out16[size_t(q) * ATTN + h * HEAD_DIM + d] = uint16_t(bits(o));
         else p.out[size_t(q) * ATTN + h * HEAD_DIM + d] = o;
     }
@@ -704,6 +826,10 @@ void launch_attention(bool full, const AttnParams& p, int rows, hipStream_t s) {
     const dim3 grid(p.parts, rows), block(256);
     if (full) hipLaunchKernelGGL(attn_decode_kernel<true>, grid, block, 0, s, p);
     else hipLaunchKernelGGL(attn_decode_kernel<false>, grid, block, 0, s, p);
+}
+
+void launch_head_merge(const DecodeBuffers& b, int blocks, hipStream_t s) {
+    hipLaunchKernelGGL(head_merge_kernel, dim3(1), dim3(256), 0, s, b, blocks);
 }
 
 void launch_step_begin(const DecodeBuffers& b, hipStream_t s) {

@@ -21,6 +21,8 @@ __device__ __forceinline__ uint32_t bits(float x) {
 __device__ __forceinline__ float roundbf(float x) { return bf(bits(x)); }
 __device__ __forceinline__ float lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+__device__ __forceinline__ float lo_bf(uint32_t w) { return lo(w); }
+__device__ __forceinline__ float hi_bf(uint32_t w) { return hi(w); }
 
 // Butterfly reductions over the 64-lane wavefront; every lane ends with the same bits.
 __device__ __forceinline__ float wave_sum(float v) {
@@ -92,9 +94,33 @@ __device__ __forceinline__ float exp_det(float x) {
 
 // Rotate-half RoPE of the pair (a = x[d], b = x[d+64]) (Kernels.metal:261-274):
 // out[d] = roundbf(roundbf(a*c) + roundbf(-b*s)), out[d+64] = roundbf(roundbf(b*c) + roundbf(a*s)).
-__device__ __forceinline__ void rope_pair(float a, float b, float2 cs, float& ra, float& rb) {
-    ra = roundbf(roundbf(a * cs.x) + roundbf(-b * cs.y));
-    rb = roundbf(roundbf(b * cs.x) + roundbf(a * cs.y));
+// `cs` packs the BF16 table entry: cos in the low half, sin in the high half.
+__device__ __forceinline__ void rope_pair(float a, float b, uint32_t cs, float& ra, float& rb) {
+    const float c = lo(cs), s = hi(cs);
+    const float na = roundbf(roundbf(a * c) + roundbf(-b * s));
+    const float nb = roundbf(roundbf(b * c) + roundbf(a * s));
+    ra = na;
+    rb = nb;
+}
+
+// q/k RMSNorm over 128 with +1 offset (Kernels.metal:236-246) for the 8 dims a lane of a
+// 16-lane group owns: d = sub*4+j and d+64 (j = 0..3).  Squares are summed in that order,
+// then over the 16 lanes by an XOR butterfly.
+__device__ __forceinline__ void head_norm8(const float4 lo, const float4 hi, const uint2 glo, const uint2 ghi,
+                                           float z[8]) {
+    float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ss += v[j] * v[j];
+    ss = group16_sum(ss);
+    const float r = 1.0f / sqrtf(ss / 128.0f + 1e-6f);
+    const uint32_t g[4] = {glo.x, glo.y, ghi.x, ghi.y};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const uint32_t gw = g[j >> 1];
+        const float gain = roundbf((j & 1 ? hi_bf(gw) : lo_bf(gw)) + 1.0f);
+        z[j] = roundbf(roundbf(v[j] * r) * gain);
+    }
 }
 
 }  // namespace dev

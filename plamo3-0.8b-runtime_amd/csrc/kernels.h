@@ -41,7 +41,7 @@ struct DecodeBuffers {
     uint32_t* banned;         // [ROWS][VOCAB/32]
     float* head_v;            // [ROWS][HEAD_BLOCKS] argmax partials
     uint32_t* head_i;
-    uint32_t* tickets;        // [1] LM-head ticket, zero between launches
+    uint32_t* tickets;        // [1] spare ticket, zero between launches
 };
 
 enum Prologue { PRO_PLAIN = 0, PRO_EMBED = 1, PRO_RESID = 2 };
@@ -80,8 +80,8 @@ struct AttnParams {
     uint16_t* keys;           // [lanes][capacity][128]
     uint16_t* values;
     uint32_t capacity;
-    const float2* local_rope; // [2064][64] (cos, sin)
-    const float2* global_rope;// [context][64]
+    const uint32_t* local_rope;  // [2064][64] BF16 (cos | sin << 16)
+    const uint32_t* global_rope; // [context][64]
     float* part_m;            // [ROWS][parts][16]
     float* part_l;
     float* part_o;            // [ROWS][parts][16][128]
@@ -95,6 +95,7 @@ void launch_gemv(int n, bool packed, int maxr, Prologue pro, Epilogue epi, const
                  hipStream_t s);
 void launch_attention(bool full, const AttnParams& p, int rows, hipStream_t s);
 void launch_step_begin(const DecodeBuffers& b, hipStream_t s);
+void launch_head_merge(const DecodeBuffers& b, int blocks, hipStream_t s);
 void launch_argmax(const void* x, uint32_t* out, int n, int rows, bool bf16, hipStream_t s);
 void launch_select(float* logits, int n, const int32_t* history, int hist, float penalty, int ngram, float frequency,
                    float presence, int32_t* out, hipStream_t s);

@@ -37,7 +37,7 @@ struct KvWriteParams {
     uint32_t capacity, p0;
     int tokens;
     int full;
-    const float2* global_rope;
+    const uint32_t* global_rope;  // [context][64] BF16 (cos | sin << 16)
 };
 
 void launch_gemm(bool packed, GemmEpilogue epi, const GemmParams& p, hipStream_t s);

@@ -175,35 +175,29 @@ __global__ __launch_bounds__(256) void rows_norm_kernel(const RowsNormParams p) 
 // 16 lanes per token: k RMSNorm (+1), RoPE at the absolute position for global layers,
 // then K/V to slot pos % capacity (Kernels.metal:236-257).
 __global__ __launch_bounds__(256) void kv_write_kernel(const KvWriteParams p) {
-    __shared__ float zs[16][HEAD_DIM];
     const int tl = threadIdx.x >> 4, sub = threadIdx.x & 15;
     const int t = blockIdx.x * 16 + tl;
     const bool valid = t < p.tokens;
-    const uint32_t pos = p.p0 + t;
+    const uint32_t pos = p.p0 + (valid ? t : 0);
     const float* x = p.qkv + size_t(valid ? t : 0) * QKV;
-    float v[8], ss = 0.f;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        v[j] = x[ATTN + sub * 8 + j];
-        ss += v[j] * v[j];
-    }
-    ss = group16_sum(ss);
-    const float r = 1.0f / sqrtf(ss / 128.0f + 1e-6f);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const int d = sub * 8 + j;
-        zs[tl][d] = roundbf(roundbf(v[j] * r) * roundbf(bf(p.k_norm[d]) + 1.0f));
-    }
-    __syncthreads();
+    const float4 klo = *reinterpret_cast<const float4*>(x + ATTN + sub * 4);
+    const float4 khi = *reinterpret_cast<const float4*>(x + ATTN + 64 + sub * 4);
+    const uint2 gl = *reinterpret_cast<const uint2*>(p.k_norm + sub * 4);
+    const uint2 gh = *reinterpret_cast<const uint2*>(p.k_norm + 64 + sub * 4);
+    float z[8];
+    head_norm8(klo, khi, gl, gh, z);
     if (!valid) return;
+    if (p.full) {
+        const uint4 gr = *reinterpret_cast<const uint4*>(p.global_rope + size_t(pos) * 64 + sub * 4);
+        const uint32_t c4[4] = {gr.x, gr.y, gr.z, gr.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) rope_pair(z[j], z[4 + j], c4[j], z[j], z[4 + j]);
+    }
     const size_t slot = size_t(pos % p.capacity) * HEAD_DIM;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const int d = sub * 4 + j;  // 0..63: the pair (d, d+64)
-        float a = zs[tl][d], b = zs[tl][d + 64];
-        if (p.full) rope_pair(a, b, p.global_rope[size_t(pos) * 64 + d], a, b);
-        p.keys[slot + d] = uint16_t(bits(a));
-        p.keys[slot + d + 64] = uint16_t(bits(b));
+        p.keys[slot + sub * 4 + j] = uint16_t(bits(z[j]));
+        p.keys[slot + 64 + sub * 4 + j] = uint16_t(bits(z[4 + j]));
     }
 #pragma unroll
     for (int j = 0; j < 8; ++j) {

@@ -100,8 +100,8 @@ void read_frequencies(const std::string& dir, std::vector<double>& local, std::v
 // Local table: (bits(cos), bits(sin)) of float(pos)*f (Kernels.metal:212-219).  Global
 // factors: roundbf(roundbf(cos(angle))*1.5545177444479562f) (Kernels.metal:264-267).  cos
 // and sin of the FP32 angle are evaluated in double precision and rounded to FP32.
-std::vector<float2> rope_table(const std::vector<double>& freqs, int rows, bool global) {
-    std::vector<float2> t(size_t(rows) * 64);
+std::vector<uint32_t> rope_table(const std::vector<double>& freqs, int rows, bool global) {
+    std::vector<uint32_t> t(size_t(rows) * 64);
     const float mscale = 1.5545177444479562f;
     for (int p = 0; p < rows; ++p)
         for (int d = 0; d < 64; ++d) {
@@ -112,7 +112,7 @@ std::vector<float2> rope_table(const std::vector<double>& freqs, int rows, bool 
                 c = host_bf(host_bits(c * mscale));
                 s = host_bf(host_bits(s * mscale));
             }
-            t[size_t(p) * 64 + d] = make_float2(c, s);
+            t[size_t(p) * 64 + d] = uint32_t(host_bits(c)) | (uint32_t(host_bits(s)) << 16);
         }
     return t;
 }
@@ -203,8 +203,8 @@ std::shared_ptr<Model> load_model(const std::string& dir, int context, bool pack
     m->embed = upload<uint16_t>(a, st.embedding().data, st.embedding().bytes);
     auto lt = rope_table(flocal, LOCAL_ROPE_ROWS, false);
     auto gt = rope_table(ffull, context, true);
-    m->local_rope = upload<float2>(a, lt.data(), lt.size() * sizeof(float2));
-    m->global_rope = upload<float2>(a, gt.data(), gt.size() * sizeof(float2));
+    m->local_rope = upload<uint32_t>(a, lt.data(), lt.size() * sizeof(uint32_t));
+    m->global_rope = upload<uint32_t>(a, gt.data(), gt.size() * sizeof(uint32_t));
     m->weight_bytes = int64_t(a.bytes());
     return m;
 }
@@ -306,6 +306,7 @@ void Engine::enqueue_head(const float* in, const float* resid_in) {
     g.out16 = logits;
     g.bufs = bufs;
     launch_gemv(HIDDEN, m.packed, maxr, PRO_RESID, EPI_LOGITS, g, HEAD_BLOCKS, stream);
+    launch_head_merge(bufs, HEAD_BLOCKS, stream);
 }
 
 // One decode step (Runtime.swift:376-458 for one token per row; Batch.swift:147-165).

@@ -47,8 +47,8 @@ struct Model {
     Linear head;
     const uint16_t* final_norm = nullptr;
     const uint16_t* embed = nullptr;
-    float2* local_rope = nullptr;   // [2064][64]
-    float2* global_rope = nullptr;  // [context][64]
+    uint32_t* local_rope = nullptr;   // [2064][64] BF16 cos | sin << 16
+    uint32_t* global_rope = nullptr;  // [context][64]
     int64_t weight_bytes = 0, linear_bytes = 0;
     DeviceArena arena;
 };
