@@ -237,6 +237,17 @@ int plamo_kernel_select(uint64_t logits, int32_t n, uint64_t history, int32_t hi
 int plamo_kernel_gemm(uint64_t w, uint64_t table, uint64_t x, uint64_t y, int32_t n, int32_t m, int32_t tokens,
                       int32_t out_mode, uint64_t stream);
 
+/* Prefill attention of `tokens` queries at positions p0.. (Runtime.swift:389-444 with the
+ * `matrix_rotary`/`softmax`/`attend` dispatches, Kernels.metal:276-437) as MFMA flash
+ * attention.  q16: BF16 [tokens][16][128] normalised, rotated queries; keys/values: BF16
+ * [capacity][128] with position p in slot p % capacity (keys of global layers rotated at
+ * their position, local keys unrotated); full != 0: causal over all keys, else the
+ * 2048-key window with keys rotated at key_pos - base of each 16-token chunk
+ * (local_rope: [2064][64] uint32 = BF16 cos | sin << 16).  out16: BF16 [tokens][2048]. */
+int plamo_kernel_attention_prefill(uint64_t q16, uint64_t keys, uint64_t values, int32_t capacity, int32_t p0,
+                                   int32_t tokens, int32_t full, uint64_t local_rope, uint64_t out16,
+                                   uint64_t stream);
+
 /* Library build identification (gfx arch, HIP version). */
 const char* plamo_version(void);
 

@@ -508,4 +508,29 @@ int plamo_kernel_gemm(uint64_t w, uint64_t table, uint64_t x, uint64_t y, int32_
     });
 }
 
+int plamo_kernel_attention_prefill(uint64_t q16, uint64_t keys, uint64_t values, int32_t capacity, int32_t p0,
+                                   int32_t tokens, int32_t full, uint64_t local_rope, uint64_t out16,
+                                   uint64_t stream) {
+    return guard(nullptr, 0, [&] {
+        if (tokens < 1 || p0 < 0 || capacity < 1 || !q16 || !keys || !values || !out16 || (!full && !local_rope))
+            throw plamo::Error(plamo::E_INVAL, "bad attention arguments");
+        // every visible key of every query must be resident in the ring
+        const int64_t span = full ? int64_t(p0) + tokens
+                                  : std::min<int64_t>(int64_t(p0) + tokens, int64_t(plamo::WINDOW) - 1 + tokens);
+        if (span > capacity) throw plamo::Error(plamo::E_INVAL, "attention keys exceed the cache capacity");
+        plamo::FlashParams f{};
+        f.q = reinterpret_cast<const uint16_t*>(q16);
+        f.keys = reinterpret_cast<const uint16_t*>(keys);
+        f.values = reinterpret_cast<const uint16_t*>(values);
+        f.local_rope = reinterpret_cast<const uint32_t*>(local_rope);
+        f.out = reinterpret_cast<uint16_t*>(out16);
+        f.capacity = uint32_t(capacity);
+        f.p0 = uint32_t(p0);
+        f.tokens = tokens;
+        f.full = full ? 1 : 0;
+        plamo::launch_flash_prefill(f, reinterpret_cast<hipStream_t>(stream));
+        PLAMO_HIP(hipGetLastError());
+    });
+}
+
 }  // extern "C"

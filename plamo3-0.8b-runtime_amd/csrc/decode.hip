@@ -379,26 +379,14 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     // Row geometry.  Visible keys are the absolute positions first..pos (window 2048 on the
     // local layers); key r sits at ring slot (first + r) % capacity.  Local keys rotate
-    // with coordinate coff + r and the query with qcoord, both relative to the RoPE base
-    // of the reference's 16-token chunk: base = max(0, chunk_start - 2047)
-    // (Runtime.swift:389, Kernels.metal:251,283-284).  Decode is a chunk of one token.
-    uint32_t pos, lanei, first, coff, qcoord;
-    if (st) {
-        if (st->stopped || q >= int(st->rows)) return;
-        pos = st->pos[q];
-        lanei = st->lane[q];
-        first = FULL ? 0u : (pos > uint32_t(WINDOW - 1) ? pos - uint32_t(WINDOW - 1) : 0u);
-        coff = 0;
-        qcoord = FULL ? pos : pos - first;
-    } else {
-        pos = p.p0 + q;
-        lanei = p.lane;
-        const uint32_t chunk = p.p0 + (uint32_t(q) / CHUNK) * CHUNK;
-        const uint32_t base = chunk > uint32_t(WINDOW - 1) ? chunk - uint32_t(WINDOW - 1) : 0u;
-        first = FULL ? 0u : (pos > uint32_t(WINDOW - 1) ? pos - uint32_t(WINDOW - 1) : 0u);
-        coff = first - base;
-        qcoord = FULL ? pos : pos - base;
-    }
+    // with coordinate r and the query with pos - first: a decode step is a 16-token chunk
+    // of one token, whose RoPE base max(0, pos - 2047) is `first` (Runtime.swift:389,
+    // Kernels.metal:251,283-284).
+    if (st->stopped || q >= int(st->rows)) return;
+    const uint32_t pos = st->pos[q];
+    const uint32_t lanei = st->lane[q];
+    const uint32_t first = FULL ? 0u : (pos > uint32_t(WINDOW - 1) ? pos - uint32_t(WINDOW - 1) : 0u);
+    const uint32_t qcoord = FULL ? pos : pos - first;
     const uint32_t count = pos + 1 - first;
     const uint32_t k0 = blockIdx.x * KP;
     const uint32_t cap = p.capacity;
@@ -408,7 +396,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
     const size_t pslot = size_t(q) * p.parts + blockIdx.x;
 
     if (k0 < count) {
-        const uint32_t newest = st ? count - 1 : 0xffffffffu;  // prefill keys are already cached
+        const uint32_t newest = count - 1;
         const bool has_new = newest >= k0 && newest < k0 + KP;
         const float* x = p.qkv + size_t(q) * QKV;
         // ---- every independent global load first
@@ -437,7 +425,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
             for (int i = 0; i < 4; ++i) vv[i] = *reinterpret_cast<const uint4*>(vrow + 8 * i);
         }
         if (!FULL && kr < count) {
-            const uint4* rrow = reinterpret_cast<const uint4*>(p.local_rope + size_t(coff + kr) * 64 + ksub * 16);
+            const uint4* rrow = reinterpret_cast<const uint4*>(p.local_rope + size_t(kr) * 64 + ksub * 16);
 #pragma unroll
             for (int i = 0; i < 4; ++i) rr[i] = rrow[i];
         }
@@ -484,7 +472,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
             vs[int(newest - k0) * HEAD_DIM + d] = uint16_t(bv);
         }
         __syncthreads();
-        // ---- keys: (newest from LDS) rotate with coordinate coff + r, stage FP32 in LDS
+        // ---- keys: (newest from LDS) rotate with coordinate r, stage FP32 in LDS
         {
             float a[16], b[16];
             const uint32_t aw[8] = {ka[0].x, ka[0].y, ka[0].z, ka[0].w, ka[1].x, ka[1].y, ka[1].z, ka[1].w};
@@ -615,9 +603,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
                 num = num + p.part_o[((row0 + k) * HEADS + h) * HEAD_DIM + d] *
                                 exp_det(p.part_m[(row0 + k) * HEADS + h] - M);
         }
-        const float o = roundbf(num / den_s[h]);
-        if (p.out16) p.out16[size_t(q) * ATTN + h * HEAD_DIM + d] = uint16_t(bits(o));
-        else p.out[size_t(q) * ATTN + h * HEAD_DIM + d] = o;
+        p.out[size_t(q) * ATTN + h * HEAD_DIM + d] = roundbf(num / den_s[h]);
     }
     if (tid == 0) p.tickets[q] = 0;
 }

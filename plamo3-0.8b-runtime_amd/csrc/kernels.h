@@ -69,11 +69,7 @@ struct GemvParams {
 };
 
 struct AttnParams {
-    const StepState* state;   // decode: rows from the step state; null for prefill
-    uint32_t p0;              // prefill: position of token 0 (16-token RoPE groups start here)
-    uint32_t tokens;          // prefill: rows
-    uint32_t lane;            // prefill: KV slice
-    uint16_t* out16;          // prefill: BF16 output [tokens][2048]
+    const StepState* state;   // rows, positions and KV slices of the step
     const float* qkv;         // [rows][2304] (BF16-valued FP32)
     const uint16_t* q_norm;   // [128]
     const uint16_t* k_norm;
@@ -87,7 +83,7 @@ struct AttnParams {
     float* part_o;            // [ROWS][parts][16][128]
     uint32_t parts;           // grid.x
     uint32_t* tickets;        // [rows], zero between launches
-    float* out;               // decode: FP32 [rows][2048]
+    float* out;               // FP32 [rows][2048]
 };
 
 // decode.hip

@@ -29,19 +29,34 @@ struct RowsNormParams {
     uint16_t* xn;              // next-norm output BF16 [T][1536] (optional)
 };
 
-struct KvWriteParams {
+struct QkPrepParams {
     const float* qkv;          // [T][2304]
+    const uint16_t* q_norm;
     const uint16_t* k_norm;
+    uint16_t* q16;             // out: [T][16][128] BF16, normalised and rotated queries
     uint16_t* keys;            // lane slice [capacity][128]
     uint16_t* values;
     uint32_t capacity, p0;
     int tokens;
     int full;
-    const uint32_t* global_rope;  // [context][64] BF16 (cos | sin << 16)
+    const uint32_t* local_rope;   // [2064][64] BF16 (cos | sin << 16)
+    const uint32_t* global_rope;  // [context][64]
+};
+
+struct FlashParams {
+    const uint16_t* q;         // [T][16][128] BF16, normalised and rotated
+    const uint16_t* keys;      // lane slice [capacity][128]
+    const uint16_t* values;
+    const uint32_t* local_rope;   // local layers: keys rotate with chunk-relative coordinates
+    uint16_t* out;             // [T][2048] BF16
+    uint32_t capacity, p0;
+    int tokens;
+    int full;
 };
 
 void launch_gemm(bool packed, GemmEpilogue epi, const GemmParams& p, hipStream_t s);
 void launch_rows_norm(const RowsNormParams& p, int tokens, hipStream_t s);
-void launch_kv_write(const KvWriteParams& p, hipStream_t s);
+void launch_qk_prep(const QkPrepParams& p, hipStream_t s);
+void launch_flash_prefill(const FlashParams& p, hipStream_t s);
 
 }  // namespace plamo

@@ -6,8 +6,9 @@
 //                   the projections and `swiglu` (Kernels.metal:202-210) as an epilogue.
 //   rows_norm       `norm` (Kernels.metal:46-90) for T rows: embedding gather + norm, or
 //                   post-norm + residual + next norm.
-//   kv_write        the K/V half of `qkv` (Kernels.metal:236-257): k RMSNorm, RoPE for the
-//                   global layers, cache slot pos % capacity.
+//   qk_prep         `qkv` (Kernels.metal:223-259) for a chunk: q/k RMSNorm, RoPE, K/V to
+//                   cache slot pos % capacity, normalised rotated queries as BF16.
+//   flash_prefill   prefill attention (Runtime.swift:389-444) as MFMA flash attention.
 #include <hip/hip_runtime.h>
 
 #include "common.h"
@@ -171,39 +172,302 @@ __global__ __launch_bounds__(256) void rows_norm_kernel(const RowsNormParams p) 
     }
 }
 
-// ---------------------------------------------------------------------------- kv write
-// 16 lanes per token: k RMSNorm (+1), RoPE at the absolute position for global layers,
-// then K/V to slot pos % capacity (Kernels.metal:236-257).
-__global__ __launch_bounds__(256) void kv_write_kernel(const KvWriteParams p) {
-    const int tl = threadIdx.x >> 4, sub = threadIdx.x & 15;
-    const int t = blockIdx.x * 16 + tl;
-    const bool valid = t < p.tokens;
-    const uint32_t pos = p.p0 + (valid ? t : 0);
-    const float* x = p.qkv + size_t(valid ? t : 0) * QKV;
-    const float4 klo = *reinterpret_cast<const float4*>(x + ATTN + sub * 4);
-    const float4 khi = *reinterpret_cast<const float4*>(x + ATTN + 64 + sub * 4);
-    const uint2 gl = *reinterpret_cast<const uint2*>(p.k_norm + sub * 4);
-    const uint2 gh = *reinterpret_cast<const uint2*>(p.k_norm + 64 + sub * 4);
-    float z[8];
-    head_norm8(klo, khi, gl, gh, z);
-    if (!valid) return;
-    if (p.full) {
-        const uint4 gr = *reinterpret_cast<const uint4*>(p.global_rope + size_t(pos) * 64 + sub * 4);
-        const uint32_t c4[4] = {gr.x, gr.y, gr.z, gr.w};
+// ---------------------------------------------------------------------------- qk prep
+// One workgroup per token (the `qkv` kernel, Kernels.metal:223-259, for a prefill chunk):
+// thread (h, s) = (tid/16, tid%16) normalises and rotates RoPE pairs (d, d+64) for
+// d = 4s..4s+3 of query head h -- global layers at the absolute position, local layers at
+// pos - base with base = max(0, chunk_start - 2047) of the token's 16-token chunk
+// (Runtime.swift:389, Kernels.metal:251,283-284).  Threads 0..15 do the same for the key
+// (rotated only on global layers; local keys are cached unrotated) and write it to slot
+// pos % capacity; threads 64..191 copy the value row.
+__global__ __launch_bounds__(256) void qk_prep_kernel(const QkPrepParams p) {
+    const int t = blockIdx.x, tid = threadIdx.x;
+    const int hq = tid >> 4, sq = tid & 15;
+    const uint32_t pos = p.p0 + uint32_t(t);
+    const uint32_t chunk = p.p0 + (uint32_t(t) / CHUNK) * CHUNK;
+    const uint32_t base = chunk > uint32_t(WINDOW - 1) ? chunk - uint32_t(WINDOW - 1) : 0u;
+    const uint32_t qcoord = p.full ? pos : pos - base;
+    const float* x = p.qkv + size_t(t) * QKV;
+    {
+        const float4 qlo = *reinterpret_cast<const float4*>(x + hq * HEAD_DIM + sq * 4);
+        const float4 qhi = *reinterpret_cast<const float4*>(x + hq * HEAD_DIM + 64 + sq * 4);
+        const uint2 glo = *reinterpret_cast<const uint2*>(p.q_norm + sq * 4);
+        const uint2 ghi = *reinterpret_cast<const uint2*>(p.q_norm + 64 + sq * 4);
+        const uint4 qr = *reinterpret_cast<const uint4*>((p.full ? p.global_rope : p.local_rope) + size_t(qcoord) * 64 + sq * 4);
+        float z[8];
+        head_norm8(qlo, qhi, glo, ghi, z);
+        const uint32_t c4[4] = {qr.x, qr.y, qr.z, qr.w};
+        uint16_t ra[4], rb[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) rope_pair(z[j], z[4 + j], c4[j], z[j], z[4 + j]);
+        for (int j = 0; j < 4; ++j) {
+            float a, b;
+            rope_pair(z[j], z[4 + j], c4[j], a, b);
+            ra[j] = uint16_t(bits(a));
+            rb[j] = uint16_t(bits(b));
+        }
+        uint16_t* qo = p.q16 + (size_t(t) * HEADS + hq) * HEAD_DIM;
+        *reinterpret_cast<uint2*>(qo + sq * 4) = make_uint2(ra[0] | (uint32_t(ra[1]) << 16), ra[2] | (uint32_t(ra[3]) << 16));
+        *reinterpret_cast<uint2*>(qo + 64 + sq * 4) = make_uint2(rb[0] | (uint32_t(rb[1]) << 16), rb[2] | (uint32_t(rb[3]) << 16));
     }
     const size_t slot = size_t(pos % p.capacity) * HEAD_DIM;
+    if (tid < 16) {
+        const float4 klo = *reinterpret_cast<const float4*>(x + ATTN + tid * 4);
+        const float4 khi = *reinterpret_cast<const float4*>(x + ATTN + 64 + tid * 4);
+        const uint2 gl = *reinterpret_cast<const uint2*>(p.k_norm + tid * 4);
+        const uint2 gh = *reinterpret_cast<const uint2*>(p.k_norm + 64 + tid * 4);
+        float z[8];
+        head_norm8(klo, khi, gl, gh, z);
+        if (p.full) {
+            const uint4 gr = *reinterpret_cast<const uint4*>(p.global_rope + size_t(pos) * 64 + tid * 4);
+            const uint32_t c4[4] = {gr.x, gr.y, gr.z, gr.w};
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        p.keys[slot + sub * 4 + j] = uint16_t(bits(z[j]));
-        p.keys[slot + 64 + sub * 4 + j] = uint16_t(bits(z[4 + j]));
+            for (int j = 0; j < 4; ++j) rope_pair(z[j], z[4 + j], c4[j], z[j], z[4 + j]);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            p.keys[slot + tid * 4 + j] = uint16_t(bits(z[j]));
+            p.keys[slot + 64 + tid * 4 + j] = uint16_t(bits(z[4 + j]));
+        }
     }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const int d = sub * 8 + j;
+    if (tid >= 64 && tid < 64 + HEAD_DIM) {
+        const int d = tid - 64;
         p.values[slot + d] = uint16_t(bits(x[ATTN + HEAD_DIM + d]));
     }
+}
+
+// --------------------------------------------------------------------- flash attention
+// Prefill attention (Runtime.swift:389-444: scores, scale 1/sqrt(128) before the max,
+// softmax, roundbf(sum p v)) as MFMA flash attention over the cached keys.
+//
+// A workgroup takes 8 tokens x 16 heads = 128 query columns; wave w owns tokens 2w, 2w+1:
+// lane column c = lane%32 is token 2w + c/16, head c%16 (MQA: every head reads the same
+// keys, so one K/V tile serves all 128 columns).  With keys as rows,
+//   S^T = K Q^T   and   O^T = V^T P^T,
+// a query's 64 scores of a tile sit in one lane column (two halves of 32 lanes), so the
+// online-softmax statistics need a single cross-half exchange, and the S^T accumulator is
+// already the B operand layout of the P.V product.  P is split as hi + lo BF16 so the
+// P.V product keeps ~16 significant bits of the FP32 probabilities.
+//
+// Keys of local layers are rotated while staged, with coordinate key_pos - base of the
+// workgroup's 16-token chunk (base = max(0, chunk_start - 2047)).
+constexpr int FT = 8;                 // tokens per workgroup
+constexpr int FK = 64;                // keys per tile
+constexpr int KST = HEAD_DIM + 8;     // K tile row stride (BF16), 16-byte aligned rows
+constexpr int VST = FK + 8;           // V^T tile row stride (BF16)
+constexpr float LOG2E = 1.4426950408889634f;
+
+struct KvStage {
+    uint4 ka[2], kb[2], rr[4], v[4];
+};
+
+// Global loads of one tile: thread -> key tid/4 with RoPE pairs (d, d+64), d = 16*(tid%4)
+// .. +16; and values of keys 4*(tid/16) .. +4 at dims 8*(tid%16) .. +8.
+__device__ __forceinline__ void flash_load(const FlashParams& p, uint32_t k0, uint32_t khi, uint32_t base,
+                                           KvStage& s) {
+    const int tid = threadIdx.x;
+    const int part = tid & 3;
+    const uint32_t kp = k0 + uint32_t(tid >> 2);
+    const uint4 z = make_uint4(0, 0, 0, 0);
+    s.ka[0] = s.ka[1] = s.kb[0] = s.kb[1] = z;
+    s.rr[0] = s.rr[1] = s.rr[2] = s.rr[3] = z;
+    if (kp <= khi) {
+        const uint16_t* row = p.keys + size_t(kp % p.capacity) * HEAD_DIM;
+        s.ka[0] = *reinterpret_cast<const uint4*>(row + part * 16);
+        s.ka[1] = *reinterpret_cast<const uint4*>(row + part * 16 + 8);
+        s.kb[0] = *reinterpret_cast<const uint4*>(row + 64 + part * 16);
+        s.kb[1] = *reinterpret_cast<const uint4*>(row + 64 + part * 16 + 8);
+        if (!p.full) {
+            const uint4* rr = reinterpret_cast<const uint4*>(p.local_rope + size_t(kp - base) * 64 + part * 16);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) s.rr[i] = rr[i];
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t kv = k0 + uint32_t(4 * (tid >> 4) + i);
+        s.v[i] = kv <= khi ? *reinterpret_cast<const uint4*>(p.values + size_t(kv % p.capacity) * HEAD_DIM + 8 * (tid & 15))
+                           : z;
+    }
+}
+
+__device__ __forceinline__ uint32_t u16_of(const uint4& v, int k) {
+    const uint32_t w = k < 2 ? v.x : k < 4 ? v.y : k < 6 ? v.z : v.w;
+    return (k & 1) ? (w >> 16) : (w & 0xffffu);
+}
+
+__device__ __forceinline__ void flash_store(const FlashParams& p, const KvStage& s, uint16_t* Ks, uint16_t* Vt) {
+    const int tid = threadIdx.x;
+    const int part = tid & 3, key = tid >> 2;
+    uint16_t* krow = Ks + key * KST;
+    if (p.full) {
+        *reinterpret_cast<uint4*>(krow + part * 16) = s.ka[0];
+        *reinterpret_cast<uint4*>(krow + part * 16 + 8) = s.ka[1];
+        *reinterpret_cast<uint4*>(krow + 64 + part * 16) = s.kb[0];
+        *reinterpret_cast<uint4*>(krow + 64 + part * 16 + 8) = s.kb[1];
+    } else {
+        const uint32_t aw[8] = {s.ka[0].x, s.ka[0].y, s.ka[0].z, s.ka[0].w, s.ka[1].x, s.ka[1].y, s.ka[1].z, s.ka[1].w};
+        const uint32_t bw[8] = {s.kb[0].x, s.kb[0].y, s.kb[0].z, s.kb[0].w, s.kb[1].x, s.kb[1].y, s.kb[1].z, s.kb[1].w};
+        const uint32_t rw[16] = {s.rr[0].x, s.rr[0].y, s.rr[0].z, s.rr[0].w, s.rr[1].x, s.rr[1].y, s.rr[1].z, s.rr[1].w,
+                                 s.rr[2].x, s.rr[2].y, s.rr[2].z, s.rr[2].w, s.rr[3].x, s.rr[3].y, s.rr[3].z, s.rr[3].w};
+        uint32_t ao[8], bo[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            float a0, b0, a1, b1;
+            rope_pair(lo(aw[i]), lo(bw[i]), rw[2 * i], a0, b0);
+            rope_pair(hi(aw[i]), hi(bw[i]), rw[2 * i + 1], a1, b1);
+            ao[i] = (bits(a0) & 0xffffu) | (bits(a1) << 16);
+            bo[i] = (bits(b0) & 0xffffu) | (bits(b1) << 16);
+        }
+        *reinterpret_cast<uint4*>(krow + part * 16) = make_uint4(ao[0], ao[1], ao[2], ao[3]);
+        *reinterpret_cast<uint4*>(krow + part * 16 + 8) = make_uint4(ao[4], ao[5], ao[6], ao[7]);
+        *reinterpret_cast<uint4*>(krow + 64 + part * 16) = make_uint4(bo[0], bo[1], bo[2], bo[3]);
+        *reinterpret_cast<uint4*>(krow + 64 + part * 16 + 8) = make_uint4(bo[4], bo[5], bo[6], bo[7]);
+    }
+    // V^T: 4 keys of one dim per 8-byte store
+    const int kg = 4 * (tid >> 4), d0 = 8 * (tid & 15);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const uint32_t w0 = u16_of(s.v[0], j) | (u16_of(s.v[1], j) << 16);
+        const uint32_t w1 = u16_of(s.v[2], j) | (u16_of(s.v[3], j) << 16);
+        *reinterpret_cast<uint2*>(Vt + (d0 + j) * VST + kg) = make_uint2(w0, w1);
+    }
+}
+
+__device__ __forceinline__ uint32_t bf16_rne(float x) {
+    const uint32_t u = __float_as_uint(x);
+    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+
+__global__ __launch_bounds__(256) void flash_prefill_kernel(const FlashParams p) {
+    __shared__ __align__(16) uint16_t Ks[2][FK * KST];
+    __shared__ __align__(16) uint16_t Vt[2][HEAD_DIM * VST];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int col = lane & 31, half = lane >> 5;
+    const int t0 = blockIdx.x * FT;
+    const int t1 = min(t0 + FT, p.tokens);
+    const int tq = t0 + wave * 2 + (col >> 4);
+    const int head = col & 15;
+    const bool qvalid = tq < p.tokens;
+    const int tqc = qvalid ? tq : t1 - 1;
+    const uint32_t qpos = p.p0 + uint32_t(tqc);
+    const uint32_t chunk = p.p0 + (uint32_t(t0) / CHUNK) * CHUNK;
+    const uint32_t base = p.full ? 0u : (chunk > uint32_t(WINDOW - 1) ? chunk - uint32_t(WINDOW - 1) : 0u);
+    const uint32_t plo = p.p0 + uint32_t(t0), khi = p.p0 + uint32_t(t1 - 1);
+    const uint32_t klo = p.full ? 0u : (plo > uint32_t(WINDOW - 1) ? plo - uint32_t(WINDOW - 1) : 0u);
+    const int ntiles = int((khi + 1 - klo + FK - 1) / FK);
+
+    // Q^T fragments (B operand of S^T): k-step s covers dims 16s + 8*half .. +8
+    bf16x8 qf[8];
+    {
+        const uint16_t* qrow = p.q + (size_t(tqc) * HEADS + head) * HEAD_DIM;
+#pragma unroll
+        for (int s = 0; s < 8; ++s) qf[s] = as_bf16x8(*reinterpret_cast<const uint4*>(qrow + 16 * s + 8 * half));
+    }
+    floatx16 oacc[4];
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) oacc[dt][r] = 0.f;
+    float m = NEG_INF, ls = 0.f;
+
+    KvStage st;
+    flash_load(p, klo, khi, base, st);
+    flash_store(p, st, Ks[0], Vt[0]);
+    __syncthreads();
+    for (int j = 0; j < ntiles; ++j) {
+        const int buf = j & 1;
+        const uint32_t k0 = klo + uint32_t(j * FK);
+        if (j + 1 < ntiles) flash_load(p, k0 + FK, khi, base, st);
+        // S^T = K Q^T for 64 keys (two 32-row tiles)
+        floatx16 sacc[2];
+#pragma unroll
+        for (int r = 0; r < 2; ++r)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) sacc[r][i] = 0.f;
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {
+                const bf16x8 a = as_bf16x8(*reinterpret_cast<const uint4*>(&Ks[buf][(r * 32 + col) * KST + 16 * s + 8 * half]));
+                sacc[r] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[s], sacc[r], 0, 0, 0);
+            }
+        }
+        // scale, mask, online softmax; element i of tile r is key k0 + 32r + 8(i/4) + 4*half + i%4
+        float mt = NEG_INF;
+#pragma unroll
+        for (int r = 0; r < 2; ++r)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const uint32_t kp = k0 + uint32_t(32 * r + 8 * (i >> 2) + 4 * half + (i & 3));
+                const bool vis = kp <= qpos && (p.full || kp + uint32_t(WINDOW - 1) >= qpos);
+                const float sv = vis ? sacc[r][i] * SCALE : NEG_INF;
+                sacc[r][i] = sv;
+                mt = fmaxf(mt, sv);
+            }
+        mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+        const float mn = fmaxf(m, mt);
+        const bool none = mn == NEG_INF;
+        const float alpha = none ? 1.0f : exp2f((m - mn) * LOG2E);
+        ls *= alpha;
+#pragma unroll
+        for (int r = 0; r < 2; ++r)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const float e = none ? 0.0f : exp2f((sacc[r][i] - mn) * LOG2E);
+                sacc[r][i] = e;
+                ls += e;
+            }
+        m = mn;
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) oacc[dt][i] *= alpha;
+        // O^T += V^T P^T; k-step s takes keys 16s + 4*half + {0..3} and 16s + 8 + 4*half + {0..3}
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const int r = s >> 1, i0 = (s & 1) * 8;
+            uint32_t hw[4], lw[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float e0 = sacc[r][i0 + 2 * k], e1 = sacc[r][i0 + 2 * k + 1];
+                const uint32_t h0 = bf16_rne(e0), h1 = bf16_rne(e1);
+                const uint32_t l0 = bf16_rne(e0 - __uint_as_float(h0 << 16));
+                const uint32_t l1 = bf16_rne(e1 - __uint_as_float(h1 << 16));
+                hw[k] = (h0 & 0xffffu) | (h1 << 16);
+                lw[k] = (l0 & 0xffffu) | (l1 << 16);
+            }
+            const bf16x8 ph = as_bf16x8(make_uint4(hw[0], hw[1], hw[2], hw[3]));
+            const bf16x8 pl = as_bf16x8(make_uint4(lw[0], lw[1], lw[2], lw[3]));
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt) {
+                const uint16_t* vrow = &Vt[buf][(dt * 32 + col) * VST + 16 * s + 4 * half];
+                const uint2 x0 = *reinterpret_cast<const uint2*>(vrow);
+                const uint2 x1 = *reinterpret_cast<const uint2*>(vrow + 8);
+                const bf16x8 a = as_bf16x8(make_uint4(x0.x, x0.y, x1.x, x1.y));
+                oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, ph, oacc[dt], 0, 0, 0);
+                oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pl, oacc[dt], 0, 0, 0);
+            }
+        }
+        if (j + 1 < ntiles) flash_store(p, st, Ks[buf ^ 1], Vt[buf ^ 1]);
+        __syncthreads();
+    }
+    // O = O^T / l; element i of d-tile dt is dim 32dt + 8(i/4) + 4*half + i%4
+    const float lt = ls + __shfl_xor(ls, 32, 64);
+    if (!qvalid) return;
+    uint16_t* orow = p.out + size_t(tq) * ATTN + head * HEAD_DIM;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            uint32_t w[2];
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                const uint32_t a = bits(roundbf(oacc[dt][4 * g + 2 * k] / lt));
+                const uint32_t b = bits(roundbf(oacc[dt][4 * g + 2 * k + 1] / lt));
+                w[k] = (a & 0xffffu) | (b << 16);
+            }
+            *reinterpret_cast<uint2*>(orow + 32 * dt + 8 * g + 4 * half) = make_uint2(w[0], w[1]);
+        }
 }
 
 }  // namespace
@@ -231,8 +495,14 @@ void launch_rows_norm(const RowsNormParams& p, int tokens, hipStream_t s) {
     hipLaunchKernelGGL(rows_norm_kernel, dim3(tokens), dim3(256), 0, s, p);
 }
 
-void launch_kv_write(const KvWriteParams& p, hipStream_t s) {
-    hipLaunchKernelGGL(kv_write_kernel, dim3((p.tokens + 15) / 16), dim3(256), 0, s, p);
+void launch_qk_prep(const QkPrepParams& p, hipStream_t s) {
+    if (p.tokens < 1) return;
+    hipLaunchKernelGGL(qk_prep_kernel, dim3(p.tokens), dim3(256), 0, s, p);
+}
+
+void launch_flash_prefill(const FlashParams& p, hipStream_t s) {
+    if (p.tokens < 1) return;
+    hipLaunchKernelGGL(flash_prefill_kernel, dim3((p.tokens + FT - 1) / FT), dim3(256), 0, s, p);
 }
 
 }  // namespace plamo

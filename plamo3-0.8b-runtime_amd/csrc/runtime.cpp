@@ -215,11 +215,9 @@ Engine::Engine(std::shared_ptr<Model> mdl, int ctx, int nl, hipStream_t s)
     const char* ng = std::getenv("PLAMO_NO_GRAPH");
     use_graph = !(ng && ng[0] == '1');
     const int parts_max = (context + KEYS_PER_PART - 1) / KEYS_PER_PART;
-    // Prefill chunk: up to 2048 tokens, bounded so the split-K partials stay under 1 GiB.
-    const size_t part_bytes = size_t(HEADS) * (HEAD_DIM + 2) * 4;
-    size_t c = (size_t(1) << 30) / (size_t(parts_max) * part_bytes);
-    c = std::max<size_t>(CHUNK, std::min<size_t>(2048, c / CHUNK * CHUNK));
-    chunk = int(std::min<size_t>(c, size_t((context + CHUNK - 1) / CHUNK * CHUNK)));
+    // Prefill chunk: up to 2048 tokens (a multiple of the reference's 16-token chunk, so
+    // the RoPE bases of its chunks are unchanged).
+    chunk = std::min(2048, (context + CHUNK - 1) / CHUNK * CHUNK);
     // Ring = window + one prefill chunk (the reference's rule with its 16-token chunk,
     // Runtime.swift:240): the chunk's keys and the 2047 before it are resident at once.
     local_capacity = std::min(context, WINDOW + chunk);
@@ -259,17 +257,18 @@ Engine::Engine(std::shared_ptr<Model> mdl, int ctx, int nl, hipStream_t s)
     PLAMO_HIP(hipMemsetAsync(bufs.banned, 0, size_t(ROWS) * (VOCAB / 32) * 4, stream));
     decode_parts_local = uint32_t((std::min(context, WINDOW) + KEYS_PER_PART - 1) / KEYS_PER_PART);
     decode_parts_global = uint32_t(parts_max);
-    part_rows_cap = size_t(std::max(chunk, ROWS)) * parts_max;
+    part_rows_cap = size_t(ROWS) * parts_max;
     part_m = arena.alloc_n<float>(part_rows_cap * HEADS);
     part_l = arena.alloc_n<float>(part_rows_cap * HEADS);
     part_o = arena.alloc_n<float>(part_rows_cap * HEADS * HEAD_DIM);
-    attn_tickets = arena.alloc_n<uint32_t>(size_t(std::max(chunk, ROWS)));
-    PLAMO_HIP(hipMemsetAsync(attn_tickets, 0, size_t(std::max(chunk, ROWS)) * 4, stream));
+    attn_tickets = arena.alloc_n<uint32_t>(size_t(ROWS));
+    PLAMO_HIP(hipMemsetAsync(attn_tickets, 0, size_t(ROWS) * 4, stream));
     p_x = arena.alloc_n<float>(size_t(chunk) * HIDDEN);
     p_qkv = arena.alloc_n<float>(size_t(chunk) * QKV);
     p_proj = arena.alloc_n<float>(size_t(chunk) * HIDDEN);
     p_xn = arena.alloc_n<uint16_t>(size_t(chunk) * HIDDEN);
     p_att = arena.alloc_n<uint16_t>(size_t(chunk) * ATTN);
+    p_q16 = arena.alloc_n<uint16_t>(size_t(chunk) * ATTN);
     p_act = arena.alloc_n<uint16_t>(size_t(chunk) * INTER);
     p_tokens = arena.alloc_n<int32_t>(size_t(chunk));
     PLAMO_HIP(hipEventCreate(&ev0));
@@ -410,7 +409,7 @@ void Engine::run_step() {
 }
 
 // A prefill chunk of n tokens at p0 for one lane: every layer as MFMA GEMMs, K/V written
-// for the chunk, then attention of each token over its visible keys.
+// for the chunk, then MFMA flash attention of the chunk's queries over their visible keys.
 void Engine::enqueue_prefill_chunk(int n, int p0, int lane, bool last_chunk, bool output) {
     const Model& m = *model;
     const bool pk = m.packed;
@@ -427,38 +426,31 @@ void Engine::enqueue_prefill_chunk(int n, int p0, int lane, bool last_chunk, boo
         GemmParams q{};
         q.w = L.qkv.w; q.table = L.qkv.table; q.x = p_xn; q.y = p_qkv; q.m = QKV; q.k = HIDDEN; q.tokens = n;
         launch_gemm(pk, GEMM_F32, q, stream);
-        KvWriteParams kw{};
-        kw.qkv = p_qkv;
-        kw.k_norm = L.k_norm;
-        kw.keys = keys[l] + size_t(lane) * capacity[l] * HEAD_DIM;
-        kw.values = values[l] + size_t(lane) * capacity[l] * HEAD_DIM;
-        kw.capacity = uint32_t(capacity[l]);
-        kw.p0 = uint32_t(p0);
-        kw.tokens = n;
-        kw.full = full;
-        kw.global_rope = m.global_rope;
-        launch_kv_write(kw, stream);
-        AttnParams a{};
-        a.p0 = uint32_t(p0);
-        a.tokens = uint32_t(n);
-        a.lane = uint32_t(lane);
-        a.out16 = p_att;
-        a.qkv = p_qkv;
-        a.q_norm = L.q_norm;
-        a.k_norm = L.k_norm;
-        a.keys = keys[l];
-        a.values = values[l];
-        a.capacity = uint32_t(capacity[l]);
-        a.local_rope = m.local_rope;
-        a.global_rope = m.global_rope;
-        a.part_m = part_m;
-        a.part_l = part_l;
-        a.part_o = part_o;
-        const int last = p0 + n;  // keys visible to the last token
-        const int visible = full ? last : std::min(last, WINDOW);
-        a.parts = uint32_t((visible + KEYS_PER_PART - 1) / KEYS_PER_PART);
-        a.tickets = attn_tickets;
-        launch_attention(full, a, n, stream);
+        QkPrepParams qp{};
+        qp.qkv = p_qkv;
+        qp.q_norm = L.q_norm;
+        qp.k_norm = L.k_norm;
+        qp.q16 = p_q16;
+        qp.keys = keys[l] + size_t(lane) * capacity[l] * HEAD_DIM;
+        qp.values = values[l] + size_t(lane) * capacity[l] * HEAD_DIM;
+        qp.capacity = uint32_t(capacity[l]);
+        qp.p0 = uint32_t(p0);
+        qp.tokens = n;
+        qp.full = full;
+        qp.local_rope = m.local_rope;
+        qp.global_rope = m.global_rope;
+        launch_qk_prep(qp, stream);
+        FlashParams fa{};
+        fa.q = p_q16;
+        fa.keys = qp.keys;
+        fa.values = qp.values;
+        fa.local_rope = m.local_rope;
+        fa.out = p_att;
+        fa.capacity = qp.capacity;
+        fa.p0 = uint32_t(p0);
+        fa.tokens = n;
+        fa.full = full;
+        launch_flash_prefill(fa, stream);
         GemmParams o{};
         o.w = L.o.w; o.table = L.o.table; o.x = p_att; o.y = p_proj; o.m = HIDDEN; o.k = ATTN; o.tokens = n;
         launch_gemm(pk, GEMM_F32, o, stream);

@@ -76,7 +76,7 @@ class Engine {
     uint32_t decode_parts_local, decode_parts_global;
     // prefill scratch (chunk rows)
     float *p_x, *p_qkv, *p_proj;
-    uint16_t *p_xn, *p_att, *p_act;
+    uint16_t *p_xn, *p_att, *p_act, *p_q16;
     int32_t* p_tokens;
     size_t part_rows_cap;    // rows x parts the partial buffers hold
     // graph

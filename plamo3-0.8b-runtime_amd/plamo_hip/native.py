@@ -96,6 +96,8 @@ _SIGNATURES = {
                                            ctypes.c_float, ctypes.c_int32, ctypes.c_float, ctypes.c_float,
                                            ctypes.c_uint64, ctypes.c_uint64]),
     "plamo_kernel_gemm": (ctypes.c_int, [ctypes.c_uint64] * 4 + [ctypes.c_int32] * 4 + [ctypes.c_uint64]),
+    "plamo_kernel_attention_prefill": (ctypes.c_int, [ctypes.c_uint64] * 3 + [ctypes.c_int32] * 4 +
+                                       [ctypes.c_uint64] * 3),
     "plamo_version": (ctypes.c_char_p, []),
 }
 
