@@ -233,7 +233,8 @@ int plamo_kernel_select(uint64_t logits, int32_t n, uint64_t history, int32_t hi
 /* MFMA BF16 GEMM of the prefill path: Y[t][m] = sum_k X[t][k] W[m][k] with X BF16
  * [tokens][n] and W plain BF16 or .p12 ([m][n]).  out_mode 0: Y FP32 BF16-rounded
  * (`matrix` full == 0); 1: Y BF16 bits (full == 2); 2: Y raw FP32 (full == 1,
- * Kernels.metal:196-197). */
+ * Kernels.metal:196-197); 3: the gate_up projection (m = 12288, n = 1536) followed by
+ * `swiglu` (Kernels.metal:202-210), Y BF16 bits [tokens][6144]. */
 int plamo_kernel_gemm(uint64_t w, uint64_t table, uint64_t x, uint64_t y, int32_t n, int32_t m, int32_t tokens,
                       int32_t out_mode, uint64_t stream);
 

@@ -491,6 +491,7 @@ int plamo_kernel_gemm(uint64_t w, uint64_t table, uint64_t x, uint64_t y, int32_
                       int32_t out_bf16, uint64_t stream) {
     return guard(nullptr, 0, [&] {
         if (n % 128 != 0 || m < 1 || tokens < 1) throw plamo::Error(plamo::E_INVAL, "bad GEMM shape");
+        if (!w || !x || !y) throw plamo::Error(plamo::E_INVAL, "null GEMM operand");
         plamo::GemmParams g{};
         g.w = reinterpret_cast<const uint16_t*>(w);
         g.table = reinterpret_cast<const uint32_t*>(table);
@@ -500,8 +501,13 @@ int plamo_kernel_gemm(uint64_t w, uint64_t table, uint64_t x, uint64_t y, int32_
         g.m = m;
         g.k = n;
         g.tokens = tokens;
-        if (out_bf16 < 0 || out_bf16 > 2) throw plamo::Error(plamo::E_INVAL, "bad GEMM output mode");
-        const plamo::GemmEpilogue epi = out_bf16 == 1 ? plamo::GEMM_BF16 : out_bf16 == 2 ? plamo::GEMM_RAW : plamo::GEMM_F32;
+        if (out_bf16 < 0 || out_bf16 > 3) throw plamo::Error(plamo::E_INVAL, "bad GEMM output mode");
+        if (out_bf16 == 3 && (m != 2 * plamo::INTER || n != plamo::HIDDEN))
+            throw plamo::Error(plamo::E_INVAL, "SwiGLU GEMM needs the 12288 x 1536 gate_up weight");
+        const plamo::GemmEpilogue epi = out_bf16 == 1   ? plamo::GEMM_BF16
+                                        : out_bf16 == 2 ? plamo::GEMM_RAW
+                                        : out_bf16 == 3 ? plamo::GEMM_SWIGLU
+                                                        : plamo::GEMM_F32;
         plamo::launch_gemm(table != 0, epi, g,
                            reinterpret_cast<hipStream_t>(stream));
         PLAMO_HIP(hipGetLastError());

@@ -1,8 +1,8 @@
 // Prefill kernels for gfx950: MFMA BF16 GEMM (plain or .p12 weights) with fused epilogues,
 // row RMSNorm / residual kernels and the K/V cache writer.
 //
-//   gemm_kernel     Y[t][m] = sum_k X[t][k] W[m][k]; 128x128 tiles, BK 64, LDS-staged,
-//                   v_mfma_f32_32x32x16_bf16.  Replaces `matrix` (Kernels.metal:149-200) for
+//   gemm_kernel     Y[t][m] = sum_k X[t][k] W[m][k]; 128x128 tiles, BK 64, register-prefetched
+//                   double-buffered LDS, v_mfma_f32_32x32x16_bf16, XCD-grouped tiles.  Replaces `matrix` (Kernels.metal:149-200) for
 //                   the projections and `swiglu` (Kernels.metal:202-210) as an epilogue.
 //   rows_norm       `norm` (Kernels.metal:46-90) for T rows: embedding gather + norm, or
 //                   post-norm + residual + next norm.
@@ -32,96 +32,141 @@ __device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) {
     return r;
 }
 
+// Weight row feeding LDS row r of a B tile.  SwiGLU tiles interleave 32 gate and 32 up rows
+// (g0-31, u0-31, g32-63, u32-63) so each wave's two column tiles pair gate with up.
+template <int EPI>
+__device__ __forceinline__ int b_row(int n0, int r) {
+    if constexpr (EPI == GEMM_SWIGLU) return ((r >> 5) & 1 ? INTER : 0) + n0 + (r >> 6) * 32 + (r & 31);
+    else return n0 + r;
+}
+
+// One K step of operands in registers: thread tid loads 16 bytes of rows tid/8 + 32*i.
+struct GemmStage {
+    uint4 a[4], b[4];
+};
+
 template <bool PACKED, int EPI>
-__global__ __launch_bounds__(256) void gemm_kernel(const GemmParams p) {
-    __shared__ __align__(16) uint16_t As[BM * LDS_STRIDE];
-    __shared__ __align__(16) uint16_t Bs[BN * LDS_STRIDE];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int t0 = blockIdx.y * BM;
-    const int n0 = blockIdx.x * (EPI == GEMM_SWIGLU ? BN / 2 : BN);
+__device__ __forceinline__ void gemm_load(const GemmParams& p, int t0, int n0, int k0, GemmStage& g) {
+    const int tid = threadIdx.x, c8 = tid & 7;
     const int K = p.k;
-
-    floatx16 acc[4];
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
+    for (int i = 0; i < 4; ++i) {
+        const int r = (tid >> 3) + 32 * i;
+        const int t = t0 + r;
+        g.a[i] = t < p.tokens ? *reinterpret_cast<const uint4*>(p.x + size_t(t) * K + k0 + c8 * 8) : make_uint4(0, 0, 0, 0);
+    }
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc[c][r] = 0.f;
-
-    for (int k0 = 0; k0 < K; k0 += BK) {
-        // A tile: 128 token rows x 64 (X is BF16 [tokens][K])
-#pragma unroll
-        for (int e = tid; e < BM * BK / 8; e += 256) {
-            const int r = e >> 3, c8 = e & 7;
-            const int t = t0 + r;
-            uint4 v = make_uint4(0, 0, 0, 0);
-            if (t < p.tokens) v = *reinterpret_cast<const uint4*>(p.x + size_t(t) * K + k0 + c8 * 8);
-            *reinterpret_cast<uint4*>(&As[r * LDS_STRIDE + c8 * 8]) = v;
-        }
-        // B tile: 128 weight rows x 64
-#pragma unroll
-        for (int e = tid; e < BN * BK / 8; e += 256) {
-            const int r = e >> 3, c8 = e & 7;
-            int row;
-            if constexpr (EPI == GEMM_SWIGLU) row = r < BN / 2 ? n0 + r : INTER + n0 + (r - BN / 2);
-            else row = n0 + r;
-            uint4 v = make_uint4(0, 0, 0, 0);
-            if (row < p.m) {
-                const int kk = k0 + c8 * 8;
-                if constexpr (!PACKED) {
-                    v = *reinterpret_cast<const uint4*>(p.w + size_t(row) * K + kk);
-                } else {
-                    const uint32_t entry = p.table[size_t(row) * (K / 128) + kk / 128];
-                    const uint8_t* blk = reinterpret_cast<const uint8_t*>(p.w) + (entry & ~63u);
-                    const uint32_t tag = entry & 63u;
-                    const int sub = (kk % 128) / 8;
-                    if (tag == 0) v = *reinterpret_cast<const uint4*>(blk + sub * 16);
-                    else
-                        v = p12_decode8(*reinterpret_cast<const uint2*>(blk + sub * 8),
-                                        *reinterpret_cast<const uint32_t*>(blk + 128 + sub * 4), tag);
-                }
+    for (int i = 0; i < 4; ++i) {
+        const int r = (tid >> 3) + 32 * i;
+        const int row = b_row<EPI>(n0, r);
+        uint4 v = make_uint4(0, 0, 0, 0);
+        if (row < p.m) {
+            const int kk = k0 + c8 * 8;
+            if constexpr (!PACKED) {
+                v = *reinterpret_cast<const uint4*>(p.w + size_t(row) * K + kk);
+            } else {
+                const uint32_t entry = p.table[size_t(row) * (K / 128) + kk / 128];
+                const uint8_t* blk = reinterpret_cast<const uint8_t*>(p.w) + (entry & ~63u);
+                const uint32_t tag = entry & 63u;
+                const int sub = (kk % 128) / 8;
+                if (tag == 0) v = *reinterpret_cast<const uint4*>(blk + sub * 16);
+                else
+                    v = p12_decode8(*reinterpret_cast<const uint2*>(blk + sub * 8),
+                                    *reinterpret_cast<const uint32_t*>(blk + 128 + sub * 4), tag);
             }
-            *reinterpret_cast<uint4*>(&Bs[r * LDS_STRIDE + c8 * 8]) = v;
         }
-        __syncthreads();
+        g.b[i] = v;
+    }
+}
+
+__device__ __forceinline__ void gemm_store(const GemmStage& g, uint16_t* As, uint16_t* Bs) {
+    const int tid = threadIdx.x, c8 = tid & 7;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int r = (tid >> 3) + 32 * i;
+        *reinterpret_cast<uint4*>(&As[r * LDS_STRIDE + c8 * 8]) = g.a[i];
+        *reinterpret_cast<uint4*>(&Bs[r * LDS_STRIDE + c8 * 8]) = g.b[i];
+    }
+}
+
+// Y[t][m] = sum_k X[t][k] W[m][k] on 128 x 128 tiles: four waves in a 2 x 2 grid, each
+// 64 x 64 (2 x 2 MFMA 32x32x16 tiles).  The next K step is loaded into registers while
+// the current one is multiplied from LDS (double-buffered, one barrier per step).  Tiles
+// are dealt to workgroups so that each XCD (workgroup id % 8) owns a contiguous run of
+// tiles sharing weight columns, which keeps the weight tiles in that XCD's L2.
+template <bool PACKED, int EPI>
+__global__ __launch_bounds__(256) void gemm_kernel(const GemmParams p, int col_tiles, int row_tiles) {
+    __shared__ __align__(16) uint16_t As[2][BM * LDS_STRIDE];
+    __shared__ __align__(16) uint16_t Bs[2][BN * LDS_STRIDE];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int tiles = col_tiles * row_tiles;
+    const int per = (tiles + 7) / 8;
+    const int tile = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
+    if (tile >= tiles) return;
+    const int ct = tile / row_tiles, rt = tile % row_tiles;
+    const int t0 = rt * BM;
+    const int n0 = ct * (EPI == GEMM_SWIGLU ? BN / 2 : BN);
+    const int nk = p.k / BK;
+
+    floatx16 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+    GemmStage g;
+    gemm_load<PACKED, EPI>(p, t0, n0, 0, g);
+    gemm_store(g, As[0], Bs[0]);
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+        const int buf = kt & 1;
+        if (kt + 1 < nk) gemm_load<PACKED, EPI>(p, t0, n0, (kt + 1) * BK, g);
 #pragma unroll
         for (int ks = 0; ks < BK / 16; ++ks) {
             const int kc = ks * 16 + (lane >> 5) * 8;
-            const bf16x8 a = as_bf16x8(*reinterpret_cast<const uint4*>(&As[(wave * 32 + (lane & 31)) * LDS_STRIDE + kc]));
+            bf16x8 a[2], b[2];
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const bf16x8 b = as_bf16x8(*reinterpret_cast<const uint4*>(&Bs[(c * 32 + (lane & 31)) * LDS_STRIDE + kc]));
-                acc[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc[c], 0, 0, 0);
-            }
+            for (int i = 0; i < 2; ++i)
+                a[i] = as_bf16x8(*reinterpret_cast<const uint4*>(&As[buf][(wm * 64 + i * 32 + (lane & 31)) * LDS_STRIDE + kc]));
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                b[j] = as_bf16x8(*reinterpret_cast<const uint4*>(&Bs[buf][(wn * 64 + j * 32 + (lane & 31)) * LDS_STRIDE + kc]));
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
         }
+        if (kt + 1 < nk) gemm_store(g, As[buf ^ 1], Bs[buf ^ 1]);
         __syncthreads();
     }
 
-    // C layout of the 32x32 tile: column j = lane%32, row i = (r/4)*8 + (lane/32)*4 + r%4
-    const int j = lane & 31;
+    // C layout of a 32x32 tile: column j = lane%32, row i = (r/4)*8 + (lane/32)*4 + r%4
+    const int jc = lane & 31;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        const int i = (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-        const int t = t0 + wave * 32 + i;
-        if (t >= p.tokens) continue;
-        if constexpr (EPI == GEMM_SWIGLU) {
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
-            for (int c = 0; c < 2; ++c) {
-                const int m = n0 + c * 32 + j;
-                const float g = roundbf(acc[c][r]);
-                const float u = roundbf(acc[c + 2][r]);
-                p.y16[size_t(t) * INTER + m] = uint16_t(bits(roundbf(g / (1.0f + exp_det(-g))) * u));
-            }
-        } else {
+        for (int r = 0; r < 16; ++r) {
+            const int t = t0 + wm * 64 + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+            if (t >= p.tokens) continue;
+            if constexpr (EPI == GEMM_SWIGLU) {
+                const int m = n0 + wn * 32 + jc;
+                const float gt = roundbf(acc[i][0][r]);
+                const float up = roundbf(acc[i][1][r]);
+                p.y16[size_t(t) * INTER + m] = uint16_t(bits(roundbf(gt / (1.0f + exp_det(-gt))) * up));
+            } else {
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const int m = n0 + c * 32 + j;
-                if (m >= p.m) continue;
-                if constexpr (EPI == GEMM_F32) p.y[size_t(t) * p.m + m] = roundbf(acc[c][r]);
-                else if constexpr (EPI == GEMM_RAW) p.y[size_t(t) * p.m + m] = acc[c][r];
-                else p.y16[size_t(t) * p.m + m] = uint16_t(bits(acc[c][r]));
+                for (int j = 0; j < 2; ++j) {
+                    const int m = n0 + wn * 64 + j * 32 + jc;
+                    if (m >= p.m) continue;
+                    if constexpr (EPI == GEMM_F32) p.y[size_t(t) * p.m + m] = roundbf(acc[i][j][r]);
+                    else if constexpr (EPI == GEMM_RAW) p.y[size_t(t) * p.m + m] = acc[i][j][r];
+                    else p.y16[size_t(t) * p.m + m] = uint16_t(bits(acc[i][j][r]));
+                }
             }
         }
-    }
 }
 
 // ------------------------------------------------------------------------------ norms
@@ -254,7 +299,7 @@ constexpr int FT = 8;                 // tokens per workgroup
 constexpr int FK = 64;                // keys per tile
 constexpr int KST = HEAD_DIM + 8;     // K tile row stride (BF16), 16-byte aligned rows
 constexpr int VST = FK + 8;           // V^T tile row stride (BF16)
-constexpr float LOG2E = 1.4426950408889634f;
+constexpr float SCALE_LOG2E = 0.08838834764831845f * 1.4426950408889634f;
 
 struct KvStage {
     uint4 ka[2], kb[2], rr[4], v[4];
@@ -333,9 +378,17 @@ __device__ __forceinline__ void flash_store(const FlashParams& p, const KvStage&
     }
 }
 
-__device__ __forceinline__ uint32_t bf16_rne(float x) {
-    const uint32_t u = __float_as_uint(x);
-    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+// Two FP32 values as BF16 pairs hi + lo (RNE, v_cvt_pk_bf16_f32): hi + lo carries ~16
+// significant bits of each value.
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float floatx2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void split_bf16(float a, float b, uint32_t& hw, uint32_t& lw) {
+    const floatx2 v = {a, b};
+    const bf16x2 h = __builtin_convertvector(v, bf16x2);
+    __builtin_memcpy(&hw, &h, 4);
+    const floatx2 back = {__uint_as_float(hw << 16), __uint_as_float(hw & 0xffff0000u)};
+    const bf16x2 l = __builtin_convertvector(v - back, bf16x2);
+    __builtin_memcpy(&lw, &l, 4);
 }
 
 __global__ __launch_bounds__(256) void flash_prefill_kernel(const FlashParams p) {
@@ -392,28 +445,42 @@ __global__ __launch_bounds__(256) void flash_prefill_kernel(const FlashParams p)
                 sacc[r] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[s], sacc[r], 0, 0, 0);
             }
         }
-        // scale, mask, online softmax; element i of tile r is key k0 + 32r + 8(i/4) + 4*half + i%4
+        // Online softmax in the base-2 domain: x = score * scale * log2(e), p = 2^(x - max).
+        // Element i of tile r is key k0 + 32r + 8(i/4) + 4*half + i%4.  Only tiles that cross
+        // a query's causal edge or window start need the mask.
+        const bool edge = !(k0 + uint32_t(FK - 1) <= plo && (p.full || k0 + uint32_t(WINDOW - 1) >= khi));
         float mt = NEG_INF;
+        if (edge) {
 #pragma unroll
-        for (int r = 0; r < 2; ++r)
+            for (int r = 0; r < 2; ++r)
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const uint32_t kp = k0 + uint32_t(32 * r + 8 * (i >> 2) + 4 * half + (i & 3));
-                const bool vis = kp <= qpos && (p.full || kp + uint32_t(WINDOW - 1) >= qpos);
-                const float sv = vis ? sacc[r][i] * SCALE : NEG_INF;
-                sacc[r][i] = sv;
-                mt = fmaxf(mt, sv);
-            }
+                for (int i = 0; i < 16; ++i) {
+                    const uint32_t kp = k0 + uint32_t(32 * r + 8 * (i >> 2) + 4 * half + (i & 3));
+                    const bool vis = kp <= qpos && (p.full || kp + uint32_t(WINDOW - 1) >= qpos);
+                    const float x = vis ? sacc[r][i] * SCALE_LOG2E : NEG_INF;
+                    sacc[r][i] = x;
+                    mt = fmaxf(mt, x);
+                }
+        } else {
+#pragma unroll
+            for (int r = 0; r < 2; ++r)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const float x = sacc[r][i] * SCALE_LOG2E;
+                    sacc[r][i] = x;
+                    mt = fmaxf(mt, x);
+                }
+        }
         mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
         const float mn = fmaxf(m, mt);
-        const bool none = mn == NEG_INF;
-        const float alpha = none ? 1.0f : exp2f((m - mn) * LOG2E);
+        const float ms = mn == NEG_INF ? 0.0f : mn;  // nothing visible yet: every p is 0
+        const float alpha = __builtin_amdgcn_exp2f(m - ms);
         ls *= alpha;
 #pragma unroll
         for (int r = 0; r < 2; ++r)
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-                const float e = none ? 0.0f : exp2f((sacc[r][i] - mn) * LOG2E);
+                const float e = __builtin_amdgcn_exp2f(sacc[r][i] - ms);
                 sacc[r][i] = e;
                 ls += e;
             }
@@ -428,14 +495,7 @@ __global__ __launch_bounds__(256) void flash_prefill_kernel(const FlashParams p)
             const int r = s >> 1, i0 = (s & 1) * 8;
             uint32_t hw[4], lw[4];
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const float e0 = sacc[r][i0 + 2 * k], e1 = sacc[r][i0 + 2 * k + 1];
-                const uint32_t h0 = bf16_rne(e0), h1 = bf16_rne(e1);
-                const uint32_t l0 = bf16_rne(e0 - __uint_as_float(h0 << 16));
-                const uint32_t l1 = bf16_rne(e1 - __uint_as_float(h1 << 16));
-                hw[k] = (h0 & 0xffffu) | (h1 << 16);
-                lw[k] = (l0 & 0xffffu) | (l1 << 16);
-            }
+            for (int k = 0; k < 4; ++k) split_bf16(sacc[r][i0 + 2 * k], sacc[r][i0 + 2 * k + 1], hw[k], lw[k]);
             const bf16x8 ph = as_bf16x8(make_uint4(hw[0], hw[1], hw[2], hw[3]));
             const bf16x8 pl = as_bf16x8(make_uint4(lw[0], lw[1], lw[2], lw[3]));
 #pragma unroll
@@ -473,10 +533,13 @@ __global__ __launch_bounds__(256) void flash_prefill_kernel(const FlashParams p)
 }  // namespace
 
 void launch_gemm(bool packed, GemmEpilogue epi, const GemmParams& p, hipStream_t s) {
+    if (p.k % BK != 0 || p.tokens < 1 || p.m < 1 || (epi == GEMM_SWIGLU && p.m != 2 * INTER))
+        throw Error(E_INVAL, "unsupported GEMM shape");
     const int cols = epi == GEMM_SWIGLU ? INTER / (BN / 2) : (p.m + BN - 1) / BN;
-    const dim3 grid(cols, (p.tokens + BM - 1) / BM), block(256);
-    if (p.k % BK != 0 || (epi == GEMM_SWIGLU && p.m != 2 * INTER)) throw Error(E_INVAL, "unsupported GEMM shape");
-#define PLAMO_GEMM(PK, EP) hipLaunchKernelGGL((gemm_kernel<PK, EP>), grid, block, 0, s, p)
+    const int rows = (p.tokens + BM - 1) / BM;
+    const int per = (cols * rows + 7) / 8;
+    const dim3 grid(8 * per), block(256);
+#define PLAMO_GEMM(PK, EP) hipLaunchKernelGGL((gemm_kernel<PK, EP>), grid, block, 0, s, p, cols, rows)
     if (packed) {
         if (epi == GEMM_F32) PLAMO_GEMM(true, GEMM_F32);
         else if (epi == GEMM_BF16) PLAMO_GEMM(true, GEMM_BF16);

@@ -160,7 +160,8 @@ def test_linear_packed_equals_plain_and_fp32(lib, name):
                                   (plain[2:3].view(np.uint32) if mode == 0 else plain[2:3]))
 
 
-@pytest.mark.parametrize("m,n,tokens", [(2304, 1536, 130), (1536, 2048, 64), (1536, 6144, 257), (64, 1536, 17)])
+@pytest.mark.parametrize("m,n,tokens", [(2304, 1536, 130), (1536, 2048, 64), (1536, 6144, 257), (64, 1536, 17),
+                                          (2304, 1536, 2048), (200, 512, 300)])
 def test_gemm_matches_fp32_and_packed(lib, m, n, tokens):
     rng = np.random.default_rng(m + tokens)
     w = bits_np(rng.standard_normal((m, n)).astype(np.float32) * 0.02)
@@ -181,3 +182,32 @@ def test_gemm_matches_fp32_and_packed(lib, m, n, tokens):
     ref = (torch.from_numpy(bf_np(x)).double() @ torch.from_numpy(bf_np(w)).double().T).numpy()
     tol = np.abs(ref) * 2 ** -7 + 1e-5
     assert np.all(np.abs(outs[0] - ref) <= tol)
+
+
+def test_gemm_swiglu_matches_fp32_and_packed(lib):
+    """out_mode 3: the gate_up GEMM with the `swiglu` epilogue (Kernels.metal:202-210):
+    y = roundbf(roundbf(g / (1 + exp(-g))) * u) with g, u the BF16-rounded projections."""
+    m, n, tokens = 12288, 1536, 70
+    rng = np.random.default_rng(7)
+    w = bits_np(rng.standard_normal((m, n)).astype(np.float32) * 0.02)
+    x = bits_np(rng.standard_normal((tokens, n)).astype(np.float32))
+    data, offsets, minima = p12.pack(w)
+    table = p12.tag(offsets, minima)
+    outs = []
+    for packed in (False, True):
+        wd = dev(data) if packed else dev(w.view(np.int16))
+        td = dev(table.view(np.int32)) if packed else None
+        xd = dev(x.view(np.int16))
+        y = torch.empty(tokens * 6144, dtype=torch.int16, device="cuda")
+        assert lib.plamo_kernel_gemm(ptr(wd), ptr(td) if td is not None else 0, ptr(xd), ptr(y), n, m, tokens, 3,
+                                     0) == 0
+        torch.cuda.synchronize()
+        outs.append(y.cpu().numpy().view(np.uint16).reshape(tokens, 6144))
+    assert np.array_equal(outs[0], outs[1])
+    ref = (torch.from_numpy(bf_np(x)).double() @ torch.from_numpy(bf_np(w)).double().T).numpy()
+    g = roundbf_np(ref[:, :6144].astype(np.float32))
+    u = roundbf_np(ref[:, 6144:].astype(np.float32))
+    want = roundbf_np(roundbf_np(g / (np.float32(1) + np.exp(-g))) * u)
+    got = bf_np(outs[0])
+    assert np.all(np.abs(got - want) <= np.abs(want) * 2 ** -6 + 1e-6)
+    assert np.mean(got != want) < 0.02
