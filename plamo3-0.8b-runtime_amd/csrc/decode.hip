@@ -30,10 +30,27 @@ template <int N, int MAXR, int PRO>
 __device__ __forceinline__ void stage_rows(const GemvParams& p, int rows, uint16_t* xs, float* red) {
     const int tid = threadIdx.x;
     if constexpr (PRO == PRO_PLAIN) {
-        for (int q = 0; q < MAXR; ++q) {
-            if (q >= rows) break;
-            for (int i = tid; i < N; i += 256) xs[q * N + i] = uint16_t(bits(p.in[q * N + i]));
-        }
+        // every load in flight at once: ceil(N/1024) float4 per thread and row
+        constexpr int V = (N + 1023) / 1024;
+        float4 v[MAXR][V];
+#pragma unroll
+        for (int q = 0; q < MAXR; ++q)
+#pragma unroll
+            for (int k = 0; k < V; ++k) {
+                const int e = (tid + 256 * k) * 4;
+                v[q][k] = (q < rows && e < N) ? *reinterpret_cast<const float4*>(p.in + q * N + e)
+                                              : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+#pragma unroll
+        for (int q = 0; q < MAXR; ++q)
+#pragma unroll
+            for (int k = 0; k < V; ++k) {
+                const int e = (tid + 256 * k) * 4;
+                if (e >= N) continue;
+                const uint32_t lo2 = (bits(v[q][k].x) & 0xffffu) | (bits(v[q][k].y) << 16);
+                const uint32_t hi2 = (bits(v[q][k].z) & 0xffffu) | (bits(v[q][k].w) << 16);
+                *reinterpret_cast<uint2*>(&xs[q * N + e]) = make_uint2(lo2, hi2);
+            }
     } else {
         static_assert(N == HIDDEN, "norm prologue is 1536 wide");
         constexpr int E = HIDDEN / 256;  // 6 elements per thread
@@ -175,15 +192,13 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvParams p) {
 
     const StepState* st = p.state;
     if (st && st->stopped) return;
-    const int rows = st ? int(st->rows) : p.rows;
+    int rows = p.rows;  // (a select of two addresses would put the argument in scratch)
+    if (st) rows = int(st->rows);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     Controls ctl{false, 0, 1.0f, 0.0f, 0.0f};
     if constexpr (EPI == EPI_LOGITS) {
         if (st && st->sampling) ctl = Controls{true, st->ngram, st->penalty, st->frequency, st->presence};
     }
-
-    stage_rows<N, MAXR, PRO>(p, rows, xs, red);
-    __syncthreads();
 
     const int groups = (EPI == EPI_SWIGLU) ? p.m / 4 : p.m / U;
     float best_v[MAXR];
@@ -191,7 +206,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvParams p) {
 #pragma unroll
     for (int q = 0; q < MAXR; ++q) { best_v[q] = NEG_INF; best_i[q] = 0xffffffffu; }
 
-    auto rows_of = [&](int g, int* wrow) {
+    auto rows_of = [&](int g, int (&wrow)[U]) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             if constexpr (EPI == EPI_SWIGLU) wrow[u] = (u < 2) ? 2 * g + u : INTER + 2 * g + (u - 2);
@@ -199,7 +214,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvParams p) {
         }
     };
     // Software pipelined over the wave's row groups: the next group's weights are in flight
-    // while the current group is reduced and written.
+    // while the current group is reduced and written.  The first group's weights do not
+    // depend on the previous kernel, so they are requested before the activation prologue.
     const int stride = gridDim.x * 4;
     int g = blockIdx.x * 4 + wave;
     uint4 w[U][IT];
@@ -211,6 +227,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvParams p) {
 #pragma unroll
             for (int it = 0; it < IT; ++it) w[u][it] = load_w<N, PACKED>(p, wrow[u], it, lane);
     }
+    stage_rows<N, MAXR, PRO>(p, rows, xs, red);
+    __syncthreads();
     for (; g < groups; g += stride) {
         int wrow[U];
         rows_of(g, wrow);
@@ -394,8 +412,11 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
     uint16_t* K = p.keys + size_t(lanei) * cap * HEAD_DIM;
     uint16_t* V = p.values + size_t(lanei) * cap * HEAD_DIM;
     const size_t pslot = size_t(q) * p.parts + blockIdx.x;
+    const uint32_t nparts = (count + KP - 1) / KP;
+    if (blockIdx.x >= nparts) return;  // partitions past the visible keys take no ticket
+    __shared__ float l_s[HEADS];
 
-    if (k0 < count) {
+    {
         const uint32_t newest = count - 1;
         const bool has_new = newest >= k0 && newest < k0 + KP;
         const float* x = p.qkv + size_t(q) * QKV;
@@ -530,8 +551,11 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
                 const float l = wave_sum(e);
                 ps[(hb + hh) * KP + j] = e;
                 if (lane == 0) {
-                    p.part_m[pslot * HEADS + hb + hh] = m;
-                    p.part_l[pslot * HEADS + hb + hh] = l;
+                    l_s[hb + hh] = l;
+                    if (nparts > 1) {
+                        p.part_m[pslot * HEADS + hb + hh] = m;
+                        p.part_l[pslot * HEADS + hb + hh] = l;
+                    }
                 }
             }
         }
@@ -553,6 +577,13 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
                     o[hh] = o[hh] + pp.w * v3;
                 }
             }
+            if (nparts == 1) {
+                // one partition: the merge reduces to o / l (exp(0) == 1 exactly)
+#pragma unroll
+                for (int hh = 0; hh < 8; ++hh)
+                    p.out[size_t(q) * ATTN + (hb + hh) * HEAD_DIM + d] = roundbf(o[hh] / l_s[hb + hh]);
+                return;
+            }
 #pragma unroll
             for (int hh = 0; hh < 8; ++hh) p.part_o[(pslot * HEADS + hb + hh) * HEAD_DIM + d] = o[hh];
         }
@@ -562,12 +593,11 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
     __syncthreads();
     if (tid == 0) {
         const uint32_t prev = atomicAdd(&p.tickets[q], 1u);
-        s_last = prev == gridDim.x - 1;
+        s_last = prev == nparts - 1;
     }
     __syncthreads();
     if (!s_last) return;
     __threadfence();
-    const uint32_t nparts = (count + KP - 1) / KP;
     const size_t row0 = size_t(q) * p.parts;
     // per head: M = max_p m_p, w_p = exp(m_p - M), den = sum_p l_p w_p (partition order);
     // the weights go to LDS (the key tile is free now), then each (h, d) sums o_p w_p.
