@@ -15,9 +15,10 @@ correctly rounded IEEE FP32 operation, exactly as on the device):
   (k = 0..5); wave butterfly; then (w0+w1)+(w2+w3).  r = 1/sqrt(sum/n + 1e-6).
 * q/k norm (`qkv`, Kernels.metal:236-246): 16 lanes x 8 elements (the RoPE pairs d, d+64
   of 4 consecutive d), 16-lane butterfly.
-* decode attention (Kernels.metal:440-562 split form): 64-key partitions; score = ordered
-  sum over d of q*k; softmax statistics per partition with `exp_det`; P.V accumulated in key
-  order without contraction; merge over partitions in order.
+* decode attention (Kernels.metal:440-562 split form): 64-key partitions; score = four
+  ordered 32-dim chains of q*k summed as (c0 + c1) + (c2 + c3); softmax statistics per
+  partition with `exp_det`; P.V as two ordered chains over keys 0..31 and 32..63 (no
+  contraction) added at the end; merge over partitions in order.
 * `exp_det`: Cody-Waite reduction with a 16-bit ln2 head, degree-7 Taylor polynomial, exact
   2^k scale -- the same operation sequence as the device helper.
 
@@ -203,9 +204,13 @@ class ExactDecoder:
             kk = keys[k0:k0 + KP]
             vv = vals[k0:k0 + KP]
             nk = kk.shape[0]
-            sc = np.zeros((16, nk), F)
-            for d in range(128):
-                sc += q[:, d:d + 1] * kk[None, :, d]
+            quarters = []
+            for c in range(4):
+                part = np.zeros((16, nk), F)
+                for d in range(32 * c, 32 * c + 32):
+                    part += q[:, d:d + 1] * kk[None, :, d]
+                quarters.append(part)
+            sc = ((quarters[0] + quarters[1]) + (quarters[2] + quarters[3])).astype(F)
             sc = (sc * SCALE).astype(F)
             full_sc = np.full((16, 64), -np.inf, F)
             full_sc[:, :nk] = sc
@@ -213,10 +218,13 @@ class ExactDecoder:
             e = np.zeros((16, 64), F)
             e[:, :nk] = exp_det(sc - m[:, None])
             pm[p], pl[p] = m, butterfly(e)
-            o = np.zeros((16, 128), F)
-            for j in range(nk):
-                o = (o + e[:, j:j + 1] * vv[j][None, :]).astype(F)
-            po[p] = o
+            halves = []
+            for hf in range(2):
+                o = np.zeros((16, 128), F)
+                for j in range(32 * hf, min(nk, 32 * hf + 32)):
+                    o = (o + e[:, j:j + 1] * vv[j][None, :]).astype(F)
+                halves.append(o)
+            po[p] = (halves[0] + halves[1]).astype(F)
         M = pm.max(0)
         num = np.zeros((16, 128), F)
         den = np.zeros(16, F)

@@ -160,6 +160,22 @@ __device__ __forceinline__ bool better(float v, uint32_t i, float bv, uint32_t b
     return v > bv || (v == bv && i < bi);  // Kernels.metal:716
 }
 
+template <int O>
+__device__ __forceinline__ void best_step(float& bv, uint32_t& bi) {
+    const float v = xor_lane<O>(bv);
+    const uint32_t i = xor_lane<O>(bi);
+    if (better(v, i, bv, bi)) { bv = v; bi = i; }
+}
+// First maximum over the wavefront (the selection is order-independent).
+__device__ __forceinline__ void wave_best(float& bv, uint32_t& bi) {
+    best_step<32>(bv, bi);
+    best_step<16>(bv, bi);
+    best_step<8>(bv, bi);
+    best_step<4>(bv, bi);
+    best_step<2>(bv, bi);
+    best_step<1>(bv, bi);
+}
+
 struct Controls {
     bool on;
     int ngram;
@@ -354,12 +370,7 @@ __global__ __launch_bounds__(256) void head_merge_kernel(DecodeBuffers b, int bl
             const uint32_t i = b.head_i[q * HEAD_BLOCKS + k];
             if (better(v, i, bv, bi)) { bv = v; bi = i; }
         }
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-            const float v = __shfl_xor(bv, o, 64);
-            const uint32_t i = __shfl_xor(bi, o, 64);
-            if (better(v, i, bv, bi)) { bv = v; bi = i; }
-        }
+        wave_best(bv, bi);
         if (lane == 0) { cv[q * 4 + wave] = bv; ci[q * 4 + wave] = bi; }
     }
     __syncthreads();
@@ -380,20 +391,26 @@ __global__ __launch_bounds__(256) void head_merge_kernel(DecodeBuffers b, int bl
 
 // ---------------------------------------------------------------------- decode attention
 constexpr int KP = KEYS_PER_PART;
-constexpr int KS = 132;  // padded LDS row of rotated keys (16-byte aligned rows)
+constexpr int HG = 4;                // heads per workgroup (grid.y = HEADS / HG head groups)
+constexpr int KS = 132;              // padded LDS row of rotated keys (16-byte aligned rows)
 
+// Workgroup (partition x, head group y, row z): keys x*64 .. x*64+63 of the row's visible
+// keys for heads 4y .. 4y+3.  All four head groups rotate the same keys; only group 0
+// writes the newest key and value to the cache.
 template <bool FULL>
 __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
 #pragma clang fp contract(off)  // fixed rounding sequence, reproduced by the CPU oracle
-    __shared__ __align__(16) float qs[HEADS * HEAD_DIM];
+    __shared__ __align__(16) float qs[HG * HEAD_DIM];
     __shared__ __align__(16) float ks[KP * KS];
     __shared__ __align__(16) uint16_t vs[KP * HEAD_DIM];
-    __shared__ __align__(16) float ps[HEADS * KP];
+    __shared__ __align__(16) float ps[HG * KP];
     __shared__ __align__(16) float knew[HEAD_DIM];
+    __shared__ float l_s[HG];
+    __shared__ float den_s[HG];
     __shared__ int s_last;
 
     const StepState* st = p.state;
-    const int q = blockIdx.y;
+    const int q = blockIdx.z, hg = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     // Row geometry.  Visible keys are the absolute positions first..pos (window 2048 on the
     // local layers); key r sits at ring slot (first + r) % capacity.  Local keys rotate
@@ -414,185 +431,199 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
     const size_t pslot = size_t(q) * p.parts + blockIdx.x;
     const uint32_t nparts = (count + KP - 1) / KP;
     if (blockIdx.x >= nparts) return;  // partitions past the visible keys take no ticket
-    __shared__ float l_s[HEADS];
+    const uint32_t newest = count - 1;
+    const bool has_new = newest >= k0 && newest < k0 + KP;
+    const float* x = p.qkv + size_t(q) * QKV;
 
-    {
-        const uint32_t newest = count - 1;
-        const bool has_new = newest >= k0 && newest < k0 + KP;
-        const float* x = p.qkv + size_t(q) * QKV;
-        // ---- every independent global load first
-        const int hq = tid >> 4, sq = tid & 15;                 // q head, pair group (4 pairs)
-        const float4 qlo = *reinterpret_cast<const float4*>(x + hq * HEAD_DIM + sq * 4);
-        const float4 qhi = *reinterpret_cast<const float4*>(x + hq * HEAD_DIM + 64 + sq * 4);
-        const uint2 glo = *reinterpret_cast<const uint2*>(p.q_norm + sq * 4);
-        const uint2 ghi = *reinterpret_cast<const uint2*>(p.q_norm + 64 + sq * 4);
-        const uint4 qr = *reinterpret_cast<const uint4*>((FULL ? p.global_rope : p.local_rope) + size_t(qcoord) * 64 + sq * 4);
-        const int kj = tid >> 2, ksub = tid & 3;                // key, pair group (16 pairs)
-        const uint32_t kr = k0 + kj;
-        uint4 ka[2] = {make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)};
-        uint4 kb[2] = {make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)};
-        uint4 vv[4] = {make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)};
-        uint4 rr[4] = {make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)};
-        if (kr < count && kr != newest) {
-            uint32_t phys = start + kr;
-            phys = phys >= cap ? phys - cap : phys;  // visible keys (<= capacity) wrap at most once
-            const uint16_t* krow = K + size_t(phys) * HEAD_DIM;
-            ka[0] = *reinterpret_cast<const uint4*>(krow + ksub * 16);
-            ka[1] = *reinterpret_cast<const uint4*>(krow + ksub * 16 + 8);
-            kb[0] = *reinterpret_cast<const uint4*>(krow + 64 + ksub * 16);
-            kb[1] = *reinterpret_cast<const uint4*>(krow + 64 + ksub * 16 + 8);
-            const uint16_t* vrow = V + size_t(phys) * HEAD_DIM + ksub * 32;  // 32 of the 128 values
+    // ---- every independent global load first
+    const int hl = tid >> 4, sq = tid & 15;                 // local q head (threads 0..63), pair group
+    float4 qlo = make_float4(0.f, 0.f, 0.f, 0.f), qhi = qlo;
+    uint2 glo = make_uint2(0, 0), ghi = glo;
+    uint4 qr = make_uint4(0, 0, 0, 0);
+    if (tid < HG * 16) {
+        const int h = hg * HG + hl;
+        qlo = *reinterpret_cast<const float4*>(x + h * HEAD_DIM + sq * 4);
+        qhi = *reinterpret_cast<const float4*>(x + h * HEAD_DIM + 64 + sq * 4);
+        glo = *reinterpret_cast<const uint2*>(p.q_norm + sq * 4);
+        ghi = *reinterpret_cast<const uint2*>(p.q_norm + 64 + sq * 4);
+        qr = *reinterpret_cast<const uint4*>((FULL ? p.global_rope : p.local_rope) + size_t(qcoord) * 64 + sq * 4);
+    }
+    const int kj = tid >> 2, ksub = tid & 3;                // key, pair group (16 pairs)
+    const uint32_t kr = k0 + kj;
+    uint4 ka[2] = {make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)};
+    uint4 kb[2] = {make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)};
+    uint4 vv[4] = {make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)};
+    uint4 rr[4] = {make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)};
+    if (kr < count && kr != newest) {
+        uint32_t phys = start + kr;
+        phys = phys >= cap ? phys - cap : phys;  // visible keys (<= capacity) wrap at most once
+        const uint16_t* krow = K + size_t(phys) * HEAD_DIM;
+        ka[0] = *reinterpret_cast<const uint4*>(krow + ksub * 16);
+        ka[1] = *reinterpret_cast<const uint4*>(krow + ksub * 16 + 8);
+        kb[0] = *reinterpret_cast<const uint4*>(krow + 64 + ksub * 16);
+        kb[1] = *reinterpret_cast<const uint4*>(krow + 64 + ksub * 16 + 8);
+        const uint16_t* vrow = V + size_t(phys) * HEAD_DIM + ksub * 32;  // 32 of the 128 values
 #pragma unroll
-            for (int i = 0; i < 4; ++i) vv[i] = *reinterpret_cast<const uint4*>(vrow + 8 * i);
-        }
-        if (!FULL && kr < count) {
-            const uint4* rrow = reinterpret_cast<const uint4*>(p.local_rope + size_t(kr) * 64 + ksub * 16);
+        for (int i = 0; i < 4; ++i) vv[i] = *reinterpret_cast<const uint4*>(vrow + 8 * i);
+    }
+    if (!FULL && kr < count) {
+        const uint4* rrow = reinterpret_cast<const uint4*>(p.local_rope + size_t(kr) * 64 + ksub * 16);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) rr[i] = rrow[i];
-        }
-        // ---- queries: norm and RoPE in registers
-        {
-            float z[8];
-            head_norm8(qlo, qhi, glo, ghi, z);
-            const uint32_t c4[4] = {qr.x, qr.y, qr.z, qr.w};
+        for (int i = 0; i < 4; ++i) rr[i] = rrow[i];
+    }
+    // ---- queries of the group: norm and RoPE in registers
+    if (tid < HG * 16) {
+        float z[8];
+        head_norm8(qlo, qhi, glo, ghi, z);
+        const uint32_t c4[4] = {qr.x, qr.y, qr.z, qr.w};
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                float ra, rb;
-                rope_pair(z[j], z[4 + j], c4[j], ra, rb);
-                qs[hq * HEAD_DIM + sq * 4 + j] = ra;
-                qs[hq * HEAD_DIM + 64 + sq * 4 + j] = rb;
-            }
-        }
-        // ---- the newest key: k norm, RoPE at pos for global layers, KV write (Kernels.metal:253-257)
-        if (has_new && tid < 16) {
-            const float4 klo = *reinterpret_cast<const float4*>(x + ATTN + tid * 4);
-            const float4 khi = *reinterpret_cast<const float4*>(x + ATTN + 64 + tid * 4);
-            const uint2 gl = *reinterpret_cast<const uint2*>(p.k_norm + tid * 4);
-            const uint2 gh = *reinterpret_cast<const uint2*>(p.k_norm + 64 + tid * 4);
-            float z[8];
-            head_norm8(klo, khi, gl, gh, z);
-            const size_t slot = size_t(pos % cap) * HEAD_DIM;
-            if (FULL) {
-                const uint4 gr = *reinterpret_cast<const uint4*>(p.global_rope + size_t(pos) * 64 + tid * 4);
-                const uint32_t c4[4] = {gr.x, gr.y, gr.z, gr.w};
-#pragma unroll
-                for (int j = 0; j < 4; ++j) rope_pair(z[j], z[4 + j], c4[j], z[j], z[4 + j]);
-            }
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                K[slot + tid * 4 + j] = uint16_t(bits(z[j]));
-                K[slot + 64 + tid * 4 + j] = uint16_t(bits(z[4 + j]));
-                knew[tid * 4 + j] = z[j];
-                knew[64 + tid * 4 + j] = z[4 + j];
-            }
-        }
-        if (has_new && tid >= 64 && tid < 192) {
-            const int d = tid - 64;
-            const uint32_t bv = bits(x[QKV - HEAD_DIM + d]);
-            V[size_t(pos % cap) * HEAD_DIM + d] = uint16_t(bv);
-            vs[int(newest - k0) * HEAD_DIM + d] = uint16_t(bv);
-        }
-        __syncthreads();
-        // ---- keys: (newest from LDS) rotate with coordinate r, stage FP32 in LDS
-        {
-            float a[16], b[16];
-            const uint32_t aw[8] = {ka[0].x, ka[0].y, ka[0].z, ka[0].w, ka[1].x, ka[1].y, ka[1].z, ka[1].w};
-            const uint32_t bw[8] = {kb[0].x, kb[0].y, kb[0].z, kb[0].w, kb[1].x, kb[1].y, kb[1].z, kb[1].w};
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                a[2 * i] = lo(aw[i]); a[2 * i + 1] = hi(aw[i]);
-                b[2 * i] = lo(bw[i]); b[2 * i + 1] = hi(bw[i]);
-            }
-            if (kr == newest) {
-#pragma unroll
-                for (int i = 0; i < 16; ++i) { a[i] = knew[ksub * 16 + i]; b[i] = knew[64 + ksub * 16 + i]; }
-            }
-            if (!FULL && kr < count) {
-                const uint32_t rw[16] = {rr[0].x, rr[0].y, rr[0].z, rr[0].w, rr[1].x, rr[1].y, rr[1].z, rr[1].w,
-                                         rr[2].x, rr[2].y, rr[2].z, rr[2].w, rr[3].x, rr[3].y, rr[3].z, rr[3].w};
-#pragma unroll
-                for (int i = 0; i < 16; ++i) rope_pair(a[i], b[i], rw[i], a[i], b[i]);
-            }
-            float* krow = ks + kj * KS;
-#pragma unroll
-            for (int i = 0; i < 16; i += 4) {
-                *reinterpret_cast<float4*>(krow + ksub * 16 + i) = make_float4(a[i], a[i + 1], a[i + 2], a[i + 3]);
-                *reinterpret_cast<float4*>(krow + 64 + ksub * 16 + i) = make_float4(b[i], b[i + 1], b[i + 2], b[i + 3]);
-            }
-            if (kr != newest) {  // the newest V row was staged before the barrier
-#pragma unroll
-                for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(vs + kj * HEAD_DIM + ksub * 32 + 8 * i) = vv[i];
-            }
-        }
-        __syncthreads();
-        // ---- scores for 4 heads per wave, one key per lane: ordered sum over d
-        {
-            const int j = lane, hb = wave * 4;
-            float sc[4] = {0.f, 0.f, 0.f, 0.f};
-            const float* krow = ks + j * KS;
-#pragma unroll 2
-            for (int d = 0; d < HEAD_DIM; d += 4) {
-                const float4 kd = *reinterpret_cast<const float4*>(krow + d);
-#pragma unroll
-                for (int hh = 0; hh < 4; ++hh) {
-                    const float4 qd = *reinterpret_cast<const float4*>(qs + (hb + hh) * HEAD_DIM + d);
-                    sc[hh] = fmaf(qd.x, kd.x, sc[hh]);
-                    sc[hh] = fmaf(qd.y, kd.y, sc[hh]);
-                    sc[hh] = fmaf(qd.z, kd.z, sc[hh]);
-                    sc[hh] = fmaf(qd.w, kd.w, sc[hh]);
-                }
-            }
-            const bool valid = k0 + j < count;
-#pragma unroll
-            for (int hh = 0; hh < 4; ++hh) {
-                const float s = valid ? sc[hh] * SCALE : NEG_INF;
-                const float m = wave_max(s);
-                const float e = valid ? exp_det(s - m) : 0.f;
-                const float l = wave_sum(e);
-                ps[(hb + hh) * KP + j] = e;
-                if (lane == 0) {
-                    l_s[hb + hh] = l;
-                    if (nparts > 1) {
-                        p.part_m[pslot * HEADS + hb + hh] = m;
-                        p.part_l[pslot * HEADS + hb + hh] = l;
-                    }
-                }
-            }
-        }
-        __syncthreads();
-        // ---- unnormalised P.V for 8 heads x 1 dim per thread, keys in order
-        {
-            const int d = tid & 127, hb = (tid >> 7) * 8;
-            float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-#pragma unroll 2
-            for (int j = 0; j < KP; j += 4) {
-                const float v0 = bf(vs[(j + 0) * HEAD_DIM + d]), v1 = bf(vs[(j + 1) * HEAD_DIM + d]);
-                const float v2 = bf(vs[(j + 2) * HEAD_DIM + d]), v3 = bf(vs[(j + 3) * HEAD_DIM + d]);
-#pragma unroll
-                for (int hh = 0; hh < 8; ++hh) {
-                    const float4 pp = *reinterpret_cast<const float4*>(ps + (hb + hh) * KP + j);
-                    o[hh] = o[hh] + pp.x * v0;
-                    o[hh] = o[hh] + pp.y * v1;
-                    o[hh] = o[hh] + pp.z * v2;
-                    o[hh] = o[hh] + pp.w * v3;
-                }
-            }
-            if (nparts == 1) {
-                // one partition: the merge reduces to o / l (exp(0) == 1 exactly)
-#pragma unroll
-                for (int hh = 0; hh < 8; ++hh)
-                    p.out[size_t(q) * ATTN + (hb + hh) * HEAD_DIM + d] = roundbf(o[hh] / l_s[hb + hh]);
-                return;
-            }
-#pragma unroll
-            for (int hh = 0; hh < 8; ++hh) p.part_o[(pslot * HEADS + hb + hh) * HEAD_DIM + d] = o[hh];
+        for (int j = 0; j < 4; ++j) {
+            float ra, rb;
+            rope_pair(z[j], z[4 + j], c4[j], ra, rb);
+            qs[hl * HEAD_DIM + sq * 4 + j] = ra;
+            qs[hl * HEAD_DIM + 64 + sq * 4 + j] = rb;
         }
     }
-    // ticket: the last workgroup of this row merges the partitions
+    // ---- the newest key: k norm, RoPE at pos for global layers, KV write (Kernels.metal:253-257)
+    if (has_new && tid >= 64 && tid < 80) {
+        const int t = tid - 64;
+        const float4 klo = *reinterpret_cast<const float4*>(x + ATTN + t * 4);
+        const float4 khi = *reinterpret_cast<const float4*>(x + ATTN + 64 + t * 4);
+        const uint2 gl = *reinterpret_cast<const uint2*>(p.k_norm + t * 4);
+        const uint2 gh = *reinterpret_cast<const uint2*>(p.k_norm + 64 + t * 4);
+        float z[8];
+        head_norm8(klo, khi, gl, gh, z);
+        const size_t slot = size_t(pos % cap) * HEAD_DIM;
+        if (FULL) {
+            const uint4 gr = *reinterpret_cast<const uint4*>(p.global_rope + size_t(pos) * 64 + t * 4);
+            const uint32_t c4[4] = {gr.x, gr.y, gr.z, gr.w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) rope_pair(z[j], z[4 + j], c4[j], z[j], z[4 + j]);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (hg == 0) {
+                K[slot + t * 4 + j] = uint16_t(bits(z[j]));
+                K[slot + 64 + t * 4 + j] = uint16_t(bits(z[4 + j]));
+            }
+            knew[t * 4 + j] = z[j];
+            knew[64 + t * 4 + j] = z[4 + j];
+        }
+    }
+    if (has_new && tid >= 128) {
+        const int d = tid - 128;
+        const uint32_t bv = bits(x[QKV - HEAD_DIM + d]);
+        if (hg == 0) V[size_t(pos % cap) * HEAD_DIM + d] = uint16_t(bv);
+        vs[int(newest - k0) * HEAD_DIM + d] = uint16_t(bv);
+    }
+    __syncthreads();
+    // ---- keys: (newest from LDS) rotate with coordinate r, stage FP32 in LDS
+    {
+        float a[16], b[16];
+        const uint32_t aw[8] = {ka[0].x, ka[0].y, ka[0].z, ka[0].w, ka[1].x, ka[1].y, ka[1].z, ka[1].w};
+        const uint32_t bw[8] = {kb[0].x, kb[0].y, kb[0].z, kb[0].w, kb[1].x, kb[1].y, kb[1].z, kb[1].w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            a[2 * i] = lo(aw[i]); a[2 * i + 1] = hi(aw[i]);
+            b[2 * i] = lo(bw[i]); b[2 * i + 1] = hi(bw[i]);
+        }
+        if (kr == newest) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) { a[i] = knew[ksub * 16 + i]; b[i] = knew[64 + ksub * 16 + i]; }
+        }
+        if (!FULL && kr < count) {
+            const uint32_t rw[16] = {rr[0].x, rr[0].y, rr[0].z, rr[0].w, rr[1].x, rr[1].y, rr[1].z, rr[1].w,
+                                     rr[2].x, rr[2].y, rr[2].z, rr[2].w, rr[3].x, rr[3].y, rr[3].z, rr[3].w};
+#pragma unroll
+            for (int i = 0; i < 16; ++i) rope_pair(a[i], b[i], rw[i], a[i], b[i]);
+        }
+        float* krow = ks + kj * KS;
+#pragma unroll
+        for (int i = 0; i < 16; i += 4) {
+            *reinterpret_cast<float4*>(krow + ksub * 16 + i) = make_float4(a[i], a[i + 1], a[i + 2], a[i + 3]);
+            *reinterpret_cast<float4*>(krow + 64 + ksub * 16 + i) = make_float4(b[i], b[i + 1], b[i + 2], b[i + 3]);
+        }
+        if (kr != newest) {  // the newest V row was staged before the barrier
+#pragma unroll
+            for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(vs + kj * HEAD_DIM + ksub * 32 + 8 * i) = vv[i];
+        }
+    }
+    __syncthreads();
+    // ---- scores: wave w = local head w, lane = key.  Each score is four ordered 32-dim
+    //      chains (dims 32c .. 32c+31) summed as (c0 + c1) + (c2 + c3).
+    {
+        const int j = lane, w = wave;
+        float sc[4] = {0.f, 0.f, 0.f, 0.f};
+        const float* krow = ks + j * KS;
+        const float* qrow = qs + w * HEAD_DIM;
+#pragma unroll 4
+        for (int d = 0; d < 32; d += 4) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const float4 kd = *reinterpret_cast<const float4*>(krow + 32 * c + d);
+                const float4 qd = *reinterpret_cast<const float4*>(qrow + 32 * c + d);
+                sc[c] = fmaf(qd.x, kd.x, sc[c]);
+                sc[c] = fmaf(qd.y, kd.y, sc[c]);
+                sc[c] = fmaf(qd.z, kd.z, sc[c]);
+                sc[c] = fmaf(qd.w, kd.w, sc[c]);
+            }
+        }
+        const bool valid = k0 + j < count;
+        const float dot = (sc[0] + sc[1]) + (sc[2] + sc[3]);
+        const float s = valid ? dot * SCALE : NEG_INF;
+        const float m = wave_max(s);
+        const float e = valid ? exp_det(s - m) : 0.f;
+        const float l = wave_sum(e);
+        ps[w * KP + j] = e;
+        if (lane == 0) {
+            l_s[w] = l;
+            if (nparts > 1) {
+                p.part_m[pslot * HEADS + hg * HG + w] = m;
+                p.part_l[pslot * HEADS + hg * HG + w] = l;
+            }
+        }
+    }
+    __syncthreads();
+    // ---- unnormalised P.V: thread -> dim d = tid & 127 of local heads 2*(tid >> 7) + {0, 1};
+    //      keys 0..31 and 32..63 as two ordered chains, added at the end
+    {
+        const int d = tid & 127, h2 = (tid >> 7) * 2;
+        float o[2][2] = {{0.f, 0.f}, {0.f, 0.f}};
+#pragma unroll 2
+        for (int j = 0; j < KP / 2; j += 4) {
+            float v[2][4];
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) v[hf][i] = bf(vs[(hf * (KP / 2) + j + i) * HEAD_DIM + d]);
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                for (int hf = 0; hf < 2; ++hf) {
+                    const float4 pp = *reinterpret_cast<const float4*>(ps + (h2 + hh) * KP + hf * (KP / 2) + j);
+                    o[hh][hf] = o[hh][hf] + pp.x * v[hf][0];
+                    o[hh][hf] = o[hh][hf] + pp.y * v[hf][1];
+                    o[hh][hf] = o[hh][hf] + pp.z * v[hf][2];
+                    o[hh][hf] = o[hh][hf] + pp.w * v[hf][3];
+                }
+        }
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+            const float of = o[hh][0] + o[hh][1];
+            const int h = hg * HG + h2 + hh;
+            if (nparts == 1)  // one partition: the merge reduces to o / l (exp(0) == 1 exactly)
+                p.out[size_t(q) * ATTN + h * HEAD_DIM + d] = roundbf(of / l_s[h2 + hh]);
+            else
+                p.part_o[(pslot * HEADS + h) * HEAD_DIM + d] = of;
+        }
+    }
+    if (nparts == 1) return;
+    // ticket: the last workgroup of this (row, head group) merges the partitions
     __threadfence();
     __syncthreads();
+    uint32_t* ticket = p.tickets + q * (HEADS / HG) + hg;
     if (tid == 0) {
-        const uint32_t prev = atomicAdd(&p.tickets[q], 1u);
+        const uint32_t prev = atomicAdd(ticket, 1u);
         s_last = prev == nparts - 1;
     }
     __syncthreads();
@@ -600,42 +631,63 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
     __threadfence();
     const size_t row0 = size_t(q) * p.parts;
     // per head: M = max_p m_p, w_p = exp(m_p - M), den = sum_p l_p w_p (partition order);
-    // the weights go to LDS (the key tile is free now), then each (h, d) sums o_p w_p.
-    float* wts = ks;                                   // [nparts][16], nparts <= KP*KS/16
-    __shared__ float den_s[HEADS];
-    const uint32_t np = nparts <= uint32_t(KP * KS / HEADS) ? nparts : uint32_t(KP * KS / HEADS);
-    if (tid < HEADS) {
-        const int h = tid;
-        float M = NEG_INF;
-#pragma unroll 4
-        for (uint32_t k = 0; k < nparts; ++k) M = fmaxf(M, p.part_m[(row0 + k) * HEADS + h]);
-        float den = 0.f;
-#pragma unroll 4
-        for (uint32_t k = 0; k < nparts; ++k) {
-            const float w = exp_det(p.part_m[(row0 + k) * HEADS + h] - M);
-            den = den + p.part_l[(row0 + k) * HEADS + h] * w;
-            if (k < np) wts[k * HEADS + h] = w;
-        }
-        den_s[h] = den;
+    // then each (h, d) sums o_p w_p in partition order.  Partition statistics are staged in
+    // LDS (the key tile is free now) with all loads in flight together.
+    float* mm = ks;                                    // [np][HG]
+    float* wl = ks + (KP * KS) / 2;                    // [np][HG]: l, then the weights
+    const uint32_t np = nparts <= uint32_t(KP * KS / 2 / HG) ? nparts : uint32_t(KP * KS / 2 / HG);
+    for (uint32_t i = tid; i < np * HG; i += 256) {
+        const uint32_t k = i / HG, h = hg * HG + i % HG;
+        mm[i] = p.part_m[(row0 + k) * HEADS + h];
+        wl[i] = p.part_l[(row0 + k) * HEADS + h];
     }
     __syncthreads();
-    for (int e = tid; e < HEADS * HEAD_DIM; e += 256) {
-        const int h = e >> 7, d = e & 127;
-        float num = 0.f;
+    if (tid < HG) {
+        const int hh = tid, h = hg * HG + hh;
+        float M = NEG_INF, den = 0.f;
         if (nparts == np) {
-#pragma unroll 4
-            for (uint32_t k = 0; k < nparts; ++k)
-                num = num + p.part_o[((row0 + k) * HEADS + h) * HEAD_DIM + d] * wts[k * HEADS + h];
-        } else {  // more partitions than the LDS table holds: recompute the weights
-            float M = NEG_INF;
+            for (uint32_t k = 0; k < nparts; ++k) M = fmaxf(M, mm[k * HG + hh]);
+            for (uint32_t k = 0; k < nparts; ++k) {
+                const float w = exp_det(mm[k * HG + hh] - M);
+                den = den + wl[k * HG + hh] * w;
+                wl[k * HG + hh] = w;
+            }
+        } else {  // more partitions than LDS holds: read them from memory
             for (uint32_t k = 0; k < nparts; ++k) M = fmaxf(M, p.part_m[(row0 + k) * HEADS + h]);
             for (uint32_t k = 0; k < nparts; ++k)
-                num = num + p.part_o[((row0 + k) * HEADS + h) * HEAD_DIM + d] *
-                                exp_det(p.part_m[(row0 + k) * HEADS + h] - M);
+                den = den + p.part_l[(row0 + k) * HEADS + h] * exp_det(p.part_m[(row0 + k) * HEADS + h] - M);
         }
-        p.out[size_t(q) * ATTN + h * HEAD_DIM + d] = roundbf(num / den_s[h]);
+        den_s[hh] = den;
+        l_s[hh] = M;
     }
-    if (tid == 0) p.tickets[q] = 0;
+    __syncthreads();
+    {
+        // thread -> dim d = tid & 127 of local heads (tid >> 7) and (tid >> 7) + 2
+        const int d = tid & 127, hb = tid >> 7;
+        float num[2] = {0.f, 0.f};
+        if (nparts == np) {
+#pragma unroll 4
+            for (uint32_t k = 0; k < nparts; ++k) {
+                float ov[2];
+#pragma unroll
+                for (int i = 0; i < 2; ++i) ov[i] = p.part_o[((row0 + k) * HEADS + hg * HG + hb + 2 * i) * HEAD_DIM + d];
+#pragma unroll
+                for (int i = 0; i < 2; ++i) num[i] = num[i] + ov[i] * wl[k * HG + hb + 2 * i];
+            }
+        } else {
+            for (uint32_t k = 0; k < nparts; ++k)
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    const int h = hg * HG + hb + 2 * i;
+                    num[i] = num[i] + p.part_o[((row0 + k) * HEADS + h) * HEAD_DIM + d] *
+                                          exp_det(p.part_m[(row0 + k) * HEADS + h] - l_s[hb + 2 * i]);
+                }
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            p.out[size_t(q) * ATTN + (hg * HG + hb + 2 * i) * HEAD_DIM + d] = roundbf(num[i] / den_s[hb + 2 * i]);
+    }
+    if (tid == 0) *ticket = 0;
 }
 
 // ------------------------------------------------------------------------- step begin
@@ -839,7 +891,7 @@ void launch_gemv(int n, bool packed, int maxr, Prologue pro, Epilogue epi, const
 }
 
 void launch_attention(bool full, const AttnParams& p, int rows, hipStream_t s) {
-    const dim3 grid(p.parts, rows), block(256);
+    const dim3 grid(p.parts, HEADS / HG, rows), block(256);
     if (full) hipLaunchKernelGGL(attn_decode_kernel<true>, grid, block, 0, s, p);
     else hipLaunchKernelGGL(attn_decode_kernel<false>, grid, block, 0, s, p);
 }

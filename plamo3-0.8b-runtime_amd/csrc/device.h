@@ -24,21 +24,64 @@ __device__ __forceinline__ float hi(uint32_t w) { return __uint_as_float(w & 0xf
 __device__ __forceinline__ float lo_bf(uint32_t w) { return lo(w); }
 __device__ __forceinline__ float hi_bf(uint32_t w) { return hi(w); }
 
-// Butterfly reductions over the 64-lane wavefront; every lane ends with the same bits.
+// Value of lane (lane ^ O) on VALU-speed cross-lane paths instead of the LDS crossbar:
+// O = 32 / 16 by the gfx950 permlane swaps, O = 8 / 4 by DPP row rotations, O = 2 / 1 by
+// DPP quad permutes.  (Lane mappings verified on gfx950: permlane32_swap(v, v) yields
+// {lanes 0-31 of v in both halves, lanes 32-63 in both halves}; permlane16_swap(v, v)
+// {even rows, odd rows}; row_ror:n moves lane i to i + n within a row of 16.)
+template <int O>
+__device__ __forceinline__ uint32_t xor_lane(uint32_t v) {
+    const uint32_t lane = threadIdx.x & 63u;
+    if constexpr (O == 32) {
+        const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        return (lane & 32u) ? r[0] : r[1];
+    } else if constexpr (O == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+        return (lane & 16u) ? r[0] : r[1];
+    } else if constexpr (O == 8) {
+        return uint32_t(__builtin_amdgcn_update_dpp(0, int(v), 0x128, 0xf, 0xf, false));  // row_ror:8
+    } else if constexpr (O == 4) {
+        const uint32_t up = uint32_t(__builtin_amdgcn_update_dpp(0, int(v), 0x12C, 0xf, 0xf, false));  // lane + 4
+        const uint32_t dn = uint32_t(__builtin_amdgcn_update_dpp(0, int(v), 0x124, 0xf, 0xf, false));  // lane - 4
+        return (lane & 4u) ? dn : up;
+    } else if constexpr (O == 2) {
+        return uint32_t(__builtin_amdgcn_update_dpp(0, int(v), 0x4E, 0xf, 0xf, false));  // quad_perm 2,3,0,1
+    } else {
+        static_assert(O == 1, "xor offset");
+        return uint32_t(__builtin_amdgcn_update_dpp(0, int(v), 0xB1, 0xf, 0xf, false));  // quad_perm 1,0,3,2
+    }
+}
+template <int O>
+__device__ __forceinline__ float xor_lane(float v) {
+    return __uint_as_float(xor_lane<O>(__float_as_uint(v)));
+}
+
+// Butterfly reductions over the 64-lane wavefront (XOR offsets 32, 16, 8, 4, 2, 1): lane i
+// adds lane i ^ o at each level, so every lane ends with the same bits.
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    v += xor_lane<32>(v);
+    v += xor_lane<16>(v);
+    v += xor_lane<8>(v);
+    v += xor_lane<4>(v);
+    v += xor_lane<2>(v);
+    v += xor_lane<1>(v);
     return v;
 }
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    v = fmaxf(v, xor_lane<32>(v));
+    v = fmaxf(v, xor_lane<16>(v));
+    v = fmaxf(v, xor_lane<8>(v));
+    v = fmaxf(v, xor_lane<4>(v));
+    v = fmaxf(v, xor_lane<2>(v));
+    v = fmaxf(v, xor_lane<1>(v));
     return v;
 }
-// Reduction over aligned groups of 16 lanes.
+// Reduction over aligned groups of 16 lanes (offsets 8, 4, 2, 1).
 __device__ __forceinline__ float group16_sum(float v) {
-#pragma unroll
-    for (int o = 8; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    v += xor_lane<8>(v);
+    v += xor_lane<4>(v);
+    v += xor_lane<2>(v);
+    v += xor_lane<1>(v);
     return v;
 }
 

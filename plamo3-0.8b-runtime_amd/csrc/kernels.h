@@ -82,7 +82,7 @@ struct AttnParams {
     float* part_l;
     float* part_o;            // [ROWS][parts][16][128]
     uint32_t parts;           // grid.x
-    uint32_t* tickets;        // [rows], zero between launches
+    uint32_t* tickets;        // [rows][head groups], zero between launches
     float* out;               // FP32 [rows][2048]
 };
 

@@ -471,7 +471,7 @@ __global__ __launch_bounds__(256) void flash_prefill_kernel(const FlashParams p)
                     mt = fmaxf(mt, x);
                 }
         }
-        mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+        mt = fmaxf(mt, xor_lane<32>(mt));
         const float mn = fmaxf(m, mt);
         const float ms = mn == NEG_INF ? 0.0f : mn;  // nothing visible yet: every p is 0
         const float alpha = __builtin_amdgcn_exp2f(m - ms);
@@ -512,7 +512,7 @@ __global__ __launch_bounds__(256) void flash_prefill_kernel(const FlashParams p)
         __syncthreads();
     }
     // O = O^T / l; element i of d-tile dt is dim 32dt + 8(i/4) + 4*half + i%4
-    const float lt = ls + __shfl_xor(ls, 32, 64);
+    const float lt = ls + xor_lane<32>(ls);
     if (!qvalid) return;
     uint16_t* orow = p.out + size_t(tq) * ATTN + head * HEAD_DIM;
 #pragma unroll

@@ -261,8 +261,8 @@ Engine::Engine(std::shared_ptr<Model> mdl, int ctx, int nl, hipStream_t s)
     part_m = arena.alloc_n<float>(part_rows_cap * HEADS);
     part_l = arena.alloc_n<float>(part_rows_cap * HEADS);
     part_o = arena.alloc_n<float>(part_rows_cap * HEADS * HEAD_DIM);
-    attn_tickets = arena.alloc_n<uint32_t>(size_t(ROWS));
-    PLAMO_HIP(hipMemsetAsync(attn_tickets, 0, size_t(ROWS) * 4, stream));
+    attn_tickets = arena.alloc_n<uint32_t>(size_t(ROWS) * HEADS);  // [row][head group]
+    PLAMO_HIP(hipMemsetAsync(attn_tickets, 0, size_t(ROWS) * HEADS * 4, stream));
     p_x = arena.alloc_n<float>(size_t(chunk) * HIDDEN);
     p_qkv = arena.alloc_n<float>(size_t(chunk) * QKV);
     p_proj = arena.alloc_n<float>(size_t(chunk) * HIDDEN);
