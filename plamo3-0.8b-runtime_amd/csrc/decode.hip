@@ -25,64 +25,95 @@ namespace {
 
 // ---------------------------------------------------------------------------- prologues
 // Stage the BF16 activation rows into LDS.  Values are BF16-exact FP32 (every producer
-// rounds), so the BF16 copy is lossless.
+// rounds), so the BF16 copy is lossless.  The prologue is split into its loads
+// (stage_load) and its arithmetic (stage_finish) so the kernel can request the first
+// weights in between: the vector-memory counter is in order, and inputs requested before
+// the weights can be consumed while the weights are still in flight.
 template <int N, int MAXR, int PRO>
-__device__ __forceinline__ void stage_rows(const GemvParams& p, int rows, uint16_t* xs, float* red) {
+struct Staged {
+    static constexpr int V = (N + 1023) / 1024;  // PLAIN: float4 per thread and row
+    static constexpr int E = HIDDEN / 256;       // norm prologues: elements per thread
+    float4 v[PRO == PRO_PLAIN ? MAXR : 1][V];
+    float a[PRO == PRO_PLAIN ? 1 : MAXR][E];     // EMBED: embedding row; RESID: projection
+    float r[PRO == PRO_RESID ? MAXR : 1][E];     // RESID: residual stream
+    uint16_t gp[E], gn[E];
+};
+
+// rb: rows whose inputs are read (every row the buffers hold when a step state is given)
+template <int N, int MAXR, int PRO>
+__device__ __forceinline__ void stage_load(const GemvParams& p, int rb, Staged<N, MAXR, PRO>& S) {
     const int tid = threadIdx.x;
+    constexpr int V = Staged<N, MAXR, PRO>::V, E = Staged<N, MAXR, PRO>::E;
     if constexpr (PRO == PRO_PLAIN) {
-        // every load in flight at once: ceil(N/1024) float4 per thread and row
-        constexpr int V = (N + 1023) / 1024;
-        float4 v[MAXR][V];
 #pragma unroll
         for (int q = 0; q < MAXR; ++q)
 #pragma unroll
             for (int k = 0; k < V; ++k) {
                 const int e = (tid + 256 * k) * 4;
-                v[q][k] = (q < rows && e < N) ? *reinterpret_cast<const float4*>(p.in + q * N + e)
-                                              : make_float4(0.f, 0.f, 0.f, 0.f);
-            }
-#pragma unroll
-        for (int q = 0; q < MAXR; ++q)
-#pragma unroll
-            for (int k = 0; k < V; ++k) {
-                const int e = (tid + 256 * k) * 4;
-                if (e >= N) continue;
-                const uint32_t lo2 = (bits(v[q][k].x) & 0xffffu) | (bits(v[q][k].y) << 16);
-                const uint32_t hi2 = (bits(v[q][k].z) & 0xffffu) | (bits(v[q][k].w) << 16);
-                *reinterpret_cast<uint2*>(&xs[q * N + e]) = make_uint2(lo2, hi2);
+                S.v[q][k] = (q < rb && e < N) ? *reinterpret_cast<const float4*>(p.in + q * N + e)
+                                               : make_float4(0.f, 0.f, 0.f, 0.f);
             }
     } else {
         static_assert(N == HIDDEN, "norm prologue is 1536 wide");
-        constexpr int E = HIDDEN / 256;  // 6 elements per thread
-        float xv[MAXR][E];
-        float ss[MAXR];
+#pragma unroll
+        for (int k = 0; k < E; ++k) S.gn[k] = p.g_next[tid + 256 * k];
         if constexpr (PRO == PRO_EMBED) {
 #pragma unroll
             for (int q = 0; q < MAXR; ++q) {
-                int tok = (q < rows && p.state) ? p.state->token[q] : 0;
+                int tok = (q < rb && p.state) ? p.state->token[q] : 0;
                 tok = (tok < 0 || tok >= VOCAB) ? 0 : tok;  // loop guards stop before this
 #pragma unroll
                 for (int k = 0; k < E; ++k)
-                    xv[q][k] = (q < rows) ? bf(p.embed[size_t(tok) * HIDDEN + tid + 256 * k]) : 0.f;
+                    S.a[q][k] = (q < rb) ? bf(p.embed[size_t(tok) * HIDDEN + tid + 256 * k]) : 0.f;
             }
         } else {
-            // z = roundbf(roundbf(p*r) * roundbf(bf(w)+offset)); x = roundbf(x + z)
-            // (Kernels.metal:59-72, full == 1).  Every independent load is issued first.
-            float pv[MAXR][E], rv[MAXR][E], gp[E];
 #pragma unroll
-            for (int k = 0; k < E; ++k) gp[k] = bf(p.g_post[tid + 256 * k]);
+            for (int k = 0; k < E; ++k) S.gp[k] = p.g_post[tid + 256 * k];
 #pragma unroll
             for (int q = 0; q < MAXR; ++q)
 #pragma unroll
                 for (int k = 0; k < E; ++k) {
-                    pv[q][k] = (q < rows) ? p.in[q * HIDDEN + tid + 256 * k] : 0.f;
-                    rv[q][k] = (q < rows) ? p.resid_in[q * HIDDEN + tid + 256 * k] : 0.f;
+                    S.a[q][k] = (q < rb) ? p.in[q * HIDDEN + tid + 256 * k] : 0.f;
+                    S.r[q][k] = (q < rb) ? p.resid_in[q * HIDDEN + tid + 256 * k] : 0.f;
                 }
+        }
+    }
+}
+
+template <int N, int MAXR, int PRO>
+__device__ __forceinline__ void stage_finish(const GemvParams& p, int rows, const Staged<N, MAXR, PRO>& S,
+                                             uint16_t* xs, float* red) {
+    const int tid = threadIdx.x;
+    constexpr int V = Staged<N, MAXR, PRO>::V, E = Staged<N, MAXR, PRO>::E;
+    if constexpr (PRO == PRO_PLAIN) {
+#pragma unroll
+        for (int q = 0; q < MAXR; ++q) {
+            if (q >= rows) break;
+#pragma unroll
+            for (int k = 0; k < V; ++k) {
+                const int e = (tid + 256 * k) * 4;
+                if (e >= N) continue;
+                const uint32_t lo2 = (bits(S.v[q][k].x) & 0xffffu) | (bits(S.v[q][k].y) << 16);
+                const uint32_t hi2 = (bits(S.v[q][k].z) & 0xffffu) | (bits(S.v[q][k].w) << 16);
+                *reinterpret_cast<uint2*>(&xs[q * N + e]) = make_uint2(lo2, hi2);
+            }
+        }
+    } else {
+        float xv[MAXR][E];
+        float ss[MAXR];
+        if constexpr (PRO == PRO_EMBED) {
+#pragma unroll
+            for (int q = 0; q < MAXR; ++q)
+#pragma unroll
+                for (int k = 0; k < E; ++k) xv[q][k] = (q < rows) ? S.a[q][k] : 0.f;
+        } else {
+            // z = roundbf(roundbf(p*r) * roundbf(bf(w)+offset)); x = roundbf(x + z)
+            // (Kernels.metal:59-72, full == 1)
 #pragma unroll
             for (int q = 0; q < MAXR; ++q) {
                 ss[q] = 0.f;
 #pragma unroll
-                for (int k = 0; k < E; ++k) ss[q] += pv[q][k] * pv[q][k];
+                for (int k = 0; k < E; ++k) ss[q] += S.a[q][k] * S.a[q][k];
             }
 #pragma unroll
             for (int q = 0; q < MAXR; ++q) {
@@ -96,9 +127,9 @@ __device__ __forceinline__ void stage_rows(const GemvParams& p, int rows, uint16
                 const float r = 1.0f / sqrtf(total / float(HIDDEN) + 1e-6f);
 #pragma unroll
                 for (int k = 0; k < E; ++k) {
-                    const float g = roundbf(gp[k] + p.post_offset);
-                    const float z = roundbf(roundbf(pv[q][k] * r) * g);
-                    xv[q][k] = (q < rows) ? roundbf(rv[q][k] + z) : 0.f;
+                    const float g = roundbf(bf(S.gp[k]) + p.post_offset);
+                    const float z = roundbf(roundbf(S.a[q][k] * r) * g);
+                    xv[q][k] = (q < rows) ? roundbf(S.r[q][k] + z) : 0.f;
                 }
             }
             __syncthreads();
@@ -106,7 +137,7 @@ __device__ __forceinline__ void stage_rows(const GemvParams& p, int rows, uint16
         // next norm with +1 offset (Kernels.metal:76-89)
         float gn[E];
 #pragma unroll
-        for (int k = 0; k < E; ++k) gn[k] = roundbf(bf(p.g_next[tid + 256 * k]) + 1.0f);
+        for (int k = 0; k < E; ++k) gn[k] = roundbf(bf(S.gn[k]) + 1.0f);
 #pragma unroll
         for (int q = 0; q < MAXR; ++q) {
             ss[q] = 0.f;
@@ -207,16 +238,13 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvParams p) {
     __shared__ uint32_t cand_i[MAXR * 4];
 
     const StepState* st = p.state;
-    if (st && st->stopped) return;
-    int rows = p.rows;  // (a select of two addresses would put the argument in scratch)
-    if (st) rows = int(st->rows);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    Controls ctl{false, 0, 1.0f, 0.0f, 0.0f};
-    if constexpr (EPI == EPI_LOGITS) {
-        if (st && st->sampling) ctl = Controls{true, st->ngram, st->penalty, st->frequency, st->presence};
-    }
-
     const int groups = (EPI == EPI_SWIGLU) ? p.m / 4 : p.m / U;
+    // Request order = consumption order: step state, prologue inputs, first weights.
+    uint32_t stopped = 0, srows = 0;
+    if (st) { stopped = st->stopped; srows = st->rows; }
+    Staged<N, MAXR, PRO> S;
+    stage_load<N, MAXR, PRO>(p, p.rows < MAXR ? p.rows : MAXR, S);
     float best_v[MAXR];
     uint32_t best_i[MAXR];
 #pragma unroll
@@ -243,7 +271,14 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvParams p) {
 #pragma unroll
             for (int it = 0; it < IT; ++it) w[u][it] = load_w<N, PACKED>(p, wrow[u], it, lane);
     }
-    stage_rows<N, MAXR, PRO>(p, rows, xs, red);
+    if (stopped) return;
+    int rows = p.rows;  // (a select of two addresses would put the argument in scratch)
+    if (st) rows = int(srows);
+    Controls ctl{false, 0, 1.0f, 0.0f, 0.0f};
+    if constexpr (EPI == EPI_LOGITS) {
+        if (st && st->sampling) ctl = Controls{true, st->ngram, st->penalty, st->frequency, st->presence};
+    }
+    stage_finish<N, MAXR, PRO>(p, rows, S, xs, red);
     __syncthreads();
     for (; g < groups; g += stride) {
         int wrow[U];

@@ -51,7 +51,8 @@ struct GemvParams {
     const uint16_t* w;        // plain BF16 [m][n] or .p12 payload
     const uint32_t* table;    // .p12 block table (packed only)
     int m;                    // weight rows
-    int rows;                 // activation rows when no StepState is given
+    int rows;                 // rows the input buffers hold (the active rows when no
+                              // StepState is given; the state's rows never exceed it)
     const StepState* state;   // may be null (kernel-level entry points)
     // prologue
     const float* in;          // PLAIN: [rows][n]; RESID: projection output [rows][1536]

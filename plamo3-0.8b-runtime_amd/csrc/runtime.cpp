@@ -252,6 +252,7 @@ Engine::Engine(std::shared_ptr<Model> mdl, int ctx, int nl, hipStream_t s)
     bufs.head_v = arena.alloc_n<float>(size_t(ROWS) * HEAD_BLOCKS);
     bufs.head_i = arena.alloc_n<uint32_t>(size_t(ROWS) * HEAD_BLOCKS);
     bufs.tickets = arena.alloc_n<uint32_t>(1);
+
     PLAMO_HIP(hipMemsetAsync(bufs.tickets, 0, 4, stream));
     PLAMO_HIP(hipMemsetAsync(bufs.counts, 0, size_t(ROWS) * VOCAB * 4, stream));
     PLAMO_HIP(hipMemsetAsync(bufs.banned, 0, size_t(ROWS) * (VOCAB / 32) * 4, stream));
@@ -278,6 +279,7 @@ Engine::Engine(std::shared_ptr<Model> mdl, int ctx, int nl, hipStream_t s)
 
 Engine::~Engine() {
     if (graph) (void)hipGraphExecDestroy(graph);
+
     (void)hipEventDestroy(ev0);
     (void)hipEventDestroy(ev1);
     if (host_state) (void)hipHostFree(host_state);
@@ -287,11 +289,12 @@ void Engine::zero_sampler() {
     PLAMO_HIP(hipMemsetAsync(bufs.counts, 0, size_t(ROWS) * VOCAB * 4, stream));
 }
 
-void Engine::enqueue_head(const float* in, const float* resid_in) {
+void Engine::enqueue_head(const float* in, const float* resid_in, int in_rows) {
     const Model& m = *model;
     const int maxr = lanes == 1 ? 1 : ROWS;
     GemvParams g{};
     g.state = state;
+    g.rows = in_rows;
     g.m = VOCAB;
     g.w = m.head.w;
     g.table = m.head.table;
@@ -319,6 +322,7 @@ void Engine::enqueue_step(bool head) {
         const bool full = is_global_layer(l);
         GemvParams g{};
         g.state = state;
+        g.rows = ROWS;
         // QKV with the (embedding or post-MLP residual) + pre-attention norm prologue
         g.m = QKV;
         g.w = L.qkv.w;
@@ -355,6 +359,7 @@ void Engine::enqueue_step(bool head) {
         launch_attention(full, a, ROWS, stream);
         GemvParams o{};
         o.state = state;
+        o.rows = ROWS;
         o.m = HIDDEN;
         o.w = L.o.w;
         o.table = L.o.table;
@@ -363,6 +368,7 @@ void Engine::enqueue_step(bool head) {
         launch_gemv(ATTN, pk, maxr, PRO_PLAIN, EPI_ROUND, o, HIDDEN / 16, stream);
         GemvParams u{};
         u.state = state;
+        u.rows = ROWS;
         u.m = 2 * INTER;
         u.w = L.up.w;
         u.table = L.up.table;
@@ -376,6 +382,7 @@ void Engine::enqueue_step(bool head) {
         launch_gemv(HIDDEN, pk, maxr, PRO_RESID, EPI_SWIGLU, u, 2 * INTER / 16, stream);
         GemvParams d{};
         d.state = state;
+        d.rows = ROWS;
         d.m = HIDDEN;
         d.w = L.down.w;
         d.table = L.down.table;
@@ -383,7 +390,7 @@ void Engine::enqueue_step(bool head) {
         d.out = proj;
         launch_gemv(INTER, pk, maxr, PRO_PLAIN, EPI_ROUND, d, HIDDEN / 8, stream);
     }
-    if (head) enqueue_head(proj, x1);
+    if (head) enqueue_head(proj, x1, ROWS);
 }
 
 void Engine::run_step() {
@@ -473,7 +480,7 @@ void Engine::enqueue_prefill_chunk(int n, int p0, int lane, bool last_chunk, boo
     }
     if (last_chunk && output) {
         launch_step_begin(bufs, stream);
-        enqueue_head(p_proj + size_t(n - 1) * HIDDEN, p_x + size_t(n - 1) * HIDDEN);
+        enqueue_head(p_proj + size_t(n - 1) * HIDDEN, p_x + size_t(n - 1) * HIDDEN, 1);
     }
 }
 

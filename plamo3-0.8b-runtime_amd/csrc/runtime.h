@@ -82,6 +82,7 @@ class Engine {
     // graph
     hipGraphExec_t graph = nullptr;
     bool use_graph = true;
+
     hipEvent_t ev0, ev1;
 
     void enqueue_step(bool head = true);    // one decode step for state->rows rows
@@ -92,7 +93,7 @@ class Engine {
 
   private:
     void enqueue_prefill_chunk(int n, int p0, int lane, bool last_chunk, bool output);
-    void enqueue_head(const float* in, const float* resid_in);
+    void enqueue_head(const float* in, const float* resid_in, int in_rows);
 };
 
 std::shared_ptr<Model> load_model(const std::string& dir, int context, bool packed, const std::string& sha,
