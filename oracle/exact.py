@@ -11,8 +11,8 @@ correctly rounded IEEE FP32 operation, exactly as on the device):
   it*512 + l*8 .. +8; it accumulates products in column order (BF16 x BF16 products are exact
   in FP32, so fma == add of the product); the 64 lane sums are combined by an XOR
   butterfly (offsets 32,16,8,4,2,1).
-* RMSNorm (`norm`, Kernels.metal:46-90): thread t of 256 sums squares of elements t+256k
-  (k = 0..5); wave butterfly; then (w0+w1)+(w2+w3).  r = 1/sqrt(sum/n + 1e-6).
+* RMSNorm (`norm`, Kernels.metal:46-90): thread t of 256 sums squares of elements 6t..6t+5
+  in order; wave butterfly; then (w0+w1)+(w2+w3).  r = 1/sqrt(sum/n + 1e-6).
 * q/k norm (`qkv`, Kernels.metal:236-246): 16 lanes x 8 elements (the RoPE pairs d, d+64
   of 4 consecutive d), 16-lane butterfly.
 * decode attention (Kernels.metal:440-562 split form): 64-key partitions; score = four
@@ -113,11 +113,12 @@ def gemv_numpy(w, x):
 
 
 def block_sumsq(v):
-    """256-thread sum of squares of a 1536 vector: per-thread order, wave butterfly, waves."""
-    t = v.astype(F).reshape(6, 256)
+    """256-thread sum of squares of a 1536 vector: thread t sums the squares of elements
+    6t .. 6t+5 in order, then the wave butterfly, then (w0 + w1) + (w2 + w3)."""
+    t = v.astype(F).reshape(256, 6)
     ss = np.zeros(256, F)
     for k in range(6):
-        ss += t[k] * t[k]
+        ss += t[:, k] * t[:, k]
     w = butterfly(ss.reshape(4, 64))
     return F(F(w[0] + w[1]) + F(w[2] + w[3]))
 

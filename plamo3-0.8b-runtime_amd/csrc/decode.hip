@@ -23,6 +23,15 @@ using namespace dev;
 
 namespace {
 
+// Weight rows per wave group: four for one activation row; with four rows the
+// arithmetic per weight byte quadruples, so groups shrink to spread it over more waves.
+template <int N, int MAXR, int EPI>
+constexpr int gemv_u() {
+    if constexpr (EPI == EPI_SWIGLU) return MAXR == 1 ? 4 : 2;
+    else if constexpr (N >= 6144) return MAXR == 1 ? 2 : 1;
+    else return MAXR == 1 ? 4 : 2;
+}
+
 // ---------------------------------------------------------------------------- prologues
 // Stage the BF16 activation rows into LDS.  Values are BF16-exact FP32 (every producer
 // rounds), so the BF16 copy is lossless.  The prologue is split into its loads
@@ -32,50 +41,60 @@ namespace {
 template <int N, int MAXR, int PRO>
 struct Staged {
     static constexpr int V = (N + 1023) / 1024;  // PLAIN: float4 per thread and row
-    static constexpr int E = HIDDEN / 256;       // norm prologues: elements per thread
+    static constexpr int E = HIDDEN / 256;       // norm prologues: elements per thread (6t .. 6t+5)
     float4 v[PRO == PRO_PLAIN ? MAXR : 1][V];
-    float a[PRO == PRO_PLAIN ? 1 : MAXR][E];     // EMBED: embedding row; RESID: projection
-    float r[PRO == PRO_RESID ? MAXR : 1][E];     // RESID: residual stream
-    uint16_t gp[E], gn[E];
+    float2 a[PRO == PRO_RESID ? MAXR : 1][E / 2];   // RESID: projection output
+    float2 r[PRO == PRO_RESID ? MAXR : 1][E / 2];   // RESID: residual stream
+    uint32_t emb[PRO == PRO_EMBED ? MAXR : 1][E / 2];  // EMBED: embedding row (BF16 pairs)
+    uint32_t gp[E / 2], gn[E / 2];                 // norm weights (BF16 pairs)
 };
 
-// rb: rows whose inputs are read (every row the buffers hold when a step state is given)
+// Unconditional loads (rows past rb re-read row rb-1, columns past N re-read the last
+// four), kept raw: converting them here would make the compiler wait for each one.
+// rb: rows the input buffers hold.
 template <int N, int MAXR, int PRO>
 __device__ __forceinline__ void stage_load(const GemvParams& p, int rb, Staged<N, MAXR, PRO>& S) {
     const int tid = threadIdx.x;
     constexpr int V = Staged<N, MAXR, PRO>::V, E = Staged<N, MAXR, PRO>::E;
     if constexpr (PRO == PRO_PLAIN) {
 #pragma unroll
-        for (int q = 0; q < MAXR; ++q)
+        for (int q = 0; q < MAXR; ++q) {
+            const int qq = q < rb ? q : rb - 1;
 #pragma unroll
             for (int k = 0; k < V; ++k) {
                 const int e = (tid + 256 * k) * 4;
-                S.v[q][k] = (q < rb && e < N) ? *reinterpret_cast<const float4*>(p.in + q * N + e)
-                                               : make_float4(0.f, 0.f, 0.f, 0.f);
+                S.v[q][k] = *reinterpret_cast<const float4*>(p.in + qq * N + (e < N ? e : N - 4));
             }
+        }
     } else {
-        static_assert(N == HIDDEN, "norm prologue is 1536 wide");
+        static_assert(N == HIDDEN && E == 6, "norm prologue is 1536 wide");
+        const int e0 = tid * E;
+        const uint32_t* gn32 = reinterpret_cast<const uint32_t*>(p.g_next + e0);
 #pragma unroll
-        for (int k = 0; k < E; ++k) S.gn[k] = p.g_next[tid + 256 * k];
+        for (int k = 0; k < E / 2; ++k) S.gn[k] = gn32[k];
         if constexpr (PRO == PRO_EMBED) {
 #pragma unroll
             for (int q = 0; q < MAXR; ++q) {
-                int tok = (q < rb && p.state) ? p.state->token[q] : 0;
+                const int qq = q < rb ? q : rb - 1;
+                int tok = p.state->token[qq];  // the embedding prologue always runs with a step state
                 tok = (tok < 0 || tok >= VOCAB) ? 0 : tok;  // loop guards stop before this
+                const uint32_t* row = reinterpret_cast<const uint32_t*>(p.embed + size_t(tok) * HIDDEN + e0);
 #pragma unroll
-                for (int k = 0; k < E; ++k)
-                    S.a[q][k] = (q < rb) ? bf(p.embed[size_t(tok) * HIDDEN + tid + 256 * k]) : 0.f;
+                for (int k = 0; k < E / 2; ++k) S.emb[q][k] = row[k];
             }
         } else {
+            const uint32_t* gp32 = reinterpret_cast<const uint32_t*>(p.g_post + e0);
 #pragma unroll
-            for (int k = 0; k < E; ++k) S.gp[k] = p.g_post[tid + 256 * k];
+            for (int k = 0; k < E / 2; ++k) S.gp[k] = gp32[k];
 #pragma unroll
-            for (int q = 0; q < MAXR; ++q)
+            for (int q = 0; q < MAXR; ++q) {
+                const int qq = q < rb ? q : rb - 1;
 #pragma unroll
-                for (int k = 0; k < E; ++k) {
-                    S.a[q][k] = (q < rb) ? p.in[q * HIDDEN + tid + 256 * k] : 0.f;
-                    S.r[q][k] = (q < rb) ? p.resid_in[q * HIDDEN + tid + 256 * k] : 0.f;
+                for (int k = 0; k < E / 2; ++k) {
+                    S.a[q][k] = *reinterpret_cast<const float2*>(p.in + qq * HIDDEN + e0 + 2 * k);
+                    S.r[q][k] = *reinterpret_cast<const float2*>(p.resid_in + qq * HIDDEN + e0 + 2 * k);
                 }
+            }
         }
     }
 }
@@ -105,15 +124,33 @@ __device__ __forceinline__ void stage_finish(const GemvParams& p, int rows, cons
 #pragma unroll
             for (int q = 0; q < MAXR; ++q)
 #pragma unroll
-                for (int k = 0; k < E; ++k) xv[q][k] = (q < rows) ? S.a[q][k] : 0.f;
+                for (int k = 0; k < E / 2; ++k) {
+                    xv[q][2 * k] = (q < rows) ? lo(S.emb[q][k]) : 0.f;
+                    xv[q][2 * k + 1] = (q < rows) ? hi(S.emb[q][k]) : 0.f;
+                }
         } else {
             // z = roundbf(roundbf(p*r) * roundbf(bf(w)+offset)); x = roundbf(x + z)
             // (Kernels.metal:59-72, full == 1)
+            float pv[MAXR][E], rv[MAXR][E], gp[E];
+#pragma unroll
+            for (int k = 0; k < E / 2; ++k) {
+                gp[2 * k] = lo(S.gp[k]);
+                gp[2 * k + 1] = hi(S.gp[k]);
+            }
+#pragma unroll
+            for (int q = 0; q < MAXR; ++q)
+#pragma unroll
+                for (int k = 0; k < E / 2; ++k) {
+                    pv[q][2 * k] = S.a[q][k].x;
+                    pv[q][2 * k + 1] = S.a[q][k].y;
+                    rv[q][2 * k] = S.r[q][k].x;
+                    rv[q][2 * k + 1] = S.r[q][k].y;
+                }
 #pragma unroll
             for (int q = 0; q < MAXR; ++q) {
                 ss[q] = 0.f;
 #pragma unroll
-                for (int k = 0; k < E; ++k) ss[q] += S.a[q][k] * S.a[q][k];
+                for (int k = 0; k < E; ++k) ss[q] += pv[q][k] * pv[q][k];
             }
 #pragma unroll
             for (int q = 0; q < MAXR; ++q) {
@@ -127,9 +164,9 @@ __device__ __forceinline__ void stage_finish(const GemvParams& p, int rows, cons
                 const float r = 1.0f / sqrtf(total / float(HIDDEN) + 1e-6f);
 #pragma unroll
                 for (int k = 0; k < E; ++k) {
-                    const float g = roundbf(bf(S.gp[k]) + p.post_offset);
-                    const float z = roundbf(roundbf(S.a[q][k] * r) * g);
-                    xv[q][k] = (q < rows) ? roundbf(S.r[q][k] + z) : 0.f;
+                    const float g = roundbf(gp[k] + p.post_offset);
+                    const float z = roundbf(roundbf(pv[q][k] * r) * g);
+                    xv[q][k] = (q < rows) ? roundbf(rv[q][k] + z) : 0.f;
                 }
             }
             __syncthreads();
@@ -137,7 +174,10 @@ __device__ __forceinline__ void stage_finish(const GemvParams& p, int rows, cons
         // next norm with +1 offset (Kernels.metal:76-89)
         float gn[E];
 #pragma unroll
-        for (int k = 0; k < E; ++k) gn[k] = roundbf(bf(S.gn[k]) + 1.0f);
+        for (int k = 0; k < E / 2; ++k) {
+            gn[2 * k] = roundbf(lo(S.gn[k]) + 1.0f);
+            gn[2 * k + 1] = roundbf(hi(S.gn[k]) + 1.0f);
+        }
 #pragma unroll
         for (int q = 0; q < MAXR; ++q) {
             ss[q] = 0.f;
@@ -154,7 +194,7 @@ __device__ __forceinline__ void stage_finish(const GemvParams& p, int rows, cons
             const float r = 1.0f / sqrtf(total / float(HIDDEN) + 1e-6f);
 #pragma unroll
             for (int k = 0; k < E; ++k) {
-                const int i = tid + 256 * k;
+                const int i = tid * E + k;
                 const float xn = roundbf(roundbf(xv[q][k] * r) * gn[k]);
                 xs[q * HIDDEN + i] = uint16_t(bits(xn));
                 if (blockIdx.x == 0) {
@@ -170,21 +210,59 @@ __device__ __forceinline__ void stage_finish(const GemvParams& p, int rows, cons
 // Lane `lane` owns columns it*512 + lane*8 .. +8 of a row: inside .p12 block it*4+lane/16
 // at offset (lane%16)*8.  Plain and packed therefore feed identical words to dot8, so
 // packed results are bit-identical to plain ones.
-template <int N, bool PACKED>
-__device__ __forceinline__ uint4 load_w(const GemvParams& p, int row, int it, int lane) {
+// A lane's weight words as requested, decoded only when used (decoding at request time
+// would make the compiler wait for each load).  .p12: a 128-weight block is 256 raw bytes
+// (tag 0) or 128 sign/mantissa bytes + 64 exponent-nibble bytes; three branch-free loads
+// cover both layouts and stay inside the block.
+template <bool PACKED>
+struct WRaw {
+    uint4 v;
+};
+template <>
+struct WRaw<true> {
+    uint4 v;            // raw: 8 weights; packed: .x/.y = 8 sign/mantissa bytes
+    uint32_t nib, tag;  // packed: 8 exponent codes, block minimum - 107 (0: raw block)
+};
+
+// Requests for U rows x IT column steps: every .p12 table entry first, then the payload.
+template <int N, bool PACKED, int U, int IT>
+__device__ __forceinline__ void request_w(const GemvParams& p, const int (&wrow)[U], int lane,
+                                          WRaw<PACKED> (&r)[U][IT]) {
     if constexpr (!PACKED) {
-        const uint16_t* src = p.w + size_t(row) * N + it * 512 + lane * 8;
-        return *reinterpret_cast<const uint4*>(src);
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int it = 0; it < IT; ++it)
+                r[u][it].v = *reinterpret_cast<const uint4*>(p.w + size_t(wrow[u]) * N + it * 512 + lane * 8);
     } else {
-        const uint32_t entry = p.table[size_t(row) * (N / 128) + it * 4 + (lane >> 4)];
-        const uint8_t* blk = reinterpret_cast<const uint8_t*>(p.w) + (entry & ~63u);
-        const uint32_t tag = entry & 63u;
+        uint32_t e[U][IT];
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int it = 0; it < IT; ++it) e[u][it] = p.table[size_t(wrow[u]) * (N / 128) + it * 4 + (lane >> 4)];
         const int sub = lane & 15;
-        if (tag == 0) return *reinterpret_cast<const uint4*>(blk + sub * 16);
-        const uint2 sm = *reinterpret_cast<const uint2*>(blk + sub * 8);
-        const uint32_t nib = *reinterpret_cast<const uint32_t*>(blk + 128 + sub * 4);
-        return p12_decode8(sm, nib, tag);
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int it = 0; it < IT; ++it) {
+                const uint8_t* blk = reinterpret_cast<const uint8_t*>(p.w) + (e[u][it] & ~63u);
+                const uint32_t tag = e[u][it] & 63u;
+                const uint2 lo8 = *reinterpret_cast<const uint2*>(blk + (tag ? sub * 8 : sub * 16));
+                const uint2 hi8 = *reinterpret_cast<const uint2*>(blk + (tag ? 0 : sub * 16 + 8));
+                r[u][it].v = make_uint4(lo8.x, lo8.y, hi8.x, hi8.y);
+                r[u][it].nib = *reinterpret_cast<const uint32_t*>(blk + 128 + sub * 4);
+                r[u][it].tag = tag;
+            }
     }
+}
+
+// Lane `lane` owns columns it*512 + lane*8 .. +8 of a row: inside .p12 block it*4+lane/16
+// at offset (lane%16)*8.  Plain and packed therefore feed identical words to dot8, so
+// packed results are bit-identical to plain ones.
+template <bool PACKED>
+__device__ __forceinline__ uint4 decode_w(const WRaw<PACKED>& r) {
+    if constexpr (!PACKED) return r.v;
+    else return r.tag ? p12_decode8(make_uint2(r.v.x, r.v.y), r.nib, r.tag) : r.v;
 }
 
 __device__ __forceinline__ bool better(float v, uint32_t i, float bv, uint32_t bi) {
@@ -228,10 +306,11 @@ __device__ __forceinline__ float sampled(float l, int32_t count, bool banned, co
 }
 
 // ------------------------------------------------------------------------------- GEMV
-template <int N, bool PACKED, int MAXR, int PRO, int EPI>
+template <int N, bool PACKED, int MAXR, int PRO, int EPI, bool STATE>
 __global__ __launch_bounds__(256) void gemv_kernel(const GemvParams p) {
     constexpr int IT = N / 512;
-    constexpr int U = (EPI == EPI_SWIGLU) ? 4 : (N >= 6144 ? 2 : 4);
+    constexpr int U = gemv_u<N, MAXR, EPI>();
+    constexpr int H = U / 2;  // SwiGLU: gate rows (and up rows) per group
     __shared__ __align__(16) uint16_t xs[MAXR * N];
     __shared__ float red[MAXR * 4];
     __shared__ float cand_v[MAXR * 4];
@@ -239,10 +318,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvParams p) {
 
     const StepState* st = p.state;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int groups = (EPI == EPI_SWIGLU) ? p.m / 4 : p.m / U;
-    // Request order = consumption order: step state, prologue inputs, first weights.
+    const int groups = p.m / U;
+    // Request order = consumption order: prologue inputs, first weights, step state.
     uint32_t stopped = 0, srows = 0;
-    if (st) { stopped = st->stopped; srows = st->rows; }
     Staged<N, MAXR, PRO> S;
     stage_load<N, MAXR, PRO>(p, p.rows < MAXR ? p.rows : MAXR, S);
     float best_v[MAXR];
@@ -253,7 +331,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvParams p) {
     auto rows_of = [&](int g, int (&wrow)[U]) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            if constexpr (EPI == EPI_SWIGLU) wrow[u] = (u < 2) ? 2 * g + u : INTER + 2 * g + (u - 2);
+            if constexpr (EPI == EPI_SWIGLU) wrow[u] = (u < H) ? H * g + u : INTER + H * g + (u - H);
             else wrow[u] = g * U + u;
         }
     };
@@ -262,36 +340,41 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvParams p) {
     // depend on the previous kernel, so they are requested before the activation prologue.
     const int stride = gridDim.x * 4;
     int g = blockIdx.x * 4 + wave;
-    uint4 w[U][IT];
+    WRaw<PACKED> wr[U][IT];
     if (g < groups) {
         int wrow[U];
         rows_of(g, wrow);
-#pragma unroll
-        for (int u = 0; u < U; ++u)
-#pragma unroll
-            for (int it = 0; it < IT; ++it) w[u][it] = load_w<N, PACKED>(p, wrow[u], it, lane);
+        request_w<N, PACKED, U, IT>(p, wrow, lane, wr);
+    }
+    // The step state is requested only now: waiting for it must not hold back the
+    // requests above (the scheduler may not hoist it across this point).
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (STATE) {
+        stopped = st->stopped;
+        srows = st->rows;
     }
     if (stopped) return;
-    int rows = p.rows;  // (a select of two addresses would put the argument in scratch)
-    if (st) rows = int(srows);
+    int rows = p.rows;
+    if constexpr (STATE) rows = int(srows);
     Controls ctl{false, 0, 1.0f, 0.0f, 0.0f};
-    if constexpr (EPI == EPI_LOGITS) {
-        if (st && st->sampling) ctl = Controls{true, st->ngram, st->penalty, st->frequency, st->presence};
+    if constexpr (EPI == EPI_LOGITS && STATE) {
+        if (st->sampling) ctl = Controls{true, st->ngram, st->penalty, st->frequency, st->presence};
     }
     stage_finish<N, MAXR, PRO>(p, rows, S, xs, red);
     __syncthreads();
     for (; g < groups; g += stride) {
         int wrow[U];
         rows_of(g, wrow);
-        uint4 wn[U][IT];
+        uint4 w[U][IT];
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int it = 0; it < IT; ++it) w[u][it] = decode_w<PACKED>(wr[u][it]);
         const int gn = g + stride;
         if (gn < groups) {
             int nrow[U];
             rows_of(gn, nrow);
-#pragma unroll
-            for (int u = 0; u < U; ++u)
-#pragma unroll
-                for (int it = 0; it < IT; ++it) wn[u][it] = load_w<N, PACKED>(p, nrow[u], it, lane);
+            request_w<N, PACKED, U, IT>(p, nrow, lane, wr);
         }
         float acc[U][MAXR];
 #pragma unroll
@@ -336,10 +419,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvParams p) {
                 for (int q = 0; q < MAXR; ++q)
                     if (q < rows)
 #pragma unroll
-                        for (int k = 0; k < 2; ++k) {
+                        for (int k = 0; k < H; ++k) {
                             const float gt = roundbf(acc[k][q]);
-                            const float up = roundbf(acc[2 + k][q]);
-                            p.out[size_t(q) * INTER + 2 * g + k] = roundbf(roundbf(gt / (1.0f + exp_det(-gt))) * up);
+                            const float up = roundbf(acc[H + k][q]);
+                            p.out[size_t(q) * INTER + H * g + k] = roundbf(roundbf(gt / (1.0f + exp_det(-gt))) * up);
                         }
         } else {  // EPI_LOGITS
 #pragma unroll
@@ -360,12 +443,6 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvParams p) {
                     if (better(v, uint32_t(wrow[u]), best_v[q], best_i[q])) { best_v[q] = v; best_i[q] = wrow[u]; }
                 }
             }
-        }
-        if (gn < groups) {
-#pragma unroll
-            for (int u = 0; u < U; ++u)
-#pragma unroll
-                for (int it = 0; it < IT; ++it) w[u][it] = wn[u][it];
         }
     }
 
@@ -883,10 +960,17 @@ __global__ void fill_u32_kernel(uint32_t* p, uint32_t v, size_t n) {
 template <int N, bool PACKED, int MAXR>
 void gemv_dispatch_epi(Prologue pro, Epilogue epi, const GemvParams& p, int blocks, hipStream_t s) {
     const dim3 grid(blocks), block(256);
-#define PLAMO_GEMV(PRO, EPI) hipLaunchKernelGGL((gemv_kernel<N, PACKED, MAXR, PRO, EPI>), grid, block, 0, s, p)
+#define PLAMO_GEMV(PRO, EPI) hipLaunchKernelGGL((gemv_kernel<N, PACKED, MAXR, PRO, EPI, true>), grid, block, 0, s, p)
+#define PLAMO_GEMV_NOSTATE(PRO, EPI) \
+    hipLaunchKernelGGL((gemv_kernel<N, PACKED, MAXR, PRO, EPI, false>), grid, block, 0, s, p)
+    if (!p.state) {  // kernel-level entry points: plain rows, no step state
+        if (pro == PRO_PLAIN && epi == EPI_ROUND) PLAMO_GEMV_NOSTATE(PRO_PLAIN, EPI_ROUND);
+        else if (pro == PRO_PLAIN && epi == EPI_BF16) PLAMO_GEMV_NOSTATE(PRO_PLAIN, EPI_BF16);
+        else throw Error(E_INVAL, "unsupported GEMV variant");
+        return;
+    }
     if (pro == PRO_PLAIN) {
         if (epi == EPI_ROUND) PLAMO_GEMV(PRO_PLAIN, EPI_ROUND);
-        else if (epi == EPI_BF16) PLAMO_GEMV(PRO_PLAIN, EPI_BF16);
         else throw Error(E_INVAL, "unsupported GEMV variant");
         return;
     }
@@ -901,6 +985,7 @@ void gemv_dispatch_epi(Prologue pro, Epilogue epi, const GemvParams& p, int bloc
         throw Error(E_INVAL, "unsupported GEMV variant");
     }
 #undef PLAMO_GEMV
+#undef PLAMO_GEMV_NOSTATE
 }
 
 template <int N>
@@ -916,6 +1001,17 @@ void gemv_dispatch_n(bool packed, int maxr, Prologue pro, Epilogue epi, const Ge
 }
 
 }  // namespace
+
+int gemv_group_rows(int n, int maxr, Epilogue epi) {
+    if (epi == EPI_SWIGLU) return maxr == 1 ? 4 : 2;
+    if (n >= 6144) return maxr == 1 ? 2 : 1;
+    return maxr == 1 ? 4 : 2;
+}
+
+int gemv_blocks(int n, int maxr, Epilogue epi, int m) {
+    const int groups = m / gemv_group_rows(n, maxr, epi);
+    return (groups + 3) / 4;  // one group per wave
+}
 
 void launch_gemv(int n, bool packed, int maxr, Prologue pro, Epilogue epi, const GemvParams& p, int blocks,
                  hipStream_t s) {

@@ -88,6 +88,8 @@ struct AttnParams {
 };
 
 // decode.hip
+int gemv_group_rows(int n, int maxr, Epilogue epi);     // weight rows per wave group
+int gemv_blocks(int n, int maxr, Epilogue epi, int m);  // workgroups for one group per wave
 void launch_gemv(int n, bool packed, int maxr, Prologue pro, Epilogue epi, const GemvParams& p, int blocks,
                  hipStream_t s);
 void launch_attention(bool full, const AttnParams& p, int rows, hipStream_t s);

@@ -332,13 +332,13 @@ void Engine::enqueue_step(bool head) {
         g.out = qkv;
         if (l == 0) {
             g.embed = m.embed;
-            launch_gemv(HIDDEN, pk, maxr, PRO_EMBED, EPI_ROUND, g, QKV / 16, stream);
+            launch_gemv(HIDDEN, pk, maxr, PRO_EMBED, EPI_ROUND, g, gemv_blocks(HIDDEN, maxr, EPI_ROUND, QKV), stream);
         } else {
             g.in = proj;
             g.resid_in = x1;
             g.g_post = m.layers[l - 1].post_mlp;
             g.post_offset = post_mlp_offset();
-            launch_gemv(HIDDEN, pk, maxr, PRO_RESID, EPI_ROUND, g, QKV / 16, stream);
+            launch_gemv(HIDDEN, pk, maxr, PRO_RESID, EPI_ROUND, g, gemv_blocks(HIDDEN, maxr, EPI_ROUND, QKV), stream);
         }
         AttnParams a{};
         a.state = state;
@@ -365,7 +365,7 @@ void Engine::enqueue_step(bool head) {
         o.table = L.o.table;
         o.in = att;
         o.out = proj;
-        launch_gemv(ATTN, pk, maxr, PRO_PLAIN, EPI_ROUND, o, HIDDEN / 16, stream);
+        launch_gemv(ATTN, pk, maxr, PRO_PLAIN, EPI_ROUND, o, gemv_blocks(ATTN, maxr, EPI_ROUND, HIDDEN), stream);
         GemvParams u{};
         u.state = state;
         u.rows = ROWS;
@@ -379,7 +379,7 @@ void Engine::enqueue_step(bool head) {
         u.post_offset = POST_MIXER_OFFSET;
         u.g_next = L.pre_mlp;
         u.out = act;
-        launch_gemv(HIDDEN, pk, maxr, PRO_RESID, EPI_SWIGLU, u, 2 * INTER / 16, stream);
+        launch_gemv(HIDDEN, pk, maxr, PRO_RESID, EPI_SWIGLU, u, gemv_blocks(HIDDEN, maxr, EPI_SWIGLU, 2 * INTER), stream);
         GemvParams d{};
         d.state = state;
         d.rows = ROWS;
@@ -388,7 +388,7 @@ void Engine::enqueue_step(bool head) {
         d.table = L.down.table;
         d.in = act;
         d.out = proj;
-        launch_gemv(INTER, pk, maxr, PRO_PLAIN, EPI_ROUND, d, HIDDEN / 8, stream);
+        launch_gemv(INTER, pk, maxr, PRO_PLAIN, EPI_ROUND, d, gemv_blocks(INTER, maxr, EPI_ROUND, HIDDEN), stream);
     }
     if (head) enqueue_head(proj, x1, ROWS);
 }
