@@ -1,0 +1,128 @@
+"""Long context (config 5) and wrapped rings (config 4) on the GPU.
+
+Config 5: a 30,720-token prompt prefilled from the .p12 weights (15 MFMA chunks of 2048),
+then decode with the sampling controls at positions 30,720 and up.  The GPU KV cache after
+the prefill is handed to the order-exact CPU decoder (oracle/exact.py), and every following
+decode step must match it bit for bit: logits, final hidden state, the new KV rows and the
+controlled selection (Sampler.select over the generated history, Main.swift:237-244).  This
+covers the ring wrap of the 14 local layers, global attention over ~30K keys in 480
+partitions and the split-K merge at that size; the MFMA prefill itself is covered by the
+noise-floor tests.
+
+Config 4 (same shape, shorter decode): four segments with 512/384/256/128-token prompts
+decode in one batch until the longest attends over a full 2048-key window that no longer
+starts at position 0, bit-identical to scalar decode of each segment (Batch.swift:109-180
+keeps lanes independent).  (The ring wrap itself is exercised by the config-5 test: this
+build's local ring holds 2048 + one 2048-token prefill chunk.)
+"""
+import time
+
+import numpy as np
+import pytest
+
+import plamo_hip
+from oracle import exact, sampler
+from oracle.bf16 import bf_np
+
+pytestmark = pytest.mark.gpu
+
+PENALTY, FREQUENCY, NGRAM = 1.1, 0.2, 4
+
+
+@pytest.fixture(scope="module")
+def long_runtime(model_dir):
+    d, sha = model_dir
+    rt = plamo_hip.Runtime(d, 32768, packed=True, source_sha256=sha)
+    yield rt
+    rt.close()
+
+
+def long_prompt():
+    return np.random.default_rng(5).integers(1024, 107520, 30720).tolist()
+
+
+def test_long_context_decode_bit_exact(long_runtime, oracle_weights):
+    rt = long_runtime
+    rt.reset()
+    rt.set_sampling(PENALTY, FREQUENCY, 0.0, NGRAM)
+    try:
+        t0 = time.time()
+        nxt = rt.prefill(long_prompt())
+        print(f"  prefill 30720 tokens (.p12): {time.time() - t0:.2f} s", flush=True)
+        ex = exact.ExactDecoder(oracle_weights, 32768, rt.stats()["local_capacity"])
+        for layer in range(16):
+            k, v = rt.kv(layer)
+            ex.keys[layer][:] = k
+            ex.values[layer][:] = v
+        generated, pos, t = [], 30720, nxt
+        for step in range(6):
+            generated.append(t)
+            rt.observe(t)
+            got = rt.forward([t])
+            bits, hidden, _ = ex.step(t, pos)
+            assert np.array_equal(rt.logit_bits(), bits), step
+            assert np.array_equal(rt.hidden().view(np.uint32), hidden.view(np.uint32)), step
+            assert got == sampler.select(bf_np(bits).copy(), generated, PENALTY, NGRAM, FREQUENCY), step
+            print(f"  position {pos}: bit-exact, token {got}", flush=True)
+            t, pos = got, pos + 1
+        for layer in range(16):
+            k, v = rt.kv(layer)
+            cap = k.shape[0]
+            slots = [p % cap for p in range(30720, pos)]
+            assert np.array_equal(k[slots], ex.keys[layer][slots]), layer
+            assert np.array_equal(v[slots], ex.values[layer][slots]), layer
+    finally:
+        rt.set_sampling()
+
+
+def test_long_context_device_loop_matches_host_loop(long_runtime):
+    rt = long_runtime
+    rt.set_sampling(PENALTY, FREQUENCY, 0.0, NGRAM)
+    try:
+        rt.reset()
+        ids, _ = rt.generate(long_prompt(), 12)
+        rt.reset()
+        nxt = rt.prefill(long_prompt())
+        host = []
+        for i in range(12):
+            if nxt in (1, 16):
+                break
+            host.append(nxt)
+            rt.observe(nxt)
+            if i + 1 < 12:
+                nxt = rt.forward([nxt])
+    finally:
+        rt.set_sampling()
+    assert ids == host
+
+
+def test_batch_segments_cross_the_window(model_dir):
+    d, _ = model_dir
+    lengths = [512, 384, 256, 128]
+    steps = 2048 + 40 - 512
+    rng = np.random.default_rng(11)
+    prompts = [rng.integers(1024, 107520, n).tolist() for n in lengths]
+    rt = plamo_hip.Runtime(d, 2200)
+    b = plamo_hip.Batch(rt)
+    try:
+        tokens = b.prefill(prompts)
+        for _ in range(steps):
+            tokens = b.step(tokens)
+        print(f"  batch decoded {steps} steps, positions {b.positions()}", flush=True)
+        for lane, p in enumerate(prompts):
+            rt.reset()
+            nxt = rt.prefill(p)
+            for _ in range(steps):
+                nxt = rt.forward([nxt])
+            assert tokens[lane] == nxt, lane
+            assert np.array_equal(b.logit_bits(lane), rt.logit_bits()), lane
+            assert np.array_equal(b.hidden(lane).view(np.uint32), rt.hidden().view(np.uint32)), lane
+            n = len(p) + steps
+            for layer in (0, 7):
+                kb, vb = b.kv(lane, layer)
+                ks, vs = rt.kv(layer)
+                assert np.array_equal(kb[:n], ks[:n]) and np.array_equal(vb[:n], vs[:n]), (lane, layer)
+            print(f"  lane {lane} (prompt {len(p)}): batch == scalar", flush=True)
+    finally:
+        b.close()
+        rt.close()
