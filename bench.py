@@ -1,16 +1,24 @@
 """Benchmark of the PLaMo-3 0.8B token loop on one MI355X.
 
 Headline (the JSON line's `value`): batch-1 greedy decode tokens/s of the full 16-layer model
-with plain BF16 weights (BASELINE.json configs[0] shape, random-init weights, synthetic prompt),
-each step one replay of the captured decode graph with the next token fed back on the device.
-Extra fields: packed (.p12) decode, batch4 aggregate decode, 2048-token prefill with MFMA
-utilisation, the per-projection GEMV microbenchmark and the CPU oracle baseline.
+with plain BF16 weights (BASELINE.json metric "decode tok/s @bs1 ... % HBM roofline"; the
+configs[0] model shape, random-init weights, synthetic 64-token prompt), each step one replay
+of the captured decode graph with the next token fed back on the device, timed with HIP
+events on the runtime's stream.  Extra fields cover the rest of the metric and the other
+configs: .p12 decode; configs[1] GEMV shapes (plain and .p12, weights cycled through more
+copies than the 256 MB memory-side cache holds); configs[2] 2048-token prefill with MFMA
+utilisation; configs[3] batch4 segments (512/384/256/128-token prompts, up to 2048 tokens
+each, stop on EOS) against batch-1 on the same segment; configs[4] .p12 long context
+(30,720-token prefill, then sampled decode to the 32,768 cap); the CPU oracle baseline.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu]
+    python bench.py --kernels-only     # GEMV shapes + copy calibration (for rocprofv3 --pmc)
+    python bench.py --prefill-only     # three 2048-token prefills (for rocprofv3 kernel traces)
 """
 import argparse
 import json
 import os
+import re
 import sys
 import time
 
@@ -21,6 +29,8 @@ HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 SHAPES = {"qkv": (2304, 1536), "o": (1536, 2048), "gate_up": (12288, 1536), "down": (1536, 6144),
           "head": (107520, 1536)}
+DOMINANT = "gate_up"  # largest share of the decode step's kernel time (profiles/)
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemv_gate_up_hbm_traffic.md")
 
 
 def log(*a):
@@ -32,10 +42,11 @@ def kv_read_bytes(pos):
     return 512 * (14 * min(pos + 1, 2048) + 2 * (pos + 1))
 
 
-def gemv_microbench(torch, native, repeats=50):
-    """each projection shape, plain and .p12, timed with HIP events on the stream."""
+def gemv_microbench(torch, native, repeats=48):
+    """each projection shape, plain and .p12, one activation row, HIP events on
+    the launch stream.  Each shape cycles through enough copies of its weights (> 512 MB) that
+    every launch streams from HBM, as in the decode step."""
     import numpy as np
-    from plamo_hip import synth  # noqa: F401  (same package, ensures path)
     lib = native.load()
     out = {}
     rng = np.random.default_rng(0)
@@ -45,28 +56,58 @@ def gemv_microbench(torch, native, repeats=50):
         u = w.view(np.uint32)
         bits = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
         payload, entries = native.pack_tensor(bits)
+        copies = max(2, -(-512 * 2 ** 20 // bits.nbytes))
         x = torch.randn(n, device="cuda").to(torch.bfloat16).float()
         wd = torch.from_numpy(bits.view(np.int16)).cuda()
         pd = torch.from_numpy(payload).cuda()
         td = torch.from_numpy(entries.view(np.int32)).cuda()
+        wds = [wd] + [wd.clone() for _ in range(copies - 1)]
+        pds = [(pd, td)] + [(pd.clone(), td.clone()) for _ in range(copies - 1)]
         mode = 2 if name == "head" else 0
         y = torch.empty(m, dtype=torch.float32, device="cuda")
-        res = {}
-        for kind, wp, tp, nbytes in (("plain", wd.data_ptr(), 0, m * n * 2),
-                                     ("p12", pd.data_ptr(), td.data_ptr(), payload.nbytes + entries.nbytes)):
-            for _ in range(5):
-                lib.plamo_kernel_linear(wp, tp, x.data_ptr(), y.data_ptr(), n, m, 1, mode, stream.cuda_stream)
+        res = {"copies": copies}
+        for kind, nbytes in (("plain", m * n * 2), ("p12", payload.nbytes + entries.nbytes)):
+            def launch(i):
+                if kind == "plain":
+                    wp, tp = wds[i % copies].data_ptr(), 0
+                else:
+                    wp, tp = pds[i % copies][0].data_ptr(), pds[i % copies][1].data_ptr()
+                rc = lib.plamo_kernel_linear(wp, tp, x.data_ptr(), y.data_ptr(), n, m, 1, mode, stream.cuda_stream)
+                assert rc == 0
+            for i in range(2 * copies):
+                launch(i)
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record(stream)
-            for _ in range(repeats):
-                lib.plamo_kernel_linear(wp, tp, x.data_ptr(), y.data_ptr(), n, m, 1, mode, stream.cuda_stream)
+            for i in range(repeats):
+                launch(i)
             e1.record(stream)
             e1.synchronize()
             us = e0.elapsed_time(e1) * 1000.0 / repeats
             res[kind] = {"us": round(us, 2), "bytes": int(nbytes), "GBps": round(nbytes / us / 1e3, 1),
                          "hbm_frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 3)}
         out[name] = res
+        del wds, pds
     return out
+
+
+def copy_calibration(torch):
+    """A plain device copy of known size, for scaling the profiler's FETCH/WRITE_SIZE counters."""
+    a = torch.empty(64 * 2 ** 20, dtype=torch.int32, device="cuda").fill_(1)
+    b = torch.empty_like(a)
+    for _ in range(4):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    return {"bytes": a.numel() * 4, "launches": 4}
+
+
+def traffic_from_profile():
+    """HBM bytes per launch of the dominant GEMV, from the committed rocprofv3 --pmc summary."""
+    try:
+        with open(TRAFFIC_PROFILE) as f:
+            m = re.search(r"traffic_bytes_per_launch:\s*([0-9]+)", f.read())
+        return int(m.group(1)) if m else None
+    except OSError:
+        return None
 
 
 def cpu_baseline(model_dir, prompt, decode_tokens):
@@ -88,6 +129,58 @@ def cpu_baseline(model_dir, prompt, decode_tokens):
                       f"{decode_tokens} batch-1 decode steps of the full model"}
 
 
+def bench_batch4(plamo_hip, np, model_dir):
+    """four segments, prompts of 512/384/256/128 random tokens, each decoding up to
+    2048 tokens (stop on EOS ids 1 / 16), one weight pass per step for all active lanes."""
+    lengths, limit = (512, 384, 256, 128), 2048
+    prompts = [np.random.default_rng(20 + i).integers(1024, 107520, n).tolist() for i, n in enumerate(lengths)]
+    rt = plamo_hip.Runtime(model_dir, 512 + limit + 8)
+    b = plamo_hip.Batch(rt)
+    b.generate([p[:16] for p in prompts], [8] * 4)  # warm-up (graph capture)
+    b.reset()
+    t0 = time.perf_counter()
+    outs = b.generate(prompts, [limit] * 4)
+    dt = time.perf_counter() - t0
+    produced = sum(len(ids) for ids, _ in outs)
+    # batch 1 on segment 0 with the same device loop, same limit
+    rt.reset()
+    rt.generate(prompts[0][:16], 8)
+    rt.reset()
+    t0 = time.perf_counter()
+    ids1, _ = rt.generate(prompts[0], limit)
+    dt1 = time.perf_counter() - t0
+    b.close()
+    rt.close()
+    res = {"segments": [len(ids) for ids, _ in outs], "reasons": [r for _, r in outs], "tokens": produced,
+           "s": round(dt, 4), "aggregate_tok_s": round(produced / dt, 1),
+           "bs1_same_segment_tok_s": round(len(ids1) / dt1, 1), "bs1_tokens": len(ids1)}
+    res["ratio_vs_bs1"] = round(res["aggregate_tok_s"] / res["bs1_same_segment_tok_s"], 3)
+    return res
+
+
+def bench_long(plamo_hip, np, model_dir, sha):
+    """.p12 weights, 30,720-token prefill, then sampled decode (repetition 1.1,
+    frequency 0.2, no-repeat-ngram 4, on the GPU) to the 32,768-token cap."""
+    rt = plamo_hip.Runtime(model_dir, 32768, packed=True, source_sha256=sha)
+    prompt = np.random.default_rng(5).integers(1024, 107520, 30720).tolist()
+    rt.prefill(prompt[:2048])  # warm-up
+    rt.reset()
+    t0 = time.perf_counter()
+    rt.prefill(prompt)
+    t_pre = time.perf_counter() - t0
+    rt.reset()
+    rt.set_sampling(1.1, 0.2, 0.0, 4)
+    t0 = time.perf_counter()
+    ids, reason = rt.generate(prompt, 32768 - 30720)
+    t_all = time.perf_counter() - t0
+    rt.set_sampling()
+    rt.close()
+    t_dec = max(t_all - t_pre, 1e-9)
+    return {"prefill_tokens": 30720, "prefill_s": round(t_pre, 4), "prefill_tok_s": round(30720 / t_pre, 1),
+            "decode_tokens": len(ids), "stop": reason, "decode_s": round(t_dec, 4),
+            "decode_tok_s": round(len(ids) / t_dec, 1)}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -95,6 +188,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--quick", action="store_true", help="skip the secondary measurements")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--kernels-only", action="store_true", help="GEMV shapes and a copy calibration only")
+    ap.add_argument("--prefill-only", action="store_true", help="three 2048-token prefills only")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one MI355X; multi-GPU runs are not part of it",
@@ -106,13 +201,29 @@ def main():
     from plamo_hip import native, synth
 
     native.load()
+    if args.kernels_only:
+        gemv = gemv_microbench(torch, native)
+        cal = copy_calibration(torch)
+        print(json.dumps({"gemv": gemv, "copy_calibration": cal}), flush=True)
+        return
     log("model: generating/packing synthetic seed-0 weights")
     model_dir, sha = synth.ensure_model(packed=True)
+    if args.prefill_only:
+        rt = plamo_hip.Runtime(model_dir, 2048 + 64)
+        p2 = np.random.default_rng(3).integers(1024, 107520, 2048).tolist()
+        for _ in range(3):
+            rt.reset()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            rt.prefill(p2)
+            log(f"prefill 2048: {(time.perf_counter() - t0) * 1e3:.2f} ms")
+        rt.close()
+        return
     prompt = np.random.default_rng(1).integers(1024, 107520, 64).tolist()
     ctx = 64 + args.warmup + args.steps + 8
     results = {}
 
-    # --- batch-1 decode, plain and packed
+    # --- batch-1 decode, plain and packed (the headline)
     for packed in (False, True):
         rt = plamo_hip.Runtime(model_dir, ctx, packed=packed, source_sha256=sha)
         rt.prefill(prompt)
@@ -122,6 +233,7 @@ def main():
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         ms = rt.bench_decode(args.steps)
+        torch.cuda.synchronize()
         wall = time.perf_counter() - t0
         st = rt.stats()
         mid = start_pos + args.steps // 2
@@ -133,39 +245,12 @@ def main():
         log(f"decode {'p12' if packed else 'bf16'}: {ms:.3f} ms/step {1000 / ms:.1f} tok/s")
         rt.close()
 
-    # --- batch4 aggregate (4 lanes, one weight pass per step)
     if not args.quick:
-        rt = plamo_hip.Runtime(model_dir, 64 + 128 + 8)
-        b = plamo_hip.Batch(rt)
-        prompts = [np.random.default_rng(10 + i).integers(1024, 107520, n).tolist() for i, n in
-                   enumerate((64, 48, 32, 16))]
-        toks = b.prefill(prompts)
-        for _ in range(4):
-            toks = b.step(toks)
-        torch.cuda.synchronize()
-        n = 100
-        t0 = time.perf_counter()
-        for _ in range(n):
-            toks = b.step(toks)
-        dt = time.perf_counter() - t0
-        results["batch4"] = {"steps": n, "ms_per_step": dt * 1000 / n, "aggregate_tok_s": 4 * n / dt}
-        # the same host-driven loop at batch 1 for a like-for-like ratio
-        rt.reset()
-        t = rt.prefill(prompts[0])
-        for _ in range(4):
-            t = rt.forward([t])
-        t0 = time.perf_counter()
-        for _ in range(n):
-            t = rt.forward([t])
-        dt1 = time.perf_counter() - t0
-        results["batch4"]["host_loop_bs1_tok_s"] = n / dt1
-        results["batch4"]["ratio_vs_bs1_host_loop"] = results["batch4"]["aggregate_tok_s"] / (n / dt1)
+        results["batch4"] = bench_batch4(plamo_hip, np, model_dir)
         log(f"batch4: {results['batch4']}")
-        b.close()
-        rt.close()
-
-    # --- prefill of 2048 tokens
-    if not args.quick:
+        results["long_context"] = bench_long(plamo_hip, np, model_dir, sha)
+        log(f"long_context: {results['long_context']}")
+        # --- prefill of 2048 tokens
         rt = plamo_hip.Runtime(model_dir, 2048 + 64)
         p2 = np.random.default_rng(3).integers(1024, 107520, 2048).tolist()
         rt.prefill(p2)
@@ -175,7 +260,7 @@ def main():
         rt.prefill(p2)
         dt = time.perf_counter() - t0
         gemm_flop = 2 * 34996224 * 16 * 2048
-        attn_flop = 4 * 16 * 128 * sum(t + 1 for t in range(2048)) * 16
+        attn_flop = 4 * 16 * 128 * sum(min(t + 1, 2048) for t in range(2048)) * 16
         results["prefill2048"] = {"s": dt, "tok_s": 2048 / dt, "gemm_tflop": gemm_flop / 1e12,
                                   "attn_tflop": attn_flop / 1e12,
                                   "overall_TFLOPs": (gemm_flop + attn_flop) / dt / 1e12,
@@ -183,11 +268,11 @@ def main():
         log(f"prefill2048: {results['prefill2048']}")
         rt.close()
 
-    # --- GEMV microbenchmark; the dominant decode kernel's roofline
+    # --- GEMV shapes; the dominant decode kernel's roofline
     gemv = gemv_microbench(torch, native)
     results["gemv"] = gemv
     log(f"gemv: {json.dumps(gemv)}")
-    dom = gemv["gate_up"]["plain"]
+    dom = gemv[DOMINANT]["plain"]
 
     cpu = None
     if not args.no_cpu:
@@ -201,14 +286,15 @@ def main():
         "warmup": args.warmup, "ms_per_step": round(plain["ms_per_step"], 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "bf16 (fp32 accumulate)",
         "data": "synthetic: random-init N(0,0.02) BF16 weights (seed 0), uniform random 64-token prompt",
-        "config": {"workload": "configs[0]/[1]: batch-1 greedy decode of the PLaMo-3 0.8B-shaped model "
-                               "(hidden 1536, 16 layers, MQA 16x128, inter 6144, vocab 107520), "
+        "config": {"workload": "configs[0] model shape: batch-1 greedy decode of the PLaMo-3 0.8B-shaped "
+                               "model (hidden 1536, 16 layers, MQA 16x128, inter 6144, vocab 107520), "
                                f"64-token prompt then {args.steps} graph-replayed steps",
                    "global_batch": 1, "seq_len": ctx, "parallelism": "single GPU"},
         "step_hbm_frac": round(plain["hbm_frac"], 4),
         "roofline": {"bound": "hbm", "achieved": dom["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(dom["GBps"] / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "gemv gate_up 12288x1536 BF16 (37,748,736 B per launch)"},
+                     "frac": round(dom["GBps"] / HBM_PEAK_GBS, 4), "traffic": traffic_from_profile(),
+                     "kernel": f"gemv {DOMINANT} 12288x1536 BF16, one row, weights streamed from HBM "
+                               "(37,748,736 B per launch)"},
         "cpu_baseline": cpu,
         "details": results,
     }
