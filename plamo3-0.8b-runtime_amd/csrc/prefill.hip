@@ -90,8 +90,8 @@ __device__ __forceinline__ void gemm_store(const GemmStage& g, uint16_t* As, uin
 }
 
 // Y[t][m] = sum_k X[t][k] W[m][k] on 128 x 128 tiles: four waves in a 2 x 2 grid, each
-// 64 x 64 (2 x 2 MFMA 32x32x16 tiles).  The next K step is loaded into registers while
-// the current one is multiplied from LDS (double-buffered, one barrier per step).  Tiles
+// 64 x 64 (2 x 2 MFMA 32x32x16 tiles).  The next two K steps are in flight in registers
+// while the current one is multiplied from LDS (double-buffered, one barrier per step).  Tiles
 // are dealt to workgroups so that each XCD (workgroup id % 8) owns a contiguous run of
 // tiles sharing weight columns, which keeps the weight tiles in that XCD's L2.
 template <bool PACKED, int EPI>
@@ -117,30 +117,40 @@ __global__ __launch_bounds__(256) void gemm_kernel(const GemmParams p, int col_t
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-    GemmStage g;
-    gemm_load<PACKED, EPI>(p, t0, n0, 0, g);
-    gemm_store(g, As[0], Bs[0]);
-    __syncthreads();
-    for (int kt = 0; kt < nk; ++kt) {
-        const int buf = kt & 1;
-        if (kt + 1 < nk) gemm_load<PACKED, EPI>(p, t0, n0, (kt + 1) * BK, g);
+    // Two K steps of operands are in flight in registers while one is multiplied from LDS:
+    // step kt+1 was requested one iteration ago, step kt+2 is requested now.
+    auto mma_step = [&](const uint16_t* A, const uint16_t* B) {
 #pragma unroll
         for (int ks = 0; ks < BK / 16; ++ks) {
             const int kc = ks * 16 + (lane >> 5) * 8;
             bf16x8 a[2], b[2];
 #pragma unroll
             for (int i = 0; i < 2; ++i)
-                a[i] = as_bf16x8(*reinterpret_cast<const uint4*>(&As[buf][(wm * 64 + i * 32 + (lane & 31)) * LDS_STRIDE + kc]));
+                a[i] = as_bf16x8(*reinterpret_cast<const uint4*>(&A[(wm * 64 + i * 32 + (lane & 31)) * LDS_STRIDE + kc]));
 #pragma unroll
             for (int j = 0; j < 2; ++j)
-                b[j] = as_bf16x8(*reinterpret_cast<const uint4*>(&Bs[buf][(wn * 64 + j * 32 + (lane & 31)) * LDS_STRIDE + kc]));
+                b[j] = as_bf16x8(*reinterpret_cast<const uint4*>(&B[(wn * 64 + j * 32 + (lane & 31)) * LDS_STRIDE + kc]));
 #pragma unroll
             for (int i = 0; i < 2; ++i)
 #pragma unroll
                 for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
         }
-        if (kt + 1 < nk) gemm_store(g, As[buf ^ 1], Bs[buf ^ 1]);
+    };
+    GemmStage g[2];
+    gemm_load<PACKED, EPI>(p, t0, n0, 0, g[0]);
+    if (nk > 1) gemm_load<PACKED, EPI>(p, t0, n0, BK, g[1]);
+    gemm_store(g[0], As[0], Bs[0]);
+    __syncthreads();
+    auto step = [&](int kt, GemmStage& next, GemmStage& later) {
+        const int buf = kt & 1;
+        if (kt + 2 < nk) gemm_load<PACKED, EPI>(p, t0, n0, (kt + 2) * BK, later);
+        mma_step(As[buf], Bs[buf]);
+        if (kt + 1 < nk) gemm_store(next, As[buf ^ 1], Bs[buf ^ 1]);
         __syncthreads();
+    };
+    for (int kt = 0; kt < nk; kt += 2) {
+        step(kt, g[1], g[0]);
+        if (kt + 1 < nk) step(kt + 1, g[0], g[1]);
     }
 
     // C layout of a 32x32 tile: column j = lane%32, row i = (r/4)*8 + (lane/32)*4 + r%4
@@ -298,7 +308,8 @@ __global__ __launch_bounds__(256) void qk_prep_kernel(const QkPrepParams p) {
 constexpr int FT = 8;                 // tokens per workgroup
 constexpr int FK = 64;                // keys per tile
 constexpr int KST = HEAD_DIM + 8;     // K tile row stride (BF16), 16-byte aligned rows
-constexpr int VST = FK + 8;           // V^T tile row stride (BF16)
+constexpr int VST = FK + 4;           // V^T tile row stride (BF16): 34 dwords, so 16 lanes reading
+                                      // 8 bytes from 16 consecutive rows hit 32 distinct banks
 constexpr float SCALE_LOG2E = 0.08838834764831845f * 1.4426950408889634f;
 
 struct KvStage {
@@ -306,7 +317,7 @@ struct KvStage {
 };
 
 // Global loads of one tile: thread -> key tid/4 with RoPE pairs (d, d+64), d = 16*(tid%4)
-// .. +16; and values of keys 4*(tid/16) .. +4 at dims 8*(tid%16) .. +8.
+// .. +16; and values of keys 4*(tid%16) .. +4 at dims 8*(tid/16) .. +8.
 __device__ __forceinline__ void flash_load(const FlashParams& p, uint32_t k0, uint32_t khi, uint32_t base,
                                            KvStage& s) {
     const int tid = threadIdx.x;
@@ -329,8 +340,8 @@ __device__ __forceinline__ void flash_load(const FlashParams& p, uint32_t k0, ui
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const uint32_t kv = k0 + uint32_t(4 * (tid >> 4) + i);
-        s.v[i] = kv <= khi ? *reinterpret_cast<const uint4*>(p.values + size_t(kv % p.capacity) * HEAD_DIM + 8 * (tid & 15))
+        const uint32_t kv = k0 + uint32_t(4 * (tid & 15) + i);
+        s.v[i] = kv <= khi ? *reinterpret_cast<const uint4*>(p.values + size_t(kv % p.capacity) * HEAD_DIM + 8 * (tid >> 4))
                            : z;
     }
 }
@@ -369,7 +380,7 @@ __device__ __forceinline__ void flash_store(const FlashParams& p, const KvStage&
         *reinterpret_cast<uint4*>(krow + 64 + part * 16 + 8) = make_uint4(bo[4], bo[5], bo[6], bo[7]);
     }
     // V^T: 4 keys of one dim per 8-byte store
-    const int kg = 4 * (tid >> 4), d0 = 8 * (tid & 15);
+    const int kg = 4 * (tid & 15), d0 = 8 * (tid >> 4);  // consecutive lanes: consecutive key groups
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
         const uint32_t w0 = u16_of(s.v[0], j) | (u16_of(s.v[1], j) << 16);
