@@ -319,8 +319,17 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvParams p) {
     const StepState* st = p.state;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int groups = p.m / U;
-    // Request order = consumption order: prologue inputs, first weights, step state.
+    // Request order = consumption order: step state, prologue inputs, first weights.  The
+    // state is read through a lane-dependent address (lane_mask is 0, so every lane reads
+    // the same words): that makes it a vector load, first in the in-order vector-memory
+    // queue, instead of a scalar load whose wait would also cover the kernel arguments the
+    // weight addresses need.
     uint32_t stopped = 0, srows = 0;
+    if constexpr (STATE) {
+        const StepState* sv = st + (threadIdx.x & p.lane_mask);
+        stopped = sv->stopped;
+        srows = sv->rows;
+    }
     Staged<N, MAXR, PRO> S;
     stage_load<N, MAXR, PRO>(p, p.rows < MAXR ? p.rows : MAXR, S);
     float best_v[MAXR];
@@ -341,21 +350,17 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvParams p) {
     const int stride = gridDim.x * 4;
     int g = blockIdx.x * 4 + wave;
     WRaw<PACKED> wr[U][IT];
-    if (g < groups) {
+    {
+        // unconditional (a wave without a group re-reads the last one) so the compiler
+        // can count the requests in flight exactly
         int wrow[U];
-        rows_of(g, wrow);
+        rows_of(g < groups ? g : groups - 1, wrow);
         request_w<N, PACKED, U, IT>(p, wrow, lane, wr);
     }
-    // The step state is requested only now: waiting for it must not hold back the
-    // requests above (the scheduler may not hoist it across this point).
-    __builtin_amdgcn_sched_barrier(0);
-    if constexpr (STATE) {
-        stopped = st->stopped;
-        srows = st->rows;
-    }
-    if (stopped) return;
+    // A stopped device loop runs the kernel with no rows (an early return here would let
+    // the compiler sink every request above below a wait for the state).
     int rows = p.rows;
-    if constexpr (STATE) rows = int(srows);
+    if constexpr (STATE) rows = stopped ? 0 : int(srows);
     Controls ctl{false, 0, 1.0f, 0.0f, 0.0f};
     if constexpr (EPI == EPI_LOGITS && STATE) {
         if (st->sampling) ctl = Controls{true, st->ngram, st->penalty, st->frequency, st->presence};
@@ -696,35 +701,37 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
         }
     }
     __syncthreads();
-    // ---- unnormalised P.V: thread -> dim d = tid & 127 of local heads 2*(tid >> 7) + {0, 1};
-    //      keys 0..31 and 32..63 as two ordered chains, added at the end
+    // ---- unnormalised P.V: thread -> dims 2e, 2e+1 (e = tid & 63) of local head tid >> 6;
+    //      keys 0..31 and 32..63 as two ordered chains per dim, added at the end
     {
-        const int d = tid & 127, h2 = (tid >> 7) * 2;
-        float o[2][2] = {{0.f, 0.f}, {0.f, 0.f}};
+        const int e = tid & 63, hl = tid >> 6;
+        const uint32_t* v32 = reinterpret_cast<const uint32_t*>(vs);
+        float o[2][2] = {{0.f, 0.f}, {0.f, 0.f}};  // [dim][half]
 #pragma unroll 2
         for (int j = 0; j < KP / 2; j += 4) {
-            float v[2][4];
+            uint32_t vw[2][4];
 #pragma unroll
             for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) v[hf][i] = bf(vs[(hf * (KP / 2) + j + i) * HEAD_DIM + d]);
+                for (int i = 0; i < 4; ++i) vw[hf][i] = v32[(hf * (KP / 2) + j + i) * (HEAD_DIM / 2) + e];
 #pragma unroll
-            for (int hh = 0; hh < 2; ++hh)
+            for (int hf = 0; hf < 2; ++hf) {
+                const float4 pp = *reinterpret_cast<const float4*>(ps + hl * KP + hf * (KP / 2) + j);
+                const float pw[4] = {pp.x, pp.y, pp.z, pp.w};
 #pragma unroll
-                for (int hf = 0; hf < 2; ++hf) {
-                    const float4 pp = *reinterpret_cast<const float4*>(ps + (h2 + hh) * KP + hf * (KP / 2) + j);
-                    o[hh][hf] = o[hh][hf] + pp.x * v[hf][0];
-                    o[hh][hf] = o[hh][hf] + pp.y * v[hf][1];
-                    o[hh][hf] = o[hh][hf] + pp.z * v[hf][2];
-                    o[hh][hf] = o[hh][hf] + pp.w * v[hf][3];
+                for (int i = 0; i < 4; ++i) {
+                    o[0][hf] = o[0][hf] + pw[i] * lo(vw[hf][i]);
+                    o[1][hf] = o[1][hf] + pw[i] * hi(vw[hf][i]);
                 }
+            }
         }
+        const int h = hg * HG + hl;
 #pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-            const float of = o[hh][0] + o[hh][1];
-            const int h = hg * HG + h2 + hh;
+        for (int c = 0; c < 2; ++c) {
+            const float of = o[c][0] + o[c][1];
+            const int d = 2 * e + c;
             if (nparts == 1)  // one partition: the merge reduces to o / l (exp(0) == 1 exactly)
-                p.out[size_t(q) * ATTN + h * HEAD_DIM + d] = roundbf(of / l_s[h2 + hh]);
+                p.out[size_t(q) * ATTN + h * HEAD_DIM + d] = roundbf(of / l_s[hl]);
             else
                 p.part_o[(pslot * HEADS + h) * HEAD_DIM + d] = of;
         }
@@ -754,47 +761,55 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
         wl[i] = p.part_l[(row0 + k) * HEADS + h];
     }
     __syncthreads();
-    if (tid < HG) {
-        const int hh = tid, h = hg * HG + hh;
-        float M = NEG_INF, den = 0.f;
-        if (nparts == np) {
-            for (uint32_t k = 0; k < nparts; ++k) M = fmaxf(M, mm[k * HG + hh]);
-            for (uint32_t k = 0; k < nparts; ++k) {
-                const float w = exp_det(mm[k * HG + hh] - M);
-                den = den + wl[k * HG + hh] * w;
-                wl[k * HG + hh] = w;
+    if (nparts == np) {
+        // M per head; then every weight exp(m_p - M) in parallel (in place of m_p); then each
+        // thread forms den for its own two heads (partition order) while summing o_p w_p
+        if (tid < HG) {
+            float M = NEG_INF;
+            for (uint32_t k = 0; k < nparts; ++k) M = fmaxf(M, mm[k * HG + tid]);
+            l_s[tid] = M;
+        }
+        __syncthreads();
+        for (uint32_t i = tid; i < np * HG; i += 256) mm[i] = exp_det(mm[i] - l_s[i % HG]);
+        __syncthreads();
+        // thread -> dim d = tid & 127 of local heads (tid >> 7) and (tid >> 7) + 2
+        const int d = tid & 127, hb = tid >> 7;
+        float num[2] = {0.f, 0.f}, den[2] = {0.f, 0.f};
+#pragma unroll 8
+        for (uint32_t k = 0; k < nparts; ++k) {
+            float ov[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) ov[i] = p.part_o[((row0 + k) * HEADS + hg * HG + hb + 2 * i) * HEAD_DIM + d];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const float w = mm[k * HG + hb + 2 * i];
+                num[i] = num[i] + ov[i] * w;
+                den[i] = den[i] + wl[k * HG + hb + 2 * i] * w;
             }
-        } else {  // more partitions than LDS holds: read them from memory
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            p.out[size_t(q) * ATTN + (hg * HG + hb + 2 * i) * HEAD_DIM + d] = roundbf(num[i] / den[i]);
+    } else {  // more partitions than LDS holds: read them from memory
+        if (tid < HG) {
+            const int h = hg * HG + tid;
+            float M = NEG_INF, den = 0.f;
             for (uint32_t k = 0; k < nparts; ++k) M = fmaxf(M, p.part_m[(row0 + k) * HEADS + h]);
             for (uint32_t k = 0; k < nparts; ++k)
                 den = den + p.part_l[(row0 + k) * HEADS + h] * exp_det(p.part_m[(row0 + k) * HEADS + h] - M);
+            den_s[tid] = den;
+            l_s[tid] = M;
         }
-        den_s[hh] = den;
-        l_s[hh] = M;
-    }
-    __syncthreads();
-    {
-        // thread -> dim d = tid & 127 of local heads (tid >> 7) and (tid >> 7) + 2
+        __syncthreads();
         const int d = tid & 127, hb = tid >> 7;
         float num[2] = {0.f, 0.f};
-        if (nparts == np) {
-#pragma unroll 4
-            for (uint32_t k = 0; k < nparts; ++k) {
-                float ov[2];
+        for (uint32_t k = 0; k < nparts; ++k)
 #pragma unroll
-                for (int i = 0; i < 2; ++i) ov[i] = p.part_o[((row0 + k) * HEADS + hg * HG + hb + 2 * i) * HEAD_DIM + d];
-#pragma unroll
-                for (int i = 0; i < 2; ++i) num[i] = num[i] + ov[i] * wl[k * HG + hb + 2 * i];
+            for (int i = 0; i < 2; ++i) {
+                const int h = hg * HG + hb + 2 * i;
+                num[i] = num[i] + p.part_o[((row0 + k) * HEADS + h) * HEAD_DIM + d] *
+                                      exp_det(p.part_m[(row0 + k) * HEADS + h] - l_s[hb + 2 * i]);
             }
-        } else {
-            for (uint32_t k = 0; k < nparts; ++k)
-#pragma unroll
-                for (int i = 0; i < 2; ++i) {
-                    const int h = hg * HG + hb + 2 * i;
-                    num[i] = num[i] + p.part_o[((row0 + k) * HEADS + h) * HEAD_DIM + d] *
-                                          exp_det(p.part_m[(row0 + k) * HEADS + h] - l_s[hb + 2 * i]);
-                }
-        }
 #pragma unroll
         for (int i = 0; i < 2; ++i)
             p.out[size_t(q) * ATTN + (hg * HG + hb + 2 * i) * HEAD_DIM + d] = roundbf(num[i] / den_s[hb + 2 * i]);

@@ -54,6 +54,7 @@ struct GemvParams {
     int rows;                 // rows the input buffers hold (the active rows when no
                               // StepState is given; the state's rows never exceed it)
     const StepState* state;   // may be null (kernel-level entry points)
+    uint32_t lane_mask;       // always 0: makes the state read a per-lane (vector) load
     // prologue
     const float* in;          // PLAIN: [rows][n]; RESID: projection output [rows][1536]
     const float* resid_in;    // RESID: residual stream x
