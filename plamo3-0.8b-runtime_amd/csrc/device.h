@@ -114,6 +114,39 @@ __device__ __forceinline__ uint4 p12_decode8(uint2 sm, uint32_t nib, uint32_t ta
     return r;
 }
 
+// Raw buffer views (gfx9 resource word 3 = 0x00020000): base + 32-bit byte offset held in one
+// VGPR; a read at or past `bytes` returns zero instead of touching memory.
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_view(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, int(bytes), 0x00020000);
+}
+__device__ __forceinline__ uint4 buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
+// Same, marked volatile: the compiler issues it where it stands and may not sink it towards
+// its first use (software-pipelined prefetches rely on that).
+__device__ __forceinline__ uint4 buffer_prefetch16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, int(0x80000000u));
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ uint2 buffer_load8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+    return make_uint2(v[0], v[1]);
+}
+__device__ __forceinline__ uint32_t buffer_load4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+}
+// Stores at or past the view's size are dropped (OOB_OFFSET is past every view).
+constexpr uint32_t OOB_OFFSET = 0x80000000u;
+__device__ __forceinline__ void buffer_store4(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t v) {
+    __builtin_amdgcn_raw_buffer_store_b32(v, r, off, 0, 0);
+}
+__device__ __forceinline__ void buffer_store2(__amdgpu_buffer_rsrc_t r, uint32_t off, uint16_t v) {
+    __builtin_amdgcn_raw_buffer_store_b16(v, r, off, 0, 0);
+}
+
 // exp(x) with a fixed operation sequence the CPU oracle reproduces bit for bit:
 // Cody-Waite reduction x = k*ln2 + r (ln2 split in a 16-bit head, so k*LN2_HI is exact for
 // |k| <= 128), degree-7 Taylor polynomial of e^r in Horner form, then an exact 2^k scale.

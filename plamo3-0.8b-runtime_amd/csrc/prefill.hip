@@ -1,9 +1,12 @@
 // Prefill kernels for gfx950: MFMA BF16 GEMM (plain or .p12 weights) with fused epilogues,
 // row RMSNorm / residual kernels and the K/V cache writer.
 //
-//   gemm_kernel     Y[t][m] = sum_k X[t][k] W[m][k]; 128x128 tiles, BK 64, register-prefetched
-//                   double-buffered LDS, v_mfma_f32_32x32x16_bf16, XCD-grouped tiles.  Replaces `matrix` (Kernels.metal:149-200) for
-//                   the projections and `swiglu` (Kernels.metal:202-210) as an epilogue.
+//   gemm_dma_kernel Y[t][m] = sum_k X[t][k] W[m][k] for plain BF16 weights: 256x128 or 128x128
+//                   tiles, BK 64, operands loaded straight into three swizzled LDS stages,
+//                   v_mfma_f32_32x32x16_bf16, XCD-grouped tiles.
+//   gemm_kernel     the same product for .p12 weights, expanded in registers on the way to a
+//                   double-buffered LDS tile.  Both replace `matrix` (Kernels.metal:149-200)
+//                   for the projections and `swiglu` (Kernels.metal:202-210) as an epilogue.
 //   rows_norm       `norm` (Kernels.metal:46-90) for T rows: embedding gather + norm, or
 //                   post-norm + residual + next norm.
 //   qk_prep         `qkv` (Kernels.metal:223-259) for a chunk: q/k RMSNorm, RoPE, K/V to
@@ -24,7 +27,7 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
-constexpr int BM = 128, BN = 128, BK = 64, LDS_STRIDE = BK + 8;  // +16 B per row against bank conflicts
+constexpr int BK = 64, LDS_STRIDE = BK + 8;  // +16 B per row against bank conflicts
 
 __device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) {
     bf16x8 r;
@@ -33,7 +36,7 @@ __device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) {
 }
 
 // Weight row feeding LDS row r of a B tile.  SwiGLU tiles interleave 32 gate and 32 up rows
-// (g0-31, u0-31, g32-63, u32-63) so each wave's two column tiles pair gate with up.
+// (g0-31, u0-31, g32-63, u32-63, ...) so that each wave's column tiles pair gate with up.
 template <int EPI>
 __device__ __forceinline__ int b_row(int n0, int r) {
     if constexpr (EPI == GEMM_SWIGLU) return ((r >> 5) & 1 ? INTER : 0) + n0 + (r >> 6) * 32 + (r & 31);
@@ -41,142 +44,299 @@ __device__ __forceinline__ int b_row(int n0, int r) {
 }
 
 // One K step of operands in registers: thread tid loads 16 bytes of rows tid/8 + 32*i.
+template <int BT, int BW, int NT>
 struct GemmStage {
-    uint4 a[4], b[4];
+    static constexpr int RP = NT / 8;  // rows covered by one pass of the workgroup
+    uint4 a[BT / RP], b[BW / RP];
 };
 
-template <bool PACKED, int EPI>
-__device__ __forceinline__ void gemm_load(const GemmParams& p, int t0, int n0, int k0, GemmStage& g) {
+// Operand views of one GEMM: rows past `tokens` (activations) or `m` (plain weights) read as
+// zero.  .p12 payload offsets come from the validated block table.
+struct GemmViews {
+    __amdgpu_buffer_rsrc_t x, w, table;
+};
+
+__device__ __forceinline__ GemmViews gemm_views(const GemmParams& p, bool packed) {
+    GemmViews v;
+    v.x = buffer_view(p.x, uint32_t(p.tokens) * uint32_t(p.k) * 2u);
+    v.w = buffer_view(p.w, packed ? 0x7fffffffu : uint32_t(p.m) * uint32_t(p.k) * 2u);
+    v.table = buffer_view(p.table, packed ? uint32_t(p.m) * uint32_t(p.k / 128) * 4u : 0u);
+    return v;
+}
+
+// Loads K step k0 of both operands.  A step past the end (live == false) is still issued, with
+// every offset outside its view: it reads zeros without touching memory, and the loads stay
+// unconditional, so the wait before each LDS store counts only the loads of the step it stores.
+template <bool PACKED, int EPI, int BT, int BW, int NT>
+__device__ __forceinline__ void gemm_load(const GemmParams& p, const GemmViews& v, int t0, int n0, int k0, bool live,
+                                          GemmStage<BT, BW, NT>& g) {
+    constexpr int RP = GemmStage<BT, BW, NT>::RP;
     const int tid = threadIdx.x, c8 = tid & 7;
-    const int K = p.k;
+    const uint32_t K = uint32_t(p.k);
+    const uint32_t kk = uint32_t(k0 + c8 * 8);
+    const uint32_t kill = live ? 0u : OOB_OFFSET;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int r = (tid >> 3) + 32 * i;
-        const int t = t0 + r;
-        g.a[i] = t < p.tokens ? *reinterpret_cast<const uint4*>(p.x + size_t(t) * K + k0 + c8 * 8) : make_uint4(0, 0, 0, 0);
+    for (int i = 0; i < BT / RP; ++i) {
+        const uint32_t t = uint32_t(t0 + (tid >> 3) + RP * i);
+        g.a[i] = buffer_prefetch16(v.x, ((t * K + kk) * 2u) | kill);
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int r = (tid >> 3) + 32 * i;
-        const int row = b_row<EPI>(n0, r);
-        uint4 v = make_uint4(0, 0, 0, 0);
-        if (row < p.m) {
-            const int kk = k0 + c8 * 8;
-            if constexpr (!PACKED) {
-                v = *reinterpret_cast<const uint4*>(p.w + size_t(row) * K + kk);
+    for (int i = 0; i < BW / RP; ++i) {
+        const uint32_t row = uint32_t(b_row<EPI>(n0, (tid >> 3) + RP * i));
+        if constexpr (!PACKED) {
+            g.b[i] = buffer_prefetch16(v.w, ((row * K + kk) * 2u) | kill);
+        } else {
+            const uint32_t entry = buffer_load4(v.table, ((row * (K / 128) + kk / 128) * 4u) | kill);
+            const uint32_t blk = (entry & ~63u) | kill, tag = entry & 63u;
+            const uint32_t sub = (kk % 128) / 8;
+            if (tag == 0) g.b[i] = buffer_load16(v.w, blk + sub * 16);
+            else g.b[i] = p12_decode8(buffer_load8(v.w, blk + sub * 8), buffer_load4(v.w, blk + 128 + sub * 4), tag);
+        }
+    }
+}
+
+template <int BT, int BW, int NT>
+__device__ __forceinline__ void gemm_store(const GemmStage<BT, BW, NT>& g, uint16_t* As, uint16_t* Bs) {
+    constexpr int RP = GemmStage<BT, BW, NT>::RP;
+    const int tid = threadIdx.x, c8 = tid & 7;
+#pragma unroll
+    for (int i = 0; i < BT / RP; ++i)
+        *reinterpret_cast<uint4*>(&As[((tid >> 3) + RP * i) * LDS_STRIDE + c8 * 8]) = g.a[i];
+#pragma unroll
+    for (int i = 0; i < BW / RP; ++i)
+        *reinterpret_cast<uint4*>(&Bs[((tid >> 3) + RP * i) * LDS_STRIDE + c8 * 8]) = g.b[i];
+}
+
+// Writes a wave's TT x TW accumulator tiles (tokens from tw0, LDS weight-row tiles of wave
+// column ww) with the chosen epilogue.
+template <int EPI, int TT, int TW>
+__device__ __forceinline__ void gemm_epilogue(const GemmParams& p, const floatx16 (&acc)[TT][TW], int tw0, int n0, int ww,
+                                              int lane) {
+    // C layout of a 32x32 tile: column j = lane%32, row i = (r/4)*8 + (lane/32)*4 + r%4.
+    // Stores go through views bounded by the output size, so rows past `tokens` are dropped
+    // without branches (columns past m get an offset outside the view).
+    const int jc = lane & 31;
+    const uint32_t M = uint32_t(p.m);
+    const __amdgpu_buffer_rsrc_t yv =
+        EPI == GEMM_SWIGLU ? buffer_view(p.y16, uint32_t(p.tokens) * INTER * 2u)
+                           : (EPI == GEMM_BF16 ? buffer_view(p.y16, uint32_t(p.tokens) * M * 2u)
+                                               : buffer_view(p.y, uint32_t(p.tokens) * M * 4u));
+#pragma unroll
+    for (int i = 0; i < TT; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const uint32_t t = uint32_t(tw0 + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3));
+            if constexpr (EPI == GEMM_SWIGLU) {
+#pragma unroll
+                for (int j = 0; j < TW; j += 2) {  // LDS rows of tile j are gate rows, of j + 1 the matching up rows
+                    const uint32_t m = uint32_t(n0 + ((ww * TW + j) >> 1) * 32 + jc);
+                    const float gt = roundbf(acc[i][j][r]);
+                    const float up = roundbf(acc[i][j + 1][r]);
+                    buffer_store2(yv, (t * INTER + m) * 2u, uint16_t(bits(roundbf(gt / (1.0f + exp_det(-gt))) * up)));
+                }
             } else {
-                const uint32_t entry = p.table[size_t(row) * (K / 128) + kk / 128];
-                const uint8_t* blk = reinterpret_cast<const uint8_t*>(p.w) + (entry & ~63u);
-                const uint32_t tag = entry & 63u;
-                const int sub = (kk % 128) / 8;
-                if (tag == 0) v = *reinterpret_cast<const uint4*>(blk + sub * 16);
-                else
-                    v = p12_decode8(*reinterpret_cast<const uint2*>(blk + sub * 8),
-                                    *reinterpret_cast<const uint32_t*>(blk + 128 + sub * 4), tag);
+#pragma unroll
+                for (int j = 0; j < TW; ++j) {
+                    const uint32_t m = uint32_t(n0 + ww * TW * 32 + j * 32 + jc);
+                    const uint32_t e = m < M ? t * M + m : OOB_OFFSET / 4;
+                    if constexpr (EPI == GEMM_F32) buffer_store4(yv, e * 4u, __float_as_uint(roundbf(acc[i][j][r])));
+                    else if constexpr (EPI == GEMM_RAW) buffer_store4(yv, e * 4u, __float_as_uint(acc[i][j][r]));
+                    else buffer_store2(yv, e * 2u, uint16_t(bits(acc[i][j][r])));
+                }
             }
         }
-        g.b[i] = v;
-    }
 }
 
-__device__ __forceinline__ void gemm_store(const GemmStage& g, uint16_t* As, uint16_t* Bs) {
-    const int tid = threadIdx.x, c8 = tid & 7;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int r = (tid >> 3) + 32 * i;
-        *reinterpret_cast<uint4*>(&As[r * LDS_STRIDE + c8 * 8]) = g.a[i];
-        *reinterpret_cast<uint4*>(&Bs[r * LDS_STRIDE + c8 * 8]) = g.b[i];
-    }
-}
-
-// Y[t][m] = sum_k X[t][k] W[m][k] on 128 x 128 tiles: four waves in a 2 x 2 grid, each
-// 64 x 64 (2 x 2 MFMA 32x32x16 tiles).  The next two K steps are in flight in registers
-// while the current one is multiplied from LDS (double-buffered, one barrier per step).  Tiles
-// are dealt to workgroups so that each XCD (workgroup id % 8) owns a contiguous run of
-// tiles sharing weight columns, which keeps the weight tiles in that XCD's L2.
-template <bool PACKED, int EPI>
-__global__ __launch_bounds__(256) void gemm_kernel(const GemmParams p, int col_tiles, int row_tiles) {
-    __shared__ __align__(16) uint16_t As[2][BM * LDS_STRIDE];
-    __shared__ __align__(16) uint16_t Bs[2][BN * LDS_STRIDE];
+// Y[t][m] = sum_k X[t][k] W[m][k] on BT x BW tiles (tokens x weight rows): four waves in a
+// WT x (4 / WT) grid, each owning (BT / WT) x (BW * WT / 4) outputs as 32x32 MFMA tiles.  The
+// next two K steps are in flight in registers while the current one is multiplied from LDS
+// (double-buffered, one barrier per step).  Tiles are dealt to workgroups so that each XCD
+// (workgroup id % 8) owns a contiguous run of tiles sharing weight columns, which keeps the
+// weight tiles in that XCD's L2.  Larger tiles read fewer operand bytes per FLOP from L2.
+template <bool PACKED, int EPI, int BT, int BW, int WT, int NT>
+__global__ __launch_bounds__(NT) void gemm_kernel(const GemmParams p, int col_tiles, int row_tiles) {
+    constexpr int WW = NT / 64 / WT, TT = BT / WT / 32, TW = BW / WW / 32;
+    static_assert(EPI != GEMM_SWIGLU || TW % 2 == 0, "SwiGLU pairs gate and up tiles inside a wave");
+    __shared__ __align__(16) uint16_t As[2][BT * LDS_STRIDE];
+    __shared__ __align__(16) uint16_t Bs[2][BW * LDS_STRIDE];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wt = wave / WW, ww = wave % WW;
     const int tiles = col_tiles * row_tiles;
     const int per = (tiles + 7) / 8;
     const int tile = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
     if (tile >= tiles) return;
     const int ct = tile / row_tiles, rt = tile % row_tiles;
-    const int t0 = rt * BM;
-    const int n0 = ct * (EPI == GEMM_SWIGLU ? BN / 2 : BN);
+    const int t0 = rt * BT;
+    const int n0 = ct * (EPI == GEMM_SWIGLU ? BW / 2 : BW);
     const int nk = p.k / BK;
 
-    floatx16 acc[2][2];
+    floatx16 acc[TT][TW];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < TT; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < TW; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
     // Two K steps of operands are in flight in registers while one is multiplied from LDS:
-    // step kt+1 was requested one iteration ago, step kt+2 is requested now.
-    auto mma_step = [&](const uint16_t* A, const uint16_t* B) {
+    // step kt+1 was requested one iteration ago and goes to the other LDS buffer during this
+    // step, step kt+2 is requested now.  Inside a step the operands of 16-deep K slice ks+1 are
+    // read from LDS while slice ks is multiplied.
+    auto read_ops = [&](const uint16_t* A, const uint16_t* B, int ks, bf16x8 (&a)[TT], bf16x8 (&b)[TW]) {
+        const int kc = ks * 16 + (lane >> 5) * 8;
 #pragma unroll
-        for (int ks = 0; ks < BK / 16; ++ks) {
-            const int kc = ks * 16 + (lane >> 5) * 8;
-            bf16x8 a[2], b[2];
+        for (int i = 0; i < TT; ++i)
+            a[i] = as_bf16x8(*reinterpret_cast<const uint4*>(&A[(wt * TT * 32 + i * 32 + (lane & 31)) * LDS_STRIDE + kc]));
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
-                a[i] = as_bf16x8(*reinterpret_cast<const uint4*>(&A[(wm * 64 + i * 32 + (lane & 31)) * LDS_STRIDE + kc]));
-#pragma unroll
-            for (int j = 0; j < 2; ++j)
-                b[j] = as_bf16x8(*reinterpret_cast<const uint4*>(&B[(wn * 64 + j * 32 + (lane & 31)) * LDS_STRIDE + kc]));
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
-        }
+        for (int j = 0; j < TW; ++j)
+            b[j] = as_bf16x8(*reinterpret_cast<const uint4*>(&B[(ww * TW * 32 + j * 32 + (lane & 31)) * LDS_STRIDE + kc]));
     };
-    GemmStage g[2];
-    gemm_load<PACKED, EPI>(p, t0, n0, 0, g[0]);
-    if (nk > 1) gemm_load<PACKED, EPI>(p, t0, n0, BK, g[1]);
+    const GemmViews views = gemm_views(p, PACKED);
+    GemmStage<BT, BW, NT> g[2];
+    gemm_load<PACKED, EPI>(p, views, t0, n0, 0, true, g[0]);
+    gemm_load<PACKED, EPI>(p, views, t0, n0, BK, nk > 1, g[1]);
     gemm_store(g[0], As[0], Bs[0]);
     __syncthreads();
-    auto step = [&](int kt, GemmStage& next, GemmStage& later) {
+    auto step = [&](int kt, GemmStage<BT, BW, NT>& next, GemmStage<BT, BW, NT>& later) {
         const int buf = kt & 1;
-        if (kt + 2 < nk) gemm_load<PACKED, EPI>(p, t0, n0, (kt + 2) * BK, later);
-        mma_step(As[buf], Bs[buf]);
-        if (kt + 1 < nk) gemm_store(next, As[buf ^ 1], Bs[buf ^ 1]);
+        const uint16_t* A = As[buf];
+        const uint16_t* B = Bs[buf];
+        bf16x8 a[2][TT], b[2][TW];
+        read_ops(A, B, 0, a[0], b[0]);
+        gemm_load<PACKED, EPI>(p, views, t0, n0, (kt + 2) * BK, kt + 2 < nk, later);
+        // the other buffer was last read before the previous barrier; past the last step the
+        // stored stage is zeros that nobody reads, so the store needs no branch
+        gemm_store(next, As[buf ^ 1], Bs[buf ^ 1]);
+#pragma unroll
+        for (int ks = 0; ks < BK / 16; ++ks) {
+            if (ks + 1 < BK / 16) read_ops(A, B, ks + 1, a[(ks + 1) & 1], b[(ks + 1) & 1]);
+#pragma unroll
+            for (int i = 0; i < TT; ++i)
+#pragma unroll
+                for (int j = 0; j < TW; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[ks & 1][i], b[ks & 1][j], acc[i][j], 0, 0, 0);
+        }
         __syncthreads();
     };
-    for (int kt = 0; kt < nk; kt += 2) {
+    // both halves of the loop body are unconditional, so each stage keeps its registers
+    int kt = 0;
+    for (; kt + 1 < nk; kt += 2) {
         step(kt, g[1], g[0]);
-        if (kt + 1 < nk) step(kt + 1, g[0], g[1]);
+        step(kt + 1, g[0], g[1]);
     }
+    if (kt < nk) step(kt, g[1], g[0]);
 
-    // C layout of a 32x32 tile: column j = lane%32, row i = (r/4)*8 + (lane/32)*4 + r%4
-    const int jc = lane & 31;
+    gemm_epilogue<EPI, TT, TW>(p, acc, t0 + wt * TT * 32, n0, ww, lane);
+}
+
+// s_waitcnt on the vector-memory counter only (gfx9 encoding: expcnt and lgkmcnt at maximum).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
+}
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+__device__ __forceinline__ void load_to_lds(__amdgpu_buffer_rsrc_t v, void* lds, uint32_t off) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(v, (lds_ptr_t)lds, 16, off, 0, 0, 0);
+}
+
+// Plain-weight GEMM whose operand tiles go from memory straight into LDS (buffer loads with
+// the LDS destination): no staging registers and no LDS store instructions.  Three LDS
+// stages, two K steps in flight.  A stage holds BT activation rows then BW weight rows of 128
+// bytes (64 K values); the 16-byte chunk c of row R sits in slot c ^ ((R >> 1) & 7), which
+// spreads both the loads' 8-lane row segments and the operand reads' 16-row columns over
+// all banks.  Each wave loads Q 1 KB blocks (8 rows) per stage.  Waves synchronise with a
+// bare s_barrier after waiting for their own stage loads, so the stage two steps ahead stays
+// in flight across the barrier.
+template <int EPI, int BT, int BW, int WT, int NT>
+__global__ __launch_bounds__(NT) void gemm_dma_kernel(const GemmParams p, int col_tiles, int row_tiles) {
+    constexpr int NW = NT / 64, WW = NW / WT, TT = BT / WT / 32, TW = BW / WW / 32;
+    constexpr int ROWS = BT + BW, STAGE = ROWS * 128, Q = ROWS / 8 / NW;
+    static_assert(ROWS % (8 * NW) == 0 && BT % 16 == 0, "stage blocks per wave");
+    static_assert(EPI != GEMM_SWIGLU || TW % 2 == 0, "SwiGLU pairs gate and up tiles inside a wave");
+    __shared__ __align__(1024) uint8_t S0[STAGE];
+    __shared__ __align__(1024) uint8_t S1[STAGE];
+    __shared__ __align__(1024) uint8_t S2[STAGE];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wt = wave / WW, ww = wave % WW;
+    const int tiles = col_tiles * row_tiles;
+    const int per = (tiles + 7) / 8;
+    const int tile = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
+    if (tile >= tiles) return;
+    const int ct = tile / row_tiles, rt = tile % row_tiles;
+    const int t0 = rt * BT;
+    const int n0 = ct * (EPI == GEMM_SWIGLU ? BW / 2 : BW);
+    const int nk = p.k / BK;
+    const uint32_t K = uint32_t(p.k);
+    const GemmViews views = gemm_views(p, false);
+
+    // this lane's source offset (K step 0) for each of the wave's Q blocks
+    uint32_t goff[Q];
+    bool from_x[Q];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int q = 0; q < Q; ++q) {
+        const int R = (wave * Q + q) * 8 + (lane >> 3);
+        const uint32_t c = uint32_t((lane & 7) ^ ((R >> 1) & 7));
+        from_x[q] = (wave * Q + q) * 8 < BT;
+        const uint32_t row = from_x[q] ? uint32_t(t0 + R) : uint32_t(b_row<EPI>(n0, R - BT));
+        goff[q] = (row * K + c * 8) * 2u;
+    }
+    auto issue = [&](uint8_t* stage, int kt) {
+        const uint32_t kill = kt < nk ? 0u : OOB_OFFSET;
+        const uint32_t kb = uint32_t(kt) * BK * 2u;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int t = t0 + wm * 64 + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-            if (t >= p.tokens) continue;
-            if constexpr (EPI == GEMM_SWIGLU) {
-                const int m = n0 + wn * 32 + jc;
-                const float gt = roundbf(acc[i][0][r]);
-                const float up = roundbf(acc[i][1][r]);
-                p.y16[size_t(t) * INTER + m] = uint16_t(bits(roundbf(gt / (1.0f + exp_det(-gt))) * up));
-            } else {
+        for (int q = 0; q < Q; ++q)
+            load_to_lds(from_x[q] ? views.x : views.w, stage + (wave * Q + q) * 1024, (goff[q] + kb) | kill);
+    };
+    floatx16 acc[TT][TW];
 #pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    const int m = n0 + wn * 64 + j * 32 + jc;
-                    if (m >= p.m) continue;
-                    if constexpr (EPI == GEMM_F32) p.y[size_t(t) * p.m + m] = roundbf(acc[i][j][r]);
-                    else if constexpr (EPI == GEMM_RAW) p.y[size_t(t) * p.m + m] = acc[i][j][r];
-                    else p.y16[size_t(t) * p.m + m] = uint16_t(bits(acc[i][j][r]));
-                }
+    for (int i = 0; i < TT; ++i)
+#pragma unroll
+        for (int j = 0; j < TW; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+    auto compute = [&](const uint8_t* stage) {
+#pragma unroll
+        for (int ks = 0; ks < BK / 16; ++ks) {
+            const int c = ks * 2 + (lane >> 5);
+            bf16x8 a[TT], b[TW];
+#pragma unroll
+            for (int i = 0; i < TT; ++i) {
+                const int R = wt * TT * 32 + i * 32 + (lane & 31);
+                a[i] = as_bf16x8(*reinterpret_cast<const uint4*>(stage + R * 128 + ((c ^ ((R >> 1) & 7)) << 4)));
             }
+#pragma unroll
+            for (int j = 0; j < TW; ++j) {
+                const int R = BT + ww * TW * 32 + j * 32 + (lane & 31);
+                b[j] = as_bf16x8(*reinterpret_cast<const uint4*>(stage + R * 128 + ((c ^ ((R >> 1) & 7)) << 4)));
+            }
+#pragma unroll
+            for (int i = 0; i < TT; ++i)
+#pragma unroll
+                for (int j = 0; j < TW; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
         }
+    };
+    // step kt: this wave's loads of stage kt are done once at most the Q loads of stage kt+1
+    // are outstanding; after the barrier every wave's are, and the buffer of stage kt-1 is free
+    auto step = [&](const uint8_t* cur, uint8_t* freed, int kt) {
+        wait_vmcnt<Q>();
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        issue(freed, kt + 2);
+        compute(cur);
+    };
+    issue(S0, 0);
+    issue(S1, 1);
+    int kt = 0;
+    for (; kt + 3 <= nk; kt += 3) {
+        step(S0, S2, kt);
+        step(S1, S0, kt + 1);
+        step(S2, S1, kt + 2);
+    }
+    if (kt < nk) step(S0, S2, kt);
+    if (kt + 1 < nk) step(S1, S0, kt + 1);
+    gemm_epilogue<EPI, TT, TW>(p, acc, t0 + wt * TT * 32, n0, ww, lane);
 }
 
 // ------------------------------------------------------------------------------ norms
@@ -541,28 +701,56 @@ __global__ __launch_bounds__(256) void flash_prefill_kernel(const FlashParams p)
         }
 }
 
+template <int BT, int BW, int WT, int NT>
+void launch_gemm_dma(GemmEpilogue epi, const GemmParams& p, hipStream_t s) {
+    const int cols = epi == GEMM_SWIGLU ? INTER / (BW / 2) : (p.m + BW - 1) / BW;
+    const int rows = (p.tokens + BT - 1) / BT;
+    const int per = (cols * rows + 7) / 8;
+    const dim3 grid(8 * per), block(NT);
+#define PLAMO_GEMM(EP) hipLaunchKernelGGL((gemm_dma_kernel<EP, BT, BW, WT, NT>), grid, block, 0, s, p, cols, rows)
+    if (epi == GEMM_F32) PLAMO_GEMM(GEMM_F32);
+    else if (epi == GEMM_BF16) PLAMO_GEMM(GEMM_BF16);
+    else if (epi == GEMM_RAW) PLAMO_GEMM(GEMM_RAW);
+    else PLAMO_GEMM(GEMM_SWIGLU);
+#undef PLAMO_GEMM
+}
+
+template <int BT, int BW, int WT, int NT>
+void launch_gemm_packed(GemmEpilogue epi, const GemmParams& p, hipStream_t s) {
+    const int cols = epi == GEMM_SWIGLU ? INTER / (BW / 2) : (p.m + BW - 1) / BW;
+    const int rows = (p.tokens + BT - 1) / BT;
+    const int per = (cols * rows + 7) / 8;
+    const dim3 grid(8 * per), block(NT);
+#define PLAMO_GEMM(PK, EP) hipLaunchKernelGGL((gemm_kernel<PK, EP, BT, BW, WT, NT>), grid, block, 0, s, p, cols, rows)
+    if (epi == GEMM_F32) PLAMO_GEMM(true, GEMM_F32);
+    else if (epi == GEMM_BF16) PLAMO_GEMM(true, GEMM_BF16);
+    else if (epi == GEMM_RAW) PLAMO_GEMM(true, GEMM_RAW);
+    else PLAMO_GEMM(true, GEMM_SWIGLU);
+#undef PLAMO_GEMM
+}
+
 }  // namespace
 
 void launch_gemm(bool packed, GemmEpilogue epi, const GemmParams& p, hipStream_t s) {
     if (p.k % BK != 0 || p.tokens < 1 || p.m < 1 || (epi == GEMM_SWIGLU && p.m != 2 * INTER))
         throw Error(E_INVAL, "unsupported GEMM shape");
-    const int cols = epi == GEMM_SWIGLU ? INTER / (BN / 2) : (p.m + BN - 1) / BN;
-    const int rows = (p.tokens + BM - 1) / BM;
-    const int per = (cols * rows + 7) / 8;
-    const dim3 grid(8 * per), block(256);
-#define PLAMO_GEMM(PK, EP) hipLaunchKernelGGL((gemm_kernel<PK, EP>), grid, block, 0, s, p, cols, rows)
+    // operand and output views take 32-bit byte offsets (rows of the last tile included)
+    const uint64_t t_pad = uint64_t(p.tokens) + 256;
+    if (t_pad * uint64_t(p.k) * 2 >= (1ull << 31) || uint64_t(p.m) * uint64_t(p.k) * 2 >= (1ull << 31) ||
+        t_pad * uint64_t(p.m) * 4 >= (1ull << 31))
+        throw Error(E_INVAL, "GEMM operands exceed 2 GiB");
+    // Tile choice (measured on the prefill shapes, 2048 tokens): 256 x 128 tiles for the wide
+    // projections (gate_up, qkv), 128 x 128 for the 1536-row ones (o, down), where larger
+    // tiles leave CUs idle; plain weights go straight to LDS, .p12 weights are expanded in
+    // registers on the way.
+    const bool wide = p.tokens > 128 && (epi == GEMM_SWIGLU || p.m > 2048);
     if (packed) {
-        if (epi == GEMM_F32) PLAMO_GEMM(true, GEMM_F32);
-        else if (epi == GEMM_BF16) PLAMO_GEMM(true, GEMM_BF16);
-        else if (epi == GEMM_RAW) PLAMO_GEMM(true, GEMM_RAW);
-        else PLAMO_GEMM(true, GEMM_SWIGLU);
+        if (wide) launch_gemm_packed<256, 128, 4, 512>(epi, p, s);
+        else launch_gemm_packed<128, 128, 2, 256>(epi, p, s);
     } else {
-        if (epi == GEMM_F32) PLAMO_GEMM(false, GEMM_F32);
-        else if (epi == GEMM_BF16) PLAMO_GEMM(false, GEMM_BF16);
-        else if (epi == GEMM_RAW) PLAMO_GEMM(false, GEMM_RAW);
-        else PLAMO_GEMM(false, GEMM_SWIGLU);
+        if (wide) launch_gemm_dma<256, 128, 4, 512>(epi, p, s);
+        else launch_gemm_dma<128, 128, 4, 512>(epi, p, s);
     }
-#undef PLAMO_GEMM
 }
 
 void launch_rows_norm(const RowsNormParams& p, int tokens, hipStream_t s) {
