@@ -1,6 +1,8 @@
 // extern "C" boundary (include/plamo_hip.h).  No C++ exception crosses it.
 #include <cstdio>
 #include <cstring>
+#include <map>
+#include <mutex>
 #include <functional>
 
 #include "../../include/plamo_hip.h"
@@ -515,6 +517,41 @@ int plamo_kernel_gemm(uint64_t w, uint64_t table, uint64_t x, uint64_t y, int32_
     });
 }
 
+namespace {
+// Workspace of the split flash prefill for the kernel-level entry, per device, grown on demand
+// (the runtime keeps its own).  Growing synchronises the device before freeing the old one.
+struct FlashWorkspace {
+    float* o = nullptr;
+    float* ml = nullptr;
+    uint32_t* tickets = nullptr;
+    int tokens = 0;
+};
+std::mutex g_flash_ws_mu;
+std::map<int, FlashWorkspace> g_flash_ws;
+
+FlashWorkspace flash_workspace(int tokens) {
+    std::lock_guard<std::mutex> lk(g_flash_ws_mu);
+    int dev = 0;
+    PLAMO_HIP(hipGetDevice(&dev));
+    FlashWorkspace& w = g_flash_ws[dev];
+    if (w.tokens < tokens) {
+        if (w.o) {
+            PLAMO_HIP(hipDeviceSynchronize());
+            (void)hipFree(w.o);
+            (void)hipFree(w.ml);
+            (void)hipFree(w.tickets);
+            w = FlashWorkspace{};
+        }
+        PLAMO_HIP(hipMalloc(&w.o, plamo::flash_part_o_floats(tokens) * 4));
+        PLAMO_HIP(hipMalloc(&w.ml, plamo::flash_part_ml_floats(tokens) * 4));
+        PLAMO_HIP(hipMalloc(&w.tickets, size_t(plamo::flash_blocks(tokens)) * 4));
+        PLAMO_HIP(hipMemset(w.tickets, 0, size_t(plamo::flash_blocks(tokens)) * 4));
+        w.tokens = tokens;
+    }
+    return w;
+}
+}  // namespace
+
 int plamo_kernel_attention_prefill(uint64_t q16, uint64_t keys, uint64_t values, int32_t capacity, int32_t p0,
                                    int32_t tokens, int32_t full, uint64_t local_rope, uint64_t out16,
                                    uint64_t stream) {
@@ -535,6 +572,10 @@ int plamo_kernel_attention_prefill(uint64_t q16, uint64_t keys, uint64_t values,
         f.p0 = uint32_t(p0);
         f.tokens = tokens;
         f.full = full ? 1 : 0;
+        const FlashWorkspace ws = flash_workspace(tokens);
+        f.part_o = ws.o;
+        f.part_ml = ws.ml;
+        f.tickets = ws.tickets;
         plamo::launch_flash_prefill(f, reinterpret_cast<hipStream_t>(stream));
         PLAMO_HIP(hipGetLastError());
     });

@@ -546,6 +546,11 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
     uint16_t* K = p.keys + size_t(lanei) * cap * HEAD_DIM;
     uint16_t* V = p.values + size_t(lanei) * cap * HEAD_DIM;
     const size_t pslot = size_t(q) * p.parts + blockIdx.x;
+    // partition results travel between workgroups with sc1 stores and loads (no cache fences)
+    const uint32_t pstats = uint32_t(ROWS) * p.parts * HEADS;
+    const __amdgpu_buffer_rsrc_t mview = buffer_view(p.part_m, pstats * 4u);
+    const __amdgpu_buffer_rsrc_t lview = buffer_view(p.part_l, pstats * 4u);
+    const __amdgpu_buffer_rsrc_t oview = buffer_view(p.part_o, pstats * HEAD_DIM * 4u);
     const uint32_t nparts = (count + KP - 1) / KP;
     if (blockIdx.x >= nparts) return;  // partitions past the visible keys take no ticket
     const uint32_t newest = count - 1;
@@ -695,8 +700,8 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
         if (lane == 0) {
             l_s[w] = l;
             if (nparts > 1) {
-                p.part_m[pslot * HEADS + hg * HG + w] = m;
-                p.part_l[pslot * HEADS + hg * HG + w] = l;
+                buffer_store4_sc1(mview, uint32_t(pslot * HEADS + hg * HG + w) * 4u, __float_as_uint(m));
+                buffer_store4_sc1(lview, uint32_t(pslot * HEADS + hg * HG + w) * 4u, __float_as_uint(l));
             }
         }
     }
@@ -726,19 +731,19 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
             }
         }
         const int h = hg * HG + hl;
-#pragma unroll
-        for (int c = 0; c < 2; ++c) {
-            const float of = o[c][0] + o[c][1];
-            const int d = 2 * e + c;
-            if (nparts == 1)  // one partition: the merge reduces to o / l (exp(0) == 1 exactly)
-                p.out[size_t(q) * ATTN + h * HEAD_DIM + d] = roundbf(of / l_s[hl]);
-            else
-                p.part_o[(pslot * HEADS + h) * HEAD_DIM + d] = of;
+        const float of0 = o[0][0] + o[0][1], of1 = o[1][0] + o[1][1];
+        if (nparts == 1) {  // one partition: the merge reduces to o / l (exp(0) == 1 exactly)
+            p.out[size_t(q) * ATTN + h * HEAD_DIM + 2 * e] = roundbf(of0 / l_s[hl]);
+            p.out[size_t(q) * ATTN + h * HEAD_DIM + 2 * e + 1] = roundbf(of1 / l_s[hl]);
+        } else {
+            buffer_store8_sc1(oview, uint32_t((pslot * HEADS + h) * HEAD_DIM + 2 * e) * 4u,
+                              make_uint2(__float_as_uint(of0), __float_as_uint(of1)));
         }
     }
     if (nparts == 1) return;
-    // ticket: the last workgroup of this (row, head group) merges the partitions
-    __threadfence();
+    // ticket: the last workgroup of this (row, head group) merges the partitions; every
+    // wave's partition stores have completed before the ticket is taken
+    wait_stores();
     __syncthreads();
     uint32_t* ticket = p.tickets + q * (HEADS / HG) + hg;
     if (tid == 0) {
@@ -747,7 +752,6 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
     }
     __syncthreads();
     if (!s_last) return;
-    __threadfence();
     const size_t row0 = size_t(q) * p.parts;
     // per head: M = max_p m_p, w_p = exp(m_p - M), den = sum_p l_p w_p (partition order);
     // then each (h, d) sums o_p w_p in partition order.  Partition statistics are staged in
@@ -757,8 +761,8 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
     const uint32_t np = nparts <= uint32_t(KP * KS / 2 / HG) ? nparts : uint32_t(KP * KS / 2 / HG);
     for (uint32_t i = tid; i < np * HG; i += 256) {
         const uint32_t k = i / HG, h = hg * HG + i % HG;
-        mm[i] = p.part_m[(row0 + k) * HEADS + h];
-        wl[i] = p.part_l[(row0 + k) * HEADS + h];
+        mm[i] = __uint_as_float(buffer_load4_sc1(mview, uint32_t((row0 + k) * HEADS + h) * 4u));
+        wl[i] = __uint_as_float(buffer_load4_sc1(lview, uint32_t((row0 + k) * HEADS + h) * 4u));
     }
     __syncthreads();
     if (nparts == np) {
@@ -779,7 +783,9 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
         for (uint32_t k = 0; k < nparts; ++k) {
             float ov[2];
 #pragma unroll
-            for (int i = 0; i < 2; ++i) ov[i] = p.part_o[((row0 + k) * HEADS + hg * HG + hb + 2 * i) * HEAD_DIM + d];
+            for (int i = 0; i < 2; ++i)
+                ov[i] = __uint_as_float(
+                    buffer_load4_sc1(oview, uint32_t(((row0 + k) * HEADS + hg * HG + hb + 2 * i) * HEAD_DIM + d) * 4u));
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
                 const float w = mm[k * HG + hb + 2 * i];
@@ -794,9 +800,10 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
         if (tid < HG) {
             const int h = hg * HG + tid;
             float M = NEG_INF, den = 0.f;
-            for (uint32_t k = 0; k < nparts; ++k) M = fmaxf(M, p.part_m[(row0 + k) * HEADS + h]);
-            for (uint32_t k = 0; k < nparts; ++k)
-                den = den + p.part_l[(row0 + k) * HEADS + h] * exp_det(p.part_m[(row0 + k) * HEADS + h] - M);
+            auto pm = [&](uint32_t k) { return __uint_as_float(buffer_load4_sc1(mview, uint32_t((row0 + k) * HEADS + h) * 4u)); };
+            auto pl = [&](uint32_t k) { return __uint_as_float(buffer_load4_sc1(lview, uint32_t((row0 + k) * HEADS + h) * 4u)); };
+            for (uint32_t k = 0; k < nparts; ++k) M = fmaxf(M, pm(k));
+            for (uint32_t k = 0; k < nparts; ++k) den = den + pl(k) * exp_det(pm(k) - M);
             den_s[tid] = den;
             l_s[tid] = M;
         }
@@ -807,14 +814,15 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
                 const int h = hg * HG + hb + 2 * i;
-                num[i] = num[i] + p.part_o[((row0 + k) * HEADS + h) * HEAD_DIM + d] *
-                                      exp_det(p.part_m[(row0 + k) * HEADS + h] - l_s[hb + 2 * i]);
+                const float ov = __uint_as_float(buffer_load4_sc1(oview, uint32_t(((row0 + k) * HEADS + h) * HEAD_DIM + d) * 4u));
+                const float mk = __uint_as_float(buffer_load4_sc1(mview, uint32_t((row0 + k) * HEADS + h) * 4u));
+                num[i] = num[i] + ov * exp_det(mk - l_s[hb + 2 * i]);
             }
 #pragma unroll
         for (int i = 0; i < 2; ++i)
             p.out[size_t(q) * ATTN + (hg * HG + hb + 2 * i) * HEAD_DIM + d] = roundbf(num[i] / den_s[hb + 2 * i]);
     }
-    if (tid == 0) *ticket = 0;
+    if (tid == 0) atomicExch(ticket, 0u);  // ready for the next launch
 }
 
 // ------------------------------------------------------------------------- step begin

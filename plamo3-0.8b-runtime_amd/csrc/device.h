@@ -138,6 +138,35 @@ __device__ __forceinline__ uint2 buffer_load8(__amdgpu_buffer_rsrc_t r, uint32_t
 __device__ __forceinline__ uint32_t buffer_load4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
 }
+// Device-coherent exchange between workgroups without whole-cache fences: stores with the
+// sc1 policy write through this XCD's L2, loads with sc1 read the coherent copy (the cache
+// policy of agent-scope relaxed atomics).  A writer waits for its stores (vmcnt 0) before it
+// publishes them with an atomic; a reader issues its loads after observing the atomic.
+constexpr int SC1 = 16;
+__device__ __forceinline__ void buffer_store16_sc1(__amdgpu_buffer_rsrc_t r, uint32_t off, uint4 v) {
+    const u32x4_t w = {v.x, v.y, v.z, v.w};
+    __builtin_amdgcn_raw_buffer_store_b128(w, r, off, 0, SC1);
+}
+__device__ __forceinline__ void buffer_store8_sc1(__amdgpu_buffer_rsrc_t r, uint32_t off, uint2 v) {
+    const u32x2_t w = {v.x, v.y};
+    __builtin_amdgcn_raw_buffer_store_b64(w, r, off, 0, SC1);
+}
+__device__ __forceinline__ uint4 buffer_load16_sc1(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, SC1);
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ uint2 buffer_load8_sc1(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, SC1);
+    return make_uint2(v[0], v[1]);
+}
+__device__ __forceinline__ void buffer_store4_sc1(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t v) {
+    __builtin_amdgcn_raw_buffer_store_b32(v, r, off, 0, SC1);
+}
+__device__ __forceinline__ uint32_t buffer_load4_sc1(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, SC1);
+}
+__device__ __forceinline__ void wait_stores() { __builtin_amdgcn_s_waitcnt(0); }
+
 // Stores at or past the view's size are dropped (OOB_OFFSET is past every view).
 constexpr uint32_t OOB_OFFSET = 0x80000000u;
 __device__ __forceinline__ void buffer_store4(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t v) {

@@ -43,6 +43,15 @@ struct QkPrepParams {
     const uint32_t* global_rope;  // [context][64]
 };
 
+// Flash prefill splits the key tiles of a query block (8 tokens x 16 heads) over up to
+// FLASH_PARTS workgroups; their partial results meet in a workspace.
+constexpr int FLASH_PARTS = 2;
+constexpr int FLASH_PART_TILES = 16;         // 64-key tiles a part aims at
+__host__ __device__ inline int flash_blocks(int tokens) { return (tokens + 7) / 8; }
+// workspace floats: per block and part, O^T [128 columns][128 dims] and (m, l) per column
+inline size_t flash_part_o_floats(int tokens) { return size_t(flash_blocks(tokens)) * FLASH_PARTS * 128 * 128; }
+inline size_t flash_part_ml_floats(int tokens) { return size_t(flash_blocks(tokens)) * FLASH_PARTS * 128 * 2; }
+
 struct FlashParams {
     const uint16_t* q;         // [T][16][128] BF16, normalised and rotated
     const uint16_t* keys;      // lane slice [capacity][128]
@@ -52,6 +61,9 @@ struct FlashParams {
     uint32_t capacity, p0;
     int tokens;
     int full;
+    float* part_o;             // flash_part_o_floats(tokens)
+    float* part_ml;            // flash_part_ml_floats(tokens)
+    uint32_t* tickets;         // flash_blocks(tokens), zero between launches
 };
 
 void launch_gemm(bool packed, GemmEpilogue epi, const GemmParams& p, hipStream_t s);

@@ -26,6 +26,8 @@ namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float floatx2 __attribute__((ext_vector_type(2)));
 
 constexpr int BK = 64, LDS_STRIDE = BK + 8;  // +16 B per row against bank conflicts
 
@@ -465,7 +467,7 @@ __global__ __launch_bounds__(256) void qk_prep_kernel(const QkPrepParams p) {
 //
 // Keys of local layers are rotated while staged, with coordinate key_pos - base of the
 // workgroup's 16-token chunk (base = max(0, chunk_start - 2047)).
-constexpr int FT = 8;                 // tokens per workgroup
+constexpr int FT = 8;                 // tokens per query block (workgroup)
 constexpr int FK = 64;                // keys per tile
 constexpr int KST = HEAD_DIM + 8;     // K tile row stride (BF16), 16-byte aligned rows
 constexpr int VST = FK + 4;           // V^T tile row stride (BF16): 34 dwords, so 16 lanes reading
@@ -486,8 +488,15 @@ __device__ __forceinline__ void flash_load(const FlashParams& p, uint32_t k0, ui
     const uint4 z = make_uint4(0, 0, 0, 0);
     s.ka[0] = s.ka[1] = s.kb[0] = s.kb[1] = z;
     s.rr[0] = s.rr[1] = s.rr[2] = s.rr[3] = z;
+    // ring slots: one modulo per tile, then at most a wrap per key (tiles are 64 keys)
+    const uint32_t slot0 = k0 % p.capacity;
+    auto ring = [&](uint32_t off) {
+        uint32_t slot = slot0 + off;
+        while (slot >= p.capacity) slot -= p.capacity;
+        return slot;
+    };
     if (kp <= khi) {
-        const uint16_t* row = p.keys + size_t(kp % p.capacity) * HEAD_DIM;
+        const uint16_t* row = p.keys + size_t(ring(uint32_t(tid >> 2))) * HEAD_DIM;
         s.ka[0] = *reinterpret_cast<const uint4*>(row + part * 16);
         s.ka[1] = *reinterpret_cast<const uint4*>(row + part * 16 + 8);
         s.kb[0] = *reinterpret_cast<const uint4*>(row + 64 + part * 16);
@@ -501,7 +510,8 @@ __device__ __forceinline__ void flash_load(const FlashParams& p, uint32_t k0, ui
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const uint32_t kv = k0 + uint32_t(4 * (tid & 15) + i);
-        s.v[i] = kv <= khi ? *reinterpret_cast<const uint4*>(p.values + size_t(kv % p.capacity) * HEAD_DIM + 8 * (tid >> 4))
+        s.v[i] = kv <= khi ? *reinterpret_cast<const uint4*>(p.values + size_t(ring(uint32_t(4 * (tid & 15) + i))) * HEAD_DIM +
+                                                             8 * (tid >> 4))
                            : z;
     }
 }
@@ -509,6 +519,26 @@ __device__ __forceinline__ void flash_load(const FlashParams& p, uint32_t k0, ui
 __device__ __forceinline__ uint32_t u16_of(const uint4& v, int k) {
     const uint32_t w = k < 2 ? v.x : k < 4 ? v.y : k < 6 ? v.z : v.w;
     return (k & 1) ? (w >> 16) : (w & 0xffffu);
+}
+
+// rope_pair on two BF16 pairs at once (a = packed x[d], x'[d]; b = packed x[d+64], x'[d+64];
+// cs0 / cs1 their cos | sin << 16) with the hardware round-to-nearest-even packed conversion
+// (v_cvt_pk_bf16_f32).  Equal to rope_pair for finite, normal values; used for the prefill
+// key tiles only.
+__device__ __forceinline__ uint32_t pack_bf16(float x, float y) {
+    const floatx2 v = {x, y};
+    const bf16x2 h = __builtin_convertvector(v, bf16x2);
+    uint32_t w;
+    __builtin_memcpy(&w, &h, 4);
+    return w;
+}
+__device__ __forceinline__ void rope_pair_x2(uint32_t a, uint32_t b, uint32_t cs0, uint32_t cs1, uint32_t& na, uint32_t& nb) {
+    const float a0 = lo(a), a1 = hi(a), b0 = lo(b), b1 = hi(b);
+    const float c0 = lo(cs0), s0 = hi(cs0), c1 = lo(cs1), s1 = hi(cs1);
+    const uint32_t ac = pack_bf16(a0 * c0, a1 * c1), bs = pack_bf16(-b0 * s0, -b1 * s1);
+    const uint32_t bc = pack_bf16(b0 * c0, b1 * c1), as = pack_bf16(a0 * s0, a1 * s1);
+    na = pack_bf16(lo(ac) + lo(bs), hi(ac) + hi(bs));
+    nb = pack_bf16(lo(bc) + lo(as), hi(bc) + hi(as));
 }
 
 __device__ __forceinline__ void flash_store(const FlashParams& p, const KvStage& s, uint16_t* Ks, uint16_t* Vt) {
@@ -527,13 +557,7 @@ __device__ __forceinline__ void flash_store(const FlashParams& p, const KvStage&
                                  s.rr[2].x, s.rr[2].y, s.rr[2].z, s.rr[2].w, s.rr[3].x, s.rr[3].y, s.rr[3].z, s.rr[3].w};
         uint32_t ao[8], bo[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            float a0, b0, a1, b1;
-            rope_pair(lo(aw[i]), lo(bw[i]), rw[2 * i], a0, b0);
-            rope_pair(hi(aw[i]), hi(bw[i]), rw[2 * i + 1], a1, b1);
-            ao[i] = (bits(a0) & 0xffffu) | (bits(a1) << 16);
-            bo[i] = (bits(b0) & 0xffffu) | (bits(b1) << 16);
-        }
+        for (int i = 0; i < 8; ++i) rope_pair_x2(aw[i], bw[i], rw[2 * i], rw[2 * i + 1], ao[i], bo[i]);
         *reinterpret_cast<uint4*>(krow + part * 16) = make_uint4(ao[0], ao[1], ao[2], ao[3]);
         *reinterpret_cast<uint4*>(krow + part * 16 + 8) = make_uint4(ao[4], ao[5], ao[6], ao[7]);
         *reinterpret_cast<uint4*>(krow + 64 + part * 16) = make_uint4(bo[0], bo[1], bo[2], bo[3]);
@@ -551,8 +575,6 @@ __device__ __forceinline__ void flash_store(const FlashParams& p, const KvStage&
 
 // Two FP32 values as BF16 pairs hi + lo (RNE, v_cvt_pk_bf16_f32): hi + lo carries ~16
 // significant bits of each value.
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-typedef float floatx2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ void split_bf16(float a, float b, uint32_t& hw, uint32_t& lw) {
     const floatx2 v = {a, b};
     const bf16x2 h = __builtin_convertvector(v, bf16x2);
@@ -565,9 +587,14 @@ __device__ __forceinline__ void split_bf16(float a, float b, uint32_t& hw, uint3
 __global__ __launch_bounds__(256) void flash_prefill_kernel(const FlashParams p) {
     __shared__ __align__(16) uint16_t Ks[2][FK * KST];
     __shared__ __align__(16) uint16_t Vt[2][HEAD_DIM * VST];
+    __shared__ int s_last;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int col = lane & 31, half = lane >> 5;
-    const int t0 = blockIdx.x * FT;
+    // workgroup w -> part w / blocks of query block blocks - 1 - w % blocks: consecutive
+    // workgroups (dealt round-robin to the XCDs) take different blocks, longest first
+    const int nqb = flash_blocks(p.tokens);
+    const int qb = nqb - 1 - int(blockIdx.x) % nqb, part = int(blockIdx.x) / nqb;
+    const int t0 = qb * FT;
     const int t1 = min(t0 + FT, p.tokens);
     const int tq = t0 + wave * 2 + (col >> 4);
     const int head = col & 15;
@@ -579,6 +606,11 @@ __global__ __launch_bounds__(256) void flash_prefill_kernel(const FlashParams p)
     const uint32_t plo = p.p0 + uint32_t(t0), khi = p.p0 + uint32_t(t1 - 1);
     const uint32_t klo = p.full ? 0u : (plo > uint32_t(WINDOW - 1) ? plo - uint32_t(WINDOW - 1) : 0u);
     const int ntiles = int((khi + 1 - klo + FK - 1) / FK);
+    // The block's key tiles are split over up to FLASH_PARTS workgroups of about
+    // FLASH_PART_TILES tiles each, so long (late) query blocks do not set the kernel's length.
+    const int parts = min(FLASH_PARTS, (ntiles + FLASH_PART_TILES - 1) / FLASH_PART_TILES);
+    if (part >= parts) return;
+    const int j0 = part * ntiles / parts, j1 = (part + 1) * ntiles / parts;
 
     // Q^T fragments (B operand of S^T): k-step s covers dims 16s + 8*half .. +8
     bf16x8 qf[8];
@@ -595,13 +627,13 @@ __global__ __launch_bounds__(256) void flash_prefill_kernel(const FlashParams p)
     float m = NEG_INF, ls = 0.f;
 
     KvStage st;
-    flash_load(p, klo, khi, base, st);
+    flash_load(p, klo + uint32_t(j0 * FK), khi, base, st);
     flash_store(p, st, Ks[0], Vt[0]);
     __syncthreads();
-    for (int j = 0; j < ntiles; ++j) {
-        const int buf = j & 1;
+    for (int j = j0; j < j1; ++j) {
+        const int buf = (j - j0) & 1;
         const uint32_t k0 = klo + uint32_t(j * FK);
-        if (j + 1 < ntiles) flash_load(p, k0 + FK, khi, base, st);
+        if (j + 1 < j1) flash_load(p, k0 + FK, khi, base, st);
         // S^T = K Q^T for 64 keys (two 32-row tiles)
         floatx16 sacc[2];
 #pragma unroll
@@ -679,11 +711,69 @@ __global__ __launch_bounds__(256) void flash_prefill_kernel(const FlashParams p)
                 oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pl, oacc[dt], 0, 0, 0);
             }
         }
-        if (j + 1 < ntiles) flash_store(p, st, Ks[buf ^ 1], Vt[buf ^ 1]);
+        if (j + 1 < j1) flash_store(p, st, Ks[buf ^ 1], Vt[buf ^ 1]);
         __syncthreads();
     }
     // O = O^T / l; element i of d-tile dt is dim 32dt + 8(i/4) + 4*half + i%4
-    const float lt = ls + xor_lane<32>(ls);
+    float lt = ls + xor_lane<32>(ls);
+    if (parts > 1) {
+        // Partial (m, l, unnormalised O^T) of this part; the last part to finish merges all
+        // parts of the block in part order: M = max m_q, w_q = 2^(m_q - M),
+        // O = sum O_q w_q / sum l_q w_q.
+        const int colg = wave * 32 + col;
+        const uint32_t nslots = uint32_t(flash_blocks(p.tokens)) * FLASH_PARTS;
+        const __amdgpu_buffer_rsrc_t ov = buffer_view(p.part_o, nslots * (FT * HEADS) * HEAD_DIM * 4u);
+        const __amdgpu_buffer_rsrc_t mv = buffer_view(p.part_ml, nslots * (FT * HEADS) * 8u);
+        auto o_off = [&](int q) { return uint32_t(((size_t(qb) * FLASH_PARTS + q) * (FT * HEADS) + colg) * HEAD_DIM * 4); };
+        auto ml_off = [&](int q) { return uint32_t(((size_t(qb) * FLASH_PARTS + q) * (FT * HEADS) + colg) * 8); };
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+                buffer_store16_sc1(ov, o_off(part) + (32 * dt + 8 * g + 4 * half) * 4,
+                                   make_uint4(__float_as_uint(oacc[dt][4 * g]), __float_as_uint(oacc[dt][4 * g + 1]),
+                                              __float_as_uint(oacc[dt][4 * g + 2]), __float_as_uint(oacc[dt][4 * g + 3])));
+        if (half == 0) buffer_store8_sc1(mv, ml_off(part), make_uint2(__float_as_uint(m), __float_as_uint(lt)));
+        wait_stores();
+        __syncthreads();
+        if (tid == 0) s_last = atomicAdd(p.tickets + qb, 1u) == uint32_t(parts - 1);
+        __syncthreads();
+        if (!s_last) return;
+        float mq[FLASH_PARTS], lq[FLASH_PARTS];
+        float M = NEG_INF;
+#pragma unroll
+        for (int q = 0; q < FLASH_PARTS; ++q) {
+            if (q < parts) {
+                const uint2 v = buffer_load8_sc1(mv, ml_off(q));
+                mq[q] = __uint_as_float(v.x);
+                lq[q] = __uint_as_float(v.y);
+                M = fmaxf(M, mq[q]);
+            }
+        }
+        lt = 0.f;
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) oacc[dt][r] = 0.f;
+#pragma unroll
+        for (int q = 0; q < FLASH_PARTS; ++q) {
+            if (q < parts) {
+                const float w = __builtin_amdgcn_exp2f(mq[q] - M);
+                lt += lq[q] * w;
+#pragma unroll
+                for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        const uint4 v = buffer_load16_sc1(ov, o_off(q) + (32 * dt + 8 * g + 4 * half) * 4);
+                        oacc[dt][4 * g] += __uint_as_float(v.x) * w;
+                        oacc[dt][4 * g + 1] += __uint_as_float(v.y) * w;
+                        oacc[dt][4 * g + 2] += __uint_as_float(v.z) * w;
+                        oacc[dt][4 * g + 3] += __uint_as_float(v.w) * w;
+                    }
+            }
+        }
+        if (tid == 0) atomicExch(p.tickets + qb, 0u);  // ready for the next launch
+    }
     if (!qvalid) return;
     uint16_t* orow = p.out + size_t(tq) * ATTN + head * HEAD_DIM;
 #pragma unroll
@@ -764,7 +854,8 @@ void launch_qk_prep(const QkPrepParams& p, hipStream_t s) {
 
 void launch_flash_prefill(const FlashParams& p, hipStream_t s) {
     if (p.tokens < 1) return;
-    hipLaunchKernelGGL(flash_prefill_kernel, dim3((p.tokens + FT - 1) / FT), dim3(256), 0, s, p);
+    if (p.tokens > 65536 / FLASH_PARTS * 8) throw Error(E_INVAL, "flash prefill: too many tokens in one call");
+    hipLaunchKernelGGL(flash_prefill_kernel, dim3(flash_blocks(p.tokens) * FLASH_PARTS), dim3(256), 0, s, p);
 }
 
 }  // namespace plamo

@@ -270,6 +270,10 @@ Engine::Engine(std::shared_ptr<Model> mdl, int ctx, int nl, hipStream_t s)
     p_xn = arena.alloc_n<uint16_t>(size_t(chunk) * HIDDEN);
     p_att = arena.alloc_n<uint16_t>(size_t(chunk) * ATTN);
     p_q16 = arena.alloc_n<uint16_t>(size_t(chunk) * ATTN);
+    p_flash_o = arena.alloc_n<float>(flash_part_o_floats(chunk));
+    p_flash_ml = arena.alloc_n<float>(flash_part_ml_floats(chunk));
+    p_flash_tickets = arena.alloc_n<uint32_t>(size_t(flash_blocks(chunk)));
+    PLAMO_HIP(hipMemsetAsync(p_flash_tickets, 0, size_t(flash_blocks(chunk)) * 4, stream));
     p_act = arena.alloc_n<uint16_t>(size_t(chunk) * INTER);
     p_tokens = arena.alloc_n<int32_t>(size_t(chunk));
     PLAMO_HIP(hipEventCreate(&ev0));
@@ -457,6 +461,9 @@ void Engine::enqueue_prefill_chunk(int n, int p0, int lane, bool last_chunk, boo
         fa.p0 = uint32_t(p0);
         fa.tokens = n;
         fa.full = full;
+        fa.part_o = p_flash_o;
+        fa.part_ml = p_flash_ml;
+        fa.tickets = p_flash_tickets;
         launch_flash_prefill(fa, stream);
         GemmParams o{};
         o.w = L.o.w; o.table = L.o.table; o.x = p_att; o.y = p_proj; o.m = HIDDEN; o.k = ATTN; o.tokens = n;

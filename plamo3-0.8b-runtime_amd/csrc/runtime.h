@@ -77,6 +77,8 @@ class Engine {
     // prefill scratch (chunk rows)
     float *p_x, *p_qkv, *p_proj;
     uint16_t *p_xn, *p_att, *p_act, *p_q16;
+    float *p_flash_o, *p_flash_ml;  // split flash prefill workspace
+    uint32_t* p_flash_tickets;
     int32_t* p_tokens;
     size_t part_rows_cap;    // rows x parts the partial buffers hold
     // graph

@@ -83,7 +83,8 @@ def lib():
     (2040, 24, 2080, False),   # chunk bases 0 and 9 in one call
     (3000, 40, 2112, False),   # chunk-relative coordinates and a wrapped ring
     (0, 64, 64, True),         # global, keys exactly the tokens
-    (500, 37, 600, True),      # global, long prefix
+    (500, 37, 600, True),      # global, long prefix: key tiles split over two workgroups
+    (1100, 50, 1200, True),    # global, three parts merged
 ])
 def test_flash_prefill_matches_fp32(lib, p0, tokens, cap, full):
     print(f"  flash p0={p0} tokens={tokens} cap={cap} full={full}", flush=True)
