@@ -14,6 +14,8 @@
 //                     sampler history (counts, no-repeat-n-gram ban).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 #include "common.h"
 #include "device.h"
 #include "kernels.h"
@@ -27,7 +29,7 @@ namespace {
 // arithmetic per weight byte quadruples, so groups shrink to spread it over more waves.
 template <int N, int MAXR, int EPI>
 constexpr int gemv_u() {
-    if constexpr (EPI == EPI_SWIGLU) return MAXR == 1 ? 4 : 2;
+    if constexpr (EPI == EPI_SWIGLU) return 4;
     else if constexpr (N >= 6144) return MAXR == 1 ? 2 : 1;
     else return MAXR == 1 ? 4 : 2;
 }
@@ -1026,14 +1028,18 @@ void gemv_dispatch_n(bool packed, int maxr, Prologue pro, Epilogue epi, const Ge
 }  // namespace
 
 int gemv_group_rows(int n, int maxr, Epilogue epi) {
-    if (epi == EPI_SWIGLU) return maxr == 1 ? 4 : 2;
+    if (epi == EPI_SWIGLU) return 4;
     if (n >= 6144) return maxr == 1 ? 2 : 1;
     return maxr == 1 ? 4 : 2;
 }
 
 int gemv_blocks(int n, int maxr, Epilogue epi, int m) {
     const int groups = m / gemv_group_rows(n, maxr, epi);
-    return (groups + 3) / 4;  // one group per wave
+    const int b = (groups + 3) / 4;  // one group per wave
+    // Multi-row kernels: at most two workgroups per CU, each wave walking several groups
+    // (weights of the next in flight), so the activation prologue every workgroup
+    // recomputes is paid twice per CU instead of four to six times.
+    return maxr > 1 ? std::min(b, 512) : b;
 }
 
 void launch_gemv(int n, bool packed, int maxr, Prologue pro, Epilogue epi, const GemvParams& p, int blocks,
