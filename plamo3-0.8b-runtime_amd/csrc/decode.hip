@@ -220,6 +220,21 @@ template <bool PACKED>
 struct WRaw {
     uint4 v;
 };
+// Weight streams are read once per step: non-temporal loads, so they do not displace the
+// activations, KV rows and .p12 tables from the caches.
+__device__ __forceinline__ uint4 stream_load16(const void* p) {
+    typedef uint32_t v4 __attribute__((ext_vector_type(4)));
+    const v4 v = __builtin_nontemporal_load(reinterpret_cast<const v4*>(p));
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ uint2 stream_load8(const void* p) {
+    typedef uint32_t v2 __attribute__((ext_vector_type(2)));
+    const v2 v = __builtin_nontemporal_load(reinterpret_cast<const v2*>(p));
+    return make_uint2(v[0], v[1]);
+}
+__device__ __forceinline__ uint32_t stream_load4(const void* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p));
+}
 template <>
 struct WRaw<true> {
     uint4 v;            // raw: 8 weights; packed: .x/.y = 8 sign/mantissa bytes
@@ -235,7 +250,7 @@ __device__ __forceinline__ void request_w(const GemvParams& p, const int (&wrow)
         for (int u = 0; u < U; ++u)
 #pragma unroll
             for (int it = 0; it < IT; ++it)
-                r[u][it].v = *reinterpret_cast<const uint4*>(p.w + size_t(wrow[u]) * N + it * 512 + lane * 8);
+                r[u][it].v = stream_load16(p.w + size_t(wrow[u]) * N + it * 512 + lane * 8);
     } else {
         uint32_t e[U][IT];
 #pragma unroll
@@ -249,10 +264,10 @@ __device__ __forceinline__ void request_w(const GemvParams& p, const int (&wrow)
             for (int it = 0; it < IT; ++it) {
                 const uint8_t* blk = reinterpret_cast<const uint8_t*>(p.w) + (e[u][it] & ~63u);
                 const uint32_t tag = e[u][it] & 63u;
-                const uint2 lo8 = *reinterpret_cast<const uint2*>(blk + (tag ? sub * 8 : sub * 16));
-                const uint2 hi8 = *reinterpret_cast<const uint2*>(blk + (tag ? 0 : sub * 16 + 8));
+                const uint2 lo8 = stream_load8(blk + (tag ? sub * 8 : sub * 16));
+                const uint2 hi8 = stream_load8(blk + (tag ? 0 : sub * 16 + 8));
                 r[u][it].v = make_uint4(lo8.x, lo8.y, hi8.x, hi8.y);
-                r[u][it].nib = *reinterpret_cast<const uint32_t*>(blk + 128 + sub * 4);
+                r[u][it].nib = stream_load4(blk + 128 + sub * 4);
                 r[u][it].tag = tag;
             }
     }
