@@ -674,7 +674,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
             const uint32_t rw[16] = {rr[0].x, rr[0].y, rr[0].z, rr[0].w, rr[1].x, rr[1].y, rr[1].z, rr[1].w,
                                      rr[2].x, rr[2].y, rr[2].z, rr[2].w, rr[3].x, rr[3].y, rr[3].z, rr[3].w};
 #pragma unroll
-            for (int i = 0; i < 16; ++i) rope_pair(a[i], b[i], rw[i], a[i], b[i]);
+            for (int i = 0; i < 16; i += 2) rope_pair_x2f(a[i], b[i], rw[i], a[i + 1], b[i + 1], rw[i + 1]);
         }
         float* krow = ks + kj * KS;
 #pragma unroll

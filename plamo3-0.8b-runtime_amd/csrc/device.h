@@ -208,6 +208,39 @@ __device__ __forceinline__ void rope_pair(float a, float b, uint32_t cs, float& 
     rb = nb;
 }
 
+// rope_pair on two BF16 pairs at once (a = packed x[d], x'[d]; b = packed x[d+64], x'[d+64];
+// cs0 / cs1 their cos | sin << 16) with the hardware round-to-nearest-even packed conversion
+// (v_cvt_pk_bf16_f32), which rounds every non-NaN FP32 value (denormals included, FP32
+// denormals are not flushed) exactly as `bits` does: the results equal two rope_pair calls.
+typedef __bf16 dev_bf16x2 __attribute__((ext_vector_type(2)));
+typedef float dev_floatx2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_bf16(float x, float y) {
+    const dev_floatx2 v = {x, y};
+    const dev_bf16x2 h = __builtin_convertvector(v, dev_bf16x2);
+    uint32_t w;
+    __builtin_memcpy(&w, &h, 4);
+    return w;
+}
+__device__ __forceinline__ void rope_pair_x2(uint32_t a, uint32_t b, uint32_t cs0, uint32_t cs1, uint32_t& na, uint32_t& nb) {
+    const float a0 = lo(a), a1 = hi(a), b0 = lo(b), b1 = hi(b);
+    const float c0 = lo(cs0), s0 = hi(cs0), c1 = lo(cs1), s1 = hi(cs1);
+    const uint32_t ac = pack_bf16(a0 * c0, a1 * c1), bs = pack_bf16(-b0 * s0, -b1 * s1);
+    const uint32_t bc = pack_bf16(b0 * c0, b1 * c1), as = pack_bf16(a0 * s0, a1 * s1);
+    na = pack_bf16(lo(ac) + lo(bs), hi(ac) + hi(bs));
+    nb = pack_bf16(lo(bc) + lo(as), hi(bc) + hi(as));
+}
+
+// Same on FP32 operands (BF16-valued), results as FP32: (a0, b0) with cs0 and (a1, b1) with cs1.
+__device__ __forceinline__ void rope_pair_x2f(float& a0, float& b0, uint32_t cs0, float& a1, float& b1, uint32_t cs1) {
+    const float c0 = lo(cs0), s0 = hi(cs0), c1 = lo(cs1), s1 = hi(cs1);
+    const uint32_t ac = pack_bf16(a0 * c0, a1 * c1), bs = pack_bf16(-b0 * s0, -b1 * s1);
+    const uint32_t bc = pack_bf16(b0 * c0, b1 * c1), as = pack_bf16(a0 * s0, a1 * s1);
+    const uint32_t na = pack_bf16(lo(ac) + lo(bs), hi(ac) + hi(bs));
+    const uint32_t nb = pack_bf16(lo(bc) + lo(as), hi(bc) + hi(as));
+    a0 = lo(na); a1 = hi(na);
+    b0 = lo(nb); b1 = hi(nb);
+}
+
 // q/k RMSNorm over 128 with +1 offset (Kernels.metal:236-246) for the 8 dims a lane of a
 // 16-lane group owns: d = sub*4+j and d+64 (j = 0..3).  Squares are summed in that order,
 // then over the 16 lanes by an XOR butterfly.

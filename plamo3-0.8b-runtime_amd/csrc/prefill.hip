@@ -521,26 +521,6 @@ __device__ __forceinline__ uint32_t u16_of(const uint4& v, int k) {
     return (k & 1) ? (w >> 16) : (w & 0xffffu);
 }
 
-// rope_pair on two BF16 pairs at once (a = packed x[d], x'[d]; b = packed x[d+64], x'[d+64];
-// cs0 / cs1 their cos | sin << 16) with the hardware round-to-nearest-even packed conversion
-// (v_cvt_pk_bf16_f32).  Equal to rope_pair for finite, normal values; used for the prefill
-// key tiles only.
-__device__ __forceinline__ uint32_t pack_bf16(float x, float y) {
-    const floatx2 v = {x, y};
-    const bf16x2 h = __builtin_convertvector(v, bf16x2);
-    uint32_t w;
-    __builtin_memcpy(&w, &h, 4);
-    return w;
-}
-__device__ __forceinline__ void rope_pair_x2(uint32_t a, uint32_t b, uint32_t cs0, uint32_t cs1, uint32_t& na, uint32_t& nb) {
-    const float a0 = lo(a), a1 = hi(a), b0 = lo(b), b1 = hi(b);
-    const float c0 = lo(cs0), s0 = hi(cs0), c1 = lo(cs1), s1 = hi(cs1);
-    const uint32_t ac = pack_bf16(a0 * c0, a1 * c1), bs = pack_bf16(-b0 * s0, -b1 * s1);
-    const uint32_t bc = pack_bf16(b0 * c0, b1 * c1), as = pack_bf16(a0 * s0, a1 * s1);
-    na = pack_bf16(lo(ac) + lo(bs), hi(ac) + hi(bs));
-    nb = pack_bf16(lo(bc) + lo(as), hi(bc) + hi(as));
-}
-
 __device__ __forceinline__ void flash_store(const FlashParams& p, const KvStage& s, uint16_t* Ks, uint16_t* Vt) {
     const int tid = threadIdx.x;
     const int part = tid & 3, key = tid >> 2;
