@@ -45,8 +45,8 @@ struct QkPrepParams {
 
 // Flash prefill splits the key tiles of a query block (8 tokens x 16 heads) over up to
 // FLASH_PARTS workgroups; their partial results meet in a workspace.
-constexpr int FLASH_PARTS = 2;
-constexpr int FLASH_PART_TILES = 16;         // 64-key tiles a part aims at
+constexpr int FLASH_PARTS = 3;
+constexpr int FLASH_PART_TILES = 11;         // 64-key tiles a part aims at
 __host__ __device__ inline int flash_blocks(int tokens) { return (tokens + 7) / 8; }
 // workspace floats: per block and part, O^T [128 columns][128 dims] and (m, l) per column
 inline size_t flash_part_o_floats(int tokens) { return size_t(flash_blocks(tokens)) * FLASH_PARTS * 128 * 128; }

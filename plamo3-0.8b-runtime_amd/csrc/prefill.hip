@@ -564,7 +564,7 @@ __device__ __forceinline__ void split_bf16(float a, float b, uint32_t& hw, uint3
     __builtin_memcpy(&lw, &l, 4);
 }
 
-__global__ __launch_bounds__(256) void flash_prefill_kernel(const FlashParams p) {
+__global__ __launch_bounds__(256, 2) void flash_prefill_kernel(const FlashParams p) {
     __shared__ __align__(16) uint16_t Ks[2][FK * KST];
     __shared__ __align__(16) uint16_t Vt[2][HEAD_DIM * VST];
     __shared__ int s_last;
