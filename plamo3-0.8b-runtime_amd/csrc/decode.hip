@@ -419,33 +419,36 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvParams p) {
 #pragma unroll
             for (int q = 0; q < MAXR; ++q) acc[u][q] = wave_sum(acc[u][q]);
 
-        if constexpr (EPI == EPI_ROUND) {
-            if (lane == 0)
+        // Every lane holds every sum after the butterflies; lane q*U + u (q*H + k for SwiGLU)
+        // writes output (row q, weight row u), so the epilogue runs once, in parallel.
+        if constexpr (EPI == EPI_ROUND || EPI == EPI_BF16) {
+            const int q = lane / U, u = lane % U;
+            float v = 0.f;
+            int r = wrow[0];
 #pragma unroll
-                for (int q = 0; q < MAXR; ++q)
-                    if (q < rows)
+            for (int qq = 0; qq < MAXR; ++qq)
 #pragma unroll
-                        for (int u = 0; u < U; ++u) p.out[size_t(q) * p.m + wrow[u]] = roundbf(acc[u][q]);
-        } else if constexpr (EPI == EPI_BF16) {
-            if (lane == 0)
-#pragma unroll
-                for (int q = 0; q < MAXR; ++q)
-                    if (q < rows)
-#pragma unroll
-                        for (int u = 0; u < U; ++u) p.out16[size_t(q) * p.m + wrow[u]] = uint16_t(bits(acc[u][q]));
+                for (int uu = 0; uu < U; ++uu)
+                    if (qq == q && uu == u) { v = acc[uu][qq]; r = wrow[uu]; }
+            if (lane < MAXR * U && q < rows) {
+                if constexpr (EPI == EPI_ROUND) p.out[size_t(q) * p.m + r] = roundbf(v);
+                else p.out16[size_t(q) * p.m + r] = uint16_t(bits(v));
+            }
         } else if constexpr (EPI == EPI_SWIGLU) {
             // gates = roundbf(g), ups = roundbf(u); y = roundbf(roundbf(g/(1+exp(-g))) * u)
             // (Kernels.metal:202-210)
-            if (lane == 0)
+            const int q = lane / H, k = lane % H;
+            float gv = 0.f, uv = 0.f;
 #pragma unroll
-                for (int q = 0; q < MAXR; ++q)
-                    if (q < rows)
+            for (int qq = 0; qq < MAXR; ++qq)
 #pragma unroll
-                        for (int k = 0; k < H; ++k) {
-                            const float gt = roundbf(acc[k][q]);
-                            const float up = roundbf(acc[H + k][q]);
-                            p.out[size_t(q) * INTER + H * g + k] = roundbf(roundbf(gt / (1.0f + exp_det(-gt))) * up);
-                        }
+                for (int kk = 0; kk < H; ++kk)
+                    if (qq == q && kk == k) { gv = acc[kk][qq]; uv = acc[H + kk][qq]; }
+            if (lane < MAXR * H && q < rows) {
+                const float gt = roundbf(gv);
+                const float up = roundbf(uv);
+                p.out[size_t(q) * INTER + H * g + k] = roundbf(roundbf(gt / (1.0f + exp_det(-gt))) * up);
+            }
         } else {  // EPI_LOGITS
 #pragma unroll
             for (int q = 0; q < MAXR; ++q) {
