@@ -414,42 +414,43 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvParams p) {
                 }
             }
         }
+        if constexpr (EPI == EPI_ROUND || EPI == EPI_BF16 || EPI == EPI_SWIGLU) {
+            // Reduce-scatter: lane holds the sum of value idx = u * MAXR + q, idx = lane >> S
+            // (the gate/up split is the top bit of idx, so a SwiGLU gate lane finds its up
+            // sum 32 lanes away).  Lane (idx << S) writes output (row q, weight row u).
+            constexpr int K = U * MAXR, S = 6 - log2_pow2(K);
+            float vals[K];
 #pragma unroll
-        for (int u = 0; u < U; ++u)
+            for (int u = 0; u < U; ++u)
 #pragma unroll
-            for (int q = 0; q < MAXR; ++q) acc[u][q] = wave_sum(acc[u][q]);
-
-        // Every lane holds every sum after the butterflies; lane q*U + u (q*H + k for SwiGLU)
-        // writes output (row q, weight row u), so the epilogue runs once, in parallel.
-        if constexpr (EPI == EPI_ROUND || EPI == EPI_BF16) {
-            const int q = lane / U, u = lane % U;
-            float v = 0.f;
-            int r = wrow[0];
+                for (int q = 0; q < MAXR; ++q) vals[u * MAXR + q] = acc[u][q];
+            const float t = wave_sum_scatter<K>(vals);
+            const int idx = lane >> S, u = idx / MAXR, q = idx % MAXR;
+            const bool writer = (lane & ((1 << S) - 1)) == 0 && q < rows;
+            if constexpr (EPI == EPI_SWIGLU) {
+                // gates = roundbf(g), ups = roundbf(u); y = roundbf(roundbf(g/(1+exp(-g))) * u)
+                // (Kernels.metal:202-210)
+                const float upv = xor_lane<32>(t);
+                if (writer && u < H) {
+                    const float gt = roundbf(t);
+                    const float up = roundbf(upv);
+                    p.out[size_t(q) * INTER + H * g + u] = roundbf(roundbf(gt / (1.0f + exp_det(-gt))) * up);
+                }
+            } else {
+                int r = wrow[0];
 #pragma unroll
-            for (int qq = 0; qq < MAXR; ++qq)
-#pragma unroll
-                for (int uu = 0; uu < U; ++uu)
-                    if (qq == q && uu == u) { v = acc[uu][qq]; r = wrow[uu]; }
-            if (lane < MAXR * U && q < rows) {
-                if constexpr (EPI == EPI_ROUND) p.out[size_t(q) * p.m + r] = roundbf(v);
-                else p.out16[size_t(q) * p.m + r] = uint16_t(bits(v));
-            }
-        } else if constexpr (EPI == EPI_SWIGLU) {
-            // gates = roundbf(g), ups = roundbf(u); y = roundbf(roundbf(g/(1+exp(-g))) * u)
-            // (Kernels.metal:202-210)
-            const int q = lane / H, k = lane % H;
-            float gv = 0.f, uv = 0.f;
-#pragma unroll
-            for (int qq = 0; qq < MAXR; ++qq)
-#pragma unroll
-                for (int kk = 0; kk < H; ++kk)
-                    if (qq == q && kk == k) { gv = acc[kk][qq]; uv = acc[H + kk][qq]; }
-            if (lane < MAXR * H && q < rows) {
-                const float gt = roundbf(gv);
-                const float up = roundbf(uv);
-                p.out[size_t(q) * INTER + H * g + k] = roundbf(roundbf(gt / (1.0f + exp_det(-gt))) * up);
+                for (int uu = 1; uu < U; ++uu)
+                    if (uu == u) r = wrow[uu];
+                if (writer) {
+                    if constexpr (EPI == EPI_ROUND) p.out[size_t(q) * p.m + r] = roundbf(t);
+                    else p.out16[size_t(q) * p.m + r] = uint16_t(bits(t));
+                }
             }
         } else {  // EPI_LOGITS
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+#pragma unroll
+                for (int q = 0; q < MAXR; ++q) acc[u][q] = wave_sum(acc[u][q]);
 #pragma unroll
             for (int q = 0; q < MAXR; ++q) {
                 if (q >= rows) continue;

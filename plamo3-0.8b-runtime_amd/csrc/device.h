@@ -56,6 +56,44 @@ __device__ __forceinline__ float xor_lane(float v) {
     return __uint_as_float(xor_lane<O>(__float_as_uint(v)));
 }
 
+// One level of a reduce-scatter over K live values: lanes with bit O set keep the upper half,
+// the others the lower half, each adding the partner lane's copy (own + partner, as the
+// butterfly does).
+template <int K, int O>
+__device__ __forceinline__ void rs_level(float* v, uint32_t lane) {
+    const bool upper = (lane & uint32_t(O)) != 0;
+#pragma unroll
+    for (int i = 0; i < K / 2; ++i) {
+        const float keep = upper ? v[i + K / 2] : v[i];
+        const float send = upper ? v[i] : v[i + K / 2];
+        v[i] = keep + xor_lane<O>(send);
+    }
+}
+
+// Sums of K values over the wavefront (K a power of two, at most 64) with exactly the
+// pairwise additions of K butterflies, but one exchange per value and level only while the
+// values last: afterwards every lane holds the total of value lane >> (6 - log2 K).
+template <int K>
+__device__ __forceinline__ float wave_sum_scatter(float (&v)[K]) {
+    static_assert(K >= 1 && K <= 64 && (K & (K - 1)) == 0, "power of two up to 64");
+    const uint32_t lane = threadIdx.x & 63u;
+    if constexpr (K >= 2) rs_level<K, 32>(v, lane);
+    if constexpr (K >= 4) rs_level<K / 2, 16>(v, lane);
+    if constexpr (K >= 8) rs_level<K / 4, 8>(v, lane);
+    if constexpr (K >= 16) rs_level<K / 8, 4>(v, lane);
+    if constexpr (K >= 32) rs_level<K / 16, 2>(v, lane);
+    if constexpr (K >= 64) rs_level<K / 32, 1>(v, lane);
+    float t = v[0];
+    if constexpr (K < 2) t += xor_lane<32>(t);
+    if constexpr (K < 4) t += xor_lane<16>(t);
+    if constexpr (K < 8) t += xor_lane<8>(t);
+    if constexpr (K < 16) t += xor_lane<4>(t);
+    if constexpr (K < 32) t += xor_lane<2>(t);
+    if constexpr (K < 64) t += xor_lane<1>(t);
+    return t;
+}
+constexpr int log2_pow2(int k) { return k <= 1 ? 0 : 1 + log2_pow2(k / 2); }
+
 // Butterfly reductions over the 64-lane wavefront (XOR offsets 32, 16, 8, 4, 2, 1): lane i
 // adds lane i ^ o at each level, so every lane ends with the same bits.
 __device__ __forceinline__ float wave_sum(float v) {
