@@ -43,8 +43,10 @@ constexpr int gemv_u() {
 template <int N, int MAXR, int PRO>
 struct Staged {
     static constexpr int V = (N + 1023) / 1024;  // PLAIN: float4 per thread and row
+    static constexpr int V16 = (N + 2047) / 2048; // PLAIN16: 8 BF16 per thread and row
     static constexpr int E = HIDDEN / 256;       // norm prologues: elements per thread (6t .. 6t+5)
     float4 v[PRO == PRO_PLAIN ? MAXR : 1][V];
+    uint4 h[PRO == PRO_PLAIN16 ? MAXR : 1][V16];
     float2 a[PRO == PRO_RESID ? MAXR : 1][E / 2];   // RESID: projection output
     float2 r[PRO == PRO_RESID ? MAXR : 1][E / 2];   // RESID: residual stream
     uint32_t emb[PRO == PRO_EMBED ? MAXR : 1][E / 2];  // EMBED: embedding row (BF16 pairs)
@@ -66,6 +68,17 @@ __device__ __forceinline__ void stage_load(const GemvParams& p, int rb, Staged<N
             for (int k = 0; k < V; ++k) {
                 const int e = (tid + 256 * k) * 4;
                 S.v[q][k] = *reinterpret_cast<const float4*>(p.in + qq * N + (e < N ? e : N - 4));
+            }
+        }
+    } else if constexpr (PRO == PRO_PLAIN16) {
+        constexpr int V16 = Staged<N, MAXR, PRO>::V16;
+#pragma unroll
+        for (int q = 0; q < MAXR; ++q) {
+            const int qq = q < rb ? q : rb - 1;
+#pragma unroll
+            for (int k = 0; k < V16; ++k) {
+                const int e = (tid + 256 * k) * 8;
+                S.h[q][k] = *reinterpret_cast<const uint4*>(p.in16 + qq * N + (e < N ? e : N - 8));
             }
         }
     } else {
@@ -117,6 +130,17 @@ __device__ __forceinline__ void stage_finish(const GemvParams& p, int rows, cons
                 const uint32_t lo2 = (bits(S.v[q][k].x) & 0xffffu) | (bits(S.v[q][k].y) << 16);
                 const uint32_t hi2 = (bits(S.v[q][k].z) & 0xffffu) | (bits(S.v[q][k].w) << 16);
                 *reinterpret_cast<uint2*>(&xs[q * N + e]) = make_uint2(lo2, hi2);
+            }
+        }
+    } else if constexpr (PRO == PRO_PLAIN16) {
+        constexpr int V16 = Staged<N, MAXR, PRO>::V16;
+#pragma unroll
+        for (int q = 0; q < MAXR; ++q) {
+            if (q >= rows) break;
+#pragma unroll
+            for (int k = 0; k < V16; ++k) {
+                const int e = (tid + 256 * k) * 8;
+                if (e < N) *reinterpret_cast<uint4*>(&xs[q * N + e]) = S.h[q][k];
             }
         }
     } else {
@@ -434,7 +458,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvParams p) {
                 if (writer && u < H) {
                     const float gt = roundbf(t);
                     const float up = roundbf(upv);
-                    p.out[size_t(q) * INTER + H * g + u] = roundbf(roundbf(gt / (1.0f + exp_det(-gt))) * up);
+                    p.out16[size_t(q) * INTER + H * g + u] = uint16_t(bits(roundbf(gt / (1.0f + exp_det(-gt))) * up));
                 }
             } else {
                 int r = wrow[0];
@@ -754,8 +778,8 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
         const int h = hg * HG + hl;
         const float of0 = o[0][0] + o[0][1], of1 = o[1][0] + o[1][1];
         if (nparts == 1) {  // one partition: the merge reduces to o / l (exp(0) == 1 exactly)
-            p.out[size_t(q) * ATTN + h * HEAD_DIM + 2 * e] = roundbf(of0 / l_s[hl]);
-            p.out[size_t(q) * ATTN + h * HEAD_DIM + 2 * e + 1] = roundbf(of1 / l_s[hl]);
+            p.out16[size_t(q) * ATTN + h * HEAD_DIM + 2 * e] = uint16_t(bits(of0 / l_s[hl]));
+            p.out16[size_t(q) * ATTN + h * HEAD_DIM + 2 * e + 1] = uint16_t(bits(of1 / l_s[hl]));
         } else {
             buffer_store8_sc1(oview, uint32_t((pslot * HEADS + h) * HEAD_DIM + 2 * e) * 4u,
                               make_uint2(__float_as_uint(of0), __float_as_uint(of1)));
@@ -816,7 +840,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
         }
 #pragma unroll
         for (int i = 0; i < 2; ++i)
-            p.out[size_t(q) * ATTN + (hg * HG + hb + 2 * i) * HEAD_DIM + d] = roundbf(num[i] / den[i]);
+            p.out16[size_t(q) * ATTN + (hg * HG + hb + 2 * i) * HEAD_DIM + d] = uint16_t(bits(num[i] / den[i]));
     } else {  // more partitions than LDS holds: read them from memory
         if (tid < HG) {
             const int h = hg * HG + tid;
@@ -841,7 +865,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
             }
 #pragma unroll
         for (int i = 0; i < 2; ++i)
-            p.out[size_t(q) * ATTN + (hg * HG + hb + 2 * i) * HEAD_DIM + d] = roundbf(num[i] / den_s[hb + 2 * i]);
+            p.out16[size_t(q) * ATTN + (hg * HG + hb + 2 * i) * HEAD_DIM + d] = uint16_t(bits(num[i] / den_s[hb + 2 * i]));
     }
     if (tid == 0) atomicExch(ticket, 0u);  // ready for the next launch
 }
@@ -1013,8 +1037,8 @@ void gemv_dispatch_epi(Prologue pro, Epilogue epi, const GemvParams& p, int bloc
         else throw Error(E_INVAL, "unsupported GEMV variant");
         return;
     }
-    if (pro == PRO_PLAIN) {
-        if (epi == EPI_ROUND) PLAMO_GEMV(PRO_PLAIN, EPI_ROUND);
+    if (pro == PRO_PLAIN16) {
+        if (epi == EPI_ROUND) PLAMO_GEMV(PRO_PLAIN16, EPI_ROUND);
         else throw Error(E_INVAL, "unsupported GEMV variant");
         return;
     }

@@ -44,7 +44,7 @@ struct DecodeBuffers {
     uint32_t* tickets;        // [1] spare ticket, zero between launches
 };
 
-enum Prologue { PRO_PLAIN = 0, PRO_EMBED = 1, PRO_RESID = 2 };
+enum Prologue { PRO_PLAIN = 0, PRO_EMBED = 1, PRO_RESID = 2, PRO_PLAIN16 = 3 };
 enum Epilogue { EPI_ROUND = 0, EPI_SWIGLU = 1, EPI_LOGITS = 2, EPI_BF16 = 3 };
 
 struct GemvParams {
@@ -57,6 +57,7 @@ struct GemvParams {
     uint32_t lane_mask;       // always 0: makes the state read a per-lane (vector) load
     // prologue
     const float* in;          // PLAIN: [rows][n]; RESID: projection output [rows][1536]
+    const uint16_t* in16;     // PLAIN16: BF16 [rows][n] (half the bytes every workgroup stages)
     const float* resid_in;    // RESID: residual stream x
     float* resid_out;         // EMBED/RESID: updated residual (written by block 0)
     const uint16_t* g_post;   // RESID: post norm weight
@@ -65,8 +66,8 @@ struct GemvParams {
     const uint16_t* embed;    // EMBED: embedding table [VOCAB][1536]
     float* hidden;            // optional: normalised rows (final hidden)
     // epilogue
-    float* out;               // ROUND/SWIGLU: FP32 [rows][m or m/2]
-    uint16_t* out16;          // LOGITS/BF16: [rows][m]
+    float* out;               // ROUND: FP32 [rows][m]
+    uint16_t* out16;          // LOGITS/BF16: [rows][m]; SWIGLU: BF16 [rows][m/2]
     DecodeBuffers bufs;       // LOGITS: sampler + argmax partials + state update
 };
 
@@ -85,7 +86,7 @@ struct AttnParams {
     float* part_o;            // [ROWS][parts][16][128]
     uint32_t parts;           // grid.x
     uint32_t* tickets;        // [rows][head groups], zero between launches
-    float* out;               // FP32 [rows][2048]
+    uint16_t* out16;          // BF16 [rows][2048]
 };
 
 // decode.hip

@@ -230,11 +230,11 @@ Engine::Engine(std::shared_ptr<Model> mdl, int ctx, int nl, hipStream_t s)
         PLAMO_HIP(hipMemsetAsync(values[l], 0, n * 2, stream));
     }
     qkv = arena.alloc_n<float>(ROWS * QKV);
-    att = arena.alloc_n<float>(ROWS * ATTN);
+    att = arena.alloc_n<uint16_t>(ROWS * ATTN);
     proj = arena.alloc_n<float>(ROWS * HIDDEN);
     x0 = arena.alloc_n<float>(ROWS * HIDDEN);
     x1 = arena.alloc_n<float>(ROWS * HIDDEN);
-    act = arena.alloc_n<float>(ROWS * INTER);
+    act = arena.alloc_n<uint16_t>(ROWS * INTER);
     hidden = arena.alloc_n<float>(ROWS * HIDDEN);
     resid_scratch = arena.alloc_n<float>(ROWS * HIDDEN);
     logits = arena.alloc_n<uint16_t>(size_t(ROWS) * VOCAB);
@@ -359,7 +359,7 @@ void Engine::enqueue_step(bool head) {
         a.part_o = part_o;
         a.parts = full ? decode_parts_global : decode_parts_local;
         a.tickets = attn_tickets;
-        a.out = att;
+        a.out16 = att;
         launch_attention(full, a, ROWS, stream);
         GemvParams o{};
         o.state = state;
@@ -367,9 +367,9 @@ void Engine::enqueue_step(bool head) {
         o.m = HIDDEN;
         o.w = L.o.w;
         o.table = L.o.table;
-        o.in = att;
+        o.in16 = att;
         o.out = proj;
-        launch_gemv(ATTN, pk, maxr, PRO_PLAIN, EPI_ROUND, o, gemv_blocks(ATTN, maxr, EPI_ROUND, HIDDEN), stream);
+        launch_gemv(ATTN, pk, maxr, PRO_PLAIN16, EPI_ROUND, o, gemv_blocks(ATTN, maxr, EPI_ROUND, HIDDEN), stream);
         GemvParams u{};
         u.state = state;
         u.rows = ROWS;
@@ -382,7 +382,7 @@ void Engine::enqueue_step(bool head) {
         u.g_post = L.post;
         u.post_offset = POST_MIXER_OFFSET;
         u.g_next = L.pre_mlp;
-        u.out = act;
+        u.out16 = act;
         launch_gemv(HIDDEN, pk, maxr, PRO_RESID, EPI_SWIGLU, u, gemv_blocks(HIDDEN, maxr, EPI_SWIGLU, 2 * INTER), stream);
         GemvParams d{};
         d.state = state;
@@ -390,9 +390,9 @@ void Engine::enqueue_step(bool head) {
         d.m = HIDDEN;
         d.w = L.down.w;
         d.table = L.down.table;
-        d.in = act;
+        d.in16 = act;
         d.out = proj;
-        launch_gemv(INTER, pk, maxr, PRO_PLAIN, EPI_ROUND, d, gemv_blocks(INTER, maxr, EPI_ROUND, HIDDEN), stream);
+        launch_gemv(INTER, pk, maxr, PRO_PLAIN16, EPI_ROUND, d, gemv_blocks(INTER, maxr, EPI_ROUND, HIDDEN), stream);
     }
     if (head) enqueue_head(proj, x1, ROWS);
 }

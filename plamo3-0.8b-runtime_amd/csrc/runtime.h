@@ -66,7 +66,8 @@ class Engine {
     uint16_t *keys[LAYERS], *values[LAYERS];
     int capacity[LAYERS];
     // decode scratch (ROWS rows)
-    float *qkv, *att, *proj, *x0, *x1, *act, *hidden, *resid_scratch;
+    float *qkv, *proj, *x0, *x1, *hidden, *resid_scratch;
+    uint16_t *att, *act;  // BF16 attention output and SwiGLU activations
     uint16_t* logits;
     StepState* state;        // device
     StepState* host_state;   // pinned mirror
