@@ -184,15 +184,22 @@ __device__ __forceinline__ void stage_finish(const GemvParams& p, int rows, cons
                 if ((tid & 63) == 0) red[q * 4 + (tid >> 6)] = ss[q];
             }
             __syncthreads();
+            // BF16 roundings two at a time (packed RNE conversion, identical to `roundbf`)
+            float g[E];
+#pragma unroll
+            for (int k = 0; k < E; k += 2) round_bf16x2(gp[k] + p.post_offset, gp[k + 1] + p.post_offset, g[k], g[k + 1]);
 #pragma unroll
             for (int q = 0; q < MAXR; ++q) {
                 const float total = (red[q * 4] + red[q * 4 + 1]) + (red[q * 4 + 2] + red[q * 4 + 3]);
                 const float r = 1.0f / sqrtf(total / float(HIDDEN) + 1e-6f);
 #pragma unroll
-                for (int k = 0; k < E; ++k) {
-                    const float g = roundbf(gp[k] + p.post_offset);
-                    const float z = roundbf(roundbf(pv[q][k] * r) * g);
-                    xv[q][k] = (q < rows) ? roundbf(rv[q][k] + z) : 0.f;
+                for (int k = 0; k < E; k += 2) {
+                    float t0, t1, z0, z1, x0, x1;
+                    round_bf16x2(pv[q][k] * r, pv[q][k + 1] * r, t0, t1);
+                    round_bf16x2(t0 * g[k], t1 * g[k + 1], z0, z1);
+                    round_bf16x2(rv[q][k] + z0, rv[q][k + 1] + z1, x0, x1);
+                    xv[q][k] = (q < rows) ? x0 : 0.f;
+                    xv[q][k + 1] = (q < rows) ? x1 : 0.f;
                 }
             }
             __syncthreads();
@@ -200,10 +207,7 @@ __device__ __forceinline__ void stage_finish(const GemvParams& p, int rows, cons
         // next norm with +1 offset (Kernels.metal:76-89)
         float gn[E];
 #pragma unroll
-        for (int k = 0; k < E / 2; ++k) {
-            gn[2 * k] = roundbf(lo(S.gn[k]) + 1.0f);
-            gn[2 * k + 1] = roundbf(hi(S.gn[k]) + 1.0f);
-        }
+        for (int k = 0; k < E / 2; ++k) round_bf16x2(lo(S.gn[k]) + 1.0f, hi(S.gn[k]) + 1.0f, gn[2 * k], gn[2 * k + 1]);
 #pragma unroll
         for (int q = 0; q < MAXR; ++q) {
             ss[q] = 0.f;
@@ -219,13 +223,19 @@ __device__ __forceinline__ void stage_finish(const GemvParams& p, int rows, cons
             const float total = (red[q * 4] + red[q * 4 + 1]) + (red[q * 4 + 2] + red[q * 4 + 3]);
             const float r = 1.0f / sqrtf(total / float(HIDDEN) + 1e-6f);
 #pragma unroll
-            for (int k = 0; k < E; ++k) {
+            for (int k = 0; k < E; k += 2) {
                 const int i = tid * E + k;
-                const float xn = roundbf(roundbf(xv[q][k] * r) * gn[k]);
-                xs[q * HIDDEN + i] = uint16_t(bits(xn));
+                float t0, t1;
+                round_bf16x2(xv[q][k] * r, xv[q][k + 1] * r, t0, t1);
+                const uint32_t xn2 = pack_bf16(t0 * gn[k], t1 * gn[k + 1]);  // the two BF16 results
+                *reinterpret_cast<uint32_t*>(&xs[q * HIDDEN + i]) = xn2;
                 if (blockIdx.x == 0) {
                     p.resid_out[q * HIDDEN + i] = xv[q][k];
-                    if (p.hidden) p.hidden[q * HIDDEN + i] = xn;
+                    p.resid_out[q * HIDDEN + i + 1] = xv[q][k + 1];
+                    if (p.hidden) {
+                        p.hidden[q * HIDDEN + i] = lo(xn2);
+                        p.hidden[q * HIDDEN + i + 1] = hi(xn2);
+                    }
                 }
             }
         }

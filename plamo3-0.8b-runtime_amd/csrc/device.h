@@ -246,6 +246,9 @@ __device__ __forceinline__ void rope_pair(float a, float b, uint32_t cs, float& 
     rb = nb;
 }
 
+// roundbf of two values with one packed conversion (same bits as two `roundbf` calls).
+__device__ __forceinline__ void round_bf16x2(float x, float y, float& rx, float& ry);
+
 // rope_pair on two BF16 pairs at once (a = packed x[d], x'[d]; b = packed x[d+64], x'[d+64];
 // cs0 / cs1 their cos | sin << 16) with the hardware round-to-nearest-even packed conversion
 // (v_cvt_pk_bf16_f32), which rounds every non-NaN FP32 value (denormals included, FP32
@@ -266,6 +269,12 @@ __device__ __forceinline__ void rope_pair_x2(uint32_t a, uint32_t b, uint32_t cs
     const uint32_t bc = pack_bf16(b0 * c0, b1 * c1), as = pack_bf16(a0 * s0, a1 * s1);
     na = pack_bf16(lo(ac) + lo(bs), hi(ac) + hi(bs));
     nb = pack_bf16(lo(bc) + lo(as), hi(bc) + hi(as));
+}
+
+__device__ __forceinline__ void round_bf16x2(float x, float y, float& rx, float& ry) {
+    const uint32_t w = pack_bf16(x, y);
+    rx = lo(w);
+    ry = hi(w);
 }
 
 // Same on FP32 operands (BF16-valued), results as FP32: (a0, b0) with cs0 and (a1, b1) with cs1.
