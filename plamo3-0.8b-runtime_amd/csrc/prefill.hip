@@ -14,6 +14,8 @@
 //   flash_prefill   prefill attention (Runtime.swift:389-444) as MFMA flash attention.
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "common.h"
 #include "device.h"
 #include "kernels.h"
@@ -132,9 +134,12 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, const floatx1
 #pragma unroll
                 for (int j = 0; j < TW; j += 2) {  // LDS rows of tile j are gate rows, of j + 1 the matching up rows
                     const uint32_t m = uint32_t(n0 + ((ww * TW + j) >> 1) * 32 + jc);
+                    // hardware exp2 and reciprocal: the prefill is checked against a tolerance
+                    // (decode keeps the exact sequence of `exp_det` and IEEE division)
                     const float gt = roundbf(acc[i][j][r]);
                     const float up = roundbf(acc[i][j + 1][r]);
-                    buffer_store2(yv, (t * INTER + m) * 2u, uint16_t(bits(roundbf(gt / (1.0f + exp_det(-gt))) * up)));
+                    const float silu = gt * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-gt * 1.4426950408889634f));
+                    buffer_store2(yv, (t * INTER + m) * 2u, uint16_t(bits(roundbf(silu) * up)));
                 }
             } else {
 #pragma unroll
@@ -238,28 +243,56 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
 }
 
+// Calls f(std::integral_constant<int, I>) for I = B .. E-1.
+template <int B, int E, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (B < E) {
+        f(std::integral_constant<int, B>{});
+        static_for<B + 1, E>(f);
+    }
+}
+
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 __device__ __forceinline__ void load_to_lds(__amdgpu_buffer_rsrc_t v, void* lds, uint32_t off) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(v, (lds_ptr_t)lds, 16, off, 0, 0, 0);
 }
 
 // Plain-weight GEMM whose operand tiles go from memory straight into LDS (buffer loads with
-// the LDS destination): no staging registers and no LDS store instructions.  Three LDS
-// stages, two K steps in flight.  A stage holds BT activation rows then BW weight rows of 128
-// bytes (64 K values); the 16-byte chunk c of row R sits in slot c ^ ((R >> 1) & 7), which
-// spreads both the loads' 8-lane row segments and the operand reads' 16-row columns over
-// all banks.  Each wave loads Q 1 KB blocks (8 rows) per stage.  Waves synchronise with a
-// bare s_barrier after waiting for their own stage loads, so the stage two steps ahead stays
-// in flight across the barrier.
-template <int EPI, int BT, int BW, int WT, int NT>
+// the LDS destination): no staging registers and no LDS store instructions.  NS LDS stages of
+// KD K values each, NS - 1 stages in flight.  A stage holds BT activation rows then BW weight
+// rows of KD * 2 bytes; the 16-byte chunk c of row R sits in slot c ^ ((R >> SH) & (CPR - 1))
+// (SH = 1 for 128-byte rows, 2 for 64-byte rows), which spreads both the loads' row segments
+// and the operand reads' 16-row columns over all banks.  Each wave loads Q 1 KB blocks per
+// stage.  Waves synchronise with a bare s_barrier after waiting for their own stage loads, so
+// the later stages stay in flight across the barrier.
+template <int EPI, int BT, int BW, int WT, int NT, int KD, int NS>
 __global__ __launch_bounds__(NT) void gemm_dma_kernel(const GemmParams p, int col_tiles, int row_tiles) {
     constexpr int NW = NT / 64, WW = NW / WT, TT = BT / WT / 32, TW = BW / WW / 32;
-    constexpr int ROWS = BT + BW, STAGE = ROWS * 128, Q = ROWS / 8 / NW;
-    static_assert(ROWS % (8 * NW) == 0 && BT % 16 == 0, "stage blocks per wave");
+    constexpr int ROWB = KD * 2, CPR = ROWB / 16, RPI = 1024 / ROWB, SH = ROWB == 128 ? 1 : 2;
+    constexpr int ROWS = BT + BW, STAGE = ROWS * ROWB, Q = ROWS / RPI / NW;
+    static_assert(KD == 64 || KD == 32, "stage depth");
+    static_assert(ROWS % (RPI * NW) == 0 && BT % 16 == 0, "stage blocks per wave");
     static_assert(EPI != GEMM_SWIGLU || TW % 2 == 0, "SwiGLU pairs gate and up tiles inside a wave");
+    static_assert(NS >= 3, "at least two stages in flight");
+    // one array per stage: the compiler then tells the stages apart and waits for the loads
+    // into a stage only before reading that stage (one shared array would make every read
+    // wait for every load in flight)
     __shared__ __align__(1024) uint8_t S0[STAGE];
     __shared__ __align__(1024) uint8_t S1[STAGE];
     __shared__ __align__(1024) uint8_t S2[STAGE];
+    __shared__ __align__(1024) uint8_t S3[NS > 3 ? STAGE : 16];
+    __shared__ __align__(1024) uint8_t S4[NS > 4 ? STAGE : 16];
+    __shared__ __align__(1024) uint8_t S5[NS > 5 ? STAGE : 16];
+    static_assert(NS <= 6, "at most six stages");
+    auto stage_of = [&](auto idx) -> uint8_t* {
+        constexpr int i = decltype(idx)::value;
+        if constexpr (i == 0) return S0;
+        else if constexpr (i == 1) return S1;
+        else if constexpr (i == 2) return S2;
+        else if constexpr (i == 3) return S3;
+        else if constexpr (i == 4) return S4;
+        else return S5;
+    };
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wt = wave / WW, ww = wave % WW;
     const int tiles = col_tiles * row_tiles;
@@ -269,7 +302,7 @@ __global__ __launch_bounds__(NT) void gemm_dma_kernel(const GemmParams p, int co
     const int ct = tile / row_tiles, rt = tile % row_tiles;
     const int t0 = rt * BT;
     const int n0 = ct * (EPI == GEMM_SWIGLU ? BW / 2 : BW);
-    const int nk = p.k / BK;
+    const int nk = p.k / KD;
     const uint32_t K = uint32_t(p.k);
     const GemmViews views = gemm_views(p, false);
 
@@ -278,15 +311,15 @@ __global__ __launch_bounds__(NT) void gemm_dma_kernel(const GemmParams p, int co
     bool from_x[Q];
 #pragma unroll
     for (int q = 0; q < Q; ++q) {
-        const int R = (wave * Q + q) * 8 + (lane >> 3);
-        const uint32_t c = uint32_t((lane & 7) ^ ((R >> 1) & 7));
-        from_x[q] = (wave * Q + q) * 8 < BT;
+        const int R = (wave * Q + q) * RPI + lane / CPR;
+        const uint32_t c = uint32_t((lane % CPR) ^ ((R >> SH) & (CPR - 1)));
+        from_x[q] = (wave * Q + q) * RPI < BT;
         const uint32_t row = from_x[q] ? uint32_t(t0 + R) : uint32_t(b_row<EPI>(n0, R - BT));
         goff[q] = (row * K + c * 8) * 2u;
     }
     auto issue = [&](uint8_t* stage, int kt) {
         const uint32_t kill = kt < nk ? 0u : OOB_OFFSET;
-        const uint32_t kb = uint32_t(kt) * BK * 2u;
+        const uint32_t kb = uint32_t(kt) * KD * 2u;
 #pragma unroll
         for (int q = 0; q < Q; ++q)
             load_to_lds(from_x[q] ? views.x : views.w, stage + (wave * Q + q) * 1024, (goff[q] + kb) | kill);
@@ -300,18 +333,18 @@ __global__ __launch_bounds__(NT) void gemm_dma_kernel(const GemmParams p, int co
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
     auto compute = [&](const uint8_t* stage) {
 #pragma unroll
-        for (int ks = 0; ks < BK / 16; ++ks) {
+        for (int ks = 0; ks < KD / 16; ++ks) {
             const int c = ks * 2 + (lane >> 5);
             bf16x8 a[TT], b[TW];
 #pragma unroll
             for (int i = 0; i < TT; ++i) {
                 const int R = wt * TT * 32 + i * 32 + (lane & 31);
-                a[i] = as_bf16x8(*reinterpret_cast<const uint4*>(stage + R * 128 + ((c ^ ((R >> 1) & 7)) << 4)));
+                a[i] = as_bf16x8(*reinterpret_cast<const uint4*>(stage + R * ROWB + ((c ^ ((R >> SH) & (CPR - 1))) << 4)));
             }
 #pragma unroll
             for (int j = 0; j < TW; ++j) {
                 const int R = BT + ww * TW * 32 + j * 32 + (lane & 31);
-                b[j] = as_bf16x8(*reinterpret_cast<const uint4*>(stage + R * 128 + ((c ^ ((R >> 1) & 7)) << 4)));
+                b[j] = as_bf16x8(*reinterpret_cast<const uint4*>(stage + R * ROWB + ((c ^ ((R >> SH) & (CPR - 1))) << 4)));
             }
 #pragma unroll
             for (int i = 0; i < TT; ++i)
@@ -319,25 +352,27 @@ __global__ __launch_bounds__(NT) void gemm_dma_kernel(const GemmParams p, int co
                 for (int j = 0; j < TW; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
         }
     };
-    // step kt: this wave's loads of stage kt are done once at most the Q loads of stage kt+1
-    // are outstanding; after the barrier every wave's are, and the buffer of stage kt-1 is free
+    // step kt: this wave's loads of stage kt are done once at most the loads of the NS - 2
+    // later stages are outstanding; after the barrier every wave's are, and the buffer of
+    // stage kt - 1 is free for stage kt + NS - 1
     auto step = [&](const uint8_t* cur, uint8_t* freed, int kt) {
-        wait_vmcnt<Q>();
+        wait_vmcnt<(NS - 2) * Q>();
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-        issue(freed, kt + 2);
+        issue(freed, kt + NS - 1);
         compute(cur);
     };
-    issue(S0, 0);
-    issue(S1, 1);
+    static_for<0, NS - 1>([&](auto b) { issue(stage_of(b), decltype(b)::value); });
     int kt = 0;
-    for (; kt + 3 <= nk; kt += 3) {
-        step(S0, S2, kt);
-        step(S1, S0, kt + 1);
-        step(S2, S1, kt + 2);
-    }
-    if (kt < nk) step(S0, S2, kt);
-    if (kt + 1 < nk) step(S1, S0, kt + 1);
+    for (; kt + NS <= nk; kt += NS)
+        static_for<0, NS>([&](auto b) {
+            constexpr int i = decltype(b)::value;
+            step(stage_of(b), stage_of(std::integral_constant<int, (i + NS - 1) % NS>{}), kt + i);
+        });
+    static_for<0, NS - 1>([&](auto b) {
+        constexpr int i = decltype(b)::value;
+        if (kt + i < nk) step(stage_of(b), stage_of(std::integral_constant<int, (i + NS - 1) % NS>{}), kt + i);
+    });
     gemm_epilogue<EPI, TT, TW>(p, acc, t0 + wt * TT * 32, n0, ww, lane);
 }
 
@@ -771,13 +806,13 @@ __global__ __launch_bounds__(256, 2) void flash_prefill_kernel(const FlashParams
         }
 }
 
-template <int BT, int BW, int WT, int NT>
+template <int BT, int BW, int WT, int NT, int KD, int NS>
 void launch_gemm_dma(GemmEpilogue epi, const GemmParams& p, hipStream_t s) {
     const int cols = epi == GEMM_SWIGLU ? INTER / (BW / 2) : (p.m + BW - 1) / BW;
     const int rows = (p.tokens + BT - 1) / BT;
     const int per = (cols * rows + 7) / 8;
     const dim3 grid(8 * per), block(NT);
-#define PLAMO_GEMM(EP) hipLaunchKernelGGL((gemm_dma_kernel<EP, BT, BW, WT, NT>), grid, block, 0, s, p, cols, rows)
+#define PLAMO_GEMM(EP) hipLaunchKernelGGL((gemm_dma_kernel<EP, BT, BW, WT, NT, KD, NS>), grid, block, 0, s, p, cols, rows)
     if (epi == GEMM_F32) PLAMO_GEMM(GEMM_F32);
     else if (epi == GEMM_BF16) PLAMO_GEMM(GEMM_BF16);
     else if (epi == GEMM_RAW) PLAMO_GEMM(GEMM_RAW);
@@ -818,8 +853,9 @@ void launch_gemm(bool packed, GemmEpilogue epi, const GemmParams& p, hipStream_t
         if (wide) launch_gemm_packed<256, 128, 4, 512>(epi, p, s);
         else launch_gemm_packed<128, 128, 2, 256>(epi, p, s);
     } else {
-        if (wide) launch_gemm_dma<256, 128, 4, 512>(epi, p, s);
-        else launch_gemm_dma<128, 128, 4, 512>(epi, p, s);
+        // 32-deep stages: five (wide) or six stages, so four or five are in flight
+        if (wide) launch_gemm_dma<256, 128, 4, 512, 32, 5>(epi, p, s);
+        else launch_gemm_dma<128, 128, 4, 512, 32, 6>(epi, p, s);
     }
 }
 
