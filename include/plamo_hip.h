@@ -177,6 +177,15 @@ int plamo_batch_generate(plamo_batch* b, const int32_t* tokens, const int32_t* l
                          int32_t count, int32_t stop_on_truncation, int32_t* ids, int32_t ids_stride,
                          int32_t* out_lengths, int32_t* reasons, int32_t* lanes, char* err, size_t errlen);
 
+/* decodeBatch(initial:limits:step: Batch.step, stopOnTruncation:) (BatchDecode.swift:8-37,
+ * as Batch.generate calls it at BatchDecode.swift:44-46) after plamo_batch_prefill: the lane
+ * pass and the token feedback run on the device, 16 steps per host synchronisation.
+ * `initial[count]` are the lanes' first predictions (count = the prefilled lanes).  Outputs
+ * as plamo_decode_batch; lane positions and predictions advance as with plamo_batch_step. */
+int plamo_batch_decode(plamo_batch* b, const int32_t* initial, const int32_t* limits, int32_t count,
+                       int32_t stop_on_truncation, int32_t* ids, int32_t ids_stride, int32_t* lengths,
+                       int32_t* reasons, int32_t* lanes, char* err, size_t errlen);
+
 /* ---- Weight formats (Runtime.swift:23-111, Packed.swift, scripts/pack_weights.py) ---- */
 
 typedef struct plamo_pack_report {

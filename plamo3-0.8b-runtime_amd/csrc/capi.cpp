@@ -378,15 +378,36 @@ int plamo_batch_generate(plamo_batch* b, const int32_t* tokens, const int32_t* l
                 throw plamo::Error(plamo::E_INVAL, "Quad output budget exceeds context");
         try {
             auto first = b->impl->prefill(prompts);
-            auto res = decode_batch(
-                first, std::vector<int32_t>(limits, limits + count),
-                [&](const std::vector<int32_t>& t) { return b->impl->step(t); }, [](int, int) {},
-                [](int, const LaneOutput&) {}, stop_on_truncation != 0);
+            // decodeBatch with no callbacks runs as the device loop: same lane pass, no host
+            // round trip per step
+            auto dec = b->impl->decode(first, std::vector<int32_t>(limits, limits + count), stop_on_truncation != 0);
+            std::vector<LaneOutput> res(dec.ids.size());
+            for (size_t i = 0; i < res.size(); ++i) {
+                res[i].ids = std::move(dec.ids[i]);
+                res[i].reason = dec.reasons[i];
+            }
             write_outputs(res, ids, ids_stride, out_lengths, reasons, lanes);
         } catch (...) {
             b->impl->reset();
             throw;
         }
+    });
+}
+
+int plamo_batch_decode(plamo_batch* b, const int32_t* initial, const int32_t* limits, int32_t count,
+                       int32_t stop_on_truncation, int32_t* ids, int32_t ids_stride, int32_t* lengths,
+                       int32_t* reasons, int32_t* lanes, char* err, size_t errlen) {
+    return guard(err, errlen, [&] {
+        if (!b || !initial || !limits || count < 1 || count > plamo::ROWS)
+            throw plamo::Error(plamo::E_INVAL, "Invalid quad decode inputs");
+        auto dec = b->impl->decode(std::vector<int32_t>(initial, initial + count),
+                                   std::vector<int32_t>(limits, limits + count), stop_on_truncation != 0);
+        std::vector<LaneOutput> res(dec.ids.size());
+        for (size_t i = 0; i < res.size(); ++i) {
+            res[i].ids = std::move(dec.ids[i]);
+            res[i].reason = dec.reasons[i];
+        }
+        write_outputs(res, ids, ids_stride, lengths, reasons, lanes);
     });
 }
 

@@ -233,8 +233,9 @@ __device__ __forceinline__ void stage_finish(const GemvParams& p, int rows, cons
                     p.resid_out[q * HIDDEN + i] = xv[q][k];
                     p.resid_out[q * HIDDEN + i + 1] = xv[q][k + 1];
                     if (p.hidden) {
-                        p.hidden[q * HIDDEN + i] = lo(xn2);
-                        p.hidden[q * HIDDEN + i + 1] = hi(xn2);
+                        const size_t hrow = p.state ? size_t(p.state->lane[q]) : size_t(q);
+                        p.hidden[hrow * HIDDEN + i] = lo(xn2);
+                        p.hidden[hrow * HIDDEN + i + 1] = hi(xn2);
                     }
                 }
             }
@@ -413,8 +414,14 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvParams p) {
     int rows = p.rows;
     if constexpr (STATE) rows = stopped ? 0 : int(srows);
     Controls ctl{false, 0, 1.0f, 0.0f, 0.0f};
+    // logits rows land in the slot of the row's lane (lane-indexed outputs need no copies)
+    uint32_t orow[MAXR];
+#pragma unroll
+    for (int q = 0; q < MAXR; ++q) orow[q] = uint32_t(q);
     if constexpr (EPI == EPI_LOGITS && STATE) {
         if (st->sampling) ctl = Controls{true, st->ngram, st->penalty, st->frequency, st->presence};
+#pragma unroll
+        for (int q = 0; q < MAXR; ++q) orow[q] = st->lane[q];
     }
     stage_finish<N, MAXR, PRO>(p, rows, S, xs, red);
     __syncthreads();
@@ -491,7 +498,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvParams p) {
 #pragma unroll
                 for (int u = 0; u < U; ++u) {
                     const uint32_t b = bits(acc[u][q]);
-                    if (lane == 0) p.out16[size_t(q) * VOCAB + wrow[u]] = uint16_t(b);
+                    if (lane == 0) p.out16[size_t(orow[q]) * VOCAB + wrow[u]] = uint16_t(b);
                     float v = bf(b);
                     if (ctl.on) {
                         const uint32_t r = uint32_t(wrow[u]);
@@ -557,6 +564,12 @@ __global__ __launch_bounds__(256) void head_merge_kernel(DecodeBuffers b, int bl
         if (st->loop) {
             st->token[q] = int32_t(bi);
             st->pos[q] += 1;
+        }
+        if (st->quad) {
+            const uint32_t ln = st->lane[q];
+            st->lnext[ln] = int32_t(bi);
+            st->lpos[ln] += 1;
+            if (bi >= uint32_t(VOCAB)) { st->stopped = 1; st->reason = 3; }  // invalid prediction
         }
     }
 }
@@ -890,7 +903,38 @@ __global__ __launch_bounds__(256) void step_begin_kernel(DecodeBuffers b) {
     const int tid = threadIdx.x;
     if (tid == 0) {
         s_stop = 0;
-        if (st->loop) {
+        if (st->quad) {
+            // decodeBatch's lane pass (BatchDecode.swift:16-31): a lane stops at its limit or
+            // on token 1 / 16, otherwise emits its prediction and, below the limit, feeds it
+            // back; running lanes are packed into rows in lane order (Batch.swift:130-146).
+            uint32_t rows = 0, last = st->last;
+            for (uint32_t ln = 0; ln < st->lanes && ln < uint32_t(ROWS); ++ln) {
+                if (ln > last) break;
+                if (st->lreason[ln]) continue;
+                const int32_t nx = st->lnext[ln];
+                uint32_t reason = 0;
+                if (st->lcount[ln] == st->llimit[ln]) reason = 2;
+                else if (nx == 1 || nx == 16) reason = 1;
+                else {
+                    b.out_ids[size_t(ln) * st->out_stride + st->lcount[ln]] = nx;
+                    st->lcount[ln] += 1;
+                    if (st->lcount[ln] == st->llimit[ln]) reason = 2;
+                    else {
+                        st->lane[rows] = ln;
+                        st->pos[rows] = st->lpos[ln];
+                        st->token[rows] = nx;
+                        ++rows;
+                    }
+                }
+                if (reason) {
+                    st->lreason[ln] = reason;
+                    if (st->trunc_stop && reason == 2 && ln < last) last = ln;
+                }
+            }
+            st->last = last;
+            st->rows = rows;
+            if (!rows) { st->stopped = 1; s_stop = 1; }
+        } else if (st->loop) {
             const int32_t tok = st->token[0];
             if (st->stop_enabled && (tok == 1 || tok == 16)) {
                 st->stopped = 1; st->reason = 1; s_stop = 1;

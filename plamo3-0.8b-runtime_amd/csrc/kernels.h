@@ -29,6 +29,18 @@ struct StepState {
     uint32_t next[ROWS];      // selected next token of each row
     uint32_t hist_len[ROWS];  // generated-history length (sampler)
     uint32_t counted[ROWS];   // history entries already folded into the counts
+    // Device-driven batch loop (decodeBatch, BatchDecode.swift:8-37): lane bookkeeping
+    // before each step packs the running lanes into rows; the head feeds predictions back.
+    uint32_t quad;            // batch loop active
+    uint32_t lanes;           // lanes in the batch (1..4)
+    uint32_t last;            // last lane still served (stopOnTruncation lowers it)
+    uint32_t trunc_stop;      // stopOnTruncation
+    uint32_t out_stride;      // out_ids entries per lane
+    uint32_t lpos[ROWS];      // position of each lane's next input token
+    int32_t lnext[ROWS];      // each lane's latest prediction
+    uint32_t lcount[ROWS];    // tokens emitted per lane
+    uint32_t llimit[ROWS];    // per-lane token limit
+    uint32_t lreason[ROWS];   // 0 running, 1 stop token, 2 length
 };
 
 // Buffers the decode kernels share.

@@ -244,7 +244,7 @@ Engine::Engine(std::shared_ptr<Model> mdl, int ctx, int nl, hipStream_t s)
     host_state->penalty = 1.0f;
     PLAMO_HIP(hipMemsetAsync(state, 0, sizeof(StepState), stream));
     bufs.state = state;
-    bufs.out_ids = arena.alloc_n<int32_t>(size_t(context) + 1);
+    bufs.out_ids = arena.alloc_n<int32_t>(size_t(ROWS) * (size_t(context) + 1));  // [lane][context + 1]
     bufs.hist_cap = uint32_t(context);
     bufs.history = arena.alloc_n<int32_t>(size_t(ROWS) * context);
     bufs.counts = arena.alloc_n<int32_t>(size_t(ROWS) * VOCAB);
@@ -621,8 +621,9 @@ BatchImpl::BatchImpl(RuntimeImpl* r) : rt(r) {
     if (rt->context < 1 || rt->context >= 8192)
         throw Error(E_INVAL, "Batch requires dense greedy inference with context below 8192");  // Batch.swift:34-36
     eng = std::make_unique<Engine>(rt->model, rt->context, ROWS, rt->stream);
-    lane_logits = eng->arena.alloc_n<uint16_t>(size_t(ROWS) * VOCAB);
-    lane_hidden = eng->arena.alloc_n<float>(size_t(ROWS) * HIDDEN);
+    // The LM head writes each row's logits and final hidden state into its lane's slot.
+    lane_logits = eng->logits;
+    lane_hidden = eng->hidden;
     for (auto& v : lane_next) v = 0;
 }
 
@@ -660,8 +661,6 @@ std::vector<int32_t> BatchImpl::prefill(const std::vector<std::vector<int32_t>>&
         if (p.size() == 1) e.run_step();
         else e.prefill(p.data(), int(p.size()), 0, int(lane), true);
         PLAMO_HIP(hipEventRecord(e.ev1, s));
-        PLAMO_HIP(hipMemcpyAsync(lane_logits + lane * VOCAB, e.logits, VOCAB * 2, hipMemcpyDeviceToDevice, s));
-        PLAMO_HIP(hipMemcpyAsync(lane_hidden + lane * HIDDEN, e.hidden, HIDDEN * 4, hipMemcpyDeviceToDevice, s));
         PLAMO_HIP(hipMemcpyAsync(&hs, e.state, sizeof(StepState), hipMemcpyDeviceToHost, s));
         PLAMO_HIP(hipStreamSynchronize(s));
         PLAMO_HIP(hipGetLastError());
@@ -705,14 +704,8 @@ std::vector<int32_t> BatchImpl::step(const std::vector<int32_t>& tokens) {
     PLAMO_HIP(hipEventRecord(e.ev0, s));
     e.run_step();
     PLAMO_HIP(hipEventRecord(e.ev1, s));
-    // Packed query rows are temporary; persistent outputs stay indexed by lane (Batch.swift:167-173).
-    for (size_t q = 0; q < active.size(); ++q) {
-        const int lane = active[q];
-        PLAMO_HIP(hipMemcpyAsync(lane_logits + size_t(lane) * VOCAB, e.logits + q * VOCAB, VOCAB * 2,
-                                 hipMemcpyDeviceToDevice, s));
-        PLAMO_HIP(hipMemcpyAsync(lane_hidden + size_t(lane) * HIDDEN, e.hidden + q * HIDDEN, HIDDEN * 4,
-                                 hipMemcpyDeviceToDevice, s));
-    }
+    // Packed query rows are temporary; the head writes logits and hidden state at each row's
+    // lane, so persistent outputs stay indexed by lane (Batch.swift:167-173).
     PLAMO_HIP(hipMemcpyAsync(&hs, e.state, sizeof(StepState), hipMemcpyDeviceToHost, s));
     const hipError_t sync = hipStreamSynchronize(s);
     if (sync != hipSuccess) {
@@ -727,6 +720,77 @@ std::vector<int32_t> BatchImpl::step(const std::vector<int32_t>& tokens) {
         positions[active[q]] += 1;
     }
     return std::vector<int32_t>(lane_next, lane_next + positions.size());
+}
+
+// decodeBatch (BatchDecode.swift:8-37) after a prefill, with the lane bookkeeping and the
+// token feedback on the device: 16 graph replays per host synchronisation.
+BatchImpl::Decoded BatchImpl::decode(const std::vector<int32_t>& first, const std::vector<int32_t>& limits,
+                                     bool stop_on_truncation) {
+    const int count = int(first.size());
+    bool ok = ready && count >= 1 && count <= ROWS && int(limits.size()) == count && count == int(positions.size());
+    for (int i = 0; ok && i < count; ++i)
+        ok = first[i] >= 0 && first[i] < VOCAB && limits[i] >= 0 && limits[i] <= 8191 &&
+             positions[i] + limits[i] <= rt->context;
+    if (!ok) throw Error(E_INVAL, "Invalid quad decode inputs");
+    Engine& e = *eng;
+    hipStream_t s = e.stream;
+    StepState& hs = *e.host_state;
+    std::memset(&hs, 0, sizeof(StepState));
+    hs.penalty = 1.0f;
+    hs.quad = 1;
+    hs.lanes = uint32_t(count);
+    hs.last = uint32_t(count - 1);
+    hs.trunc_stop = stop_on_truncation ? 1u : 0u;
+    hs.out_stride = uint32_t(rt->context) + 1;
+    int max_steps = 0;
+    for (int i = 0; i < count; ++i) {
+        hs.lpos[i] = uint32_t(positions[i]);
+        hs.lnext[i] = first[i];
+        hs.llimit[i] = uint32_t(limits[i]);
+        max_steps = std::max(max_steps, limits[i]);
+    }
+    PLAMO_HIP(hipMemcpyAsync(e.state, &hs, sizeof(StepState), hipMemcpyHostToDevice, s));
+    PLAMO_HIP(hipEventRecord(e.ev0, s));
+    // every step with running lanes emits a token on each of them, so the lane pass stops
+    // the loop after at most max(limit) + 1 steps
+    int launched = 0;
+    while (true) {
+        for (int k = 0; k < 16; ++k) e.run_step();
+        launched += 16;
+        PLAMO_HIP(hipMemcpyAsync(&hs, e.state, sizeof(StepState), hipMemcpyDeviceToHost, s));
+        const hipError_t sync = hipStreamSynchronize(s);
+        if (sync != hipSuccess) {
+            ready = false;
+            throw Error(E_DEVICE, std::string("Quad execution failed: ") + hipGetErrorString(sync));
+        }
+        if (hs.stopped) break;
+        if (launched > max_steps + 16) {
+            ready = false;
+            throw Error(E_DEVICE, "Quad device loop did not stop");
+        }
+    }
+    PLAMO_HIP(hipEventRecord(e.ev1, s));
+    PLAMO_HIP(hipEventSynchronize(e.ev1));
+    float ms = 0;
+    PLAMO_HIP(hipEventElapsedTime(&ms, e.ev0, e.ev1));
+    gpu_seconds += ms / 1000.0;
+    for (int i = 0; i < count; ++i) {
+        positions[i] = int64_t(hs.lpos[i]);
+        lane_next[i] = hs.lnext[i];
+    }
+    if (hs.reason == 3) throw Error(E_INVAL, "Invalid quad predictions");
+    Decoded out;
+    const int lanes_out = int(hs.last) + 1;
+    out.ids.resize(size_t(lanes_out));
+    out.reasons.resize(size_t(lanes_out));
+    for (int i = 0; i < lanes_out; ++i) {
+        out.reasons[i] = int(hs.lreason[i]);
+        out.ids[i].resize(hs.lcount[i]);
+        if (hs.lcount[i])
+            PLAMO_HIP(hipMemcpy(out.ids[i].data(), e.bufs.out_ids + size_t(i) * hs.out_stride, size_t(hs.lcount[i]) * 4,
+                                hipMemcpyDeviceToHost));
+    }
+    return out;
 }
 
 }  // namespace plamo

@@ -136,7 +136,7 @@ struct BatchImpl {
     std::vector<int64_t> positions;
     bool ready = false;
     double gpu_seconds = 0;
-    uint16_t* lane_logits;   // [4][VOCAB]
+    uint16_t* lane_logits;   // [4][VOCAB] (the engine's head output, indexed by lane)
     float* lane_hidden;      // [4][1536]
     int32_t lane_next[ROWS];
 
@@ -144,6 +144,11 @@ struct BatchImpl {
     ~BatchImpl();
     std::vector<int32_t> prefill(const std::vector<std::vector<int32_t>>& prompts);
     std::vector<int32_t> step(const std::vector<int32_t>& tokens);
+    struct Decoded {
+        std::vector<std::vector<int32_t>> ids;  // emitted tokens of lanes 0..last
+        std::vector<int> reasons;               // 1 stop token, 2 length
+    };
+    Decoded decode(const std::vector<int32_t>& first, const std::vector<int32_t>& limits, bool stop_on_truncation);
     void reset();
 };
 

@@ -218,6 +218,17 @@ class Batch:
                     reasons, ctypes.byref(lanes))
         return [([ids[i * stride + k] for k in range(lengths[i])], REASONS[reasons[i]]) for i in range(lanes.value)]
 
+    def decode(self, initial, limits, stop_on_truncation=False):
+        """decodeBatch(initial, limits, step: self.step) (BatchDecode.swift:8-37) as a device loop
+        after prefill -> [(ids, reason)]."""
+        stride = max(1, max(limits))
+        ids = (ctypes.c_int32 * (4 * stride))()
+        lengths, reasons, lanes = (ctypes.c_int32 * 4)(), (ctypes.c_int32 * 4)(), ctypes.c_int32()
+        native.call(self._lib.plamo_batch_decode, self._h, native.i32([int(t) for t in initial]),
+                    native.i32(list(limits)), len(initial), 1 if stop_on_truncation else 0, ids, stride, lengths,
+                    reasons, ctypes.byref(lanes))
+        return [([ids[i * stride + k] for k in range(lengths[i])], REASONS[reasons[i]]) for i in range(lanes.value)]
+
 
 def decode_batch(initial, limits, step, emit=None, finish=None, stop_on_truncation=False):
     """decodeBatch (BatchDecode.swift:8-37) through the native scheduler -> [(ids, reason)]."""

@@ -79,6 +79,8 @@ _SIGNATURES = {
     "plamo_batch_generate": (ctypes.c_int, [ctypes.c_void_p, c_i32p, c_i32p, c_i32p, ctypes.c_int32,
                                             ctypes.c_int32, c_i32p, ctypes.c_int32, c_i32p, c_i32p, c_i32p,
                                             ctypes.c_char_p, ctypes.c_size_t]),
+    "plamo_batch_decode": (ctypes.c_int, [ctypes.c_void_p, c_i32p, c_i32p, ctypes.c_int32, ctypes.c_int32, c_i32p,
+                                          ctypes.c_int32, c_i32p, c_i32p, c_i32p, ctypes.c_char_p, ctypes.c_size_t]),
     "plamo_pack": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(PackReport),
                                   ctypes.c_char_p, ctypes.c_size_t]),
     "plamo_pack_tensor": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64,

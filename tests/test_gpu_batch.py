@@ -80,6 +80,31 @@ def test_generate_matches_sequential(engines):
         assert reason == ("stop" if r == "stop" else "length")
 
 
+@pytest.mark.parametrize("limits,override,trunc", [
+    ([12, 5, 0, 8], {}, False),            # a zero limit ends its lane before any step
+    ([6, 6, 6, 6], {1: 16, 3: 1}, False),  # stop tokens end lanes 1 and 3 at once
+    ([9, 3, 9, 9], {}, True),              # lane 1 truncates: lanes 2 and 3 are dropped
+    ([4, 7, 2], {0: 1}, True),             # stop (not truncation) keeps the later lanes
+])
+def test_device_loop_matches_host_loop(engines, limits, override, trunc):
+    # the device lane pass and token feedback against decodeBatch driving Batch.step
+    rt, b = engines
+    prompts = prompts_for([20, 14, 9, 30][:len(limits)])
+    first = b.prefill(prompts)
+    initial = [override.get(i, t) for i, t in enumerate(first)]
+    want = plamo_hip.decode_batch(initial, limits, b.step, stop_on_truncation=trunc)
+    want_pos = b.positions()
+    want_logits = [b.logit_bits(i).copy() for i in range(len(prompts))]
+    want_hidden = [b.hidden(i).copy() for i in range(len(prompts))]
+    assert b.prefill(prompts) == first
+    got = b.decode(initial, limits, stop_on_truncation=trunc)
+    assert got == want
+    assert b.positions() == want_pos
+    for i in range(len(prompts)):
+        assert np.array_equal(b.logit_bits(i), want_logits[i]), i
+        assert np.array_equal(b.hidden(i).view(np.uint32), want_hidden[i].view(np.uint32)), i
+
+
 def test_batch_validation(engines, model_dir):
     rt, b = engines
     with pytest.raises(plamo_hip.PlamoError, match="Expected one to four valid prompts"):
