@@ -49,6 +49,8 @@ struct Staged {
     uint4 h[PRO == PRO_PLAIN16 ? MAXR : 1][V16];
     float2 a[PRO == PRO_RESID ? MAXR : 1][E / 2];   // RESID: projection output
     float2 r[PRO == PRO_RESID ? MAXR : 1][E / 2];   // RESID: residual stream
+    uint32_t a16[PRO == PRO_RESID16 ? MAXR : 1][E / 2];  // RESID16: projection output (BF16 pairs)
+    uint32_t r16[PRO == PRO_RESID16 ? MAXR : 1][E / 2];  // RESID16: residual stream (BF16 pairs)
     uint32_t emb[PRO == PRO_EMBED ? MAXR : 1][E / 2];  // EMBED: embedding row (BF16 pairs)
     uint32_t gp[E / 2], gn[E / 2];                 // norm weights (BF16 pairs)
 };
@@ -106,8 +108,13 @@ __device__ __forceinline__ void stage_load(const GemvParams& p, int rb, Staged<N
                 const int qq = q < rb ? q : rb - 1;
 #pragma unroll
                 for (int k = 0; k < E / 2; ++k) {
-                    S.a[q][k] = *reinterpret_cast<const float2*>(p.in + qq * HIDDEN + e0 + 2 * k);
-                    S.r[q][k] = *reinterpret_cast<const float2*>(p.resid_in + qq * HIDDEN + e0 + 2 * k);
+                    if constexpr (PRO == PRO_RESID16) {
+                        S.a16[q][k] = *reinterpret_cast<const uint32_t*>(p.in16 + qq * HIDDEN + e0 + 2 * k);
+                        S.r16[q][k] = *reinterpret_cast<const uint32_t*>(p.resid16_in + qq * HIDDEN + e0 + 2 * k);
+                    } else {
+                        S.a[q][k] = *reinterpret_cast<const float2*>(p.in + qq * HIDDEN + e0 + 2 * k);
+                        S.r[q][k] = *reinterpret_cast<const float2*>(p.resid_in + qq * HIDDEN + e0 + 2 * k);
+                    }
                 }
             }
         }
@@ -167,10 +174,17 @@ __device__ __forceinline__ void stage_finish(const GemvParams& p, int rows, cons
             for (int q = 0; q < MAXR; ++q)
 #pragma unroll
                 for (int k = 0; k < E / 2; ++k) {
-                    pv[q][2 * k] = S.a[q][k].x;
-                    pv[q][2 * k + 1] = S.a[q][k].y;
-                    rv[q][2 * k] = S.r[q][k].x;
-                    rv[q][2 * k + 1] = S.r[q][k].y;
+                    if constexpr (PRO == PRO_RESID16) {
+                        pv[q][2 * k] = lo(S.a16[q][k]);
+                        pv[q][2 * k + 1] = hi(S.a16[q][k]);
+                        rv[q][2 * k] = lo(S.r16[q][k]);
+                        rv[q][2 * k + 1] = hi(S.r16[q][k]);
+                    } else {
+                        pv[q][2 * k] = S.a[q][k].x;
+                        pv[q][2 * k + 1] = S.a[q][k].y;
+                        rv[q][2 * k] = S.r[q][k].x;
+                        rv[q][2 * k + 1] = S.r[q][k].y;
+                    }
                 }
 #pragma unroll
             for (int q = 0; q < MAXR; ++q) {
@@ -230,8 +244,12 @@ __device__ __forceinline__ void stage_finish(const GemvParams& p, int rows, cons
                 const uint32_t xn2 = pack_bf16(t0 * gn[k], t1 * gn[k + 1]);  // the two BF16 results
                 *reinterpret_cast<uint32_t*>(&xs[q * HIDDEN + i]) = xn2;
                 if (blockIdx.x == 0) {
-                    p.resid_out[q * HIDDEN + i] = xv[q][k];
-                    p.resid_out[q * HIDDEN + i + 1] = xv[q][k + 1];
+                    if constexpr (PRO == PRO_RESID) {
+                        p.resid_out[q * HIDDEN + i] = xv[q][k];
+                        p.resid_out[q * HIDDEN + i + 1] = xv[q][k + 1];
+                    } else {  // BF16-exact residual: the BF16 pair is lossless
+                        *reinterpret_cast<uint32_t*>(&p.resid16_out[q * HIDDEN + i]) = pack_bf16(xv[q][k], xv[q][k + 1]);
+                    }
                     if (p.hidden) {
                         const size_t hrow = p.state ? size_t(p.state->lane[q]) : size_t(q);
                         p.hidden[hrow * HIDDEN + i] = lo(xn2);
@@ -1092,14 +1110,15 @@ void gemv_dispatch_epi(Prologue pro, Epilogue epi, const GemvParams& p, int bloc
         return;
     }
     if (pro == PRO_PLAIN16) {
-        if (epi == EPI_ROUND) PLAMO_GEMV(PRO_PLAIN16, EPI_ROUND);
+        if (epi == EPI_BF16) PLAMO_GEMV(PRO_PLAIN16, EPI_BF16);
         else throw Error(E_INVAL, "unsupported GEMV variant");
         return;
     }
     if constexpr (N == HIDDEN) {
         if (pro == PRO_EMBED && epi == EPI_ROUND) PLAMO_GEMV(PRO_EMBED, EPI_ROUND);
-        else if (pro == PRO_RESID && epi == EPI_ROUND) PLAMO_GEMV(PRO_RESID, EPI_ROUND);
-        else if (pro == PRO_RESID && epi == EPI_SWIGLU) PLAMO_GEMV(PRO_RESID, EPI_SWIGLU);
+        else if (pro == PRO_RESID16 && epi == EPI_ROUND) PLAMO_GEMV(PRO_RESID16, EPI_ROUND);
+        else if (pro == PRO_RESID16 && epi == EPI_SWIGLU) PLAMO_GEMV(PRO_RESID16, EPI_SWIGLU);
+        else if (pro == PRO_RESID16 && epi == EPI_LOGITS) PLAMO_GEMV(PRO_RESID16, EPI_LOGITS);
         else if (pro == PRO_RESID && epi == EPI_LOGITS) PLAMO_GEMV(PRO_RESID, EPI_LOGITS);
         else if (pro == PRO_PLAIN && epi == EPI_LOGITS) PLAMO_GEMV(PRO_PLAIN, EPI_LOGITS);
         else throw Error(E_INVAL, "unsupported GEMV variant");

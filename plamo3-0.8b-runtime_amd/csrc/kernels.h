@@ -56,7 +56,7 @@ struct DecodeBuffers {
     uint32_t* tickets;        // [1] spare ticket, zero between launches
 };
 
-enum Prologue { PRO_PLAIN = 0, PRO_EMBED = 1, PRO_RESID = 2, PRO_PLAIN16 = 3 };
+enum Prologue { PRO_PLAIN = 0, PRO_EMBED = 1, PRO_RESID = 2, PRO_PLAIN16 = 3, PRO_RESID16 = 4 };
 enum Epilogue { EPI_ROUND = 0, EPI_SWIGLU = 1, EPI_LOGITS = 2, EPI_BF16 = 3 };
 
 struct GemvParams {
@@ -69,9 +69,12 @@ struct GemvParams {
     uint32_t lane_mask;       // always 0: makes the state read a per-lane (vector) load
     // prologue
     const float* in;          // PLAIN: [rows][n]; RESID: projection output [rows][1536]
-    const uint16_t* in16;     // PLAIN16: BF16 [rows][n] (half the bytes every workgroup stages)
+    const uint16_t* in16;     // PLAIN16: BF16 [rows][n] (half the bytes every workgroup stages);
+                              // RESID16: BF16 projection output [rows][1536]
     const float* resid_in;    // RESID: residual stream x
-    float* resid_out;         // EMBED/RESID: updated residual (written by block 0)
+    float* resid_out;         // RESID: updated residual (written by block 0)
+    const uint16_t* resid16_in;  // RESID16: residual stream x as BF16 (every value is BF16-exact)
+    uint16_t* resid16_out;    // EMBED/RESID16: updated residual as BF16 (written by block 0)
     const uint16_t* g_post;   // RESID: post norm weight
     float post_offset;
     const uint16_t* g_next;   // EMBED/RESID: following norm weight (+1.0)

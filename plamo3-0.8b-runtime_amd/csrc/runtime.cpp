@@ -231,9 +231,9 @@ Engine::Engine(std::shared_ptr<Model> mdl, int ctx, int nl, hipStream_t s)
     }
     qkv = arena.alloc_n<float>(ROWS * QKV);
     att = arena.alloc_n<uint16_t>(ROWS * ATTN);
-    proj = arena.alloc_n<float>(ROWS * HIDDEN);
-    x0 = arena.alloc_n<float>(ROWS * HIDDEN);
-    x1 = arena.alloc_n<float>(ROWS * HIDDEN);
+    proj = arena.alloc_n<uint16_t>(ROWS * HIDDEN);
+    x0 = arena.alloc_n<uint16_t>(ROWS * HIDDEN);
+    x1 = arena.alloc_n<uint16_t>(ROWS * HIDDEN);
     act = arena.alloc_n<uint16_t>(ROWS * INTER);
     hidden = arena.alloc_n<float>(ROWS * HIDDEN);
     resid_scratch = arena.alloc_n<float>(ROWS * HIDDEN);
@@ -315,6 +315,28 @@ void Engine::enqueue_head(const float* in, const float* resid_in, int in_rows) {
     launch_head_merge(bufs, HEAD_BLOCKS, stream);
 }
 
+void Engine::enqueue_head16() {
+    const Model& m = *model;
+    const int maxr = lanes == 1 ? 1 : ROWS;
+    GemvParams g{};
+    g.state = state;
+    g.rows = ROWS;
+    g.m = VOCAB;
+    g.w = m.head.w;
+    g.table = m.head.table;
+    g.in16 = proj;
+    g.resid16_in = x1;
+    g.resid16_out = x0;  // final residual, not read again
+    g.g_post = m.layers[LAYERS - 1].post_mlp;
+    g.post_offset = post_mlp_offset();
+    g.g_next = m.final_norm;
+    g.hidden = hidden;
+    g.out16 = logits;
+    g.bufs = bufs;
+    launch_gemv(HIDDEN, m.packed, maxr, PRO_RESID16, EPI_LOGITS, g, HEAD_BLOCKS, stream);
+    launch_head_merge(bufs, HEAD_BLOCKS, stream);
+}
+
 // One decode step (Runtime.swift:376-458 for one token per row; Batch.swift:147-165).
 void Engine::enqueue_step(bool head) {
     const Model& m = *model;
@@ -331,18 +353,18 @@ void Engine::enqueue_step(bool head) {
         g.m = QKV;
         g.w = L.qkv.w;
         g.table = L.qkv.table;
-        g.resid_out = x0;
+        g.resid16_out = x0;
         g.g_next = L.pre;
         g.out = qkv;
         if (l == 0) {
             g.embed = m.embed;
             launch_gemv(HIDDEN, pk, maxr, PRO_EMBED, EPI_ROUND, g, gemv_blocks(HIDDEN, maxr, EPI_ROUND, QKV), stream);
         } else {
-            g.in = proj;
-            g.resid_in = x1;
+            g.in16 = proj;
+            g.resid16_in = x1;
             g.g_post = m.layers[l - 1].post_mlp;
             g.post_offset = post_mlp_offset();
-            launch_gemv(HIDDEN, pk, maxr, PRO_RESID, EPI_ROUND, g, gemv_blocks(HIDDEN, maxr, EPI_ROUND, QKV), stream);
+            launch_gemv(HIDDEN, pk, maxr, PRO_RESID16, EPI_ROUND, g, gemv_blocks(HIDDEN, maxr, EPI_ROUND, QKV), stream);
         }
         AttnParams a{};
         a.state = state;
@@ -368,22 +390,22 @@ void Engine::enqueue_step(bool head) {
         o.w = L.o.w;
         o.table = L.o.table;
         o.in16 = att;
-        o.out = proj;
-        launch_gemv(ATTN, pk, maxr, PRO_PLAIN16, EPI_ROUND, o, gemv_blocks(ATTN, maxr, EPI_ROUND, HIDDEN), stream);
+        o.out16 = proj;
+        launch_gemv(ATTN, pk, maxr, PRO_PLAIN16, EPI_BF16, o, gemv_blocks(ATTN, maxr, EPI_BF16, HIDDEN), stream);
         GemvParams u{};
         u.state = state;
         u.rows = ROWS;
         u.m = 2 * INTER;
         u.w = L.up.w;
         u.table = L.up.table;
-        u.in = proj;
-        u.resid_in = x0;
-        u.resid_out = x1;
+        u.in16 = proj;
+        u.resid16_in = x0;
+        u.resid16_out = x1;
         u.g_post = L.post;
         u.post_offset = POST_MIXER_OFFSET;
         u.g_next = L.pre_mlp;
         u.out16 = act;
-        launch_gemv(HIDDEN, pk, maxr, PRO_RESID, EPI_SWIGLU, u, gemv_blocks(HIDDEN, maxr, EPI_SWIGLU, 2 * INTER), stream);
+        launch_gemv(HIDDEN, pk, maxr, PRO_RESID16, EPI_SWIGLU, u, gemv_blocks(HIDDEN, maxr, EPI_SWIGLU, 2 * INTER), stream);
         GemvParams d{};
         d.state = state;
         d.rows = ROWS;
@@ -391,10 +413,10 @@ void Engine::enqueue_step(bool head) {
         d.w = L.down.w;
         d.table = L.down.table;
         d.in16 = act;
-        d.out = proj;
-        launch_gemv(INTER, pk, maxr, PRO_PLAIN16, EPI_ROUND, d, gemv_blocks(INTER, maxr, EPI_ROUND, HIDDEN), stream);
+        d.out16 = proj;
+        launch_gemv(INTER, pk, maxr, PRO_PLAIN16, EPI_BF16, d, gemv_blocks(INTER, maxr, EPI_BF16, HIDDEN), stream);
     }
-    if (head) enqueue_head(proj, x1, ROWS);
+    if (head) enqueue_head16();
 }
 
 void Engine::run_step() {

@@ -66,7 +66,8 @@ class Engine {
     uint16_t *keys[LAYERS], *values[LAYERS];
     int capacity[LAYERS];
     // decode scratch (ROWS rows)
-    float *qkv, *proj, *x0, *x1, *hidden, *resid_scratch;
+    float *qkv, *hidden, *resid_scratch;
+    uint16_t *proj, *x0, *x1;  // BF16 projection output and residual stream (BF16-exact values)
     uint16_t *att, *act;  // BF16 attention output and SwiGLU activations
     uint16_t* logits;
     StepState* state;        // device
@@ -96,7 +97,8 @@ class Engine {
 
   private:
     void enqueue_prefill_chunk(int n, int p0, int lane, bool last_chunk, bool output);
-    void enqueue_head(const float* in, const float* resid_in, int in_rows);
+    void enqueue_head(const float* in, const float* resid_in, int in_rows);  // prefill: FP32 rows
+    void enqueue_head16();                                                    // decode: BF16 stream
 };
 
 std::shared_ptr<Model> load_model(const std::string& dir, int context, bool packed, const std::string& sha,
