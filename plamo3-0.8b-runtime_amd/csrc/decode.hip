@@ -1155,6 +1155,7 @@ int gemv_blocks(int n, int maxr, Epilogue epi, int m) {
     // Multi-row kernels: at most two workgroups per CU, each wave walking several groups
     // (weights of the next in flight), so the activation prologue every workgroup
     // recomputes is paid twice per CU instead of four to six times.
+    if (maxr > 1 && n == HIDDEN && epi == EPI_ROUND) return (b + 1) / 2;  // QKV: two groups per wave
     return maxr > 1 ? std::min(b, 512) : b;
 }
 
