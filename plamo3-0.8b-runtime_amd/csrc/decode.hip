@@ -552,21 +552,48 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvParams p) {
 // First maximum over the LM-head block partials (Kernels.metal:704-729 semantics: ties to
 // the lowest index, NaN never wins, none -> 0xffffffff; Sampler.select defaults to 0), then
 // the device side of the token loop: feed the token back and advance the position.
+// The step state travels as one parallel copy into LDS and back: the single-workgroup
+// bookkeeping kernels then pay one memory round trip instead of one per dependent field.
+constexpr int STATE_WORDS = int(sizeof(StepState) / 4);
+static_assert(sizeof(StepState) % 4 == 0 && STATE_WORDS <= 256, "state copy: one word per thread");
+__device__ __forceinline__ void state_in(StepState& ls, const StepState* st) {
+    if (threadIdx.x < STATE_WORDS)
+        reinterpret_cast<uint32_t*>(&ls)[threadIdx.x] = reinterpret_cast<const uint32_t*>(st)[threadIdx.x];
+}
+__device__ __forceinline__ void state_out(StepState* st, const StepState& ls) {
+    if (threadIdx.x < STATE_WORDS)
+        reinterpret_cast<uint32_t*>(st)[threadIdx.x] = reinterpret_cast<const uint32_t*>(&ls)[threadIdx.x];
+}
+
 __global__ __launch_bounds__(256) void head_merge_kernel(DecodeBuffers b, int blocks) {
     __shared__ float cv[ROWS * 4];
     __shared__ uint32_t ci[ROWS * 4];
-    StepState* st = b.state;
-    if (st->stopped) return;
+    __shared__ StepState ls;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int rows = int(st->rows);
-    for (int q = 0; q < rows && q < ROWS; ++q) {
+    // every row's partials requested together with the state (rows past the step's are not used)
+    constexpr int PER = HEAD_BLOCKS / 256;
+    float pv[ROWS][PER];
+    uint32_t pi[ROWS][PER];
+#pragma unroll
+    for (int q = 0; q < ROWS; ++q)
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+            const int k = tid + 256 * j;
+            pv[q][j] = k < blocks ? b.head_v[q * HEAD_BLOCKS + k] : NEG_INF;
+            pi[q][j] = k < blocks ? b.head_i[q * HEAD_BLOCKS + k] : 0xffffffffu;
+        }
+    state_in(ls, b.state);
+    __syncthreads();
+    if (ls.stopped) return;
+    const int rows = int(ls.rows);
+#pragma unroll
+    for (int q = 0; q < ROWS; ++q) {
+        if (q >= rows) break;
         float bv = NEG_INF;
         uint32_t bi = 0xffffffffu;
-        for (int k = tid; k < blocks; k += 256) {
-            const float v = b.head_v[q * HEAD_BLOCKS + k];
-            const uint32_t i = b.head_i[q * HEAD_BLOCKS + k];
-            if (better(v, i, bv, bi)) { bv = v; bi = i; }
-        }
+#pragma unroll
+        for (int j = 0; j < PER; ++j)
+            if (better(pv[q][j], pi[q][j], bv, bi)) { bv = pv[q][j]; bi = pi[q][j]; }
         wave_best(bv, bi);
         if (lane == 0) { cv[q * 4 + wave] = bv; ci[q * 4 + wave] = bi; }
     }
@@ -577,19 +604,21 @@ __global__ __launch_bounds__(256) void head_merge_kernel(DecodeBuffers b, int bl
         uint32_t bi = ci[q * 4];
         for (int k = 1; k < 4; ++k)
             if (better(cv[q * 4 + k], ci[q * 4 + k], bv, bi)) { bv = cv[q * 4 + k]; bi = ci[q * 4 + k]; }
-        if (st->sampling && bi == 0xffffffffu) bi = 0;  // Sampler.select default index (Sampler.swift:26)
-        st->next[q] = bi;
-        if (st->loop) {
-            st->token[q] = int32_t(bi);
-            st->pos[q] += 1;
+        if (ls.sampling && bi == 0xffffffffu) bi = 0;  // Sampler.select default index (Sampler.swift:26)
+        ls.next[q] = bi;
+        if (ls.loop) {
+            ls.token[q] = int32_t(bi);
+            ls.pos[q] += 1;
         }
-        if (st->quad) {
-            const uint32_t ln = st->lane[q];
-            st->lnext[ln] = int32_t(bi);
-            st->lpos[ln] += 1;
-            if (bi >= uint32_t(VOCAB)) { st->stopped = 1; st->reason = 3; }  // invalid prediction
+        if (ls.quad) {
+            const uint32_t ln = ls.lane[q];
+            ls.lnext[ln] = int32_t(bi);
+            ls.lpos[ln] += 1;
+            if (bi >= uint32_t(VOCAB)) { ls.stopped = 1; ls.reason = 3; }  // invalid prediction
         }
     }
+    __syncthreads();
+    state_out(b.state, ls);
 }
 
 // ---------------------------------------------------------------------- decode attention
@@ -915,91 +944,96 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
 // Device side of the token loop (Main.swift:278-287) and of the sampler history
 // (Main.swift:237-244; Sampler.swift:11-24,54-70).
 __global__ __launch_bounds__(256) void step_begin_kernel(DecodeBuffers b) {
-    StepState* st = b.state;
+    __shared__ StepState ls;
     __shared__ int s_stop;
-    if (st->stopped) return;
+    state_in(ls, b.state);
+    __syncthreads();
+    if (ls.stopped) return;
     const int tid = threadIdx.x;
     if (tid == 0) {
         s_stop = 0;
-        if (st->quad) {
+        if (ls.quad) {
             // decodeBatch's lane pass (BatchDecode.swift:16-31): a lane stops at its limit or
             // on token 1 / 16, otherwise emits its prediction and, below the limit, feeds it
             // back; running lanes are packed into rows in lane order (Batch.swift:130-146).
-            uint32_t rows = 0, last = st->last;
-            for (uint32_t ln = 0; ln < st->lanes && ln < uint32_t(ROWS); ++ln) {
+            uint32_t rows = 0, last = ls.last;
+            for (uint32_t ln = 0; ln < ls.lanes && ln < uint32_t(ROWS); ++ln) {
                 if (ln > last) break;
-                if (st->lreason[ln]) continue;
-                const int32_t nx = st->lnext[ln];
+                if (ls.lreason[ln]) continue;
+                const int32_t nx = ls.lnext[ln];
                 uint32_t reason = 0;
-                if (st->lcount[ln] == st->llimit[ln]) reason = 2;
+                if (ls.lcount[ln] == ls.llimit[ln]) reason = 2;
                 else if (nx == 1 || nx == 16) reason = 1;
                 else {
-                    b.out_ids[size_t(ln) * st->out_stride + st->lcount[ln]] = nx;
-                    st->lcount[ln] += 1;
-                    if (st->lcount[ln] == st->llimit[ln]) reason = 2;
+                    b.out_ids[size_t(ln) * ls.out_stride + ls.lcount[ln]] = nx;
+                    ls.lcount[ln] += 1;
+                    if (ls.lcount[ln] == ls.llimit[ln]) reason = 2;
                     else {
-                        st->lane[rows] = ln;
-                        st->pos[rows] = st->lpos[ln];
-                        st->token[rows] = nx;
+                        ls.lane[rows] = ln;
+                        ls.pos[rows] = ls.lpos[ln];
+                        ls.token[rows] = nx;
                         ++rows;
                     }
                 }
                 if (reason) {
-                    st->lreason[ln] = reason;
-                    if (st->trunc_stop && reason == 2 && ln < last) last = ln;
+                    ls.lreason[ln] = reason;
+                    if (ls.trunc_stop && reason == 2 && ln < last) last = ln;
                 }
             }
-            st->last = last;
-            st->rows = rows;
-            if (!rows) { st->stopped = 1; s_stop = 1; }
-        } else if (st->loop) {
-            const int32_t tok = st->token[0];
-            if (st->stop_enabled && (tok == 1 || tok == 16)) {
-                st->stopped = 1; st->reason = 1; s_stop = 1;
+            ls.last = last;
+            ls.rows = rows;
+            if (!rows) { ls.stopped = 1; s_stop = 1; }
+        } else if (ls.loop) {
+            const int32_t tok = ls.token[0];
+            if (ls.stop_enabled && (tok == 1 || tok == 16)) {
+                ls.stopped = 1; ls.reason = 1; s_stop = 1;
             } else if (tok < 0 || tok >= VOCAB) {
-                st->stopped = 1; st->reason = 3; s_stop = 1;
+                ls.stopped = 1; ls.reason = 3; s_stop = 1;
             } else {
-                b.out_ids[st->produced] = tok;
-                st->produced += 1;
-                if (st->sampling && st->hist_len[0] < b.hist_cap) {
-                    b.history[st->hist_len[0]] = tok;
-                    st->hist_len[0] += 1;
+                b.out_ids[ls.produced] = tok;
+                ls.produced += 1;
+                if (ls.sampling && ls.hist_len[0] < b.hist_cap) {
+                    b.history[ls.hist_len[0]] = tok;
+                    ls.hist_len[0] += 1;
                 }
-                if (st->produced >= st->max_tokens) { st->stopped = 1; st->reason = 2; s_stop = 1; }
+                if (ls.produced >= ls.max_tokens) { ls.stopped = 1; ls.reason = 2; s_stop = 1; }
             }
         }
     }
     __syncthreads();
-    if (s_stop || !st->sampling) return;
-    for (uint32_t q = 0; q < st->rows; ++q) {
-        const int32_t* hist = b.history + size_t(q) * b.hist_cap;
-        const uint32_t len = st->hist_len[q];
-        if (tid == 0) {
-            for (uint32_t i = st->counted[q]; i < len; ++i) {
-                const int32_t id = hist[i];
-                if (id >= 0 && id < VOCAB) b.counts[size_t(q) * VOCAB + id] += 1;
+    if (!s_stop && ls.sampling) {
+        for (uint32_t q = 0; q < ls.rows; ++q) {
+            const int32_t* hist = b.history + size_t(q) * b.hist_cap;
+            const uint32_t len = ls.hist_len[q];
+            if (tid == 0) {
+                for (uint32_t i = ls.counted[q]; i < len; ++i) {
+                    const int32_t id = hist[i];
+                    if (id >= 0 && id < VOCAB) b.counts[size_t(q) * VOCAB + id] += 1;
+                }
+                ls.counted[q] = len;
             }
-            st->counted[q] = len;
-        }
-        if (st->ngram > 1) {
-            uint32_t* ban = b.banned + size_t(q) * (VOCAB / 32);
-            for (int i = tid; i < VOCAB / 32; i += 256) ban[i] = 0;
-            __syncthreads();
-            const int n = st->ngram, span = n - 1;
-            if (int(len) >= n) {
-                const int last = int(len) - span;
-                for (int s = tid; s < last; s += 256) {
-                    bool match = true;
-                    for (int k = 0; k < span && match; ++k) match = hist[s + k] == hist[last + k];
-                    if (match) {
-                        const int32_t id = hist[s + span];
-                        if (id >= 0 && id < VOCAB) atomicOr(&ban[id >> 5], 1u << (id & 31));
+            if (ls.ngram > 1) {
+                uint32_t* ban = b.banned + size_t(q) * (VOCAB / 32);
+                for (int i = tid; i < VOCAB / 32; i += 256) ban[i] = 0;
+                __syncthreads();
+                const int n = ls.ngram, span = n - 1;
+                if (int(len) >= n) {
+                    const int last = int(len) - span;
+                    for (int s = tid; s < last; s += 256) {
+                        bool match = true;
+                        for (int k = 0; k < span && match; ++k) match = hist[s + k] == hist[last + k];
+                        if (match) {
+                            const int32_t id = hist[s + span];
+                            if (id >= 0 && id < VOCAB) atomicOr(&ban[id >> 5], 1u << (id & 31));
+                        }
                     }
                 }
             }
+            __syncthreads();
         }
-        __syncthreads();
     }
+    __syncthreads();
+    state_out(b.state, ls);
 }
 
 // ---------------------------------------------------------------- kernel-level helpers
