@@ -14,6 +14,7 @@ each, stop on EOS) against batch-1 on the same segment; configs[4] .p12 long con
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu]
     python bench.py --kernels-only     # GEMV shapes + copy calibration (for rocprofv3 --pmc)
     python bench.py --prefill-only     # three 2048-token prefills (for rocprofv3 kernel traces)
+    python bench.py --batch4-only      # the configs[3] batch4 measurement alone
 """
 import argparse
 import json
@@ -190,6 +191,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--kernels-only", action="store_true", help="GEMV shapes and a copy calibration only")
     ap.add_argument("--prefill-only", action="store_true", help="three 2048-token prefills only")
+    ap.add_argument("--batch4-only", action="store_true", help="the configs[3] batch4 measurement only")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one MI355X; multi-GPU runs are not part of it",
@@ -208,6 +210,9 @@ def main():
         return
     log("model: generating/packing synthetic seed-0 weights")
     model_dir, sha = synth.ensure_model(packed=True)
+    if args.batch4_only:
+        print(json.dumps({"batch4": bench_batch4(plamo_hip, np, model_dir)}), flush=True)
+        return
     if args.prefill_only:
         rt = plamo_hip.Runtime(model_dir, 2048 + 64)
         p2 = np.random.default_rng(3).integers(1024, 107520, 2048).tolist()
