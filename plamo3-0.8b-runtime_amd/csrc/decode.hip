@@ -126,10 +126,11 @@ __device__ __forceinline__ void stage_finish(const GemvParams& p, int rows, cons
                                              uint16_t* xs, float* red) {
     const int tid = threadIdx.x;
     constexpr int V = Staged<N, MAXR, PRO>::V, E = Staged<N, MAXR, PRO>::E;
+    // Every LDS row is written: rows past the step's hold re-read buffer rows or zeros, so the
+    // main loop can run all MAXR rows without branches (their results are never stored).
     if constexpr (PRO == PRO_PLAIN) {
 #pragma unroll
         for (int q = 0; q < MAXR; ++q) {
-            if (q >= rows) break;
 #pragma unroll
             for (int k = 0; k < V; ++k) {
                 const int e = (tid + 256 * k) * 4;
@@ -143,7 +144,6 @@ __device__ __forceinline__ void stage_finish(const GemvParams& p, int rows, cons
         constexpr int V16 = Staged<N, MAXR, PRO>::V16;
 #pragma unroll
         for (int q = 0; q < MAXR; ++q) {
-            if (q >= rows) break;
 #pragma unroll
             for (int k = 0; k < V16; ++k) {
                 const int e = (tid + 256 * k) * 8;
@@ -233,7 +233,6 @@ __device__ __forceinline__ void stage_finish(const GemvParams& p, int rows, cons
         __syncthreads();
 #pragma unroll
         for (int q = 0; q < MAXR; ++q) {
-            if (q >= rows) break;
             const float total = (red[q * 4] + red[q * 4 + 1]) + (red[q * 4 + 2] + red[q * 4 + 3]);
             const float r = 1.0f / sqrtf(total / float(HIDDEN) + 1e-6f);
 #pragma unroll
@@ -243,7 +242,7 @@ __device__ __forceinline__ void stage_finish(const GemvParams& p, int rows, cons
                 round_bf16x2(xv[q][k] * r, xv[q][k + 1] * r, t0, t1);
                 const uint32_t xn2 = pack_bf16(t0 * gn[k], t1 * gn[k + 1]);  // the two BF16 results
                 *reinterpret_cast<uint32_t*>(&xs[q * HIDDEN + i]) = xn2;
-                if (blockIdx.x == 0) {
+                if (blockIdx.x == 0 && q < rows) {
                     if constexpr (PRO == PRO_RESID) {
                         p.resid_out[q * HIDDEN + i] = xv[q][k];
                         p.resid_out[q * HIDDEN + i + 1] = xv[q][k + 1];
@@ -443,20 +442,16 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvParams p) {
     }
     stage_finish<N, MAXR, PRO>(p, rows, S, xs, red);
     __syncthreads();
-    for (; g < groups; g += stride) {
-        int wrow[U];
-        rows_of(g, wrow);
-        uint4 w[U][IT];
+    auto decode_all = [&](const WRaw<PACKED> (&cur)[U][IT], uint4 (&w)[U][IT]) {
 #pragma unroll
         for (int u = 0; u < U; ++u)
 #pragma unroll
-            for (int it = 0; it < IT; ++it) w[u][it] = decode_w<PACKED>(wr[u][it]);
-        const int gn = g + stride;
-        if (gn < groups) {
-            int nrow[U];
-            rows_of(gn, nrow);
-            request_w<N, PACKED, U, IT>(p, nrow, lane, wr);
-        }
+            for (int it = 0; it < IT; ++it) w[u][it] = decode_w<PACKED>(cur[u][it]);
+    };
+    // One row group with its weights `w`.
+    auto group = [&](const int g, const uint4 (&w)[U][IT]) {
+        int wrow[U];
+        rows_of(g, wrow);
         float acc[U][MAXR];
 #pragma unroll
         for (int u = 0; u < U; ++u)
@@ -466,11 +461,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvParams p) {
         for (int it = 0; it < IT; ++it) {
 #pragma unroll
             for (int q = 0; q < MAXR; ++q) {
-                if (q < rows) {
-                    const uint4 xv = *reinterpret_cast<const uint4*>(&xs[q * N + it * 512 + lane * 8]);
+                if (MAXR > 1 && q >= rows) break;
+                const uint4 xv = *reinterpret_cast<const uint4*>(&xs[q * N + it * 512 + lane * 8]);
 #pragma unroll
-                    for (int u = 0; u < U; ++u) acc[u][q] = dot8(w[u][it], xv, acc[u][q]);
-                }
+                for (int u = 0; u < U; ++u) acc[u][q] = dot8(w[u][it], xv, acc[u][q]);
             }
         }
         if constexpr (EPI == EPI_ROUND || EPI == EPI_BF16 || EPI == EPI_SWIGLU) {
@@ -528,6 +522,43 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvParams p) {
                     if (better(v, uint32_t(wrow[u]), best_v[q], best_i[q])) { best_v[q] = v; best_i[q] = wrow[u]; }
                 }
             }
+        }
+    };
+    if constexpr (!PACKED) {
+        // plain weights: two request buffers in turn (the next group's requests land in the
+        // other buffer, so no register copies between groups)
+        WRaw<PACKED> wb[U][IT];
+        for (; g < groups; g += 2 * stride) {
+            const int g1 = g + stride, g2 = g1 + stride;
+            int nrow[U];
+            if (g1 < groups) {
+                rows_of(g1, nrow);
+                request_w<N, PACKED, U, IT>(p, nrow, lane, wb);
+            }
+            uint4 w[U][IT];
+            decode_all(wr, w);
+            group(g, w);
+            if (g1 >= groups) break;
+            if (g2 < groups) {
+                rows_of(g2, nrow);
+                request_w<N, PACKED, U, IT>(p, nrow, lane, wr);
+            }
+            decode_all(wb, w);
+            group(g1, w);
+        }
+    } else {
+        // .p12: decode, then request the next group into the same buffer (fewer registers
+        // than two buffers of payload, table words and tags)
+        for (; g < groups; g += stride) {
+            uint4 w[U][IT];
+            decode_all(wr, w);
+            const int gn = g + stride;
+            if (gn < groups) {
+                int nrow[U];
+                rows_of(gn, nrow);
+                request_w<N, PACKED, U, IT>(p, nrow, lane, wr);
+            }
+            group(g, w);
         }
     }
 
