@@ -15,6 +15,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "common.h"
 #include "device.h"
@@ -35,6 +36,16 @@ constexpr int gemv_u() {
 }
 
 // ---------------------------------------------------------------------------- prologues
+// Staged activation rows in LDS.  FP32 form: column c of a 512-column block sits at
+// (c & 4 ? 256 : 0) + 4 * ((c >> 3) & 63) + (c & 3), so the 8 columns a lane owns are two
+// float4 reads at 16-byte lane strides (no bank conflicts) and need no unpacking.  The
+// four-row 6144-wide rows stay BF16 (96 KB of FP32 would leave one workgroup per CU).
+template <int N, int MAXR>
+constexpr bool xs_f32() { return !(N == INTER && MAXR > 1); }
+template <int N, int MAXR>
+using xs_t = typename std::conditional<xs_f32<N, MAXR>(), float, uint16_t>::type;
+__device__ __forceinline__ int xpos(int c) { return (c & ~511) | ((c & 4) << 6) | (((c >> 3) & 63) << 2) | (c & 3); }
+
 // Stage the BF16 activation rows into LDS.  Values are BF16-exact FP32 (every producer
 // rounds), so the BF16 copy is lossless.  The prologue is split into its loads
 // (stage_load) and its arithmetic (stage_finish) so the kernel can request the first
@@ -123,7 +134,8 @@ __device__ __forceinline__ void stage_load(const GemvParams& p, int rb, Staged<N
 
 template <int N, int MAXR, int PRO>
 __device__ __forceinline__ void stage_finish(const GemvParams& p, int rows, const Staged<N, MAXR, PRO>& S,
-                                             uint16_t* xs, float* red) {
+                                             xs_t<N, MAXR>* xs, float* red) {
+    constexpr bool XF = xs_f32<N, MAXR>();
     const int tid = threadIdx.x;
     constexpr int V = Staged<N, MAXR, PRO>::V, E = Staged<N, MAXR, PRO>::E;
     // Every LDS row is written: rows past the step's hold re-read buffer rows or zeros, so the
@@ -135,9 +147,14 @@ __device__ __forceinline__ void stage_finish(const GemvParams& p, int rows, cons
             for (int k = 0; k < V; ++k) {
                 const int e = (tid + 256 * k) * 4;
                 if (e >= N) continue;
-                const uint32_t lo2 = (bits(S.v[q][k].x) & 0xffffu) | (bits(S.v[q][k].y) << 16);
-                const uint32_t hi2 = (bits(S.v[q][k].z) & 0xffffu) | (bits(S.v[q][k].w) << 16);
-                *reinterpret_cast<uint2*>(&xs[q * N + e]) = make_uint2(lo2, hi2);
+                if constexpr (XF) {
+                    *reinterpret_cast<float4*>(&xs[q * N + xpos(e)]) = make_float4(
+                        roundbf(S.v[q][k].x), roundbf(S.v[q][k].y), roundbf(S.v[q][k].z), roundbf(S.v[q][k].w));
+                } else {
+                    const uint32_t lo2 = (bits(S.v[q][k].x) & 0xffffu) | (bits(S.v[q][k].y) << 16);
+                    const uint32_t hi2 = (bits(S.v[q][k].z) & 0xffffu) | (bits(S.v[q][k].w) << 16);
+                    *reinterpret_cast<uint2*>(&xs[q * N + e]) = make_uint2(lo2, hi2);
+                }
             }
         }
     } else if constexpr (PRO == PRO_PLAIN16) {
@@ -147,7 +164,15 @@ __device__ __forceinline__ void stage_finish(const GemvParams& p, int rows, cons
 #pragma unroll
             for (int k = 0; k < V16; ++k) {
                 const int e = (tid + 256 * k) * 8;
-                if (e < N) *reinterpret_cast<uint4*>(&xs[q * N + e]) = S.h[q][k];
+                if (e >= N) continue;
+                const uint4 h = S.h[q][k];
+                if constexpr (XF) {
+                    float* d = reinterpret_cast<float*>(xs) + q * N + xpos(e);
+                    *reinterpret_cast<float4*>(d) = make_float4(lo(h.x), hi(h.x), lo(h.y), hi(h.y));
+                    *reinterpret_cast<float4*>(d + 256) = make_float4(lo(h.z), hi(h.z), lo(h.w), hi(h.w));
+                } else {
+                    *reinterpret_cast<uint4*>(&xs[q * N + e]) = h;
+                }
             }
         }
     } else {
@@ -241,7 +266,8 @@ __device__ __forceinline__ void stage_finish(const GemvParams& p, int rows, cons
                 float t0, t1;
                 round_bf16x2(xv[q][k] * r, xv[q][k + 1] * r, t0, t1);
                 const uint32_t xn2 = pack_bf16(t0 * gn[k], t1 * gn[k + 1]);  // the two BF16 results
-                *reinterpret_cast<uint32_t*>(&xs[q * HIDDEN + i]) = xn2;
+                if constexpr (XF) *reinterpret_cast<float2*>(&xs[q * HIDDEN + xpos(i)]) = make_float2(lo(xn2), hi(xn2));
+                else *reinterpret_cast<uint32_t*>(&xs[q * HIDDEN + i]) = xn2;
                 if (blockIdx.x == 0 && q < rows) {
                     if constexpr (PRO == PRO_RESID) {
                         p.resid_out[q * HIDDEN + i] = xv[q][k];
@@ -380,7 +406,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvParams p) {
     constexpr int IT = N / 512;
     constexpr int U = gemv_u<N, MAXR, EPI>();
     constexpr int H = U / 2;  // SwiGLU: gate rows (and up rows) per group
-    __shared__ __align__(16) uint16_t xs[MAXR * N];
+    __shared__ __align__(16) xs_t<N, MAXR> xs[MAXR * N];
     __shared__ float red[MAXR * 4];
     __shared__ float cand_v[MAXR * 4];
     __shared__ uint32_t cand_i[MAXR * 4];
@@ -462,9 +488,17 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvParams p) {
 #pragma unroll
             for (int q = 0; q < MAXR; ++q) {
                 if (MAXR > 1 && q >= rows) break;
-                const uint4 xv = *reinterpret_cast<const uint4*>(&xs[q * N + it * 512 + lane * 8]);
+                if constexpr (xs_f32<N, MAXR>()) {
+                    const float* xr = reinterpret_cast<const float*>(xs) + q * N + it * 512 + lane * 4;
+                    const float4 xa = *reinterpret_cast<const float4*>(xr);
+                    const float4 xb = *reinterpret_cast<const float4*>(xr + 256);
 #pragma unroll
-                for (int u = 0; u < U; ++u) acc[u][q] = dot8(w[u][it], xv, acc[u][q]);
+                    for (int u = 0; u < U; ++u) acc[u][q] = dot8f(w[u][it], xa, xb, acc[u][q]);
+                } else {
+                    const uint4 xv = *reinterpret_cast<const uint4*>(&xs[q * N + it * 512 + lane * 8]);
+#pragma unroll
+                    for (int u = 0; u < U; ++u) acc[u][q] = dot8(w[u][it], xv, acc[u][q]);
+                }
             }
         }
         if constexpr (EPI == EPI_ROUND || EPI == EPI_BF16 || EPI == EPI_SWIGLU) {

@@ -152,6 +152,19 @@ __device__ __forceinline__ uint4 p12_decode8(uint2 sm, uint32_t nib, uint32_t ta
     return r;
 }
 
+// The same over 8 BF16 weights and 8 FP32 activations (a = elements 0..3, b = 4..7).
+__device__ __forceinline__ float dot8f(const uint4 w, const float4 a, const float4 b, float acc) {
+    acc = fmaf(lo(w.x), a.x, acc);
+    acc = fmaf(hi(w.x), a.y, acc);
+    acc = fmaf(lo(w.y), a.z, acc);
+    acc = fmaf(hi(w.y), a.w, acc);
+    acc = fmaf(lo(w.z), b.x, acc);
+    acc = fmaf(hi(w.z), b.y, acc);
+    acc = fmaf(lo(w.w), b.z, acc);
+    acc = fmaf(hi(w.w), b.w, acc);
+    return acc;
+}
+
 // Raw buffer views (gfx9 resource word 3 = 0x00020000): base + 32-bit byte offset held in one
 // VGPR; a read at or past `bytes` returns zero instead of touching memory.
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
