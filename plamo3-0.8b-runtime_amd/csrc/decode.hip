@@ -466,6 +466,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvParams p) {
 #pragma unroll
         for (int q = 0; q < MAXR; ++q) orow[q] = st->lane[q];
     }
+    uint32_t orow_packed = 0;  // lanes are below 4: one byte each
+#pragma unroll
+    for (int q = 0; q < MAXR; ++q) orow_packed |= (orow[q] & 0xffu) << (8 * q);
     stage_finish<N, MAXR, PRO>(p, rows, S, xs, red);
     __syncthreads();
     auto decode_all = [&](const WRaw<PACKED> (&cur)[U][IT], uint4 (&w)[U][IT]) {
@@ -534,27 +537,30 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvParams p) {
                 }
             }
         } else {  // EPI_LOGITS
+            // Same reduce-scatter: lane holds the logit of value idx = lane >> S (weight row
+            // u = idx / MAXR of row q = idx % MAXR), written by lane idx << S; every lane keeps
+            // the first maximum of the values it held (its q never changes).
+            constexpr int K = U * MAXR, S = 6 - log2_pow2(K);
+            float vals[K];
 #pragma unroll
             for (int u = 0; u < U; ++u)
 #pragma unroll
-                for (int q = 0; q < MAXR; ++q) acc[u][q] = wave_sum(acc[u][q]);
-#pragma unroll
-            for (int q = 0; q < MAXR; ++q) {
-                if (q >= rows) continue;
-#pragma unroll
-                for (int u = 0; u < U; ++u) {
-                    const uint32_t b = bits(acc[u][q]);
-                    if (lane == 0) p.out16[size_t(orow[q]) * VOCAB + wrow[u]] = uint16_t(b);
-                    float v = bf(b);
-                    if (ctl.on) {
-                        const uint32_t r = uint32_t(wrow[u]);
-                        const int32_t c = p.bufs.counts[size_t(q) * VOCAB + r];
-                        const bool ban = ctl.ngram > 1 &&
-                                         ((p.bufs.banned[size_t(q) * (VOCAB / 32) + (r >> 5)] >> (r & 31)) & 1u);
-                        v = sampled(v, c, ban, ctl);
-                    }
-                    if (better(v, uint32_t(wrow[u]), best_v[q], best_i[q])) { best_v[q] = v; best_i[q] = wrow[u]; }
+                for (int q = 0; q < MAXR; ++q) vals[u * MAXR + q] = acc[u][q];
+            const float t = wave_sum_scatter<K>(vals);
+            const int idx = lane >> S, u = idx / MAXR, q = idx % MAXR;
+            if (q < rows) {
+                const int r = g * U + u;                                   // rows_of for logits
+                const uint32_t oq = (orow_packed >> (8 * q)) & 0xffu;     // lane of row q
+                const uint32_t b = bits(t);
+                if ((lane & ((1 << S) - 1)) == 0) p.out16[size_t(oq) * VOCAB + r] = uint16_t(b);
+                float v = bf(b);
+                if (ctl.on) {
+                    const int32_t c = p.bufs.counts[size_t(q) * VOCAB + r];
+                    const bool ban = ctl.ngram > 1 &&
+                                     ((p.bufs.banned[size_t(q) * (VOCAB / 32) + (uint32_t(r) >> 5)] >> (r & 31)) & 1u);
+                    v = sampled(v, c, ban, ctl);
                 }
+                if (better(v, uint32_t(r), best_v[0], best_i[0])) { best_v[0] = v; best_i[0] = uint32_t(r); }
             }
         }
     };
@@ -597,10 +603,24 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvParams p) {
     }
 
     if constexpr (EPI == EPI_LOGITS) {
-        // block partial; head_merge_kernel reduces the partials of every block
-        if (lane == 0)
-#pragma unroll
-            for (int q = 0; q < MAXR; ++q) { cand_v[q * 4 + wave] = best_v[q]; cand_i[q * 4 + wave] = best_i[q]; }
+        // block partial; head_merge_kernel reduces the partials of every block.  Lanes with
+        // the same row q differ in the weight-row bits of the lane index (and in the low S
+        // bits, which hold copies): first maximum over the weight-row bits, then lane q << S
+        // holds the wave's best for row q.
+        constexpr int K = U * MAXR, S = 6 - log2_pow2(K), QB = S + log2_pow2(MAXR);
+        float bv = best_v[0];
+        uint32_t bi = best_i[0];
+        if constexpr (QB <= 5) best_step<32>(bv, bi);
+        if constexpr (QB <= 4) best_step<16>(bv, bi);
+        if constexpr (QB <= 3) best_step<8>(bv, bi);
+        if constexpr (QB <= 2) best_step<4>(bv, bi);
+        if constexpr (QB <= 1) best_step<2>(bv, bi);
+        if constexpr (QB <= 0) best_step<1>(bv, bi);
+        if ((lane & ((1 << S) - 1)) == 0 && (lane >> QB) == 0) {
+            const int q = lane >> S;
+            cand_v[q * 4 + wave] = bv;
+            cand_i[q * 4 + wave] = bi;
+        }
         __syncthreads();
         if (tid < MAXR && tid < rows) {
             const int q = tid;
