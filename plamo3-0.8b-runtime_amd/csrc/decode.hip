@@ -35,6 +35,14 @@ constexpr int gemv_u() {
     else return MAXR == 1 ? 4 : 2;
 }
 
+// Waves per workgroup.  Four-row kernels whose prologue (the four-row norm, or staging four
+// 6144-wide rows) every workgroup repeats run eight waves, so one workgroup per CU does it
+// once for twice the waves; the prologue itself stays on the first four (same ownership of
+// elements, same sums).
+__host__ __device__ constexpr int gemv_waves(int n, int maxr, int epi) {
+    return maxr > 1 && (epi == EPI_SWIGLU || epi == EPI_LOGITS || n == INTER) ? 8 : 4;
+}
+
 // ---------------------------------------------------------------------------- prologues
 // Staged activation rows in LDS.  FP32 form: column c of a 512-column block sits at
 // (c & 4 ? 256 : 0) + 4 * ((c >> 3) & 63) + (c & 3), so the 8 columns a lane owns are two
@@ -134,13 +142,15 @@ __device__ __forceinline__ void stage_load(const GemvParams& p, int rb, Staged<N
 
 template <int N, int MAXR, int PRO>
 __device__ __forceinline__ void stage_finish(const GemvParams& p, int rows, const Staged<N, MAXR, PRO>& S,
-                                             xs_t<N, MAXR>* xs, float* red) {
+                                             xs_t<N, MAXR>* xs, float* red, bool active) {
+    // `active`: the first 256 threads; the others only pass the same barriers.
     constexpr bool XF = xs_f32<N, MAXR>();
     const int tid = threadIdx.x;
     constexpr int V = Staged<N, MAXR, PRO>::V, E = Staged<N, MAXR, PRO>::E;
     // Every LDS row is written: rows past the step's hold re-read buffer rows or zeros, so the
     // main loop can run all MAXR rows without branches (their results are never stored).
     if constexpr (PRO == PRO_PLAIN) {
+        if (!active) return;
 #pragma unroll
         for (int q = 0; q < MAXR; ++q) {
 #pragma unroll
@@ -158,6 +168,7 @@ __device__ __forceinline__ void stage_finish(const GemvParams& p, int rows, cons
             }
         }
     } else if constexpr (PRO == PRO_PLAIN16) {
+        if (!active) return;
         constexpr int V16 = Staged<N, MAXR, PRO>::V16;
 #pragma unroll
         for (int q = 0; q < MAXR; ++q) {
@@ -179,6 +190,7 @@ __device__ __forceinline__ void stage_finish(const GemvParams& p, int rows, cons
         float xv[MAXR][E];
         float ss[MAXR];
         if constexpr (PRO == PRO_EMBED) {
+            if (active)
 #pragma unroll
             for (int q = 0; q < MAXR; ++q)
 #pragma unroll
@@ -190,6 +202,7 @@ __device__ __forceinline__ void stage_finish(const GemvParams& p, int rows, cons
             // z = roundbf(roundbf(p*r) * roundbf(bf(w)+offset)); x = roundbf(x + z)
             // (Kernels.metal:59-72, full == 1)
             float pv[MAXR][E], rv[MAXR][E], gp[E];
+            if (active) {
 #pragma unroll
             for (int k = 0; k < E / 2; ++k) {
                 gp[2 * k] = lo(S.gp[k]);
@@ -222,7 +235,9 @@ __device__ __forceinline__ void stage_finish(const GemvParams& p, int rows, cons
                 ss[q] = wave_sum(ss[q]);
                 if ((tid & 63) == 0) red[q * 4 + (tid >> 6)] = ss[q];
             }
+            }
             __syncthreads();
+            if (active) {
             // BF16 roundings two at a time (packed RNE conversion, identical to `roundbf`)
             float g[E];
 #pragma unroll
@@ -241,10 +256,12 @@ __device__ __forceinline__ void stage_finish(const GemvParams& p, int rows, cons
                     xv[q][k + 1] = (q < rows) ? x1 : 0.f;
                 }
             }
+            }
             __syncthreads();
         }
         // next norm with +1 offset (Kernels.metal:76-89)
         float gn[E];
+        if (active) {
 #pragma unroll
         for (int k = 0; k < E / 2; ++k) round_bf16x2(lo(S.gn[k]) + 1.0f, hi(S.gn[k]) + 1.0f, gn[2 * k], gn[2 * k + 1]);
 #pragma unroll
@@ -255,7 +272,9 @@ __device__ __forceinline__ void stage_finish(const GemvParams& p, int rows, cons
             ss[q] = wave_sum(ss[q]);
             if ((tid & 63) == 0) red[q * 4 + (tid >> 6)] = ss[q];
         }
+        }
         __syncthreads();
+        if (!active) return;
 #pragma unroll
         for (int q = 0; q < MAXR; ++q) {
             const float total = (red[q * 4] + red[q * 4 + 1]) + (red[q * 4 + 2] + red[q * 4 + 3]);
@@ -402,17 +421,20 @@ __device__ __forceinline__ float sampled(float l, int32_t count, bool banned, co
 
 // ------------------------------------------------------------------------------- GEMV
 template <int N, bool PACKED, int MAXR, int PRO, int EPI, bool STATE>
-__global__ __launch_bounds__(256) void gemv_kernel(const GemvParams p) {
+__global__ __launch_bounds__(64 * gemv_waves(N, MAXR, EPI)) void gemv_kernel(const GemvParams p) {
+    constexpr int NWV = gemv_waves(N, MAXR, EPI);
     constexpr int IT = N / 512;
     constexpr int U = gemv_u<N, MAXR, EPI>();
     constexpr int H = U / 2;  // SwiGLU: gate rows (and up rows) per group
     __shared__ __align__(16) xs_t<N, MAXR> xs[MAXR * N];
     __shared__ float red[MAXR * 4];
-    __shared__ float cand_v[MAXR * 4];
-    __shared__ uint32_t cand_i[MAXR * 4];
+    __shared__ float cand_v[MAXR * NWV];
+    __shared__ uint32_t cand_i[MAXR * NWV];
 
     const StepState* st = p.state;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const bool stager = wave < 4;  // the prologue runs on the first 256 threads
     const int groups = p.m / U;
     // Request order = consumption order: step state, prologue inputs, first weights.  The
     // state is read through a lane-dependent address (lane_mask is 0, so every lane reads
@@ -426,7 +448,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvParams p) {
         srows = sv->rows;
     }
     Staged<N, MAXR, PRO> S;
-    stage_load<N, MAXR, PRO>(p, p.rows < MAXR ? p.rows : MAXR, S);
+    if (stager) stage_load<N, MAXR, PRO>(p, p.rows < MAXR ? p.rows : MAXR, S);
     float best_v[MAXR];
     uint32_t best_i[MAXR];
 #pragma unroll
@@ -442,8 +464,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvParams p) {
     // Software pipelined over the wave's row groups: the next group's weights are in flight
     // while the current group is reduced and written.  The first group's weights do not
     // depend on the previous kernel, so they are requested before the activation prologue.
-    const int stride = gridDim.x * 4;
-    int g = blockIdx.x * 4 + wave;
+    const int stride = gridDim.x * NWV;
+    int g = blockIdx.x * NWV + wave;
     WRaw<PACKED> wr[U][IT];
     {
         // unconditional (a wave without a group re-reads the last one) so the compiler
@@ -469,7 +491,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvParams p) {
     uint32_t orow_packed = 0;  // lanes are below 4: one byte each
 #pragma unroll
     for (int q = 0; q < MAXR; ++q) orow_packed |= (orow[q] & 0xffu) << (8 * q);
-    stage_finish<N, MAXR, PRO>(p, rows, S, xs, red);
+    stage_finish<N, MAXR, PRO>(p, rows, S, xs, red, stager);
     __syncthreads();
     auto decode_all = [&](const WRaw<PACKED> (&cur)[U][IT], uint4 (&w)[U][IT]) {
 #pragma unroll
@@ -618,16 +640,16 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvParams p) {
         if constexpr (QB <= 0) best_step<1>(bv, bi);
         if ((lane & ((1 << S) - 1)) == 0 && (lane >> QB) == 0) {
             const int q = lane >> S;
-            cand_v[q * 4 + wave] = bv;
-            cand_i[q * 4 + wave] = bi;
+            cand_v[q * NWV + wave] = bv;
+            cand_i[q * NWV + wave] = bi;
         }
         __syncthreads();
         if (tid < MAXR && tid < rows) {
             const int q = tid;
-            float bv = cand_v[q * 4];
-            uint32_t bi = cand_i[q * 4];
-            for (int k = 1; k < 4; ++k)
-                if (better(cand_v[q * 4 + k], cand_i[q * 4 + k], bv, bi)) { bv = cand_v[q * 4 + k]; bi = cand_i[q * 4 + k]; }
+            float bv = cand_v[q * NWV];
+            uint32_t bi = cand_i[q * NWV];
+            for (int k = 1; k < NWV; ++k)
+                if (better(cand_v[q * NWV + k], cand_i[q * NWV + k], bv, bi)) { bv = cand_v[q * NWV + k]; bi = cand_i[q * NWV + k]; }
             p.bufs.head_v[q * HEAD_BLOCKS + blockIdx.x] = bv;
             p.bufs.head_i[q * HEAD_BLOCKS + blockIdx.x] = bi;
         }
@@ -1218,7 +1240,7 @@ __global__ void fill_u32_kernel(uint32_t* p, uint32_t v, size_t n) {
 
 template <int N, bool PACKED, int MAXR>
 void gemv_dispatch_epi(Prologue pro, Epilogue epi, const GemvParams& p, int blocks, hipStream_t s) {
-    const dim3 grid(blocks), block(256);
+    const dim3 grid(blocks), block(64 * gemv_waves(N, MAXR, epi));
 #define PLAMO_GEMV(PRO, EPI) hipLaunchKernelGGL((gemv_kernel<N, PACKED, MAXR, PRO, EPI, true>), grid, block, 0, s, p)
 #define PLAMO_GEMV_NOSTATE(PRO, EPI) \
     hipLaunchKernelGGL((gemv_kernel<N, PACKED, MAXR, PRO, EPI, false>), grid, block, 0, s, p)
@@ -1270,12 +1292,13 @@ int gemv_group_rows(int n, int maxr, Epilogue epi) {
 
 int gemv_blocks(int n, int maxr, Epilogue epi, int m) {
     const int groups = m / gemv_group_rows(n, maxr, epi);
-    const int b = (groups + 3) / 4;  // one group per wave
+    const int nw = gemv_waves(n, maxr, epi);
+    const int b = (groups + nw - 1) / nw;  // one group per wave
     // Multi-row kernels: at most two workgroups per CU, each wave walking several groups
     // (weights of the next in flight), so the activation prologue every workgroup
     // recomputes is paid twice per CU instead of four to six times.
     if (maxr > 1 && n == HIDDEN && epi == EPI_ROUND) return (b + 1) / 2;  // QKV: two groups per wave
-    return maxr > 1 ? std::min(b, 512) : b;
+    return maxr > 1 ? std::min(b, 2048 / nw) : b;
 }
 
 void launch_gemv(int n, bool packed, int maxr, Prologue pro, Epilogue epi, const GemvParams& p, int blocks,

@@ -311,8 +311,8 @@ void Engine::enqueue_head(const float* in, const float* resid_in, int in_rows) {
     g.hidden = hidden;
     g.out16 = logits;
     g.bufs = bufs;
-    launch_gemv(HIDDEN, m.packed, maxr, PRO_RESID, EPI_LOGITS, g, HEAD_BLOCKS, stream);
-    launch_head_merge(bufs, HEAD_BLOCKS, stream);
+    launch_gemv(HIDDEN, m.packed, maxr, PRO_RESID, EPI_LOGITS, g, head_blocks(maxr), stream);
+    launch_head_merge(bufs, head_blocks(maxr), stream);
 }
 
 void Engine::enqueue_head16() {
@@ -333,8 +333,8 @@ void Engine::enqueue_head16() {
     g.hidden = hidden;
     g.out16 = logits;
     g.bufs = bufs;
-    launch_gemv(HIDDEN, m.packed, maxr, PRO_RESID16, EPI_LOGITS, g, HEAD_BLOCKS, stream);
-    launch_head_merge(bufs, HEAD_BLOCKS, stream);
+    launch_gemv(HIDDEN, m.packed, maxr, PRO_RESID16, EPI_LOGITS, g, head_blocks(maxr), stream);
+    launch_head_merge(bufs, head_blocks(maxr), stream);
 }
 
 // One decode step (Runtime.swift:376-458 for one token per row; Batch.swift:147-165).
