@@ -676,7 +676,8 @@ __global__ __launch_bounds__(256) void head_merge_kernel(DecodeBuffers b, int bl
     __shared__ float cv[ROWS * 4];
     __shared__ uint32_t ci[ROWS * 4];
     __shared__ StepState ls;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar)
     // every row's partials requested together with the state (rows past the step's are not used)
     constexpr int PER = HEAD_BLOCKS / 256;
     float pv[ROWS][PER];
@@ -750,7 +751,8 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
 
     const StepState* st = p.state;
     const int q = blockIdx.z, hg = blockIdx.y;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar)
     // Row geometry.  Visible keys are the absolute positions first..pos (window 2048 on the
     // local layers); key r sits at ring slot (first + r) % capacity.  Local keys rotate
     // with coordinate r and the query with pos - first: a decode step is a 16-token chunk
@@ -931,7 +933,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
     // ---- unnormalised P.V: thread -> dims 2e, 2e+1 (e = tid & 63) of local head tid >> 6;
     //      keys 0..31 and 32..63 as two ordered chains per dim, added at the end
     {
-        const int e = tid & 63, hl = tid >> 6;
+        const int e = tid & 63, hl = wave;
         const uint32_t* v32 = reinterpret_cast<const uint32_t*>(vs);
         float o[2][2] = {{0.f, 0.f}, {0.f, 0.f}};  // [dim][half]
 #pragma unroll 2

@@ -166,7 +166,8 @@ __global__ __launch_bounds__(NT) void gemm_kernel(const GemmParams p, int col_ti
     static_assert(EPI != GEMM_SWIGLU || TW % 2 == 0, "SwiGLU pairs gate and up tiles inside a wave");
     __shared__ __align__(16) uint16_t As[2][BT * LDS_STRIDE];
     __shared__ __align__(16) uint16_t Bs[2][BW * LDS_STRIDE];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar)
     const int wt = wave / WW, ww = wave % WW;
     const int tiles = col_tiles * row_tiles;
     const int per = (tiles + 7) / 8;
@@ -293,7 +294,8 @@ __global__ __launch_bounds__(NT) void gemm_dma_kernel(const GemmParams p, int co
         else if constexpr (i == 4) return S4;
         else return S5;
     };
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar)
     const int wt = wave / WW, ww = wave % WW;
     const int tiles = col_tiles * row_tiles;
     const int per = (tiles + 7) / 8;
