@@ -283,6 +283,7 @@ Engine::Engine(std::shared_ptr<Model> mdl, int ctx, int nl, hipStream_t s)
 
 Engine::~Engine() {
     if (graph) (void)hipGraphExecDestroy(graph);
+    if (graph16) (void)hipGraphExecDestroy(graph16);
 
     (void)hipEventDestroy(ev0);
     (void)hipEventDestroy(ev1);
@@ -439,6 +440,31 @@ void Engine::run_step() {
         PLAMO_HIP(hipGraphDestroy(g));
     }
     PLAMO_HIP(hipGraphLaunch(graph, stream));
+}
+
+// Captures (without running) the graph of LOOP_GRAPH_STEPS consecutive steps.
+void Engine::prepare_loop_graph() {
+    if (!use_graph || graph16) return;
+    hipGraph_t g = nullptr;
+    PLAMO_HIP(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal));
+    try {
+        for (int k = 0; k < LOOP_GRAPH_STEPS; ++k) enqueue_step();
+    } catch (...) {
+        (void)hipStreamEndCapture(stream, &g);
+        if (g) (void)hipGraphDestroy(g);
+        throw;
+    }
+    PLAMO_HIP(hipStreamEndCapture(stream, &g));
+    PLAMO_HIP(hipGraphInstantiate(&graph16, g, nullptr, nullptr, 0));
+    PLAMO_HIP(hipGraphDestroy(g));
+}
+
+void Engine::run_steps(int n) {
+    if (use_graph && n >= LOOP_GRAPH_STEPS) {
+        prepare_loop_graph();
+        for (; n >= LOOP_GRAPH_STEPS; n -= LOOP_GRAPH_STEPS) PLAMO_HIP(hipGraphLaunch(graph16, stream));
+    }
+    for (; n > 0; --n) run_step();
 }
 
 // A prefill chunk of n tokens at p0 for one lane: every layer as MFMA GEMMs, K/V written
@@ -777,7 +803,7 @@ BatchImpl::Decoded BatchImpl::decode(const std::vector<int32_t>& first, const st
     // the loop after at most max(limit) + 1 steps
     int launched = 0;
     while (true) {
-        for (int k = 0; k < 16; ++k) e.run_step();
+        e.run_steps(16);
         launched += 16;
         PLAMO_HIP(hipMemcpyAsync(&hs, e.state, sizeof(StepState), hipMemcpyDeviceToHost, s));
         const hipError_t sync = hipStreamSynchronize(s);
@@ -847,7 +873,7 @@ std::vector<int32_t> RuntimeImpl::generate(const int32_t* prompt, int n, int max
     int launched = 0;
     while (launched < max_tokens) {
         const int batch = std::min(16, max_tokens - launched);
-        for (int k = 0; k < batch; ++k) e.run_step();
+        e.run_steps(batch);
         launched += batch;
         PLAMO_HIP(hipMemcpyAsync(&hs, e.state, sizeof(StepState), hipMemcpyDeviceToHost, stream));
         PLAMO_HIP(hipStreamSynchronize(stream));
@@ -887,10 +913,11 @@ double RuntimeImpl::bench_decode(int steps) {
     hs.stopped = 0;
     sync_sampler(e, 0);
     PLAMO_HIP(hipMemcpyAsync(e.state, &hs, sizeof(StepState), hipMemcpyHostToDevice, stream));
-    e.run_step();  // capture outside the timed region
+    e.run_step();            // capture outside the timed region
+    e.prepare_loop_graph();  // (captured, not run)
     PLAMO_HIP(hipStreamSynchronize(stream));
     PLAMO_HIP(hipEventRecord(e.ev0, stream));
-    for (int k = 1; k < steps; ++k) e.run_step();
+    e.run_steps(steps - 1);
     PLAMO_HIP(hipEventRecord(e.ev1, stream));
     PLAMO_HIP(hipEventSynchronize(e.ev1));
     float ms = 0;

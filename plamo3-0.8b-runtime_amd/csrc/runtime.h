@@ -85,12 +85,18 @@ class Engine {
     size_t part_rows_cap;    // rows x parts the partial buffers hold
     // graph
     hipGraphExec_t graph = nullptr;
+    hipGraphExec_t graph16 = nullptr;  // LOOP_GRAPH_STEPS consecutive steps
     bool use_graph = true;
 
     hipEvent_t ev0, ev1;
 
     void enqueue_step(bool head = true);    // one decode step for state->rows rows
     void run_step();                        // graph replay (or direct launches)
+    // n device-loop steps: replays of a LOOP_GRAPH_STEPS-step graph, then single steps (one
+    // graph launch per 16 steps instead of per step)
+    static constexpr int LOOP_GRAPH_STEPS = 16;
+    void run_steps(int n);
+    void prepare_loop_graph();
     // prefill of `n` tokens of one lane at position p0 (n > 1); head on the last token.
     void prefill(const int32_t* tokens, int n, int p0, int lane, bool output);
     void zero_sampler();
