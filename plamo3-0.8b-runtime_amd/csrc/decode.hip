@@ -753,6 +753,29 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
     const int q = blockIdx.z, hg = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar)
+    // ---- loads that do not depend on the step state go out before it arrives: the group's
+    //      queries and norm weights (threads 0..63), the newest key (64..79) and value (128..)
+    const float* x = p.qkv + size_t(q) * QKV;
+    const int hl = tid >> 4, sq = tid & 15;                 // local q head (threads 0..63), pair group
+    float4 qlo = make_float4(0.f, 0.f, 0.f, 0.f), qhi = qlo;
+    uint2 glo = make_uint2(0, 0), ghi = glo;
+    if (tid < HG * 16) {
+        const int h = hg * HG + hl;
+        qlo = *reinterpret_cast<const float4*>(x + h * HEAD_DIM + sq * 4);
+        qhi = *reinterpret_cast<const float4*>(x + h * HEAD_DIM + 64 + sq * 4);
+        glo = *reinterpret_cast<const uint2*>(p.q_norm + sq * 4);
+        ghi = *reinterpret_cast<const uint2*>(p.q_norm + 64 + sq * 4);
+    }
+    float4 klo = make_float4(0.f, 0.f, 0.f, 0.f), khi = klo;
+    uint2 kgl = make_uint2(0, 0), kgh = kgl;
+    if (tid >= 64 && tid < 80) {
+        const int t = tid - 64;
+        klo = *reinterpret_cast<const float4*>(x + ATTN + t * 4);
+        khi = *reinterpret_cast<const float4*>(x + ATTN + 64 + t * 4);
+        kgl = *reinterpret_cast<const uint2*>(p.k_norm + t * 4);
+        kgh = *reinterpret_cast<const uint2*>(p.k_norm + 64 + t * 4);
+    }
+    const float vnew = tid >= 128 ? x[QKV - HEAD_DIM + (tid - 128)] : 0.f;
     // Row geometry.  Visible keys are the absolute positions first..pos (window 2048 on the
     // local layers); key r sits at ring slot (first + r) % capacity.  Local keys rotate
     // with coordinate r and the query with pos - first: a decode step is a 16-token chunk
@@ -779,21 +802,11 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
     if (blockIdx.x >= nparts) return;  // partitions past the visible keys take no ticket
     const uint32_t newest = count - 1;
     const bool has_new = newest >= k0 && newest < k0 + KP;
-    const float* x = p.qkv + size_t(q) * QKV;
 
-    // ---- every independent global load first
-    const int hl = tid >> 4, sq = tid & 15;                 // local q head (threads 0..63), pair group
-    float4 qlo = make_float4(0.f, 0.f, 0.f, 0.f), qhi = qlo;
-    uint2 glo = make_uint2(0, 0), ghi = glo;
+    // ---- every other independent global load
     uint4 qr = make_uint4(0, 0, 0, 0);
-    if (tid < HG * 16) {
-        const int h = hg * HG + hl;
-        qlo = *reinterpret_cast<const float4*>(x + h * HEAD_DIM + sq * 4);
-        qhi = *reinterpret_cast<const float4*>(x + h * HEAD_DIM + 64 + sq * 4);
-        glo = *reinterpret_cast<const uint2*>(p.q_norm + sq * 4);
-        ghi = *reinterpret_cast<const uint2*>(p.q_norm + 64 + sq * 4);
+    if (tid < HG * 16)
         qr = *reinterpret_cast<const uint4*>((FULL ? p.global_rope : p.local_rope) + size_t(qcoord) * 64 + sq * 4);
-    }
     const int kj = tid >> 2, ksub = tid & 3;                // key, pair group (16 pairs)
     const uint32_t kr = k0 + kj;
     uint4 ka[2] = {make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)};
@@ -833,12 +846,8 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
     // ---- the newest key: k norm, RoPE at pos for global layers, KV write (Kernels.metal:253-257)
     if (has_new && tid >= 64 && tid < 80) {
         const int t = tid - 64;
-        const float4 klo = *reinterpret_cast<const float4*>(x + ATTN + t * 4);
-        const float4 khi = *reinterpret_cast<const float4*>(x + ATTN + 64 + t * 4);
-        const uint2 gl = *reinterpret_cast<const uint2*>(p.k_norm + t * 4);
-        const uint2 gh = *reinterpret_cast<const uint2*>(p.k_norm + 64 + t * 4);
         float z[8];
-        head_norm8(klo, khi, gl, gh, z);
+        head_norm8(klo, khi, kgl, kgh, z);
         const size_t slot = size_t(pos % cap) * HEAD_DIM;
         if (FULL) {
             const uint4 gr = *reinterpret_cast<const uint4*>(p.global_rope + size_t(pos) * 64 + t * 4);
@@ -858,7 +867,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
     }
     if (has_new && tid >= 128) {
         const int d = tid - 128;
-        const uint32_t bv = bits(x[QKV - HEAD_DIM + d]);
+        const uint32_t bv = bits(vnew);
         if (hg == 0) V[size_t(pos % cap) * HEAD_DIM + d] = uint16_t(bv);
         vs[int(newest - k0) * HEAD_DIM + d] = uint16_t(bv);
     }
