@@ -58,48 +58,48 @@ __device__ __forceinline__ int xpos(int c) { return (c & ~511) | ((c & 4) << 6) 
 // rounds), so the BF16 copy is lossless.  The prologue is split into its loads
 // (stage_load) and its arithmetic (stage_finish) so the kernel can request the first
 // weights in between: the vector-memory counter is in order, and inputs requested before
-// the weights can be consumed while the weights are still in flight.
-template <int N, int MAXR, int PRO>
+// the weights can be consumed while the weights are still in flight.  A group of 256
+// threads stages rows q0 .. q0+RQ-1 (thread t owns the same elements of every row).
+template <int N, int RQ, int PRO>
 struct Staged {
     static constexpr int V = (N + 1023) / 1024;  // PLAIN: float4 per thread and row
     static constexpr int V16 = (N + 2047) / 2048; // PLAIN16: 8 BF16 per thread and row
     static constexpr int E = HIDDEN / 256;       // norm prologues: elements per thread (6t .. 6t+5)
-    float4 v[PRO == PRO_PLAIN ? MAXR : 1][V];
-    uint4 h[PRO == PRO_PLAIN16 ? MAXR : 1][V16];
-    float2 a[PRO == PRO_RESID ? MAXR : 1][E / 2];   // RESID: projection output
-    float2 r[PRO == PRO_RESID ? MAXR : 1][E / 2];   // RESID: residual stream
-    uint32_t a16[PRO == PRO_RESID16 ? MAXR : 1][E / 2];  // RESID16: projection output (BF16 pairs)
-    uint32_t r16[PRO == PRO_RESID16 ? MAXR : 1][E / 2];  // RESID16: residual stream (BF16 pairs)
-    uint32_t emb[PRO == PRO_EMBED ? MAXR : 1][E / 2];  // EMBED: embedding row (BF16 pairs)
+    float4 v[PRO == PRO_PLAIN ? RQ : 1][V];
+    uint4 h[PRO == PRO_PLAIN16 ? RQ : 1][V16];
+    float2 a[PRO == PRO_RESID ? RQ : 1][E / 2];   // RESID: projection output
+    float2 r[PRO == PRO_RESID ? RQ : 1][E / 2];   // RESID: residual stream
+    uint32_t a16[PRO == PRO_RESID16 ? RQ : 1][E / 2];  // RESID16: projection output (BF16 pairs)
+    uint32_t r16[PRO == PRO_RESID16 ? RQ : 1][E / 2];  // RESID16: residual stream (BF16 pairs)
+    uint32_t emb[PRO == PRO_EMBED ? RQ : 1][E / 2];  // EMBED: embedding row (BF16 pairs)
     uint32_t gp[E / 2], gn[E / 2];                 // norm weights (BF16 pairs)
 };
 
 // Unconditional loads (rows past rb re-read row rb-1, columns past N re-read the last
 // four), kept raw: converting them here would make the compiler wait for each one.
 // rb: rows the input buffers hold.
-template <int N, int MAXR, int PRO>
-__device__ __forceinline__ void stage_load(const GemvParams& p, int rb, Staged<N, MAXR, PRO>& S) {
-    const int tid = threadIdx.x;
-    constexpr int V = Staged<N, MAXR, PRO>::V, E = Staged<N, MAXR, PRO>::E;
+template <int N, int RQ, int PRO>
+__device__ __forceinline__ void stage_load(const GemvParams& p, int rb, int q0, Staged<N, RQ, PRO>& S) {
+    const int tid = threadIdx.x & 255;
+    constexpr int V = Staged<N, RQ, PRO>::V, V16 = Staged<N, RQ, PRO>::V16, E = Staged<N, RQ, PRO>::E;
     if constexpr (PRO == PRO_PLAIN) {
 #pragma unroll
-        for (int q = 0; q < MAXR; ++q) {
-            const int qq = q < rb ? q : rb - 1;
+        for (int qi = 0; qi < RQ; ++qi) {
+            const int q = q0 + qi, qq = q < rb ? q : rb - 1;
 #pragma unroll
             for (int k = 0; k < V; ++k) {
                 const int e = (tid + 256 * k) * 4;
-                S.v[q][k] = *reinterpret_cast<const float4*>(p.in + qq * N + (e < N ? e : N - 4));
+                S.v[qi][k] = *reinterpret_cast<const float4*>(p.in + qq * N + (e < N ? e : N - 4));
             }
         }
     } else if constexpr (PRO == PRO_PLAIN16) {
-        constexpr int V16 = Staged<N, MAXR, PRO>::V16;
 #pragma unroll
-        for (int q = 0; q < MAXR; ++q) {
-            const int qq = q < rb ? q : rb - 1;
+        for (int qi = 0; qi < RQ; ++qi) {
+            const int q = q0 + qi, qq = q < rb ? q : rb - 1;
 #pragma unroll
             for (int k = 0; k < V16; ++k) {
                 const int e = (tid + 256 * k) * 8;
-                S.h[q][k] = *reinterpret_cast<const uint4*>(p.in16 + qq * N + (e < N ? e : N - 8));
+                S.h[qi][k] = *reinterpret_cast<const uint4*>(p.in16 + qq * N + (e < N ? e : N - 8));
             }
         }
     } else {
@@ -110,29 +110,29 @@ __device__ __forceinline__ void stage_load(const GemvParams& p, int rb, Staged<N
         for (int k = 0; k < E / 2; ++k) S.gn[k] = gn32[k];
         if constexpr (PRO == PRO_EMBED) {
 #pragma unroll
-            for (int q = 0; q < MAXR; ++q) {
-                const int qq = q < rb ? q : rb - 1;
+            for (int qi = 0; qi < RQ; ++qi) {
+                const int q = q0 + qi, qq = q < rb ? q : rb - 1;
                 int tok = p.state->token[qq];  // the embedding prologue always runs with a step state
                 tok = (tok < 0 || tok >= VOCAB) ? 0 : tok;  // loop guards stop before this
                 const uint32_t* row = reinterpret_cast<const uint32_t*>(p.embed + size_t(tok) * HIDDEN + e0);
 #pragma unroll
-                for (int k = 0; k < E / 2; ++k) S.emb[q][k] = row[k];
+                for (int k = 0; k < E / 2; ++k) S.emb[qi][k] = row[k];
             }
         } else {
             const uint32_t* gp32 = reinterpret_cast<const uint32_t*>(p.g_post + e0);
 #pragma unroll
             for (int k = 0; k < E / 2; ++k) S.gp[k] = gp32[k];
 #pragma unroll
-            for (int q = 0; q < MAXR; ++q) {
-                const int qq = q < rb ? q : rb - 1;
+            for (int qi = 0; qi < RQ; ++qi) {
+                const int q = q0 + qi, qq = q < rb ? q : rb - 1;
 #pragma unroll
                 for (int k = 0; k < E / 2; ++k) {
                     if constexpr (PRO == PRO_RESID16) {
-                        S.a16[q][k] = *reinterpret_cast<const uint32_t*>(p.in16 + qq * HIDDEN + e0 + 2 * k);
-                        S.r16[q][k] = *reinterpret_cast<const uint32_t*>(p.resid16_in + qq * HIDDEN + e0 + 2 * k);
+                        S.a16[qi][k] = *reinterpret_cast<const uint32_t*>(p.in16 + qq * HIDDEN + e0 + 2 * k);
+                        S.r16[qi][k] = *reinterpret_cast<const uint32_t*>(p.resid16_in + qq * HIDDEN + e0 + 2 * k);
                     } else {
-                        S.a[q][k] = *reinterpret_cast<const float2*>(p.in + qq * HIDDEN + e0 + 2 * k);
-                        S.r[q][k] = *reinterpret_cast<const float2*>(p.resid_in + qq * HIDDEN + e0 + 2 * k);
+                        S.a[qi][k] = *reinterpret_cast<const float2*>(p.in + qq * HIDDEN + e0 + 2 * k);
+                        S.r[qi][k] = *reinterpret_cast<const float2*>(p.resid_in + qq * HIDDEN + e0 + 2 * k);
                     }
                 }
             }
@@ -140,43 +140,41 @@ __device__ __forceinline__ void stage_load(const GemvParams& p, int rb, Staged<N
     }
 }
 
-template <int N, int MAXR, int PRO>
-__device__ __forceinline__ void stage_finish(const GemvParams& p, int rows, const Staged<N, MAXR, PRO>& S,
-                                             xs_t<N, MAXR>* xs, float* red, bool active) {
-    // `active`: the first 256 threads; the others only pass the same barriers.
+// Every LDS row is written: rows past the step's hold re-read buffer rows or zeros, so the
+// main loop can run all MAXR rows without branches (their results are never stored).
+template <int N, int MAXR, int RQ, int PRO>
+__device__ __forceinline__ void stage_finish(const GemvParams& p, int rows, int q0, const Staged<N, RQ, PRO>& S,
+                                             xs_t<N, MAXR>* xs, float* red) {
     constexpr bool XF = xs_f32<N, MAXR>();
-    const int tid = threadIdx.x;
-    constexpr int V = Staged<N, MAXR, PRO>::V, E = Staged<N, MAXR, PRO>::E;
-    // Every LDS row is written: rows past the step's hold re-read buffer rows or zeros, so the
-    // main loop can run all MAXR rows without branches (their results are never stored).
+    const int tid = threadIdx.x & 255;
+    constexpr int V = Staged<N, RQ, PRO>::V, V16 = Staged<N, RQ, PRO>::V16, E = Staged<N, RQ, PRO>::E;
     if constexpr (PRO == PRO_PLAIN) {
-        if (!active) return;
 #pragma unroll
-        for (int q = 0; q < MAXR; ++q) {
+        for (int qi = 0; qi < RQ; ++qi) {
+            const int q = q0 + qi;
 #pragma unroll
             for (int k = 0; k < V; ++k) {
                 const int e = (tid + 256 * k) * 4;
                 if (e >= N) continue;
                 if constexpr (XF) {
                     *reinterpret_cast<float4*>(&xs[q * N + xpos(e)]) = make_float4(
-                        roundbf(S.v[q][k].x), roundbf(S.v[q][k].y), roundbf(S.v[q][k].z), roundbf(S.v[q][k].w));
+                        roundbf(S.v[qi][k].x), roundbf(S.v[qi][k].y), roundbf(S.v[qi][k].z), roundbf(S.v[qi][k].w));
                 } else {
-                    const uint32_t lo2 = (bits(S.v[q][k].x) & 0xffffu) | (bits(S.v[q][k].y) << 16);
-                    const uint32_t hi2 = (bits(S.v[q][k].z) & 0xffffu) | (bits(S.v[q][k].w) << 16);
+                    const uint32_t lo2 = (bits(S.v[qi][k].x) & 0xffffu) | (bits(S.v[qi][k].y) << 16);
+                    const uint32_t hi2 = (bits(S.v[qi][k].z) & 0xffffu) | (bits(S.v[qi][k].w) << 16);
                     *reinterpret_cast<uint2*>(&xs[q * N + e]) = make_uint2(lo2, hi2);
                 }
             }
         }
     } else if constexpr (PRO == PRO_PLAIN16) {
-        if (!active) return;
-        constexpr int V16 = Staged<N, MAXR, PRO>::V16;
 #pragma unroll
-        for (int q = 0; q < MAXR; ++q) {
+        for (int qi = 0; qi < RQ; ++qi) {
+            const int q = q0 + qi;
 #pragma unroll
             for (int k = 0; k < V16; ++k) {
                 const int e = (tid + 256 * k) * 8;
                 if (e >= N) continue;
-                const uint4 h = S.h[q][k];
+                const uint4 h = S.h[qi][k];
                 if constexpr (XF) {
                     float* d = reinterpret_cast<float*>(xs) + q * N + xpos(e);
                     *reinterpret_cast<float4*>(d) = make_float4(lo(h.x), hi(h.x), lo(h.y), hi(h.y));
@@ -187,112 +185,107 @@ __device__ __forceinline__ void stage_finish(const GemvParams& p, int rows, cons
             }
         }
     } else {
-        float xv[MAXR][E];
-        float ss[MAXR];
+        const int wq = tid >> 6;  // this thread's wave within its group of four
+        float xv[RQ][E];
+        float ss[RQ];
         if constexpr (PRO == PRO_EMBED) {
-            if (active)
 #pragma unroll
-            for (int q = 0; q < MAXR; ++q)
+            for (int qi = 0; qi < RQ; ++qi)
 #pragma unroll
                 for (int k = 0; k < E / 2; ++k) {
-                    xv[q][2 * k] = (q < rows) ? lo(S.emb[q][k]) : 0.f;
-                    xv[q][2 * k + 1] = (q < rows) ? hi(S.emb[q][k]) : 0.f;
+                    xv[qi][2 * k] = (q0 + qi < rows) ? lo(S.emb[qi][k]) : 0.f;
+                    xv[qi][2 * k + 1] = (q0 + qi < rows) ? hi(S.emb[qi][k]) : 0.f;
                 }
         } else {
             // z = roundbf(roundbf(p*r) * roundbf(bf(w)+offset)); x = roundbf(x + z)
             // (Kernels.metal:59-72, full == 1)
-            float pv[MAXR][E], rv[MAXR][E], gp[E];
-            if (active) {
+            float pv[RQ][E], rv[RQ][E], gp[E];
 #pragma unroll
             for (int k = 0; k < E / 2; ++k) {
                 gp[2 * k] = lo(S.gp[k]);
                 gp[2 * k + 1] = hi(S.gp[k]);
             }
 #pragma unroll
-            for (int q = 0; q < MAXR; ++q)
+            for (int qi = 0; qi < RQ; ++qi)
 #pragma unroll
                 for (int k = 0; k < E / 2; ++k) {
                     if constexpr (PRO == PRO_RESID16) {
-                        pv[q][2 * k] = lo(S.a16[q][k]);
-                        pv[q][2 * k + 1] = hi(S.a16[q][k]);
-                        rv[q][2 * k] = lo(S.r16[q][k]);
-                        rv[q][2 * k + 1] = hi(S.r16[q][k]);
+                        pv[qi][2 * k] = lo(S.a16[qi][k]);
+                        pv[qi][2 * k + 1] = hi(S.a16[qi][k]);
+                        rv[qi][2 * k] = lo(S.r16[qi][k]);
+                        rv[qi][2 * k + 1] = hi(S.r16[qi][k]);
                     } else {
-                        pv[q][2 * k] = S.a[q][k].x;
-                        pv[q][2 * k + 1] = S.a[q][k].y;
-                        rv[q][2 * k] = S.r[q][k].x;
-                        rv[q][2 * k + 1] = S.r[q][k].y;
+                        pv[qi][2 * k] = S.a[qi][k].x;
+                        pv[qi][2 * k + 1] = S.a[qi][k].y;
+                        rv[qi][2 * k] = S.r[qi][k].x;
+                        rv[qi][2 * k + 1] = S.r[qi][k].y;
                     }
                 }
 #pragma unroll
-            for (int q = 0; q < MAXR; ++q) {
-                ss[q] = 0.f;
+            for (int qi = 0; qi < RQ; ++qi) {
+                ss[qi] = 0.f;
 #pragma unroll
-                for (int k = 0; k < E; ++k) ss[q] += pv[q][k] * pv[q][k];
+                for (int k = 0; k < E; ++k) ss[qi] += pv[qi][k] * pv[qi][k];
             }
 #pragma unroll
-            for (int q = 0; q < MAXR; ++q) {
-                ss[q] = wave_sum(ss[q]);
-                if ((tid & 63) == 0) red[q * 4 + (tid >> 6)] = ss[q];
-            }
+            for (int qi = 0; qi < RQ; ++qi) {
+                ss[qi] = wave_sum(ss[qi]);
+                if ((tid & 63) == 0) red[(q0 + qi) * 4 + wq] = ss[qi];
             }
             __syncthreads();
-            if (active) {
             // BF16 roundings two at a time (packed RNE conversion, identical to `roundbf`)
             float g[E];
 #pragma unroll
             for (int k = 0; k < E; k += 2) round_bf16x2(gp[k] + p.post_offset, gp[k + 1] + p.post_offset, g[k], g[k + 1]);
 #pragma unroll
-            for (int q = 0; q < MAXR; ++q) {
+            for (int qi = 0; qi < RQ; ++qi) {
+                const int q = q0 + qi;
                 const float total = (red[q * 4] + red[q * 4 + 1]) + (red[q * 4 + 2] + red[q * 4 + 3]);
                 const float r = 1.0f / sqrtf(total / float(HIDDEN) + 1e-6f);
 #pragma unroll
                 for (int k = 0; k < E; k += 2) {
                     float t0, t1, z0, z1, x0, x1;
-                    round_bf16x2(pv[q][k] * r, pv[q][k + 1] * r, t0, t1);
+                    round_bf16x2(pv[qi][k] * r, pv[qi][k + 1] * r, t0, t1);
                     round_bf16x2(t0 * g[k], t1 * g[k + 1], z0, z1);
-                    round_bf16x2(rv[q][k] + z0, rv[q][k + 1] + z1, x0, x1);
-                    xv[q][k] = (q < rows) ? x0 : 0.f;
-                    xv[q][k + 1] = (q < rows) ? x1 : 0.f;
+                    round_bf16x2(rv[qi][k] + z0, rv[qi][k + 1] + z1, x0, x1);
+                    xv[qi][k] = (q < rows) ? x0 : 0.f;
+                    xv[qi][k + 1] = (q < rows) ? x1 : 0.f;
                 }
-            }
             }
             __syncthreads();
         }
         // next norm with +1 offset (Kernels.metal:76-89)
         float gn[E];
-        if (active) {
 #pragma unroll
         for (int k = 0; k < E / 2; ++k) round_bf16x2(lo(S.gn[k]) + 1.0f, hi(S.gn[k]) + 1.0f, gn[2 * k], gn[2 * k + 1]);
 #pragma unroll
-        for (int q = 0; q < MAXR; ++q) {
-            ss[q] = 0.f;
+        for (int qi = 0; qi < RQ; ++qi) {
+            ss[qi] = 0.f;
 #pragma unroll
-            for (int k = 0; k < E; ++k) ss[q] += xv[q][k] * xv[q][k];
-            ss[q] = wave_sum(ss[q]);
-            if ((tid & 63) == 0) red[q * 4 + (tid >> 6)] = ss[q];
-        }
+            for (int k = 0; k < E; ++k) ss[qi] += xv[qi][k] * xv[qi][k];
+            ss[qi] = wave_sum(ss[qi]);
+            if ((tid & 63) == 0) red[(q0 + qi) * 4 + wq] = ss[qi];
         }
         __syncthreads();
-        if (!active) return;
 #pragma unroll
-        for (int q = 0; q < MAXR; ++q) {
+        for (int qi = 0; qi < RQ; ++qi) {
+            const int q = q0 + qi;
             const float total = (red[q * 4] + red[q * 4 + 1]) + (red[q * 4 + 2] + red[q * 4 + 3]);
             const float r = 1.0f / sqrtf(total / float(HIDDEN) + 1e-6f);
 #pragma unroll
             for (int k = 0; k < E; k += 2) {
                 const int i = tid * E + k;
                 float t0, t1;
-                round_bf16x2(xv[q][k] * r, xv[q][k + 1] * r, t0, t1);
+                round_bf16x2(xv[qi][k] * r, xv[qi][k + 1] * r, t0, t1);
                 const uint32_t xn2 = pack_bf16(t0 * gn[k], t1 * gn[k + 1]);  // the two BF16 results
                 if constexpr (XF) *reinterpret_cast<float2*>(&xs[q * HIDDEN + xpos(i)]) = make_float2(lo(xn2), hi(xn2));
                 else *reinterpret_cast<uint32_t*>(&xs[q * HIDDEN + i]) = xn2;
                 if (blockIdx.x == 0 && q < rows) {
                     if constexpr (PRO == PRO_RESID) {
-                        p.resid_out[q * HIDDEN + i] = xv[q][k];
-                        p.resid_out[q * HIDDEN + i + 1] = xv[q][k + 1];
+                        p.resid_out[q * HIDDEN + i] = xv[qi][k];
+                        p.resid_out[q * HIDDEN + i + 1] = xv[qi][k + 1];
                     } else {  // BF16-exact residual: the BF16 pair is lossless
-                        *reinterpret_cast<uint32_t*>(&p.resid16_out[q * HIDDEN + i]) = pack_bf16(xv[q][k], xv[q][k + 1]);
+                        *reinterpret_cast<uint32_t*>(&p.resid16_out[q * HIDDEN + i]) = pack_bf16(xv[qi][k], xv[qi][k + 1]);
                     }
                     if (p.hidden) {
                         const size_t hrow = p.state ? size_t(p.state->lane[q]) : size_t(q);
@@ -434,7 +427,10 @@ __global__ __launch_bounds__(64 * gemv_waves(N, MAXR, EPI)) void gemv_kernel(con
     const StepState* st = p.state;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const bool stager = wave < 4;  // the prologue runs on the first 256 threads
+    // prologue groups of 256 threads: with eight waves, each half stages half of the rows
+    constexpr int NH = NWV / 4, RQ = MAXR / NH > 0 ? MAXR / NH : 1;
+    static_assert(MAXR % NH == 0 || MAXR == 1, "rows split evenly over the prologue groups");
+    const int q0 = (wave >> 2) * RQ;
     const int groups = p.m / U;
     // Request order = consumption order: step state, prologue inputs, first weights.  The
     // state is read through a lane-dependent address (lane_mask is 0, so every lane reads
@@ -447,8 +443,8 @@ __global__ __launch_bounds__(64 * gemv_waves(N, MAXR, EPI)) void gemv_kernel(con
         stopped = sv->stopped;
         srows = sv->rows;
     }
-    Staged<N, MAXR, PRO> S;
-    if (stager) stage_load<N, MAXR, PRO>(p, p.rows < MAXR ? p.rows : MAXR, S);
+    Staged<N, RQ, PRO> S;
+    stage_load<N, RQ, PRO>(p, p.rows < MAXR ? p.rows : MAXR, q0, S);
     float best_v[MAXR];
     uint32_t best_i[MAXR];
 #pragma unroll
@@ -491,7 +487,7 @@ __global__ __launch_bounds__(64 * gemv_waves(N, MAXR, EPI)) void gemv_kernel(con
     uint32_t orow_packed = 0;  // lanes are below 4: one byte each
 #pragma unroll
     for (int q = 0; q < MAXR; ++q) orow_packed |= (orow[q] & 0xffu) << (8 * q);
-    stage_finish<N, MAXR, PRO>(p, rows, S, xs, red, stager);
+    stage_finish<N, MAXR, RQ, PRO>(p, rows, q0, S, xs, red);
     __syncthreads();
     auto decode_all = [&](const WRaw<PACKED> (&cur)[U][IT], uint4 (&w)[U][IT]) {
 #pragma unroll
@@ -1308,7 +1304,6 @@ int gemv_blocks(int n, int maxr, Epilogue epi, int m) {
     // Multi-row kernels: at most two workgroups per CU, each wave walking several groups
     // (weights of the next in flight), so the activation prologue every workgroup
     // recomputes is paid twice per CU instead of four to six times.
-    if (maxr > 1 && n == HIDDEN && epi == EPI_ROUND) return (b + 1) / 2;  // QKV: two groups per wave
     return maxr > 1 ? std::min(b, 2048 / nw) : b;
 }
 
