@@ -35,12 +35,13 @@ constexpr int gemv_u() {
     else return MAXR == 1 ? 4 : 2;
 }
 
-// Waves per workgroup.  Four-row kernels whose prologue (the four-row norm, or staging four
-// 6144-wide rows) every workgroup repeats run eight waves, so one workgroup per CU does it
-// once for twice the waves; the prologue itself stays on the first four (same ownership of
-// elements, same sums).
+// Waves per workgroup.  Four-row kernels with a norm prologue or 6144-wide rows run eight
+// waves: each half of the workgroup stages two of the rows (every row with the same
+// ownership of elements by its 256 threads, so the same sums), and one workgroup per CU
+// does the prologue once for twice the waves.
 __host__ __device__ constexpr int gemv_waves(int n, int maxr, int epi) {
-    return maxr > 1 && (epi == EPI_SWIGLU || epi == EPI_LOGITS || n == INTER) ? 8 : 4;
+    (void)epi;
+    return maxr > 1 && (n == HIDDEN || n == INTER) ? 8 : 4;
 }
 
 // ---------------------------------------------------------------------------- prologues
