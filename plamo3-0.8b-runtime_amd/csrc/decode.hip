@@ -47,10 +47,10 @@ __host__ __device__ constexpr int gemv_waves(int n, int maxr, int epi) {
 // ---------------------------------------------------------------------------- prologues
 // Staged activation rows in LDS.  FP32 form: column c of a 512-column block sits at
 // (c & 4 ? 256 : 0) + 4 * ((c >> 3) & 63) + (c & 3), so the 8 columns a lane owns are two
-// float4 reads at 16-byte lane strides (no bank conflicts) and need no unpacking.  The
-// four-row 6144-wide rows stay BF16 (96 KB of FP32 would leave one workgroup per CU).
+// float4 reads at 16-byte lane strides (no bank conflicts) and need no unpacking.  (Four
+// 6144-wide rows take 96 KB: their eight-wave workgroups run one per CU anyway.)
 template <int N, int MAXR>
-constexpr bool xs_f32() { return !(N == INTER && MAXR > 1); }
+constexpr bool xs_f32() { return true; }
 template <int N, int MAXR>
 using xs_t = typename std::conditional<xs_f32<N, MAXR>(), float, uint16_t>::type;
 __device__ __forceinline__ int xpos(int c) { return (c & ~511) | ((c & 4) << 6) | (((c >> 3) & 63) << 2) | (c & 3); }
