@@ -461,14 +461,26 @@ __global__ __launch_bounds__(64 * gemv_waves(N, MAXR, EPI)) void gemv_kernel(con
     // Software pipelined over the wave's row groups: the next group's weights are in flight
     // while the current group is reduced and written.  The first group's weights do not
     // depend on the previous kernel, so they are requested before the activation prologue.
-    const int stride = gridDim.x * NWV;
-    int g = blockIdx.x * NWV + wave;
+    // Four-row kernels: each workgroup takes an equal run of consecutive row groups, its
+    // waves in turn (every CU does the same work when groups do not divide evenly over the
+    // waves).  One row: groups dealt over the whole grid.
+    int g, gend, stride;
+    if constexpr (MAXR > 1) {
+        const int per = (groups + int(gridDim.x) - 1) / int(gridDim.x);
+        gend = min(int(blockIdx.x) * per + per, groups);
+        stride = NWV;
+        g = int(blockIdx.x) * per + wave;
+    } else {
+        gend = groups;
+        stride = int(gridDim.x) * NWV;
+        g = int(blockIdx.x) * NWV + wave;
+    }
     WRaw<PACKED> wr[U][IT];
     {
         // unconditional (a wave without a group re-reads the last one) so the compiler
         // can count the requests in flight exactly
         int wrow[U];
-        rows_of(g < groups ? g : groups - 1, wrow);
+        rows_of(g < groups ? g : groups - 1, wrow);  // (past its run: any valid rows)
         request_w<N, PACKED, U, IT>(p, wrow, lane, wr);
     }
     // A stopped device loop runs the kernel with no rows (an early return here would let
@@ -587,18 +599,18 @@ __global__ __launch_bounds__(64 * gemv_waves(N, MAXR, EPI)) void gemv_kernel(con
         // plain weights: two request buffers in turn (the next group's requests land in the
         // other buffer, so no register copies between groups)
         WRaw<PACKED> wb[U][IT];
-        for (; g < groups; g += 2 * stride) {
+        for (; g < gend; g += 2 * stride) {
             const int g1 = g + stride, g2 = g1 + stride;
             int nrow[U];
-            if (g1 < groups) {
+            if (g1 < gend) {
                 rows_of(g1, nrow);
                 request_w<N, PACKED, U, IT>(p, nrow, lane, wb);
             }
             uint4 w[U][IT];
             decode_all(wr, w);
             group(g, w);
-            if (g1 >= groups) break;
-            if (g2 < groups) {
+            if (g1 >= gend) break;
+            if (g2 < gend) {
                 rows_of(g2, nrow);
                 request_w<N, PACKED, U, IT>(p, nrow, lane, wr);
             }
@@ -608,11 +620,11 @@ __global__ __launch_bounds__(64 * gemv_waves(N, MAXR, EPI)) void gemv_kernel(con
     } else {
         // .p12: decode, then request the next group into the same buffer (fewer registers
         // than two buffers of payload, table words and tags)
-        for (; g < groups; g += stride) {
+        for (; g < gend; g += stride) {
             uint4 w[U][IT];
             decode_all(wr, w);
             const int gn = g + stride;
-            if (gn < groups) {
+            if (gn < gend) {
                 int nrow[U];
                 rows_of(gn, nrow);
                 request_w<N, PACKED, U, IT>(p, nrow, lane, wr);
