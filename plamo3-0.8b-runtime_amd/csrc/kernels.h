@@ -107,9 +107,9 @@ struct AttnParams {
 // decode.hip
 int gemv_group_rows(int n, int maxr, Epilogue epi);     // weight rows per wave group
 int gemv_blocks(int n, int maxr, Epilogue epi, int m);  // workgroups for one group per wave
-// LM-head workgroups (argmax partials, at most HEAD_BLOCKS): four waves each for one row,
-// eight for four rows.
-inline int head_blocks(int maxr) { return maxr == 1 ? HEAD_BLOCKS : HEAD_BLOCKS / 2; }
+// LM-head workgroups (argmax partials, at most HEAD_BLOCKS): four waves each for one row;
+// for four rows one eight-wave workgroup per CU.
+inline int head_blocks(int maxr) { return maxr == 1 ? HEAD_BLOCKS : HEAD_BLOCKS / 4; }
 void launch_gemv(int n, bool packed, int maxr, Prologue pro, Epilogue epi, const GemvParams& p, int blocks,
                  hipStream_t s);
 void launch_attention(bool full, const AttnParams& p, int rows, hipStream_t s);
