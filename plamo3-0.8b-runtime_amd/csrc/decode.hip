@@ -141,6 +141,25 @@ __device__ __forceinline__ void stage_load(const GemvParams& p, int rb, int q0, 
     }
 }
 
+// 1 / sqrt(mean square + eps) of rows q0 .. q0+RQ-1 from the four wave partials in red:
+// with several rows, lane i computes row q0 + i (one sequence for all rows) and the scales
+// are read back from those lanes.
+template <int RQ>
+__device__ __forceinline__ void row_scales(const float* red, int q0, float (&rs)[RQ]) {
+    const auto scale = [&](int q) {
+        const float total = (red[q * 4] + red[q * 4 + 1]) + (red[q * 4 + 2] + red[q * 4 + 3]);
+        return 1.0f / sqrtf(total / float(HIDDEN) + 1e-6f);
+    };
+    if constexpr (RQ == 1) {
+        rs[0] = scale(q0);
+    } else {
+        static_assert((RQ & (RQ - 1)) == 0, "rows per group: a power of two");
+        const float r = scale(q0 + int(threadIdx.x & (RQ - 1)));
+#pragma unroll
+        for (int qi = 0; qi < RQ; ++qi) rs[qi] = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(r), qi));
+    }
+}
+
 // Every LDS row is written: rows past the step's hold re-read buffer rows or zeros, so the
 // main loop can run all MAXR rows without branches (their results are never stored).
 template <int N, int MAXR, int RQ, int PRO>
@@ -238,11 +257,12 @@ __device__ __forceinline__ void stage_finish(const GemvParams& p, int rows, int 
             float g[E];
 #pragma unroll
             for (int k = 0; k < E; k += 2) round_bf16x2(gp[k] + p.post_offset, gp[k + 1] + p.post_offset, g[k], g[k + 1]);
+            float rs[RQ];
+            row_scales<RQ>(red, q0, rs);
 #pragma unroll
             for (int qi = 0; qi < RQ; ++qi) {
                 const int q = q0 + qi;
-                const float total = (red[q * 4] + red[q * 4 + 1]) + (red[q * 4 + 2] + red[q * 4 + 3]);
-                const float r = 1.0f / sqrtf(total / float(HIDDEN) + 1e-6f);
+                const float r = rs[qi];
 #pragma unroll
                 for (int k = 0; k < E; k += 2) {
                     float t0, t1, z0, z1, x0, x1;
@@ -268,11 +288,12 @@ __device__ __forceinline__ void stage_finish(const GemvParams& p, int rows, int 
             if ((tid & 63) == 0) red[(q0 + qi) * 4 + wq] = ss[qi];
         }
         __syncthreads();
+        float rs[RQ];
+        row_scales<RQ>(red, q0, rs);
 #pragma unroll
         for (int qi = 0; qi < RQ; ++qi) {
             const int q = q0 + qi;
-            const float total = (red[q * 4] + red[q * 4 + 1]) + (red[q * 4 + 2] + red[q * 4 + 3]);
-            const float r = 1.0f / sqrtf(total / float(HIDDEN) + 1e-6f);
+            const float r = rs[qi];
 #pragma unroll
             for (int k = 0; k < E; k += 2) {
                 const int i = tid * E + k;
