@@ -815,10 +815,12 @@ void launch_gemm_dma(GemmEpilogue epi, const GemmParams& p, hipStream_t s) {
     const int per = (cols * rows + 7) / 8;
     const dim3 grid(8 * per), block(NT);
 #define PLAMO_GEMM(EP) hipLaunchKernelGGL((gemm_dma_kernel<EP, BT, BW, WT, NT, KD, NS>), grid, block, 0, s, p, cols, rows)
+    constexpr int TW = BW / (NT / 64 / WT) / 32;  // 32-column blocks per wave
     if (epi == GEMM_F32) PLAMO_GEMM(GEMM_F32);
     else if (epi == GEMM_BF16) PLAMO_GEMM(GEMM_BF16);
     else if (epi == GEMM_RAW) PLAMO_GEMM(GEMM_RAW);
-    else PLAMO_GEMM(GEMM_SWIGLU);
+    else if constexpr (TW % 2 == 0) PLAMO_GEMM(GEMM_SWIGLU);  // gate and up blocks pair inside a wave
+    else throw Error(E_INVAL, "SwiGLU GEMM needs an even number of column blocks per wave");
 #undef PLAMO_GEMM
 }
 
@@ -847,7 +849,7 @@ void launch_gemm(bool packed, GemmEpilogue epi, const GemmParams& p, hipStream_t
         t_pad * uint64_t(p.m) * 4 >= (1ull << 31))
         throw Error(E_INVAL, "GEMM operands exceed 2 GiB");
     // Tile choice (measured on the prefill shapes, 2048 tokens): 256 x 128 tiles for the wide
-    // projections (gate_up, qkv), 128 x 128 for the 1536-row ones (o, down), where larger
+    // projections (gate_up, qkv), smaller ones for the 1536-row ones (o, down), where larger
     // tiles leave CUs idle; plain weights go straight to LDS, .p12 weights are expanded in
     // registers on the way.
     const bool wide = p.tokens > 128 && (epi == GEMM_SWIGLU || p.m > 2048);
@@ -856,7 +858,10 @@ void launch_gemm(bool packed, GemmEpilogue epi, const GemmParams& p, hipStream_t
         else launch_gemm_packed<128, 128, 2, 256>(epi, p, s);
     } else {
         // 32-deep stages: five (wide) or six stages, so four or five are in flight
+        // 1536-row projections (o, down): 128 x 96 tiles with four waves, 64-deep stages, so
+        // 2048 tokens make exactly 256 tiles (128 x 128 left a quarter of the CUs idle)
         if (wide) launch_gemm_dma<256, 128, 4, 512, 32, 5>(epi, p, s);
+        else if (epi != GEMM_SWIGLU && p.m % 96 == 0) launch_gemm_dma<128, 96, 4, 256, 64, 4>(epi, p, s);
         else launch_gemm_dma<128, 128, 4, 512, 32, 6>(epi, p, s);
     }
 }
