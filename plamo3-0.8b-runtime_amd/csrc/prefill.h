@@ -21,16 +21,17 @@ struct GemmParams {
 struct RowsNormParams {
     const int32_t* tokens_in;  // embedding mode when set
     const uint16_t* embed;
-    const float* in;           // residual mode: projection output [T][1536]
+    const uint16_t* in;        // residual mode: projection output [T][1536] BF16
     const uint16_t* g_post;
     float post_offset;
-    float* x;                  // residual stream [T][1536] (updated in place)
+    uint16_t* x;               // residual stream [T][1536] BF16 (updated in place; every value
+                               // is BF16-rounded, so the BF16 copy is lossless)
     const uint16_t* g_next;
     uint16_t* xn;              // next-norm output BF16 [T][1536] (optional)
 };
 
 struct QkPrepParams {
-    const float* qkv;          // [T][2304]
+    const uint16_t* qkv;       // [T][2304] BF16
     const uint16_t* q_norm;
     const uint16_t* k_norm;
     uint16_t* q16;             // out: [T][16][128] BF16, normalised and rotated queries

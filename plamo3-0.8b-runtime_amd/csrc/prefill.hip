@@ -403,7 +403,7 @@ __global__ __launch_bounds__(256) void rows_norm_kernel(const RowsNormParams p) 
         float pv[E], ss = 0.f;
 #pragma unroll
         for (int k = 0; k < E; ++k) {
-            pv[k] = p.in[size_t(t) * HIDDEN + tid + 256 * k];
+            pv[k] = bf(p.in[size_t(t) * HIDDEN + tid + 256 * k]);
             ss += pv[k] * pv[k];
         }
         const float r = 1.0f / sqrtf(block_sum256(ss, red) / float(HIDDEN) + 1e-6f);
@@ -411,7 +411,7 @@ __global__ __launch_bounds__(256) void rows_norm_kernel(const RowsNormParams p) 
         for (int k = 0; k < E; ++k) {
             const int i = tid + 256 * k;
             const float z = roundbf(roundbf(pv[k] * r) * roundbf(bf(p.g_post[i]) + p.post_offset));
-            xv[k] = roundbf(p.x[size_t(t) * HIDDEN + i] + z);
+            xv[k] = roundbf(bf(p.x[size_t(t) * HIDDEN + i]) + z);
         }
     }
     float ss = 0.f;
@@ -421,7 +421,7 @@ __global__ __launch_bounds__(256) void rows_norm_kernel(const RowsNormParams p) 
 #pragma unroll
     for (int k = 0; k < E; ++k) {
         const int i = tid + 256 * k;
-        p.x[size_t(t) * HIDDEN + i] = xv[k];
+        p.x[size_t(t) * HIDDEN + i] = uint16_t(bits(xv[k]));
         if (p.xn) p.xn[size_t(t) * HIDDEN + i] = uint16_t(bits(roundbf(roundbf(xv[k] * r) * roundbf(bf(p.g_next[i]) + 1.0f))));
     }
 }
@@ -441,10 +441,15 @@ __global__ __launch_bounds__(256) void qk_prep_kernel(const QkPrepParams p) {
     const uint32_t chunk = p.p0 + (uint32_t(t) / CHUNK) * CHUNK;
     const uint32_t base = chunk > uint32_t(WINDOW - 1) ? chunk - uint32_t(WINDOW - 1) : 0u;
     const uint32_t qcoord = p.full ? pos : pos - base;
-    const float* x = p.qkv + size_t(t) * QKV;
+    const uint16_t* x = p.qkv + size_t(t) * QKV;
+    // four BF16 values as FP32
+    auto load4 = [](const uint16_t* s) {
+        const uint2 w = *reinterpret_cast<const uint2*>(s);
+        return make_float4(lo(w.x), hi(w.x), lo(w.y), hi(w.y));
+    };
     {
-        const float4 qlo = *reinterpret_cast<const float4*>(x + hq * HEAD_DIM + sq * 4);
-        const float4 qhi = *reinterpret_cast<const float4*>(x + hq * HEAD_DIM + 64 + sq * 4);
+        const float4 qlo = load4(x + hq * HEAD_DIM + sq * 4);
+        const float4 qhi = load4(x + hq * HEAD_DIM + 64 + sq * 4);
         const uint2 glo = *reinterpret_cast<const uint2*>(p.q_norm + sq * 4);
         const uint2 ghi = *reinterpret_cast<const uint2*>(p.q_norm + 64 + sq * 4);
         const uint4 qr = *reinterpret_cast<const uint4*>((p.full ? p.global_rope : p.local_rope) + size_t(qcoord) * 64 + sq * 4);
@@ -465,8 +470,8 @@ __global__ __launch_bounds__(256) void qk_prep_kernel(const QkPrepParams p) {
     }
     const size_t slot = size_t(pos % p.capacity) * HEAD_DIM;
     if (tid < 16) {
-        const float4 klo = *reinterpret_cast<const float4*>(x + ATTN + tid * 4);
-        const float4 khi = *reinterpret_cast<const float4*>(x + ATTN + 64 + tid * 4);
+        const float4 klo = load4(x + ATTN + tid * 4);
+        const float4 khi = load4(x + ATTN + 64 + tid * 4);
         const uint2 gl = *reinterpret_cast<const uint2*>(p.k_norm + tid * 4);
         const uint2 gh = *reinterpret_cast<const uint2*>(p.k_norm + 64 + tid * 4);
         float z[8];
@@ -485,7 +490,7 @@ __global__ __launch_bounds__(256) void qk_prep_kernel(const QkPrepParams p) {
     }
     if (tid >= 64 && tid < 64 + HEAD_DIM) {
         const int d = tid - 64;
-        p.values[slot + d] = uint16_t(bits(x[ATTN + HEAD_DIM + d]));
+        p.values[slot + d] = x[ATTN + HEAD_DIM + d];
     }
 }
 
@@ -525,10 +530,13 @@ __device__ __forceinline__ void flash_load(const FlashParams& p, uint32_t k0, ui
     const uint4 z = make_uint4(0, 0, 0, 0);
     s.ka[0] = s.ka[1] = s.kb[0] = s.kb[1] = z;
     s.rr[0] = s.rr[1] = s.rr[2] = s.rr[3] = z;
-    // ring slots: one modulo per tile, then at most a wrap per key (tiles are 64 keys)
+    // ring slots: one modulo per tile, then at most one wrap per key when the ring holds a
+    // whole tile (offsets are below 64); smaller rings wrap by repeated subtraction
     const uint32_t slot0 = k0 % p.capacity;
+    const bool big_ring = p.capacity >= uint32_t(FK);
     auto ring = [&](uint32_t off) {
         uint32_t slot = slot0 + off;
+        if (big_ring) return slot >= p.capacity ? slot - p.capacity : slot;
         while (slot >= p.capacity) slot -= p.capacity;
         return slot;
     };
@@ -705,10 +713,14 @@ __global__ __launch_bounds__(256, 2) void flash_prefill_kernel(const FlashParams
                 ls += e;
             }
         m = mn;
+        // alpha is exactly 1 where the running maximum did not move: the wave skips the
+        // rescale when that holds in every lane (multiplying by 1 changes nothing)
+        if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
 #pragma unroll
-        for (int dt = 0; dt < 4; ++dt)
+            for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-            for (int i = 0; i < 16; ++i) oacc[dt][i] *= alpha;
+                for (int i = 0; i < 16; ++i) oacc[dt][i] *= alpha;
+        }
         // O^T += V^T P^T; k-step s takes keys 16s + 4*half + {0..3} and 16s + 8 + 4*half + {0..3}
 #pragma unroll
         for (int s = 0; s < 4; ++s) {

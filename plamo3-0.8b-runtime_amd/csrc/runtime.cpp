@@ -236,7 +236,7 @@ Engine::Engine(std::shared_ptr<Model> mdl, int ctx, int nl, hipStream_t s)
     x1 = arena.alloc_n<uint16_t>(ROWS * HIDDEN);
     act = arena.alloc_n<uint16_t>(ROWS * INTER);
     hidden = arena.alloc_n<float>(ROWS * HIDDEN);
-    resid_scratch = arena.alloc_n<float>(ROWS * HIDDEN);
+    resid_scratch = arena.alloc_n<uint16_t>(ROWS * HIDDEN);
     logits = arena.alloc_n<uint16_t>(size_t(ROWS) * VOCAB);
     state = arena.alloc_n<StepState>(1);
     PLAMO_HIP(hipHostMalloc(reinterpret_cast<void**>(&host_state), sizeof(StepState), hipHostMallocDefault));
@@ -264,9 +264,9 @@ Engine::Engine(std::shared_ptr<Model> mdl, int ctx, int nl, hipStream_t s)
     part_o = arena.alloc_n<float>(part_rows_cap * HEADS * HEAD_DIM);
     attn_tickets = arena.alloc_n<uint32_t>(size_t(ROWS) * HEADS);  // [row][head group]
     PLAMO_HIP(hipMemsetAsync(attn_tickets, 0, size_t(ROWS) * HEADS * 4, stream));
-    p_x = arena.alloc_n<float>(size_t(chunk) * HIDDEN);
-    p_qkv = arena.alloc_n<float>(size_t(chunk) * QKV);
-    p_proj = arena.alloc_n<float>(size_t(chunk) * HIDDEN);
+    p_x = arena.alloc_n<uint16_t>(size_t(chunk) * HIDDEN);
+    p_qkv = arena.alloc_n<uint16_t>(size_t(chunk) * QKV);
+    p_proj = arena.alloc_n<uint16_t>(size_t(chunk) * HIDDEN);
     p_xn = arena.alloc_n<uint16_t>(size_t(chunk) * HIDDEN);
     p_att = arena.alloc_n<uint16_t>(size_t(chunk) * ATTN);
     p_q16 = arena.alloc_n<uint16_t>(size_t(chunk) * ATTN);
@@ -294,7 +294,7 @@ void Engine::zero_sampler() {
     PLAMO_HIP(hipMemsetAsync(bufs.counts, 0, size_t(ROWS) * VOCAB * 4, stream));
 }
 
-void Engine::enqueue_head(const float* in, const float* resid_in, int in_rows) {
+void Engine::enqueue_head(const uint16_t* in, const uint16_t* resid_in, int in_rows) {
     const Model& m = *model;
     const int maxr = lanes == 1 ? 1 : ROWS;
     GemvParams g{};
@@ -303,16 +303,16 @@ void Engine::enqueue_head(const float* in, const float* resid_in, int in_rows) {
     g.m = VOCAB;
     g.w = m.head.w;
     g.table = m.head.table;
-    g.in = in;
-    g.resid_in = resid_in;
-    g.resid_out = resid_scratch;
+    g.in16 = in;
+    g.resid16_in = resid_in;
+    g.resid16_out = resid_scratch;
     g.g_post = m.layers[LAYERS - 1].post_mlp;
     g.post_offset = post_mlp_offset();
     g.g_next = m.final_norm;
     g.hidden = hidden;
     g.out16 = logits;
     g.bufs = bufs;
-    launch_gemv(HIDDEN, m.packed, maxr, PRO_RESID, EPI_LOGITS, g, head_blocks(maxr), stream);
+    launch_gemv(HIDDEN, m.packed, maxr, PRO_RESID16, EPI_LOGITS, g, head_blocks(maxr), stream);
     launch_head_merge(bufs, head_blocks(maxr), stream);
 }
 
@@ -483,8 +483,8 @@ void Engine::enqueue_prefill_chunk(int n, int p0, int lane, bool last_chunk, boo
         const LayerWeights& L = m.layers[l];
         const bool full = is_global_layer(l);
         GemmParams q{};
-        q.w = L.qkv.w; q.table = L.qkv.table; q.x = p_xn; q.y = p_qkv; q.m = QKV; q.k = HIDDEN; q.tokens = n;
-        launch_gemm(pk, GEMM_F32, q, stream);
+        q.w = L.qkv.w; q.table = L.qkv.table; q.x = p_xn; q.y16 = p_qkv; q.m = QKV; q.k = HIDDEN; q.tokens = n;
+        launch_gemm(pk, GEMM_BF16, q, stream);
         QkPrepParams qp{};
         qp.qkv = p_qkv;
         qp.q_norm = L.q_norm;
@@ -514,8 +514,8 @@ void Engine::enqueue_prefill_chunk(int n, int p0, int lane, bool last_chunk, boo
         fa.tickets = p_flash_tickets;
         launch_flash_prefill(fa, stream);
         GemmParams o{};
-        o.w = L.o.w; o.table = L.o.table; o.x = p_att; o.y = p_proj; o.m = HIDDEN; o.k = ATTN; o.tokens = n;
-        launch_gemm(pk, GEMM_F32, o, stream);
+        o.w = L.o.w; o.table = L.o.table; o.x = p_att; o.y16 = p_proj; o.m = HIDDEN; o.k = ATTN; o.tokens = n;
+        launch_gemm(pk, GEMM_BF16, o, stream);
         RowsNormParams r1{};
         r1.in = p_proj; r1.g_post = L.post; r1.post_offset = POST_MIXER_OFFSET; r1.x = p_x; r1.g_next = L.pre_mlp;
         r1.xn = p_xn;
@@ -524,8 +524,8 @@ void Engine::enqueue_prefill_chunk(int n, int p0, int lane, bool last_chunk, boo
         u.w = L.up.w; u.table = L.up.table; u.x = p_xn; u.y16 = p_act; u.m = 2 * INTER; u.k = HIDDEN; u.tokens = n;
         launch_gemm(pk, GEMM_SWIGLU, u, stream);
         GemmParams d{};
-        d.w = L.down.w; d.table = L.down.table; d.x = p_act; d.y = p_proj; d.m = HIDDEN; d.k = INTER; d.tokens = n;
-        launch_gemm(pk, GEMM_F32, d, stream);
+        d.w = L.down.w; d.table = L.down.table; d.x = p_act; d.y16 = p_proj; d.m = HIDDEN; d.k = INTER; d.tokens = n;
+        launch_gemm(pk, GEMM_BF16, d, stream);
         if (l + 1 < LAYERS) {
             RowsNormParams r2{};
             r2.in = p_proj; r2.g_post = L.post_mlp; r2.post_offset = post_mlp_offset(); r2.x = p_x;

@@ -66,7 +66,8 @@ class Engine {
     uint16_t *keys[LAYERS], *values[LAYERS];
     int capacity[LAYERS];
     // decode scratch (ROWS rows)
-    float *qkv, *hidden, *resid_scratch;
+    float *qkv, *hidden;
+    uint16_t* resid_scratch;
     uint16_t *proj, *x0, *x1;  // BF16 projection output and residual stream (BF16-exact values)
     uint16_t *att, *act;  // BF16 attention output and SwiGLU activations
     uint16_t* logits;
@@ -77,7 +78,7 @@ class Engine {
     uint32_t* attn_tickets;
     uint32_t decode_parts_local, decode_parts_global;
     // prefill scratch (chunk rows)
-    float *p_x, *p_qkv, *p_proj;
+    uint16_t *p_x, *p_qkv, *p_proj;  // BF16: every value is BF16-rounded
     uint16_t *p_xn, *p_att, *p_act, *p_q16;
     float *p_flash_o, *p_flash_ml;  // split flash prefill workspace
     uint32_t* p_flash_tickets;
@@ -103,7 +104,7 @@ class Engine {
 
   private:
     void enqueue_prefill_chunk(int n, int p0, int lane, bool last_chunk, bool output);
-    void enqueue_head(const float* in, const float* resid_in, int in_rows);  // prefill: FP32 rows
+    void enqueue_head(const uint16_t* in, const uint16_t* resid_in, int in_rows);  // prefill rows
     void enqueue_head16();                                                    // decode: BF16 stream
 };
 
