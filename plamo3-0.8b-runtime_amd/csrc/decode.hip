@@ -1027,6 +1027,21 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
         mm[i] = __uint_as_float(buffer_load4_sc1(mview, uint32_t((row0 + k) * HEADS + h) * 4u));
         wl[i] = __uint_as_float(buffer_load4_sc1(lview, uint32_t((row0 + k) * HEADS + h) * 4u));
     }
+    // thread -> dim d = tid & 127 of local heads (tid >> 7) and (tid >> 7) + 2.  Up to PRE
+    // partitions, the partition outputs are requested together with the statistics (one
+    // memory round trip instead of two).
+    const int d = tid & 127, hb = tid >> 7;
+    constexpr uint32_t PRE = 8;
+    float ovp[PRE][2];
+    if (nparts <= PRE) {
+#pragma unroll
+        for (uint32_t k = 0; k < PRE; ++k)
+            if (k < nparts)
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+                    ovp[k][i] = __uint_as_float(buffer_load4_sc1(
+                        oview, uint32_t(((row0 + k) * HEADS + hg * HG + hb + 2 * i) * HEAD_DIM + d) * 4u));
+    }
     __syncthreads();
     if (nparts == np) {
         // M per head; then every weight exp(m_p - M) in parallel (in place of m_p); then each
@@ -1039,21 +1054,32 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
         __syncthreads();
         for (uint32_t i = tid; i < np * HG; i += 256) mm[i] = exp_det(mm[i] - l_s[i % HG]);
         __syncthreads();
-        // thread -> dim d = tid & 127 of local heads (tid >> 7) and (tid >> 7) + 2
-        const int d = tid & 127, hb = tid >> 7;
         float num[2] = {0.f, 0.f}, den[2] = {0.f, 0.f};
+        if (nparts <= PRE) {
+#pragma unroll
+            for (uint32_t k = 0; k < PRE; ++k) {
+                if (k >= nparts) break;
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    const float w = mm[k * HG + hb + 2 * i];
+                    num[i] = num[i] + ovp[k][i] * w;
+                    den[i] = den[i] + wl[k * HG + hb + 2 * i] * w;
+                }
+            }
+        } else {
 #pragma unroll 8
-        for (uint32_t k = 0; k < nparts; ++k) {
-            float ov[2];
+            for (uint32_t k = 0; k < nparts; ++k) {
+                float ov[2];
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
-                ov[i] = __uint_as_float(
-                    buffer_load4_sc1(oview, uint32_t(((row0 + k) * HEADS + hg * HG + hb + 2 * i) * HEAD_DIM + d) * 4u));
+                for (int i = 0; i < 2; ++i)
+                    ov[i] = __uint_as_float(
+                        buffer_load4_sc1(oview, uint32_t(((row0 + k) * HEADS + hg * HG + hb + 2 * i) * HEAD_DIM + d) * 4u));
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const float w = mm[k * HG + hb + 2 * i];
-                num[i] = num[i] + ov[i] * w;
-                den[i] = den[i] + wl[k * HG + hb + 2 * i] * w;
+                for (int i = 0; i < 2; ++i) {
+                    const float w = mm[k * HG + hb + 2 * i];
+                    num[i] = num[i] + ov[i] * w;
+                    den[i] = den[i] + wl[k * HG + hb + 2 * i] * w;
+                }
             }
         }
 #pragma unroll
@@ -1071,7 +1097,6 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
             l_s[tid] = M;
         }
         __syncthreads();
-        const int d = tid & 127, hb = tid >> 7;
         float num[2] = {0.f, 0.f};
         for (uint32_t k = 0; k < nparts; ++k)
 #pragma unroll
