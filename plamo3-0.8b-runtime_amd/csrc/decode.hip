@@ -1027,21 +1027,24 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
         mm[i] = __uint_as_float(buffer_load4_sc1(mview, uint32_t((row0 + k) * HEADS + h) * 4u));
         wl[i] = __uint_as_float(buffer_load4_sc1(lview, uint32_t((row0 + k) * HEADS + h) * 4u));
     }
-    // thread -> dim d = tid & 127 of local heads (tid >> 7) and (tid >> 7) + 2.  Up to PRE
-    // partitions, the partition outputs are requested together with the statistics (one
-    // memory round trip instead of two).
+    // thread -> dim d = tid & 127 of local heads (tid >> 7) and (tid >> 7) + 2.  Partition
+    // outputs are read in chunks of PRE: the first chunk is requested together with the
+    // statistics, and chunk c + 1 while chunk c is summed.  Loads past the last partition
+    // re-read it, so every chunk issues the same number of requests.
     const int d = tid & 127, hb = tid >> 7;
     constexpr uint32_t PRE = 8;
     float ovp[PRE][2];
-    if (nparts <= PRE) {
+    auto load_chunk = [&](uint32_t c0, float (&dst)[PRE][2]) {
 #pragma unroll
-        for (uint32_t k = 0; k < PRE; ++k)
-            if (k < nparts)
+        for (uint32_t j = 0; j < PRE; ++j) {
+            const uint32_t k = c0 + j < nparts ? c0 + j : nparts - 1;
 #pragma unroll
-                for (int i = 0; i < 2; ++i)
-                    ovp[k][i] = __uint_as_float(buffer_load4_sc1(
-                        oview, uint32_t(((row0 + k) * HEADS + hg * HG + hb + 2 * i) * HEAD_DIM + d) * 4u));
-    }
+            for (int i = 0; i < 2; ++i)
+                dst[j][i] = __uint_as_float(
+                    buffer_load4_sc1(oview, uint32_t(((row0 + k) * HEADS + hg * HG + hb + 2 * i) * HEAD_DIM + d) * 4u));
+        }
+    };
+    if (nparts == np) load_chunk(0, ovp);
     __syncthreads();
     if (nparts == np) {
         // M per head; then every weight exp(m_p - M) in parallel (in place of m_p); then each
@@ -1055,30 +1058,26 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
         for (uint32_t i = tid; i < np * HG; i += 256) mm[i] = exp_det(mm[i] - l_s[i % HG]);
         __syncthreads();
         float num[2] = {0.f, 0.f}, den[2] = {0.f, 0.f};
-        if (nparts <= PRE) {
+        for (uint32_t c0 = 0; c0 < nparts; c0 += PRE) {
+            const bool more = c0 + PRE < nparts;
+            float nxt[PRE][2];
+            if (more) load_chunk(c0 + PRE, nxt);
 #pragma unroll
-            for (uint32_t k = 0; k < PRE; ++k) {
+            for (uint32_t j = 0; j < PRE; ++j) {
+                const uint32_t k = c0 + j;
                 if (k >= nparts) break;
 #pragma unroll
                 for (int i = 0; i < 2; ++i) {
                     const float w = mm[k * HG + hb + 2 * i];
-                    num[i] = num[i] + ovp[k][i] * w;
+                    num[i] = num[i] + ovp[j][i] * w;
                     den[i] = den[i] + wl[k * HG + hb + 2 * i] * w;
                 }
             }
-        } else {
-#pragma unroll 8
-            for (uint32_t k = 0; k < nparts; ++k) {
-                float ov[2];
+            if (more) {
 #pragma unroll
-                for (int i = 0; i < 2; ++i)
-                    ov[i] = __uint_as_float(
-                        buffer_load4_sc1(oview, uint32_t(((row0 + k) * HEADS + hg * HG + hb + 2 * i) * HEAD_DIM + d) * 4u));
-#pragma unroll
-                for (int i = 0; i < 2; ++i) {
-                    const float w = mm[k * HG + hb + 2 * i];
-                    num[i] = num[i] + ov[i] * w;
-                    den[i] = den[i] + wl[k * HG + hb + 2 * i] * w;
+                for (uint32_t j = 0; j < PRE; ++j) {
+                    ovp[j][0] = nxt[j][0];
+                    ovp[j][1] = nxt[j][1];
                 }
             }
         }
