@@ -1022,43 +1022,98 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
     float* mm = ks;                                    // [np][HG]
     float* wl = ks + (KP * KS) / 2;                    // [np][HG]: l, then the weights
     const uint32_t np = nparts <= uint32_t(KP * KS / 2 / HG) ? nparts : uint32_t(KP * KS / 2 / HG);
-    for (uint32_t i = tid; i < np * HG; i += 256) {
-        const uint32_t k = i / HG, h = hg * HG + i % HG;
-        mm[i] = __uint_as_float(buffer_load4_sc1(mview, uint32_t((row0 + k) * HEADS + h) * 4u));
-        wl[i] = __uint_as_float(buffer_load4_sc1(lview, uint32_t((row0 + k) * HEADS + h) * 4u));
+    // up to 64 partitions one entry per thread; more: eight entries per thread in flight
+    if (np * HG <= 256) {
+        if (uint32_t(tid) < np * HG) {
+            const uint32_t k = uint32_t(tid) / HG, h = hg * HG + uint32_t(tid) % HG;
+            mm[tid] = __uint_as_float(buffer_load4_sc1(mview, uint32_t((row0 + k) * HEADS + h) * 4u));
+            wl[tid] = __uint_as_float(buffer_load4_sc1(lview, uint32_t((row0 + k) * HEADS + h) * 4u));
+        }
+    } else
+    for (uint32_t i0 = tid; i0 < np * HG; i0 += 256 * 8) {
+        float mv[8], lv[8];
+#pragma unroll
+        for (uint32_t j = 0; j < 8; ++j) {
+            const uint32_t i = i0 + 256 * j;
+            if (i < np * HG) {
+                const uint32_t k = i / HG, h = hg * HG + i % HG;
+                mv[j] = __uint_as_float(buffer_load4_sc1(mview, uint32_t((row0 + k) * HEADS + h) * 4u));
+                lv[j] = __uint_as_float(buffer_load4_sc1(lview, uint32_t((row0 + k) * HEADS + h) * 4u));
+            }
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < 8; ++j) {
+            const uint32_t i = i0 + 256 * j;
+            if (i < np * HG) {
+                mm[i] = mv[j];
+                wl[i] = lv[j];
+            }
+        }
     }
-    // thread -> dim d = tid & 127 of local heads (tid >> 7) and (tid >> 7) + 2.  Partition
-    // outputs are read in chunks of PRE: the first chunk is requested together with the
-    // statistics, and chunk c + 1 while chunk c is summed.  Loads past the last partition
-    // re-read it, so every chunk issues the same number of requests.
+    // thread -> dim d = tid & 127 of local heads (tid >> 7) and (tid >> 7) + 2.  The outputs
+    // of the first F partitions are requested together with the statistics (only those that
+    // exist); the rest go in chunks of PRE, chunk c + 1 requested while chunk c is summed
+    // (loads past the last partition re-read it, so every chunk issues the same number of
+    // requests and the wait before the sums counts exactly).
     const int d = tid & 127, hb = tid >> 7;
-    constexpr uint32_t PRE = 8;
-    float ovp[PRE][2];
+    constexpr uint32_t F = 8, PRE = 32;
+    float ovf[F][2];
+    auto load_one = [&](uint32_t k, float (&dst)[2]) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            dst[i] = __uint_as_float(
+                buffer_load4_sc1(oview, uint32_t(((row0 + k) * HEADS + hg * HG + hb + 2 * i) * HEAD_DIM + d) * 4u));
+    };
     auto load_chunk = [&](uint32_t c0, float (&dst)[PRE][2]) {
 #pragma unroll
-        for (uint32_t j = 0; j < PRE; ++j) {
-            const uint32_t k = c0 + j < nparts ? c0 + j : nparts - 1;
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-                dst[j][i] = __uint_as_float(
-                    buffer_load4_sc1(oview, uint32_t(((row0 + k) * HEADS + hg * HG + hb + 2 * i) * HEAD_DIM + d) * 4u));
-        }
+        for (uint32_t j = 0; j < PRE; ++j) load_one(c0 + j < nparts ? c0 + j : nparts - 1, dst[j]);
     };
-    if (nparts == np) load_chunk(0, ovp);
+    if (nparts == np) {
+#pragma unroll
+        for (uint32_t j = 0; j < F; ++j)
+            if (j < nparts) load_one(j, ovf[j]);
+    }
     __syncthreads();
     if (nparts == np) {
         // M per head; then every weight exp(m_p - M) in parallel (in place of m_p); then each
         // thread forms den for its own two heads (partition order) while summing o_p w_p
-        if (tid < HG) {
+        // M per head: up to 16 partitions one thread per head; more: wave w takes local head w
+        // (a maximum has no rounding, so any order gives the same M)
+        static_assert(HG == 4, "one wave per local head");
+        if (nparts <= 16) {
+            if (tid < HG) {
+                float M = NEG_INF;
+                for (uint32_t k = 0; k < nparts; ++k) M = fmaxf(M, mm[k * HG + tid]);
+                l_s[tid] = M;
+            }
+        } else {
             float M = NEG_INF;
-            for (uint32_t k = 0; k < nparts; ++k) M = fmaxf(M, mm[k * HG + tid]);
-            l_s[tid] = M;
+            for (uint32_t k = uint32_t(lane); k < nparts; k += 64) M = fmaxf(M, mm[k * HG + wave]);
+            M = fmaxf(M, xor_lane<32>(M));
+            M = fmaxf(M, xor_lane<16>(M));
+            M = fmaxf(M, xor_lane<8>(M));
+            M = fmaxf(M, xor_lane<4>(M));
+            M = fmaxf(M, xor_lane<2>(M));
+            M = fmaxf(M, xor_lane<1>(M));
+            if (lane == 0) l_s[wave] = M;
         }
         __syncthreads();
         for (uint32_t i = tid; i < np * HG; i += 256) mm[i] = exp_det(mm[i] - l_s[i % HG]);
         __syncthreads();
         float num[2] = {0.f, 0.f}, den[2] = {0.f, 0.f};
-        for (uint32_t c0 = 0; c0 < nparts; c0 += PRE) {
+        float ovp[PRE][2];
+        if (F < nparts) load_chunk(F, ovp);
+#pragma unroll
+        for (uint32_t k = 0; k < F; ++k) {
+            if (k >= nparts) break;
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const float w = mm[k * HG + hb + 2 * i];
+                num[i] = num[i] + ovf[k][i] * w;
+                den[i] = den[i] + wl[k * HG + hb + 2 * i] * w;
+            }
+        }
+        for (uint32_t c0 = F; c0 < nparts; c0 += PRE) {
             const bool more = c0 + PRE < nparts;
             float nxt[PRE][2];
             if (more) load_chunk(c0 + PRE, nxt);
