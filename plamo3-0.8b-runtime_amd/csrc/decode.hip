@@ -1004,6 +1004,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
         }
     }
     if (nparts == 1) return;
+    if (p.defer != 0 && nparts > p.defer) return;  // attn_merge_kernel merges this row
     // ticket: the last workgroup of this (row, head group) merges the partitions; every
     // wave's partition stores have completed before the ticket is taken
     wait_stores();
@@ -1165,6 +1166,88 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
             p.out16[size_t(q) * ATTN + (hg * HG + hb + 2 * i) * HEAD_DIM + d] = uint16_t(bits(num[i] / den_s[hb + 2 * i]));
     }
     if (tid == 0) atomicExch(ticket, 0u);  // ready for the next launch
+}
+
+// Partition merge of global-layer rows with more than p.defer partitions (long contexts),
+// one workgroup per (32 dims of a head, head, row).  The workgroup's slice of every partition
+// output is staged in LDS with all of its loads in flight together (one workgroup keeping a
+// few partitions in flight would take tens of microseconds at 500 partitions), then 32
+// threads sum in partition order.  Same arithmetic in the same order as the attention
+// kernel's own merge: M = max_p m_p, w_p = exp(m_p - M), den = sum l_p w_p, num = sum o_p w_p.
+__global__ __launch_bounds__(256) void attn_merge_kernel(const AttnParams p) {
+#pragma clang fp contract(off)  // fixed rounding sequence, reproduced by the CPU oracle
+    constexpr uint32_t MAXP = uint32_t(MAX_CONTEXT / KP);
+    static_assert(MAXP <= 512, "two statistics per thread");
+    __shared__ __align__(16) float os[MAXP * 32];
+    __shared__ float ws[MAXP], lsh[MAXP];
+    __shared__ float red[4];
+    const StepState* st = p.state;
+    const int q = blockIdx.z, h = blockIdx.y, d0 = blockIdx.x * 32;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    if (st->stopped || q >= int(st->rows)) return;
+    const uint32_t count = st->pos[q] + 1;  // global layer: keys 0 .. pos
+    const uint32_t nparts = (count + KP - 1) / KP;
+    if (nparts <= p.defer || nparts > MAXP || nparts > p.parts) return;  // merged in the attention kernel
+    const size_t row0 = size_t(q) * p.parts;
+    const uint32_t pstats = uint32_t(ROWS) * p.parts * HEADS;
+    const __amdgpu_buffer_rsrc_t mview = buffer_view(p.part_m, pstats * 4u);
+    const __amdgpu_buffer_rsrc_t lview = buffer_view(p.part_l, pstats * 4u);
+    const __amdgpu_buffer_rsrc_t oview = buffer_view(p.part_o, pstats * HEAD_DIM * 4u);
+    // every load first: statistics of partitions tid and tid + 256, then the output slice
+    // (eight threads per partition, 16 bytes each)
+    float mv[2] = {NEG_INF, NEG_INF}, lv[2] = {0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const uint32_t k = uint32_t(tid + 256 * j);
+        if (k < nparts) {
+            mv[j] = __uint_as_float(buffer_load4_sc1(mview, uint32_t((row0 + k) * HEADS + h) * 4u));
+            lv[j] = __uint_as_float(buffer_load4_sc1(lview, uint32_t((row0 + k) * HEADS + h) * 4u));
+        }
+    }
+    constexpr int OPT = int(MAXP) / 32;  // output loads per thread
+    uint4 ov[OPT];
+    const int sub4 = (tid & 7) * 4;
+#pragma unroll
+    for (int j = 0; j < OPT; ++j) {
+        const uint32_t k = uint32_t((tid >> 3) + 32 * j);
+        if (k < nparts)
+            ov[j] = buffer_load16_sc1(oview, uint32_t(((row0 + k) * HEADS + h) * HEAD_DIM + d0 + sub4) * 4u);
+    }
+    // M: a maximum has no rounding, so any order gives the same value
+    float M = fmaxf(mv[0], mv[1]);
+    M = fmaxf(M, xor_lane<32>(M));
+    M = fmaxf(M, xor_lane<16>(M));
+    M = fmaxf(M, xor_lane<8>(M));
+    M = fmaxf(M, xor_lane<4>(M));
+    M = fmaxf(M, xor_lane<2>(M));
+    M = fmaxf(M, xor_lane<1>(M));
+    if (lane == 0) red[wave] = M;
+    __syncthreads();
+    M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const uint32_t k = uint32_t(tid + 256 * j);
+        if (k < nparts) {
+            ws[k] = exp_det(mv[j] - M);
+            lsh[k] = lv[j];
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < OPT; ++j) {
+        const uint32_t k = uint32_t((tid >> 3) + 32 * j);
+        if (k < nparts) *reinterpret_cast<uint4*>(&os[k * 32 + sub4]) = ov[j];
+    }
+    __syncthreads();
+    if (tid < 32) {
+        float num = 0.f, den = 0.f;
+        for (uint32_t k = 0; k < nparts; ++k) {
+            const float w = ws[k];
+            num = num + os[k * 32 + tid] * w;
+            den = den + lsh[k] * w;
+        }
+        p.out16[size_t(q) * ATTN + h * HEAD_DIM + d0 + tid] = uint16_t(bits(num / den));
+    }
 }
 
 // ------------------------------------------------------------------------- step begin
@@ -1432,6 +1515,11 @@ void launch_attention(bool full, const AttnParams& p, int rows, hipStream_t s) {
     const dim3 grid(p.parts, HEADS / HG, rows), block(256);
     if (full) hipLaunchKernelGGL(attn_decode_kernel<true>, grid, block, 0, s, p);
     else hipLaunchKernelGGL(attn_decode_kernel<false>, grid, block, 0, s, p);
+}
+
+void launch_attention_merge(const AttnParams& p, int rows, hipStream_t s) {
+    if (p.parts > uint32_t(MAX_CONTEXT / KEYS_PER_PART)) throw Error(E_INVAL, "attention merge: too many partitions");
+    hipLaunchKernelGGL(attn_merge_kernel, dim3(HEAD_DIM / 32, HEADS, rows), dim3(256), 0, s, p);
 }
 
 void launch_head_merge(const DecodeBuffers& b, int blocks, hipStream_t s) {

@@ -102,7 +102,11 @@ struct AttnParams {
     uint32_t parts;           // grid.x
     uint32_t* tickets;        // [rows][head groups], zero between launches
     uint16_t* out16;          // BF16 [rows][2048]
+    uint32_t defer;           // rows with more partitions than this (0: none) are merged by
+                              // attn_merge_kernel instead of the attention kernel's last workgroup
 };
+// Partitions a global-layer row may have before its merge moves to attn_merge_kernel.
+constexpr uint32_t ATTN_MERGE_INLINE = 64;
 
 // decode.hip
 int gemv_group_rows(int n, int maxr, Epilogue epi);     // weight rows per wave group
@@ -113,6 +117,7 @@ inline int head_blocks(int maxr) { return maxr == 1 ? HEAD_BLOCKS : HEAD_BLOCKS 
 void launch_gemv(int n, bool packed, int maxr, Prologue pro, Epilogue epi, const GemvParams& p, int blocks,
                  hipStream_t s);
 void launch_attention(bool full, const AttnParams& p, int rows, hipStream_t s);
+void launch_attention_merge(const AttnParams& p, int rows, hipStream_t s);  // global layers
 void launch_step_begin(const DecodeBuffers& b, hipStream_t s);
 void launch_head_merge(const DecodeBuffers& b, int blocks, hipStream_t s);
 void launch_argmax(const void* x, uint32_t* out, int n, int rows, bool bf16, hipStream_t s);

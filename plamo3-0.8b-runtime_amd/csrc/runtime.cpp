@@ -383,7 +383,10 @@ void Engine::enqueue_step(bool head) {
         a.parts = full ? decode_parts_global : decode_parts_local;
         a.tickets = attn_tickets;
         a.out16 = att;
+        // long global-layer rings: rows past ATTN_MERGE_INLINE partitions merge in their own kernel
+        a.defer = full && a.parts > ATTN_MERGE_INLINE ? ATTN_MERGE_INLINE : 0;
         launch_attention(full, a, ROWS, stream);
+        if (a.defer) launch_attention_merge(a, ROWS, stream);
         GemvParams o{};
         o.state = state;
         o.rows = ROWS;
