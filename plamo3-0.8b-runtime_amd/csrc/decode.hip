@@ -326,7 +326,7 @@ __device__ __forceinline__ void stage_finish(const GemvParams& p, int rows, int 
 // packed results are bit-identical to plain ones.
 // A lane's weight words as requested, decoded only when used (decoding at request time
 // would make the compiler wait for each load).  .p12: a 128-weight block is 256 raw bytes
-// (tag 0) or 128 sign/mantissa bytes + 64 exponent-nibble bytes; three branch-free loads
+// (tag 0) or 128 sign/mantissa bytes + 64 exponent-nibble bytes; two branch-free loads
 // cover both layouts and stay inside the block.
 template <bool PACKED>
 struct WRaw {
@@ -338,11 +338,6 @@ __device__ __forceinline__ uint4 stream_load16(const void* p) {
     typedef uint32_t v4 __attribute__((ext_vector_type(4)));
     const v4 v = __builtin_nontemporal_load(reinterpret_cast<const v4*>(p));
     return make_uint4(v[0], v[1], v[2], v[3]);
-}
-__device__ __forceinline__ uint2 stream_load8(const void* p) {
-    typedef uint32_t v2 __attribute__((ext_vector_type(2)));
-    const v2 v = __builtin_nontemporal_load(reinterpret_cast<const v2*>(p));
-    return make_uint2(v[0], v[1]);
 }
 __device__ __forceinline__ uint32_t stream_load4(const void* p) {
     return __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p));
@@ -376,9 +371,9 @@ __device__ __forceinline__ void request_w(const GemvParams& p, const int (&wrow)
             for (int it = 0; it < IT; ++it) {
                 const uint8_t* blk = reinterpret_cast<const uint8_t*>(p.w) + (e[u][it] & ~63u);
                 const uint32_t tag = e[u][it] & 63u;
-                const uint2 lo8 = stream_load8(blk + (tag ? sub * 8 : sub * 16));
-                const uint2 hi8 = stream_load8(blk + (tag ? 0 : sub * 16 + 8));
-                r[u][it].v = make_uint4(lo8.x, lo8.y, hi8.x, hi8.y);
+                // one 16-byte load: a raw block's 8 weights, or (packed) this lane's 8
+                // sign/mantissa bytes in .x/.y (the rest is the next lane's, unused)
+                r[u][it].v = stream_load16(blk + (tag ? sub * 8 : sub * 16));
                 r[u][it].nib = stream_load4(blk + 128 + sub * 4);
                 r[u][it].tag = tag;
             }
