@@ -963,7 +963,11 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
             }
         }
     }
-    __syncthreads();
+    // P.V reads only what its own wave wrote above (the probabilities and l of head w; the V
+    // rows were staged before the last barrier): a wave-level fence orders it
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     // ---- unnormalised P.V: thread -> dims 2e, 2e+1 (e = tid & 63) of local head tid >> 6;
     //      keys 0..31 and 32..63 as two ordered chains per dim, added at the end
     {
