@@ -896,7 +896,9 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
         if (hg == 0) V[size_t(pos % cap) * HEAD_DIM + d] = uint16_t(bv);
         vs[int(newest - k0) * HEAD_DIM + d] = uint16_t(bv);
     }
-    __syncthreads();
+    // the newest key and value rows are read by other threads below; the queries only after
+    // the next barrier (has_new is the same for the whole workgroup)
+    if (has_new) __syncthreads();
     // ---- keys: (newest from LDS) rotate with coordinate r, stage FP32 in LDS
     {
         float a[16], b[16];
