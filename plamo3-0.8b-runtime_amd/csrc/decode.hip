@@ -273,7 +273,7 @@ __device__ __forceinline__ void stage_finish(const GemvParams& p, int rows, int 
                     xv[qi][k + 1] = (q < rows) ? x1 : 0.f;
                 }
             }
-            __syncthreads();
+            red += MAXR * 4;  // the next norm's partials go to the second half (no barrier)
         }
         // next norm with +1 offset (Kernels.metal:76-89)
         float gn[E];
@@ -437,7 +437,7 @@ __global__ __launch_bounds__(64 * gemv_waves(N, MAXR, EPI)) void gemv_kernel(con
     constexpr int U = gemv_u<N, MAXR, EPI>();
     constexpr int H = U / 2;  // SwiGLU: gate rows (and up rows) per group
     __shared__ __align__(16) xs_t<N, MAXR> xs[MAXR * N];
-    __shared__ float red[MAXR * 4];
+    __shared__ float red[MAXR * 4 * 2];  // norm partials: post-norm half, next-norm half
     __shared__ float cand_v[MAXR * NWV];
     __shared__ uint32_t cand_i[MAXR * NWV];
 
