@@ -538,6 +538,8 @@ int plamo_kernel_gemm(uint64_t w, uint64_t table, uint64_t x, uint64_t y, int32_
     });
 }
 
+}  // extern "C" (the helper below is C++ only)
+
 namespace {
 // Workspace of the split flash prefill for the kernel-level entry, per device, grown on demand
 // (the runtime keeps its own).  Growing synchronises the device before freeing the old one.
@@ -572,6 +574,8 @@ FlashWorkspace flash_workspace(int tokens) {
     return w;
 }
 }  // namespace
+
+extern "C" {
 
 int plamo_kernel_attention_prefill(uint64_t q16, uint64_t keys, uint64_t values, int32_t capacity, int32_t p0,
                                    int32_t tokens, int32_t full, uint64_t local_rope, uint64_t out16,

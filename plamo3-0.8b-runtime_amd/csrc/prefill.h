@@ -28,6 +28,7 @@ struct RowsNormParams {
                                // is BF16-rounded, so the BF16 copy is lossless)
     const uint16_t* g_next;
     uint16_t* xn;              // next-norm output BF16 [T][1536] (optional)
+    int tokens;                // set by launch_rows_norm
 };
 
 struct QkPrepParams {

@@ -379,50 +379,71 @@ __global__ __launch_bounds__(NT) void gemm_dma_kernel(const GemmParams p, int co
 }
 
 // ------------------------------------------------------------------------------ norms
-// One workgroup per token, 6 elements per thread (Kernels.metal:46-90).
-__device__ __forceinline__ float block_sum256(float v, float* red) {
-    v = wave_sum(v);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-    __syncthreads();
-    const float r = (red[0] + red[1]) + (red[2] + red[3]);
-    __syncthreads();
-    return r;
-}
-
+// Post-norm + residual + next norm of prefill rows (Kernels.metal:46-90).  One wave per
+// token, four tokens per workgroup: lane l owns elements 512c + 8l .. +8 (c < 3), read and
+// written as 16-byte rows; both sums of squares are wave reductions.
 __global__ __launch_bounds__(256) void rows_norm_kernel(const RowsNormParams p) {
-    __shared__ float red[4];
-    constexpr int E = HIDDEN / 256;
-    const int t = blockIdx.x, tid = threadIdx.x;
-    float xv[E];
+    constexpr int C = HIDDEN / 512;
+    const int lane = threadIdx.x & 63;
+    const int t = int(blockIdx.x) * 4 + __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
+    if (t >= p.tokens) return;
+    auto unpack = [](const uint4 w, float (&f)[8]) {
+        const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) { f[2 * k] = lo(u[k]); f[2 * k + 1] = hi(u[k]); }
+    };
+    float xv[C][8];
+    const size_t row = size_t(t) * HIDDEN;
     if (p.tokens_in) {
         int tok = p.tokens_in[t];
         tok = (tok < 0 || tok >= VOCAB) ? 0 : tok;
 #pragma unroll
-        for (int k = 0; k < E; ++k) xv[k] = bf(p.embed[size_t(tok) * HIDDEN + tid + 256 * k]);
+        for (int c = 0; c < C; ++c)
+            unpack(*reinterpret_cast<const uint4*>(p.embed + size_t(tok) * HIDDEN + 512 * c + 8 * lane), xv[c]);
     } else {
-        float pv[E], ss = 0.f;
+        float pv[C][8], rv[C][8], gp[C][8];
+        float ss = 0.f;
 #pragma unroll
-        for (int k = 0; k < E; ++k) {
-            pv[k] = bf(p.in[size_t(t) * HIDDEN + tid + 256 * k]);
-            ss += pv[k] * pv[k];
+        for (int c = 0; c < C; ++c) {
+            const int i = 512 * c + 8 * lane;
+            unpack(*reinterpret_cast<const uint4*>(p.in + row + i), pv[c]);
+            unpack(*reinterpret_cast<const uint4*>(p.x + row + i), rv[c]);
+            unpack(*reinterpret_cast<const uint4*>(p.g_post + i), gp[c]);
         }
-        const float r = 1.0f / sqrtf(block_sum256(ss, red) / float(HIDDEN) + 1e-6f);
 #pragma unroll
-        for (int k = 0; k < E; ++k) {
-            const int i = tid + 256 * k;
-            const float z = roundbf(roundbf(pv[k] * r) * roundbf(bf(p.g_post[i]) + p.post_offset));
-            xv[k] = roundbf(bf(p.x[size_t(t) * HIDDEN + i]) + z);
-        }
+        for (int c = 0; c < C; ++c)
+#pragma unroll
+            for (int k = 0; k < 8; ++k) ss += pv[c][k] * pv[c][k];
+        const float r = 1.0f / sqrtf(wave_sum(ss) / float(HIDDEN) + 1e-6f);
+#pragma unroll
+        for (int c = 0; c < C; ++c)
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const float z = roundbf(roundbf(pv[c][k] * r) * roundbf(gp[c][k] + p.post_offset));
+                xv[c][k] = roundbf(rv[c][k] + z);
+            }
     }
     float ss = 0.f;
 #pragma unroll
-    for (int k = 0; k < E; ++k) ss += xv[k] * xv[k];
-    const float r = 1.0f / sqrtf(block_sum256(ss, red) / float(HIDDEN) + 1e-6f);
+    for (int c = 0; c < C; ++c)
 #pragma unroll
-    for (int k = 0; k < E; ++k) {
-        const int i = tid + 256 * k;
-        p.x[size_t(t) * HIDDEN + i] = uint16_t(bits(xv[k]));
-        if (p.xn) p.xn[size_t(t) * HIDDEN + i] = uint16_t(bits(roundbf(roundbf(xv[k] * r) * roundbf(bf(p.g_next[i]) + 1.0f))));
+        for (int k = 0; k < 8; ++k) ss += xv[c][k] * xv[c][k];
+    const float r = 1.0f / sqrtf(wave_sum(ss) / float(HIDDEN) + 1e-6f);
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+        const int i = 512 * c + 8 * lane;
+        uint32_t xw[4], nw[4];
+        float gn[8];
+        if (p.xn) unpack(*reinterpret_cast<const uint4*>(p.g_next + i), gn);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            xw[k] = bits(xv[c][2 * k]) | (bits(xv[c][2 * k + 1]) << 16);
+            if (p.xn)
+                nw[k] = bits(roundbf(roundbf(xv[c][2 * k] * r) * roundbf(gn[2 * k] + 1.0f))) |
+                        (bits(roundbf(roundbf(xv[c][2 * k + 1] * r) * roundbf(gn[2 * k + 1] + 1.0f))) << 16);
+        }
+        *reinterpret_cast<uint4*>(p.x + row + i) = make_uint4(xw[0], xw[1], xw[2], xw[3]);
+        if (p.xn) *reinterpret_cast<uint4*>(p.xn + row + i) = make_uint4(nw[0], nw[1], nw[2], nw[3]);
     }
 }
 
@@ -881,7 +902,9 @@ void launch_gemm(bool packed, GemmEpilogue epi, const GemmParams& p, hipStream_t
 }
 
 void launch_rows_norm(const RowsNormParams& p, int tokens, hipStream_t s) {
-    hipLaunchKernelGGL(rows_norm_kernel, dim3(tokens), dim3(256), 0, s, p);
+    RowsNormParams q = p;
+    q.tokens = tokens;
+    hipLaunchKernelGGL(rows_norm_kernel, dim3((tokens + 3) / 4), dim3(256), 0, s, q);
 }
 
 void launch_qk_prep(const QkPrepParams& p, hipStream_t s) {
