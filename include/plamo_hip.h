@@ -261,6 +261,43 @@ int plamo_kernel_attention_prefill(uint64_t q16, uint64_t keys, uint64_t values,
 /* Library build identification (gfx arch, HIP version). */
 const char* plamo_version(void);
 
+/* ---- Text side: the PLaMo tokenizer (Tokenizer.swift:11-282) -------------------- */
+/* Host-only (no GPU work).  Byte outputs are raw UTF-8: when `cap` is too small the call
+ * fails with PLAMO_EINVAL and `*n_out` holds the size needed. */
+typedef struct plamo_tokenizer plamo_tokenizer;
+typedef struct plamo_token_stream plamo_token_stream;
+
+/* Tokenizer.init(path:) reading tokenizer.jsonl (Tokenizer.swift:59-131): lines
+ * [piece, score, kind]; BYTE pieces "<0xNN>"; scores scaled by 1e4 and rounded half to
+ * even.  Errors "Invalid byte token", "Invalid tokenizer score", "Expected the PLaMo 3
+ * Translate 0.8B vocabulary" (Tokenizer.swift:90-118).  The reference's .trie cache
+ * (Tokenizer.swift:45-57) is pinned to the original vocabulary's SHA-256 and is not read. */
+int plamo_tokenizer_open(const char* path, plamo_tokenizer** out, char* err, size_t errlen);
+void plamo_tokenizer_close(plamo_tokenizer* t);
+
+/* Tokenizer.encode(_:bos:) (Tokenizer.swift:144-190): `text` is UTF-8 (invalid UTF-8 is
+ * PLAMO_EINVAL "Invalid UTF-8 text"). */
+int plamo_tokenizer_encode(const plamo_tokenizer* t, const char* text, size_t len, int32_t bos, int32_t* ids,
+                           size_t cap, size_t* n_out, char* err, size_t errlen);
+
+/* Tokenizer.decode(_:) as bytes (Tokenizer.swift:203-232); error "Token ID out of range". */
+int plamo_tokenizer_decode(const plamo_tokenizer* t, const int32_t* ids, size_t count, char* out, size_t cap,
+                           size_t* n_out, char* err, size_t errlen);
+
+/* Tokenizer.Stream (Tokenizer.swift:236-269): push returns the complete UTF-8 prefix of
+ * everything pushed so far, holding back an unfinished trailing sequence; finish returns
+ * the rest.  The stream keeps a pointer to its tokenizer, which must outlive it. */
+int plamo_token_stream_open(const plamo_tokenizer* t, plamo_token_stream** out, char* err, size_t errlen);
+int plamo_token_stream_push(plamo_token_stream* s, int32_t id, char* out, size_t cap, size_t* n_out, char* err,
+                            size_t errlen);
+int plamo_token_stream_finish(plamo_token_stream* s, char* out, size_t cap, size_t* n_out, char* err, size_t errlen);
+void plamo_token_stream_close(plamo_token_stream* s);
+
+/* Tokenizer.prompt(_:target:) (Tokenizer.swift:272-281): errors "Unsupported target
+ * language", "Source must be nonempty and contain no reserved PLaMo delimiters". */
+int plamo_translation_prompt(const char* text, size_t len, const char* target, char* out, size_t cap,
+                             size_t* n_out, char* err, size_t errlen);
+
 #ifdef __cplusplus
 }
 #endif

@@ -20,6 +20,8 @@ Modules (each function cites the reference file:line it restates):
 * ``sampler`` -- greedy argmax (``Kernels.metal:704-729``), ``Sampler.select`` /
                  ``forbidden`` (``Sampler.swift:9-70``) and ``decodeBatch``
                  (``BatchDecode.swift:8-37``).
+* ``tokenizer`` -- the unigram tokenizer (``Tokenizer.swift:59-269``): vocabulary rules,
+                 boundary segmentation, Viterbi with byte fallback, decode and stream.
 
 Pinning status of every function is listed in each module header.
 """

@@ -8,6 +8,7 @@
 #include "../../include/plamo_hip.h"
 #include "formats.h"
 #include "runtime.h"
+#include "tokenizer.h"
 
 struct plamo_runtime {
     plamo::RuntimeImpl impl;
@@ -603,6 +604,87 @@ int plamo_kernel_attention_prefill(uint64_t q16, uint64_t keys, uint64_t values,
         f.tickets = ws.tickets;
         plamo::launch_flash_prefill(f, reinterpret_cast<hipStream_t>(stream));
         PLAMO_HIP(hipGetLastError());
+    });
+}
+
+
+// ---- tokenizer (host only)
+struct plamo_tokenizer {
+    plamo::Tokenizer tok;
+    explicit plamo_tokenizer(const std::string& path) : tok(path) {}
+};
+struct plamo_token_stream {
+    plamo::TokenStream stream;
+    explicit plamo_token_stream(const plamo::Tokenizer& t) : stream(t) {}
+};
+
+static void put_bytes(const std::string& s, char* out, size_t cap, size_t* n_out) {
+    if (n_out) *n_out = s.size();
+    if (s.size() > cap || (!out && !s.empty())) throw plamo::Error(plamo::E_INVAL, "output buffer too small");
+    if (!s.empty()) std::memcpy(out, s.data(), s.size());
+}
+
+int plamo_tokenizer_open(const char* path, plamo_tokenizer** out, char* err, size_t errlen) {
+    return guard(err, errlen, [&] {
+        if (!path || !out) throw plamo::Error(plamo::E_INVAL, "bad tokenizer arguments");
+        *out = nullptr;
+        *out = new plamo_tokenizer(path);
+    });
+}
+
+void plamo_tokenizer_close(plamo_tokenizer* t) { delete t; }
+
+int plamo_tokenizer_encode(const plamo_tokenizer* t, const char* text, size_t len, int32_t bos, int32_t* ids,
+                           size_t cap, size_t* n_out, char* err, size_t errlen) {
+    return guard(err, errlen, [&] {
+        if (!t || (!text && len)) throw plamo::Error(plamo::E_INVAL, "bad tokenizer arguments");
+        const std::vector<int32_t> v = t->tok.encode(std::string(text ? text : "", len), bos != 0);
+        if (n_out) *n_out = v.size();
+        if (v.size() > cap || (!ids && !v.empty())) throw plamo::Error(plamo::E_INVAL, "output buffer too small");
+        if (!v.empty()) std::memcpy(ids, v.data(), v.size() * sizeof(int32_t));
+    });
+}
+
+int plamo_tokenizer_decode(const plamo_tokenizer* t, const int32_t* ids, size_t count, char* out, size_t cap,
+                           size_t* n_out, char* err, size_t errlen) {
+    return guard(err, errlen, [&] {
+        if (!t || (!ids && count)) throw plamo::Error(plamo::E_INVAL, "bad tokenizer arguments");
+        std::string s;
+        for (size_t i = 0; i < count; ++i) t->tok.append_bytes(ids[i], s);
+        put_bytes(s, out, cap, n_out);
+    });
+}
+
+int plamo_token_stream_open(const plamo_tokenizer* t, plamo_token_stream** out, char* err, size_t errlen) {
+    return guard(err, errlen, [&] {
+        if (!t || !out) throw plamo::Error(plamo::E_INVAL, "bad tokenizer arguments");
+        *out = nullptr;
+        *out = new plamo_token_stream(t->tok);
+    });
+}
+
+int plamo_token_stream_push(plamo_token_stream* s, int32_t id, char* out, size_t cap, size_t* n_out, char* err,
+                            size_t errlen) {
+    return guard(err, errlen, [&] {
+        if (!s) throw plamo::Error(plamo::E_INVAL, "bad tokenizer arguments");
+        put_bytes(s->stream.push(id), out, cap, n_out);
+    });
+}
+
+int plamo_token_stream_finish(plamo_token_stream* s, char* out, size_t cap, size_t* n_out, char* err, size_t errlen) {
+    return guard(err, errlen, [&] {
+        if (!s) throw plamo::Error(plamo::E_INVAL, "bad tokenizer arguments");
+        put_bytes(s->stream.finish(), out, cap, n_out);
+    });
+}
+
+void plamo_token_stream_close(plamo_token_stream* s) { delete s; }
+
+int plamo_translation_prompt(const char* text, size_t len, const char* target, char* out, size_t cap,
+                             size_t* n_out, char* err, size_t errlen) {
+    return guard(err, errlen, [&] {
+        if ((!text && len) || !target) throw plamo::Error(plamo::E_INVAL, "bad prompt arguments");
+        put_bytes(plamo::translation_prompt(std::string(text ? text : "", len), target), out, cap, n_out);
     });
 }
 

@@ -277,3 +277,92 @@ def decode_batch(initial, limits, step, emit=None, finish=None, stop_on_truncati
     if rc != 0:
         raise PlamoError(rc, err.value.decode())
     return [([ids[i * stride + k] for k in range(lengths[i])], REASONS[reasons[i]]) for i in range(lanes.value)]
+
+
+def _bytes_call(fn, *args):
+    """Calls a byte-returning entry point twice when the first buffer is too small."""
+    n = ctypes.c_size_t(0)
+    buf = ctypes.create_string_buffer(256)
+    err = ctypes.create_string_buffer(512)
+    rc = fn(*args, buf, 256, ctypes.byref(n), err, 512)
+    if rc != 0 and n.value > 256:
+        buf = ctypes.create_string_buffer(n.value)
+        rc = fn(*args, buf, n.value, ctypes.byref(n), err, 512)
+    if rc != 0:
+        raise PlamoError(rc, err.value.decode(errors="replace"))
+    return buf.raw[:n.value]
+
+
+class Tokenizer:
+    """Tokenizer (Tokenizer.swift:11-282) backed by the native library (host code only)."""
+
+    def __init__(self, path):
+        lib = native.load()
+        self._lib = lib
+        h = ctypes.c_void_p()
+        native.call(lib.plamo_tokenizer_open, path.encode(), ctypes.byref(h))
+        self._h = h
+
+    def close(self):
+        if self._h:
+            self._lib.plamo_tokenizer_close(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def encode(self, text, bos=False):
+        """Tokenizer.encode(_:bos:) (Tokenizer.swift:144-190)."""
+        data = text.encode("utf-8") if isinstance(text, str) else bytes(text)
+        n = ctypes.c_size_t(0)
+        cap = 2 * len(data) + 8  # at most four byte tokens per scalar, plus BOS
+        ids = (ctypes.c_int32 * cap)()
+        native.call(self._lib.plamo_tokenizer_encode, self._h, data, len(data), int(bool(bos)), ids, cap,
+                    ctypes.byref(n))
+        return list(ids[:n.value])
+
+    def decode_bytes(self, ids):
+        """Tokenizer.decode(_:) before the UTF-8 repair (Tokenizer.swift:203-232)."""
+        return _bytes_call(self._lib.plamo_tokenizer_decode, self._h, native.i32(ids), len(ids))
+
+    def decode(self, ids):
+        return self.decode_bytes(ids).decode("utf-8", errors="replace")
+
+    def stream(self):
+        return TokenStream(self)
+
+    @staticmethod
+    def prompt(text, target):
+        """Tokenizer.prompt(_:target:) (Tokenizer.swift:272-281)."""
+        data = text.encode("utf-8")
+        return _bytes_call(native.load().plamo_translation_prompt, data, len(data), target.encode()).decode("utf-8")
+
+
+class TokenStream:
+    """Tokenizer.Stream (Tokenizer.swift:236-269): bytes of complete UTF-8 sequences."""
+
+    def __init__(self, tokenizer):
+        self._t = tokenizer  # keeps the tokenizer alive
+        h = ctypes.c_void_p()
+        native.call(tokenizer._lib.plamo_token_stream_open, tokenizer._h, ctypes.byref(h))
+        self._h = h
+
+    def push(self, token_id):
+        return _bytes_call(self._t._lib.plamo_token_stream_push, self._h, int(token_id))
+
+    def finish(self):
+        return _bytes_call(self._t._lib.plamo_token_stream_finish, self._h)
+
+    def close(self):
+        if self._h:
+            self._t._lib.plamo_token_stream_close(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

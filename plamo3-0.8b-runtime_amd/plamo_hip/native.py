@@ -101,6 +101,25 @@ _SIGNATURES = {
     "plamo_kernel_attention_prefill": (ctypes.c_int, [ctypes.c_uint64] * 3 + [ctypes.c_int32] * 4 +
                                        [ctypes.c_uint64] * 3),
     "plamo_version": (ctypes.c_char_p, []),
+    "plamo_tokenizer_open": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_void_p), ctypes.c_char_p,
+                                            ctypes.c_size_t]),
+    "plamo_tokenizer_close": (None, [ctypes.c_void_p]),
+    "plamo_tokenizer_encode": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_char_p, ctypes.c_size_t, ctypes.c_int32,
+                                              c_i32p, ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t),
+                                              ctypes.c_char_p, ctypes.c_size_t]),
+    "plamo_tokenizer_decode": (ctypes.c_int, [ctypes.c_void_p, c_i32p, ctypes.c_size_t, ctypes.c_char_p,
+                                              ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t), ctypes.c_char_p,
+                                              ctypes.c_size_t]),
+    "plamo_token_stream_open": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p), ctypes.c_char_p,
+                                               ctypes.c_size_t]),
+    "plamo_token_stream_push": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, ctypes.c_char_p, ctypes.c_size_t,
+                                               ctypes.POINTER(ctypes.c_size_t), ctypes.c_char_p, ctypes.c_size_t]),
+    "plamo_token_stream_finish": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_char_p, ctypes.c_size_t,
+                                                 ctypes.POINTER(ctypes.c_size_t), ctypes.c_char_p, ctypes.c_size_t]),
+    "plamo_token_stream_close": (None, [ctypes.c_void_p]),
+    "plamo_translation_prompt": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_size_t, ctypes.c_char_p, ctypes.c_char_p,
+                                                ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t), ctypes.c_char_p,
+                                                ctypes.c_size_t]),
 }
 
 _lib = None

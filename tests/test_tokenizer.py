@@ -1,0 +1,200 @@
+"""Tokenizer (Tokenizer.swift:11-282): the native library against the CPU oracle.
+
+The original tokenizer.jsonl is not available offline, so the tests build a synthetic
+vocabulary with the original's shape (107,520 entries; controls with <|plamo:bos|> at 1 and
+<|plamo:tag|> at 16; BYTE tokens <0x80>..<0xFF> at 128-255 and <0x00>..<0x7F> at 384-511,
+where the reference's own decode tests find them, CacheTests.swift:98-101).  Encodings are
+pinned by brute force over every segmentation of short inputs, by hand-computed ties and
+boundary cases, and the native library must agree with the oracle token for token.
+"""
+import json
+import os
+import random
+import sys
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+sys.path[:0] = [ROOT, os.path.join(ROOT, "plamo3-0.8b-runtime_amd")]
+
+from oracle import tokenizer as T  # noqa: E402
+
+ALPHABET = "abc 日本語é"
+TIES = {"x": -1.0, "y": -1.0, "xy": -2.0, "yx": -2.0, "xyx": -3.0}
+
+
+def _records(seed=0):
+    rng = random.Random(seed)
+    recs = [None] * T.VOCAB_SIZE
+    controls = ["<unk>", "<|plamo:bos|>", "<|plamo:eos|>", "<|plamo:pad|>"] + \
+        [f"<|plamo:c{k}|>" for k in range(4, 16)] + ["<|plamo:tag|>", "<|plamo:msg|>", "<|plamo:key|>",
+                                                    "<|plamo:val|>"]
+    for i, p in enumerate(controls):
+        recs[i] = [p, 0.0, "CONTROL"]
+    for b in range(256):
+        recs[(128 + b - 128) if b >= 128 else 384 + b] = [f"<0x{b:02X}>", 0.0, "BYTE"]
+    normal = [c for c in ALPHABET]
+    normal += [a + b for a in ALPHABET for b in ALPHABET]
+    normal += [a + b + c for a in ALPHABET for b in ALPHABET for c in ALPHABET]
+    normal += ["<", "|", "pl", "amo", ":", ">", "\n", "\t", "  ", "語é", "日本語"]
+    scored = [[p, round(rng.uniform(-15, -1), 4), "NORMAL"] for p in normal]
+    scored += [[p, s, "NORMAL"] for p, s in TIES.items()]
+    scored.append(["ab", -0.5, "NORMAL"])  # a repeated piece: the later id wins
+    free = iter(i for i in range(T.VOCAB_SIZE) if recs[i] is None)
+    for r in scored:
+        recs[next(free)] = r
+    k = 0
+    for i in free:
+        recs[i] = [chr(0xF0000 + k), -30.0, "NORMAL"]
+        k += 1
+    return recs
+
+
+def _write(path, recs):
+    with open(path, "w", encoding="utf-8") as f:
+        for r in recs:
+            f.write(json.dumps(r, ensure_ascii=False) + "\n")
+
+
+@pytest.fixture(scope="module")
+def vocab_path(tmp_path_factory):
+    p = tmp_path_factory.mktemp("tok") / "tokenizer.jsonl"
+    _write(p, _records())
+    return str(p)
+
+
+@pytest.fixture(scope="module")
+def oracle_vocab(vocab_path):
+    return T.Vocab(vocab_path)
+
+
+@pytest.fixture(scope="module")
+def native(vocab_path):
+    import plamo_hip
+    return plamo_hip.Tokenizer(vocab_path)
+
+
+def _ids(v, *pieces):
+    return [v.lookup[p] for p in pieces]
+
+
+def test_boundary_segments_hand_cases():
+    # (<\|plamo:[^|\s\x1c-\x1f]{0,64}\|>)|(([^\n])\3{3,}| {2,}) wraps each match; U+EE00 splits
+    assert T.segments("ab  cd") == ["ab", "  ", "cd"]
+    assert T.segments("a   b") == ["a", "   ", "b"]
+    assert T.segments("a     b") == ["a", "     ", "b"]         # 4+ spaces: the repeat alternative
+    assert T.segments("aaab") == ["aaab"] and T.segments("aaaab") == ["aaaa", "b"]
+    assert T.segments("x\n\n\n\ny") == ["x\n\n\n\ny"]           # newline runs are not boundaries
+    assert T.segments("q<|plamo:tag|>r") == ["q", "<|plamo:tag|>", "r"]
+    assert T.segments("<|plamo:a b|>") == ["<|plamo:a b|>"]    # \s is outside the class
+    name64, name65 = "ab" * 32, "ab" * 32 + "c"                  # no runs of four
+    assert T.segments("<|plamo:" + name64 + "|>") == ["<|plamo:" + name64 + "|>"]
+    assert T.segments("<|plamo:" + name65 + "|>") == ["<|plamo:" + name65 + "|>"]  # no match
+    assert T.segments("<|plamo:" + "z" * 65 + "|>") == ["<|plamo:", "z" * 65, "|>"]  # a run
+    assert T.segments("ab") == ["ab"]
+    assert T.segments("a\uee00b") == ["a", "b"]                # a literal U+EE00 splits too
+    assert T.segments("\u3000\u3000a") == ["\u3000\u3000a"]    # only U+0020 runs of two or three
+    assert T.segments("日日日日本") == ["日日日日", "本"]
+
+
+def test_oracle_viterbi_is_minimum_cost(oracle_vocab):
+    rng = random.Random(1)
+    for _ in range(300):
+        s = "".join(rng.choice("abc日本語éxyz") for _ in range(rng.randint(1, 8)))
+        for seg in T.segments(s):
+            _, cost = T.viterbi(oracle_vocab, seg)
+            assert cost == T.brute_min_cost(oracle_vocab, seg), s
+
+
+def test_ties_prefer_the_longer_piece(oracle_vocab, native):
+    v = oracle_vocab
+    # x + y, xy, ... all cost the same: every position takes its longest piece
+    assert T.encode(v, "xy") == _ids(v, "xy")
+    assert T.encode(v, "xyx") == _ids(v, "xyx")
+    assert T.encode(v, "xyxy") == _ids(v, "xyx", "y")
+    assert T.encode(v, "yxy") == _ids(v, "yx", "y")
+    for s in ("xy", "xyx", "xyxy", "yxy", "yyxx"):
+        assert native.encode(s) == T.encode(v, s)
+    # the repeated piece "ab" maps to its last id
+    assert v.lookup["ab"] == max(i for i, p in enumerate(v.pieces) if p == "ab")
+
+
+def test_native_encode_matches_oracle(oracle_vocab, native):
+    rng = random.Random(2)
+    extras = ["<|plamo:tag|>", "<|plamo:zz|>", "\U0001F600", "\uee00", "aaaa", "    ", "  ", "\n", "\t", "\u3000",
+              "z", "<|plamo:" + "q" * 70 + "|>", "\x1c"]
+    for _ in range(400):
+        parts = []
+        for _ in range(rng.randint(1, 12)):
+            parts.append(rng.choice(extras) if rng.random() < 0.2 else
+                         "".join(rng.choice(ALPHABET + "xyz") for _ in range(rng.randint(1, 6))))
+        s = "".join(parts)
+        bos = rng.random() < 0.3
+        assert native.encode(s, bos=bos) == T.encode(oracle_vocab, s, bos=bos), repr(s)
+    assert native.encode("") == [] and native.encode("", bos=True) == [1]
+    # unknown scalars fall back to their UTF-8 bytes
+    assert native.encode("\U0001F600") == [oracle_vocab.bytes[b] for b in "\U0001F600".encode()]
+
+
+def test_decode_and_stream(oracle_vocab, native):
+    rng = random.Random(3)
+    for _ in range(200):
+        s = "".join(rng.choice(ALPHABET + "xyz\U0001F600\n") for _ in range(rng.randint(0, 20)))
+        ids = native.encode(s)
+        assert native.decode_bytes(ids) == s.encode() == T.decode_bytes(oracle_vocab, ids)
+    # the stream holds back unfinished UTF-8 and its pieces concatenate to the decode
+    for _ in range(200):
+        ids = [rng.choice([128 + rng.randrange(128), 384 + rng.randrange(128), rng.randrange(20, 2000)])
+               for _ in range(rng.randint(0, 12))]
+        st = native.stream()
+        out = b"".join(st.push(i) for i in ids) + st.finish()
+        assert out == native.decode_bytes(ids) == T.decode_bytes(oracle_vocab, ids)
+    st = native.stream()
+    e = "é".encode()
+    assert st.push(oracle_vocab.bytes[e[0]]) == b""
+    assert st.push(oracle_vocab.bytes[e[1]]) == e
+    assert native.decode_bytes([128]) == b"\x80" and native.decode_bytes([384]) == b"\x00"
+
+
+def test_errors(tmp_path, native):
+    import plamo_hip
+    from plamo_hip.native import PlamoError
+    recs = _records()
+    cases = [
+        (recs[:-1], "Expected the PLaMo 3 Translate 0.8B vocabulary"),
+        ([r if i != 130 else ["<0xZZ>", 0.0, "BYTE"] for i, r in enumerate(recs)], "Invalid byte token"),
+        ([r if i != 500 else ["pq", 1e300, "NORMAL"] for i, r in enumerate(recs)], "Invalid tokenizer score"),
+        ([r if i != 1 else ["<|plamo:bos2|>", 0.0, "CONTROL"] for i, r in enumerate(recs)],
+         "Expected the PLaMo 3 Translate 0.8B vocabulary"),
+    ]
+    for k, (rs, msg) in enumerate(cases):
+        p = tmp_path / f"v{k}.jsonl"
+        _write(p, rs)
+        with pytest.raises(PlamoError, match=msg):
+            plamo_hip.Tokenizer(str(p))
+        with pytest.raises(ValueError, match=msg):
+            T.Vocab(str(p))
+    # a signed byte spelling is read as Swift's Int(_:radix:) reads it
+    p = tmp_path / "signed.jsonl"
+    _write(p, [r if i != 384 + 0x0F else ["<0x+F>", 0.0, "BYTE"] for i, r in enumerate(recs)])
+    assert plamo_hip.Tokenizer(str(p)).encode("\x0f") == [384 + 0x0F]
+    with pytest.raises(PlamoError):
+        plamo_hip.Tokenizer(str(tmp_path / "missing.jsonl"))
+    with pytest.raises(PlamoError, match="Token ID out of range"):
+        native.decode_bytes([T.VOCAB_SIZE])
+    with pytest.raises(PlamoError, match="Invalid UTF-8"):
+        native.encode(b"a\xffb")
+
+
+def test_translation_prompt():
+    import plamo_hip
+    from plamo_hip.native import PlamoError
+    assert plamo_hip.Tokenizer.prompt("Hello", "ja") == (
+        "<|plamo:tag|>dataset<|plamo:msg|>translation<|plamo:tag|>input<|plamo:msg|>Hello"
+        "<|plamo:tag|>output<|plamo:key|>lang<|plamo:val|>ja<|plamo:msg|>")
+    for text, target, msg in [("Hello", "xx", "Unsupported target language"),
+                              ("", "en", "reserved PLaMo delimiters"),
+                              ("a<|plamo:tag|>", "en", "reserved PLaMo delimiters"),
+                              ("a", "en", "reserved PLaMo delimiters")]:
+        with pytest.raises(PlamoError, match=msg):
+            plamo_hip.Tokenizer.prompt(text, target)
