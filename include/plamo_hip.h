@@ -293,6 +293,20 @@ int plamo_token_stream_push(plamo_token_stream* s, int32_t id, char* out, size_t
 int plamo_token_stream_finish(plamo_token_stream* s, char* out, size_t cap, size_t* n_out, char* err, size_t errlen);
 void plamo_token_stream_close(plamo_token_stream* s);
 
+/* OrderedOutput (OrderedOutput.swift:24-67): up to four documents' tokens, emitted in
+ * document order through `emit` (repaired UTF-8 chunks; a nonzero return cancels: the
+ * calling append/finish fails with PLAMO_ESTATE "Cancelled").  The first prefix is emitted by
+ * open.  Errors "Expected one to four output prefixes", "Output after document finish",
+ * "Invalid document finish"; `reason` is "stop" or "length" (BatchDecode.swift:3-6). */
+typedef struct plamo_ordered plamo_ordered;
+typedef int (*plamo_text_fn)(void* user, const char* text, size_t len);
+int plamo_ordered_open(const plamo_tokenizer* t, const char* const* prefixes, const size_t* prefix_lens,
+                       int32_t count, const char* tail, size_t tail_len, plamo_text_fn emit, void* user,
+                       plamo_ordered** out, char* err, size_t errlen);
+int plamo_ordered_append(plamo_ordered* o, int32_t lane, int32_t id, char* err, size_t errlen);
+int plamo_ordered_finish(plamo_ordered* o, int32_t lane, const char* reason, char* err, size_t errlen);
+void plamo_ordered_close(plamo_ordered* o);
+
 /* Tokenizer.prompt(_:target:) (Tokenizer.swift:272-281): errors "Unsupported target
  * language", "Source must be nonempty and contain no reserved PLaMo delimiters". */
 int plamo_translation_prompt(const char* text, size_t len, const char* target, char* out, size_t cap,

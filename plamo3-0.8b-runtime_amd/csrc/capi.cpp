@@ -2,6 +2,7 @@
 #include <cstdio>
 #include <cstring>
 #include <map>
+#include <memory>
 #include <mutex>
 #include <functional>
 
@@ -679,6 +680,48 @@ int plamo_token_stream_finish(plamo_token_stream* s, char* out, size_t cap, size
 }
 
 void plamo_token_stream_close(plamo_token_stream* s) { delete s; }
+
+struct plamo_ordered {
+    std::unique_ptr<plamo::OrderedOutput> out;
+};
+
+static plamo::OrderedOutput::Emit text_emitter(plamo_text_fn emit, void* user) {
+    return [emit, user](const std::string& s) {
+        if (emit && emit(user, s.data(), s.size()) != 0) throw plamo::Error(plamo::E_STATE, "Cancelled");
+    };
+}
+
+int plamo_ordered_open(const plamo_tokenizer* t, const char* const* prefixes, const size_t* prefix_lens,
+                       int32_t count, const char* tail, size_t tail_len, plamo_text_fn emit, void* user,
+                       plamo_ordered** out, char* err, size_t errlen) {
+    return guard(err, errlen, [&] {
+        if (!t || !out || count < 0 || (count > 0 && (!prefixes || !prefix_lens)) || (!tail && tail_len))
+            throw plamo::Error(plamo::E_INVAL, "bad output arguments");
+        *out = nullptr;
+        std::vector<std::string> p;
+        for (int32_t i = 0; i < count; ++i) p.emplace_back(prefixes[i] ? prefixes[i] : "", prefixes[i] ? prefix_lens[i] : 0);
+        auto h = std::make_unique<plamo_ordered>();
+        h->out = std::make_unique<plamo::OrderedOutput>(t->tok, std::move(p), std::string(tail ? tail : "", tail_len),
+                                                         text_emitter(emit, user));
+        *out = h.release();
+    });
+}
+
+int plamo_ordered_append(plamo_ordered* o, int32_t lane, int32_t id, char* err, size_t errlen) {
+    return guard(err, errlen, [&] {
+        if (!o) throw plamo::Error(plamo::E_INVAL, "bad output arguments");
+        o->out->append(lane, id);
+    });
+}
+
+int plamo_ordered_finish(plamo_ordered* o, int32_t lane, const char* reason, char* err, size_t errlen) {
+    return guard(err, errlen, [&] {
+        if (!o || !reason) throw plamo::Error(plamo::E_INVAL, "bad output arguments");
+        o->out->finish(lane, reason);
+    });
+}
+
+void plamo_ordered_close(plamo_ordered* o) { delete o; }
 
 int plamo_translation_prompt(const char* text, size_t len, const char* target, char* out, size_t cap,
                              size_t* n_out, char* err, size_t errlen) {

@@ -283,6 +283,72 @@ std::string TokenStream::finish() {
     return out;
 }
 
+std::string utf8_repair(const std::string& b) {
+    std::string out;
+    out.reserve(b.size());
+    const size_t n = b.size();
+    for (size_t i = 0; i < n;) {
+        const unsigned char c = (unsigned char)b[i];
+        if (c < 0x80) { out += char(c); ++i; continue; }
+        size_t need = 0;
+        unsigned char lo = 0x80, hi = 0xBF;  // allowed range of the second byte
+        if (c >= 0xC2 && c <= 0xDF) need = 1;
+        else if (c >= 0xE0 && c <= 0xEF) { need = 2; if (c == 0xE0) lo = 0xA0; if (c == 0xED) hi = 0x9F; }
+        else if (c >= 0xF0 && c <= 0xF4) { need = 3; if (c == 0xF0) lo = 0x90; if (c == 0xF4) hi = 0x8F; }
+        size_t k = 1;
+        while (k <= need && i + k < n) {
+            const unsigned char d = (unsigned char)b[i + k];
+            if (k == 1 ? (d < lo || d > hi) : (d & 0xC0) != 0x80) break;
+            ++k;
+        }
+        if (need && k == need + 1) out.append(b, i, k);
+        else out += "\xEF\xBF\xBD";  // the maximal subpart (at least one byte) becomes U+FFFD
+        i += need && k == need + 1 ? k : (k > 1 ? k : 1);
+    }
+    return out;
+}
+
+OrderedOutput::OrderedOutput(const Tokenizer& t, std::vector<std::string> prefixes, std::string tail, Emit emit)
+    : prefixes_(std::move(prefixes)), tail_(std::move(tail)), emit_(std::move(emit)) {
+    if (prefixes_.empty() || prefixes_.size() > 4) throw Error(E_INVAL, "Expected one to four output prefixes");
+    buffers_.assign(prefixes_.size(), std::string());
+    reasons_.assign(prefixes_.size(), std::string());
+    for (size_t i = 0; i < prefixes_.size(); ++i) streams_.emplace_back(t);
+    if (!prefixes_[0].empty()) emit_(prefixes_[0]);
+}
+
+void OrderedOutput::push(int lane, const std::string& bytes) {
+    if (bytes.empty()) return;
+    const std::string text = utf8_repair(bytes);
+    if (size_t(lane) == first_) emit_(text);
+    else buffers_[size_t(lane)] += text;
+}
+
+void OrderedOutput::append(int lane, int32_t id) {
+    if (lane < 0 || size_t(lane) >= reasons_.size() || !reasons_[size_t(lane)].empty() || closed_)
+        throw Error(E_STATE, "Output after document finish");
+    push(lane, streams_[size_t(lane)].push(id));
+}
+
+void OrderedOutput::finish(int lane, const std::string& reason) {
+    if (lane < 0 || size_t(lane) >= reasons_.size() || !reasons_[size_t(lane)].empty() || closed_ ||
+        (reason != "stop" && reason != "length"))
+        throw Error(E_STATE, "Invalid document finish");
+    push(lane, streams_[size_t(lane)].finish());
+    reasons_[size_t(lane)] = reason;
+    while (first_ < reasons_.size() && !reasons_[first_].empty()) {
+        if (reasons_[first_] != "stop") { closed_ = true; return; }
+        ++first_;
+        if (first_ == reasons_.size()) {
+            closed_ = true;
+            if (!tail_.empty()) emit_(tail_);
+            return;
+        }
+        if (!prefixes_[first_].empty()) emit_(prefixes_[first_]);
+        if (!buffers_[first_].empty()) { emit_(buffers_[first_]); buffers_[first_].clear(); }
+    }
+}
+
 std::string translation_prompt(const std::string& text, const std::string& target) {
     static const std::set<std::string> languages = {
         "ar", "az", "be", "bg", "bn", "ca", "ceb", "de", "en", "es", "et", "eu", "fa", "fr", "gu", "he",

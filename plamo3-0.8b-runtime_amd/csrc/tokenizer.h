@@ -3,6 +3,7 @@
 #pragma once
 
 #include <cstdint>
+#include <functional>
 #include <string>
 #include <unordered_map>
 #include <vector>
@@ -54,6 +55,31 @@ class TokenStream {
     const Tokenizer& tok_;
     std::string pending_;
 };
+
+// Emits up to four documents' streamed tokens in document order (OrderedOutput.swift:24-67):
+// the first unfinished document streams through; later ones buffer until every earlier one
+// has stopped; a document ending on "length" closes the output (later documents and the
+// tail are dropped).  Every emitted chunk is repaired UTF-8, as Swift's String(decoding:)
+// does to each chunk.
+class OrderedOutput {
+  public:
+    using Emit = std::function<void(const std::string&)>;
+    OrderedOutput(const Tokenizer& t, std::vector<std::string> prefixes, std::string tail, Emit emit);
+    void append(int lane, int32_t id);
+    void finish(int lane, const std::string& reason);
+
+  private:
+    std::vector<std::string> prefixes_, buffers_, reasons_;
+    std::string tail_;
+    std::vector<TokenStream> streams_;
+    Emit emit_;
+    size_t first_ = 0;
+    bool closed_ = false;
+    void push(int lane, const std::string& text);
+};
+
+// UTF-8 with every ill-formed sequence replaced by U+FFFD, one per maximal subpart.
+std::string utf8_repair(const std::string& bytes);
 
 // The translation prompt (Tokenizer.swift:272-281).
 std::string translation_prompt(const std::string& text, const std::string& target);

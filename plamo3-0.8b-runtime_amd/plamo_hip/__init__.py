@@ -366,3 +366,55 @@ class TokenStream:
             self.close()
         except Exception:
             pass
+
+
+class OrderedOutput:
+    """OrderedOutput (OrderedOutput.swift:24-67): `emit(text)` receives UTF-8 text in document
+    order; an exception from `emit` cancels the current append/finish and is re-raised."""
+
+    def __init__(self, tokenizer, prefixes, tail, emit):
+        self._t, self._emit, self._failure = tokenizer, emit, []
+
+        def _cb(_, data, n):
+            try:
+                self._emit(ctypes.string_at(data, n).decode("utf-8"))
+                return 0
+            except Exception as e:  # re-raised by the caller
+                self._failure.append(e)
+                return 1
+
+        self._cb = native.TEXT_FN(_cb)
+        enc = [p.encode("utf-8") for p in prefixes]
+        arr = (ctypes.c_char_p * max(1, len(enc)))(*enc)
+        lens = (ctypes.c_size_t * max(1, len(enc)))(*[len(e) for e in enc])
+        tb = tail.encode("utf-8")
+        h = ctypes.c_void_p()
+        self._call(tokenizer._lib.plamo_ordered_open, tokenizer._h, arr, lens, len(enc), tb, len(tb),
+                   ctypes.cast(self._cb, ctypes.c_void_p), None, ctypes.byref(h))
+        self._h = h
+
+    def _call(self, fn, *args):
+        err = ctypes.create_string_buffer(512)
+        rc = fn(*args, err, 512)
+        if self._failure:
+            raise self._failure.pop(0)
+        if rc != 0:
+            raise PlamoError(rc, err.value.decode(errors="replace"))
+
+    def append(self, lane, token_id):
+        self._call(self._t._lib.plamo_ordered_append, self._h, int(lane), int(token_id))
+
+    def finish(self, lane, output):
+        """`output` is (ids, reason) as decode_batch returns it."""
+        self._call(self._t._lib.plamo_ordered_finish, self._h, int(lane), output[1].encode())
+
+    def close(self):
+        if getattr(self, "_h", None):
+            self._t._lib.plamo_ordered_close(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -117,10 +117,21 @@ _SIGNATURES = {
     "plamo_token_stream_finish": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_char_p, ctypes.c_size_t,
                                                  ctypes.POINTER(ctypes.c_size_t), ctypes.c_char_p, ctypes.c_size_t]),
     "plamo_token_stream_close": (None, [ctypes.c_void_p]),
+    "plamo_ordered_open": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(ctypes.c_char_p),
+                                          ctypes.POINTER(ctypes.c_size_t), ctypes.c_int32, ctypes.c_char_p,
+                                          ctypes.c_size_t, ctypes.c_void_p, ctypes.c_void_p,
+                                          ctypes.POINTER(ctypes.c_void_p), ctypes.c_char_p, ctypes.c_size_t]),
+    "plamo_ordered_append": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_char_p,
+                                            ctypes.c_size_t]),
+    "plamo_ordered_finish": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, ctypes.c_char_p, ctypes.c_char_p,
+                                            ctypes.c_size_t]),
+    "plamo_ordered_close": (None, [ctypes.c_void_p]),
     "plamo_translation_prompt": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_size_t, ctypes.c_char_p, ctypes.c_char_p,
                                                 ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t), ctypes.c_char_p,
                                                 ctypes.c_size_t]),
 }
+
+TEXT_FN = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t)
 
 _lib = None
 
