@@ -182,6 +182,33 @@ def bench_long(plamo_hip, np, model_dir, sha):
             "decode_tok_s": round(len(ids) / t_dec, 1)}
 
 
+def bench_tokenizer(plamo_hip, synth):
+    """Host-side tokenizer (Tokenizer.swift): load, encode and decode throughput of the native
+    library on ~1 MB of seeded text over the synthetic vocabulary's alphabet (no GPU work)."""
+    import random
+    path, alphabet = synth.ensure_tokenizer()
+    t0 = time.perf_counter()
+    tok = plamo_hip.Tokenizer(path)
+    load = time.perf_counter() - t0
+    rng = random.Random(7)
+    words = ["".join(rng.choice(alphabet) for _ in range(rng.randint(1, 9))) for _ in range(4096)]
+    text = " ".join(rng.choice(words) for _ in range(160000))[:1 << 20]
+    nbytes = len(text.encode())
+    enc, dec = [], []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        ids = tok.encode(text)
+        enc.append(time.perf_counter() - t0)
+        t0 = time.perf_counter()
+        out = tok.decode_bytes(ids)
+        dec.append(time.perf_counter() - t0)
+    assert out == text.encode(), "tokenizer round trip"
+    tok.close()
+    return {"load_s": round(load, 3), "text_bytes": nbytes, "tokens": len(ids),
+            "encode_MBps": round(nbytes / min(enc) / 1e6, 2), "encode_tok_s": round(len(ids) / min(enc)),
+            "decode_MBps": round(nbytes / min(dec) / 1e6, 2), "cores": 1}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -255,6 +282,8 @@ def main():
         log(f"batch4: {results['batch4']}")
         results["long_context"] = bench_long(plamo_hip, np, model_dir, sha)
         log(f"long_context: {results['long_context']}")
+        results["tokenizer"] = bench_tokenizer(plamo_hip, synth)
+        log(f"tokenizer: {results['tokenizer']}")
         # --- prefill of 2048 tokens
         rt = plamo_hip.Runtime(model_dir, 2048 + 64)
         p2 = np.random.default_rng(3).integers(1024, 107520, 2048).tolist()

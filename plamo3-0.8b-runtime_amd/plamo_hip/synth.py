@@ -126,3 +126,48 @@ def ensure_model(directory=None, seed=0, packed=True):
         from . import native
         native.pack(os.path.join(directory, "model.safetensors"), os.path.join(directory, "model.p12"), sha)
     return directory, sha
+
+
+def tokenizer_records(seed=0):
+    """A synthetic tokenizer.jsonl with the original's shape (Tokenizer.swift:90-95): 107,520
+    entries, <|plamo:bos|> at 1 and <|plamo:tag|> at 16, BYTE tokens <0x80>..<0xFF> at 128-255
+    and <0x00>..<0x7F> at 384-511, scored pieces of up to three characters over a small mixed
+    alphabet, and single private-use characters filling the rest."""
+    import random
+    rng = random.Random(seed)
+    n = 107520
+    recs = [None] * n
+    controls = ["<unk>", "<|plamo:bos|>", "<|plamo:eos|>", "<|plamo:pad|>"] + \
+        [f"<|plamo:c{k}|>" for k in range(4, 16)] + ["<|plamo:tag|>", "<|plamo:msg|>", "<|plamo:key|>",
+                                                    "<|plamo:val|>"]
+    for i, p in enumerate(controls):
+        recs[i] = [p, 0.0, "CONTROL"]
+    for b in range(256):
+        recs[b if b >= 128 else 384 + b] = [f"<0x{b:02X}>", 0.0, "BYTE"]
+    alphabet = "abcdefgh ijk日本語の翻訳です。é,.\n"
+    pieces = list(alphabet) + [a + b for a in alphabet for b in alphabet]
+    pieces += [a + b + c for a in alphabet[:12] for b in alphabet[:12] for c in alphabet[:12]]
+    free = iter(i for i in range(n) if recs[i] is None)
+    for p in pieces:
+        recs[next(free)] = [p, round(rng.uniform(-15, -1), 4), "NORMAL"]
+    k = 0
+    for i in free:
+        recs[i] = [chr(0xF0000 + k), -30.0, "NORMAL"]
+        k += 1
+    return recs, alphabet
+
+
+def ensure_tokenizer(directory=None, seed=0):
+    """Writes the synthetic tokenizer.jsonl once; returns (path, alphabet)."""
+    import tempfile
+    directory = directory or os.path.join(tempfile.gettempdir(), "plamo_synth_tokenizer")
+    os.makedirs(directory, exist_ok=True)
+    path = os.path.join(directory, f"tokenizer-seed{seed}.jsonl")
+    recs, alphabet = tokenizer_records(seed)
+    if not os.path.exists(path):
+        tmp = path + ".tmp"
+        with open(tmp, "w", encoding="utf-8") as f:
+            for r in recs:
+                f.write(json.dumps(r, ensure_ascii=False) + "\n")
+        os.replace(tmp, path)
+    return path, alphabet
