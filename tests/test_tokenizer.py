@@ -198,3 +198,16 @@ def test_translation_prompt():
                               ("a", "en", "reserved PLaMo delimiters")]:
         with pytest.raises(PlamoError, match=msg):
             plamo_hip.Tokenizer.prompt(text, target)
+
+
+def test_prompt_encodes_its_control_tokens(oracle_vocab, native):
+    # Segment.split encodes Tokenizer.prompt(source, target) with BOS (Segments.swift:45): each
+    # <|plamo:...|> of the prompt is a boundary segment that the trie maps to its control id
+    import plamo_hip
+    p = plamo_hip.Tokenizer.prompt("abc 日本", "ja")
+    ids = native.encode(p, bos=True)
+    assert ids == T.encode(oracle_vocab, p, bos=True)
+    assert ids[:2] == [1, 16]
+    pos = {i: ids.count(i) for i in (16, 17, 18, 19)}
+    assert pos == {16: 3, 17: 3, 18: 1, 19: 1}
+    assert native.decode_bytes(ids[1:]) == p.encode()
