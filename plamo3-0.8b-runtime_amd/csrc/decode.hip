@@ -32,7 +32,7 @@ template <int N, int MAXR, int EPI>
 constexpr int gemv_u() {
     if constexpr (EPI == EPI_SWIGLU) return 4;
     else if constexpr (N >= 6144) return MAXR == 1 ? 2 : 1;
-    else return MAXR == 1 ? 4 : 2;
+    else return MAXR == 1 ? (N == ATTN ? 2 : 4) : 2;
 }
 
 // Waves per workgroup.  Four-row kernels with a norm prologue or 6144-wide rows run eight
@@ -1491,7 +1491,7 @@ void gemv_dispatch_n(bool packed, int maxr, Prologue pro, Epilogue epi, const Ge
 int gemv_group_rows(int n, int maxr, Epilogue epi) {
     if (epi == EPI_SWIGLU) return 4;
     if (n >= 6144) return maxr == 1 ? 2 : 1;
-    return maxr == 1 ? 4 : 2;
+    return maxr == 1 ? (n == ATTN ? 2 : 4) : 2;
 }
 
 int gemv_blocks(int n, int maxr, Epilogue epi, int m) {
