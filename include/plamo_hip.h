@@ -60,6 +60,9 @@ typedef struct plamo_stats {
  * pinned checksum of the original model. */
 int plamo_open(const char* directory, int32_t context, int32_t packed, const char* source_sha256,
                plamo_runtime** out, char* err, size_t errlen);
+/* Releases the runtime.  Batches opened on it share its stream and weights: while any is
+ * open the release is deferred to the last plamo_batch_close (the handle must not be used
+ * after plamo_close either way). */
 void plamo_close(plamo_runtime* rt);
 
 /* Runtime.reset() (Runtime.swift:319); also clears the sampler history. */
@@ -257,6 +260,12 @@ int plamo_kernel_gemm(uint64_t w, uint64_t table, uint64_t x, uint64_t y, int32_
 int plamo_kernel_attention_prefill(uint64_t q16, uint64_t keys, uint64_t values, int32_t capacity, int32_t p0,
                                    int32_t tokens, int32_t full, uint64_t local_rope, uint64_t out16,
                                    uint64_t stream);
+
+/* The host RoPE table builder the runtime uploads (`init_rope`, Kernels.metal:212-219; global
+ * factors of `rotated`, Kernels.metal:264-267): `rows` x 64 entries of BF16 cos | sin << 16
+ * from 64 inverse frequencies (config-mlx.json plamo_rope_inv_freq, Runtime.swift:268-274).
+ * Host only; exposed so the tables can be compared with the CPU restatement bit for bit. */
+int plamo_rope_table(const double* freqs, int32_t rows, int32_t global, uint32_t* out, char* err, size_t errlen);
 
 /* Library build identification (gfx arch, HIP version). */
 const char* plamo_version(void);

@@ -12,7 +12,8 @@ Metal's ``cos``/``sin`` cannot be reproduced here, so both the runtime and this 
 evaluate cos/sin of the (exact) FP32 angle in double precision with the C library
 (``math.cos`` is glibc's ``cos``, the same routine the runtime's C++ table builder calls),
 round to FP32, then apply the BF16 roundings above.  Runtime and oracle tables are compared
-bit for bit in tests/test_rope.py; the closed form is pinned there by the textbook rotary
+bit for bit in tests/test_rope.py (through plamo_rope_table, the runtime's host builder); the closed
+form is pinned in tests/test_oracle_model.py by the textbook rotary
 identity (rotation preserves the pair norm to BF16 accuracy, phase 0 is the identity).
 """
 import math

@@ -13,6 +13,10 @@
 
 struct plamo_runtime {
     plamo::RuntimeImpl impl;
+    // Batches share the runtime's stream and weights: closing the runtime while batches
+    // are open defers its destruction to the last plamo_batch_close.
+    int open_batches = 0;
+    bool close_requested = false;
 };
 struct plamo_batch {
     std::unique_ptr<plamo::BatchImpl> impl;
@@ -149,7 +153,14 @@ int plamo_open(const char* directory, int32_t context, int32_t packed, const cha
     });
 }
 
-void plamo_close(plamo_runtime* rt) { delete rt; }
+void plamo_close(plamo_runtime* rt) {
+    if (!rt) return;
+    if (rt->open_batches > 0) {
+        rt->close_requested = true;
+        return;
+    }
+    delete rt;
+}
 
 void plamo_reset(plamo_runtime* rt) {
     if (rt) rt->impl.reset();
@@ -277,11 +288,17 @@ int plamo_batch_open(plamo_runtime* rt, plamo_batch** out, char* err, size_t err
         auto b = std::make_unique<plamo_batch>();
         b->rt = rt;
         b->impl = std::make_unique<plamo::BatchImpl>(&rt->impl);
+        rt->open_batches += 1;
         *out = b.release();
     });
 }
 
-void plamo_batch_close(plamo_batch* b) { delete b; }
+void plamo_batch_close(plamo_batch* b) {
+    if (!b) return;
+    plamo_runtime* rt = b->rt;
+    delete b;
+    if (rt && --rt->open_batches == 0 && rt->close_requested) delete rt;
+}
 
 int plamo_batch_prefill(plamo_batch* b, const int32_t* tokens, const int32_t* lengths, int32_t count, int32_t* next,
                         char* err, size_t errlen) {
@@ -579,6 +596,15 @@ FlashWorkspace flash_workspace(int tokens) {
 
 extern "C" {
 
+int plamo_rope_table(const double* freqs, int32_t rows, int32_t global, uint32_t* out, char* err, size_t errlen) {
+    return guard(err, errlen, [&] {
+        if (!freqs || !out || rows <= 0 || rows > plamo::MAX_CONTEXT)
+            throw plamo::Error(plamo::E_INVAL, "bad RoPE table arguments");
+        const std::vector<uint32_t> t = plamo::rope_table(std::vector<double>(freqs, freqs + 64), rows, global != 0);
+        std::memcpy(out, t.data(), t.size() * 4);
+    });
+}
+
 int plamo_kernel_attention_prefill(uint64_t q16, uint64_t keys, uint64_t values, int32_t capacity, int32_t p0,
                                    int32_t tokens, int32_t full, uint64_t local_rope, uint64_t out16,
                                    uint64_t stream) {
@@ -668,6 +694,11 @@ int plamo_token_stream_push(plamo_token_stream* s, int32_t id, char* out, size_t
                             size_t errlen) {
     return guard(err, errlen, [&] {
         if (!s) throw plamo::Error(plamo::E_INVAL, "bad tokenizer arguments");
+        // size first: a buffer that is too small fails the call with the stream unchanged,
+        // so the caller retries the same id with a larger buffer
+        const size_t need = s->stream.push_size(id);
+        if (n_out) *n_out = need;
+        if (need > cap || (!out && need)) throw plamo::Error(plamo::E_INVAL, "output buffer too small");
         put_bytes(s->stream.push(id), out, cap, n_out);
     });
 }
@@ -675,6 +706,9 @@ int plamo_token_stream_push(plamo_token_stream* s, int32_t id, char* out, size_t
 int plamo_token_stream_finish(plamo_token_stream* s, char* out, size_t cap, size_t* n_out, char* err, size_t errlen) {
     return guard(err, errlen, [&] {
         if (!s) throw plamo::Error(plamo::E_INVAL, "bad tokenizer arguments");
+        const size_t need = s->stream.finish_size();
+        if (n_out) *n_out = need;
+        if (need > cap || (!out && need)) throw plamo::Error(plamo::E_INVAL, "output buffer too small");
         put_bytes(s->stream.finish(), out, cap, n_out);
     });
 }

@@ -97,6 +97,8 @@ void read_frequencies(const std::string& dir, std::vector<double>& local, std::v
     }
 }
 
+}  // namespace
+
 // Local table: (bits(cos), bits(sin)) of float(pos)*f (Kernels.metal:212-219).  Global
 // factors: roundbf(roundbf(cos(angle))*1.5545177444479562f) (Kernels.metal:264-267).  cos
 // and sin of the FP32 angle are evaluated in double precision and rounded to FP32.
@@ -117,6 +119,7 @@ std::vector<uint32_t> rope_table(const std::vector<double>& freqs, int rows, boo
     return t;
 }
 
+namespace {
 template <class T>
 T* upload(DeviceArena& a, const void* src, size_t bytes) {
     T* p = static_cast<T*>(a.alloc(bytes));

@@ -108,6 +108,9 @@ class Engine {
     void enqueue_head16();                                                    // decode: BF16 stream
 };
 
+// RoPE table of `rows` positions, one uint32 per (position, pair): BF16 cos | sin << 16.
+std::vector<uint32_t> rope_table(const std::vector<double>& freqs, int rows, bool global);
+
 std::shared_ptr<Model> load_model(const std::string& dir, int context, bool packed, const std::string& sha,
                                   hipStream_t stream);
 

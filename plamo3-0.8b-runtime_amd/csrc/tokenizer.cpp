@@ -277,6 +277,12 @@ std::string TokenStream::push(int32_t id) {
     return out;
 }
 
+size_t TokenStream::push_size(int32_t id) const {
+    std::string trial = pending_;
+    tok_.append_bytes(id, trial);
+    return trial.size() - incomplete_suffix(trial);
+}
+
 std::string TokenStream::finish() {
     std::string out;
     out.swap(pending_);

@@ -50,6 +50,10 @@ class TokenStream {
     explicit TokenStream(const Tokenizer& t) : tok_(t) {}
     std::string push(int32_t id);
     std::string finish();
+    // Bytes push(id) would return, without changing the stream (callers with a bounded
+    // output buffer check the size first, so a failed call leaves the stream as it was).
+    size_t push_size(int32_t id) const;
+    size_t finish_size() const { return pending_.size(); }
 
   private:
     const Tokenizer& tok_;

@@ -211,3 +211,41 @@ def test_prompt_encodes_its_control_tokens(oracle_vocab, native):
     pos = {i: ids.count(i) for i in (16, 17, 18, 19)}
     assert pos == {16: 3, 17: 3, 18: 1, 19: 1}
     assert native.decode_bytes(ids[1:]) == p.encode()
+
+
+def test_stream_buffer_too_small_leaves_stream_unchanged(tmp_path, oracle_vocab):
+    # A call whose output buffer is too small fails with the stream unchanged, so the retry
+    # with a larger buffer (same id) returns every byte once: pushing <0xE3> <0x81> and then
+    # <0x82> with capacity 0 must not lose U+3042.
+    import ctypes
+    import plamo_hip
+    from plamo_hip import native as nat
+    recs = _records()
+    long_piece = "l" * 300
+    recs[-1] = [long_piece, -30.0, "NORMAL"]   # a filler entry replaced by a 300-byte piece
+    path = tmp_path / "tokenizer.jsonl"
+    _write(path, recs)
+    tok = plamo_hip.Tokenizer(str(path))
+    lib = nat.load()
+    st = tok.stream()
+    a3 = "あ".encode()
+    assert st.push(oracle_vocab.bytes[a3[0]]) == b"" and st.push(oracle_vocab.bytes[a3[1]]) == b""
+    n = ctypes.c_size_t(0)
+    err = ctypes.create_string_buffer(256)
+    buf = ctypes.create_string_buffer(16)
+    rc = lib.plamo_token_stream_push(st._h, oracle_vocab.bytes[a3[2]], buf, 0, ctypes.byref(n), err, 256)
+    assert rc == 1  # PLAMO_EINVAL
+    assert n.value == 3
+    rc = lib.plamo_token_stream_push(st._h, oracle_vocab.bytes[a3[2]], buf, 16, ctypes.byref(n), err, 256)
+    assert rc == 0 and buf.raw[:n.value] == a3
+    # finish with a pending partial sequence: too small, then the full bytes once
+    assert st.push(oracle_vocab.bytes[a3[0]]) == b""
+    rc = lib.plamo_token_stream_finish(st._h, buf, 0, ctypes.byref(n), err, 256)
+    assert rc != 0 and n.value == 1
+    assert st.finish() == a3[:1] and st.finish() == b""
+    # a piece longer than the Python binding's first 256-byte buffer goes through its retry
+    st2 = tok.stream()
+    ids = [oracle_vocab.bytes[a3[0]], len(recs) - 1, oracle_vocab.bytes[a3[1]], oracle_vocab.bytes[a3[2]]]
+    out = b"".join(st2.push(i) for i in ids) + st2.finish()
+    assert out == tok.decode_bytes(ids) == bytes([a3[0]]) + long_piece.encode() + a3[1:]
+    assert tok.decode_bytes([len(recs) - 1]) == long_piece.encode()
