@@ -261,6 +261,22 @@ int plamo_kernel_attention_prefill(uint64_t q16, uint64_t keys, uint64_t values,
                                    int32_t tokens, int32_t full, uint64_t local_rope, uint64_t out16,
                                    uint64_t stream);
 
+/* Decode attention of `rows` (1..4) one-token rows: the `qkv` (Kernels.metal:223-259) and
+ * attention dispatches of Runtime.swift:389-444 for a one-token chunk, i.e. q/k RMSNorm (+1
+ * gains `q_norm`, `k_norm`: BF16 [128]), RoPE, the new key and value written to slot
+ * pos % capacity, then split-K attention over the visible keys (`matrix_rotary`, `softmax`,
+ * `attend`, or `attention` + `attention_merge`, Kernels.metal:301-562) with the partitions
+ * merged on the device.  qkv: FP32 [rows][2304] (BF16-valued); keys/values: BF16
+ * [rows][capacity][128], row q using slice q, position p in slot p % capacity (global keys
+ * stored rotated, local keys normalised and unrotated); positions: host int32 [rows];
+ * full != 0: keys 0..pos (global layer, pos < capacity, global_rope holds capacity rows of
+ * [64] uint32 BF16 cos | sin << 16), else the 2048-key window ending at pos, keys rotated
+ * with coordinate key_pos - max(0, pos - 2047) (local_rope: [2064][64]); out16: BF16
+ * [rows][2048].  Uses a per-device workspace the library grows on demand. */
+int plamo_kernel_attention_decode(uint64_t qkv, uint64_t q_norm, uint64_t k_norm, uint64_t keys, uint64_t values,
+                                  int32_t capacity, const int32_t* positions, int32_t rows, int32_t full,
+                                  uint64_t local_rope, uint64_t global_rope, uint64_t out16, uint64_t stream);
+
 /* The host RoPE table builder the runtime uploads (`init_rope`, Kernels.metal:212-219; global
  * factors of `rotated`, Kernels.metal:264-267): `rows` x 64 entries of BF16 cos | sin << 16
  * from 64 inverse frequencies (config-mlx.json plamo_rope_inv_freq, Runtime.swift:268-274).

@@ -117,9 +117,19 @@ def rotate(z, c, s):
 
 
 class Oracle:
-    """Runtime (Runtime.swift:128-553) on the CPU for one sequence."""
+    """Runtime (Runtime.swift:128-553) on the CPU for one sequence.
 
-    def __init__(self, weights, context, local_capacity=None):
+    ``dots="fp32"`` (default) takes every dot product of the linear layers in torch's FP32
+    order; ``dots="exact"`` computes them in FP64 and rounds once to FP32 (BF16 x BF16
+    products are exact in FP64 and sums of at most 6144 of them carry ~2^-40 relative error,
+    so each dot is the correctly rounded FP32 value).  The two modes differ only in the
+    rounding of those sums; the difference of their logits is the summation-order noise
+    floor of the model (tests/test_noise_floor.py)."""
+
+    def __init__(self, weights, context, local_capacity=None, dots="fp32"):
+        assert dots in ("fp32", "exact")
+        self.dots = dots
+        self._w64 = {}
         self.w = weights
         self.context = context
         self.batch_limit = min(context, 16)
@@ -138,6 +148,15 @@ class Oracle:
         self.logit_bits = None
         self.logits_fp32 = None
         self.hidden = None
+
+    def _mm(self, x, w):
+        """x @ w.T with the dot products of the selected mode."""
+        if self.dots == "fp32":
+            return x @ w.T
+        key = id(w)
+        if key not in self._w64:
+            self._w64[key] = (w, w.double())
+        return (x.double() @ self._w64[key][1].T).float()
 
     def _attention(self, layer, q_heads, T, p0):
         """Runtime.swift:389-444 for a chunk of T tokens starting at p0."""
@@ -173,7 +192,7 @@ class Oracle:
         for i, L in enumerate(self.w.layers):
             full, cap = is_global(i), self.capacity[i]
             base = 0 if full else max(0, p0 - (WINDOW - 1))
-            qkv = roundbf_t(xn @ L["qkv"].T)
+            qkv = roundbf_t(self._mm(xn, L["qkv"]))
             heads = qkv[:, :17 * HEAD_DIM].reshape(T, 17, HEAD_DIM)
             r = 1.0 / torch.sqrt((heads * heads).sum(-1, keepdim=True) / 128.0 + torch.tensor(1e-6))
             g = torch.cat([gain(L["q_norm"], 1.0)[None].expand(16, -1), gain(L["k_norm"], 1.0)[None]], 0)
@@ -187,13 +206,13 @@ class Oracle:
             self.keys[i][pos % cap] = bits_t(k)
             self.values[i][pos % cap] = bits_t(qkv[:, 17 * HEAD_DIM:])
             att = self._attention(i, q, T, p0)
-            o = roundbf_t(att @ L["o"].T)
+            o = roundbf_t(self._mm(att, L["o"]))
             x = roundbf_t(x + norm(o, L["post"], 0.2))
             xn = norm(x, L["pre_mlp"], 1.0)
-            gu = roundbf_t(xn @ L["up"].T)
+            gu = roundbf_t(self._mm(xn, L["up"]))
             gate = gu[:, :INTER]
             act = roundbf_t(roundbf_t(gate / (1.0 + torch.exp(-gate))) * gu[:, INTER:])
-            d = roundbf_t(act @ L["down"].T)
+            d = roundbf_t(self._mm(act, L["down"]))
             x = roundbf_t(x + norm(d, L["post_mlp"], POST_MLP_OFFSET))
             if i + 1 < LAYERS:
                 xn = norm(x, self.w.layers[i + 1]["pre"], 1.0)
@@ -202,7 +221,7 @@ class Oracle:
             return -1
         h = norm(x[-1:], self.w.final, 1.0)
         self.hidden = h[0]
-        self.logits_fp32 = (h @ self.w.head.T)[0]
+        self.logits_fp32 = self._mm(h, self.w.head)[0]
         self.logit_bits = bits_t(self.logits_fp32)
         from .sampler import argmax_gpu
         return argmax_gpu(bf_t(self.logit_bits).numpy())
@@ -216,6 +235,87 @@ class Oracle:
             e = min(s + self.batch_limit, len(tokens))
             nxt = self.forward(list(tokens[s:e]), output=e == len(tokens))
         return nxt
+
+    def fill(self, tokens):
+        """``prefill`` computed a prompt at a time (long prompts).  The linear layers, norms
+        and SwiGLU act on each row independently, so they run over every prompt row at once;
+        each row's query and key coordinates follow its 16-token chunk's RoPE base
+        (Runtime.swift:389-399, chunks counted from the current position, as ``prefill``);
+        attention sees each query's visible keys, [pos-2047, pos] on local layers and
+        [0, pos] on global ones.  Every key of the prompt is written before attention, so the
+        prompt and the window before it must fit the ring without overwriting."""
+        T, p0 = len(tokens), self.position
+        if not tokens or p0 + T > self.context or any(not (0 <= t < VOCAB) for t in tokens):
+            raise ValueError("Input exceeds context")
+        if p0 + T > max(0, p0 - (WINDOW - 1)) + min(self.capacity):
+            raise ValueError("prompt does not fit the ring at once")
+        x = self.w.embed(tokens)
+        xn = norm(x, self.w.layers[0]["pre"], 1.0)
+        pos = torch.arange(T) + p0
+        chunk_base = torch.clamp(p0 + (torch.arange(T) // self.batch_limit) * self.batch_limit - (WINDOW - 1), min=0)
+        for i, L in enumerate(self.w.layers):
+            full, cap = is_global(i), self.capacity[i]
+            qkv = roundbf_t(self._mm(xn, L["qkv"]))
+            heads = qkv[:, :17 * HEAD_DIM].reshape(T, 17, HEAD_DIM)
+            r = 1.0 / torch.sqrt((heads * heads).sum(-1, keepdim=True) / 128.0 + torch.tensor(1e-6))
+            g = torch.cat([gain(L["q_norm"], 1.0)[None].expand(16, -1), gain(L["k_norm"], 1.0)[None]], 0)
+            z = roundbf_t(roundbf_t(heads * r) * g)
+            if full:
+                cq, sq = self.glob[0][pos], self.glob[1][pos]
+            else:
+                cq, sq = self.local[0][pos - chunk_base], self.local[1][pos - chunk_base]
+            q = rotate(z[:, :16], cq[:, None], sq[:, None])
+            k = rotate(z[:, 16], self.glob[0][pos], self.glob[1][pos]) if full else z[:, 16]
+            self.keys[i][pos % cap] = bits_t(k)
+            self.values[i][pos % cap] = bits_t(qkv[:, 17 * HEAD_DIM:])
+            att = torch.empty(T, HEADS * HEAD_DIM)
+            bases = [0] if full else sorted(set(chunk_base.tolist()))
+            for b in bases:
+                rows = torch.arange(T) if full else torch.nonzero(chunk_base == b)[:, 0]
+                att[rows] = self._attend_rows(i, q[rows], pos[rows], b)
+            o = roundbf_t(self._mm(att, L["o"]))
+            x = roundbf_t(x + norm(o, L["post"], 0.2))
+            xn = norm(x, L["pre_mlp"], 1.0)
+            gu = roundbf_t(self._mm(xn, L["up"]))
+            gate = gu[:, :INTER]
+            act = roundbf_t(roundbf_t(gate / (1.0 + torch.exp(-gate))) * gu[:, INTER:])
+            d = roundbf_t(self._mm(act, L["down"]))
+            x = roundbf_t(x + norm(d, L["post_mlp"], POST_MLP_OFFSET))
+            if i + 1 < LAYERS:
+                xn = norm(x, self.w.layers[i + 1]["pre"], 1.0)
+        self.position += T
+        h = norm(x[-1:], self.w.final, 1.0)
+        self.hidden = h[0]
+        self.logits_fp32 = self._mm(h, self.w.head)[0]
+        self.logit_bits = bits_t(self.logits_fp32)
+        from .sampler import argmax_gpu
+        return argmax_gpu(bf_t(self.logit_bits).numpy())
+
+    def _attend_rows(self, layer, q, pos, base, block=256):
+        """Attention of queries q [G, 16, 128] at positions `pos` whose keys rotate with RoPE
+        base `base` (local layers; 0 and unused on global ones), in the softmax/attend
+        arithmetic of ``_attention``."""
+        full, cap = is_global(layer), self.capacity[layer]
+        last = int(pos.max())
+        r = torch.arange(last + 1 - base)
+        phys = (base + r) % cap
+        keys = bf_t(self.keys[layer][phys])
+        if not full:
+            keys = rotate(keys, self.local[0][r], self.local[1][r])
+        values = bf_t(self.values[layer][phys])
+        kabs = base + r
+        out = torch.empty(q.shape[0], HEADS * HEAD_DIM)
+        for s in range(0, q.shape[0], block):
+            qq, pp = q[s:s + block], pos[s:s + block]
+            scores = torch.einsum("thd,kd->thk", qq, keys)
+            lo = torch.zeros_like(pp) if full else torch.clamp(pp - (WINDOW - 1), min=0)
+            visible = (kabs[None, :] >= lo[:, None]) & (kabs[None, :] <= pp[:, None])
+            sc = torch.where(visible[:, None, :], scores * torch.tensor(SCALE), torch.tensor(-np.inf))
+            m = sc.max(-1, keepdim=True).values
+            e = torch.exp(sc - m)
+            p = e / e.sum(-1, keepdim=True)
+            out[s:s + block] = roundbf_t(torch.einsum("thk,kd->thd", p, values)).reshape(-1, HEADS * HEAD_DIM)
+        return out
 
     def logits(self):
         """Runtime.logits(into:) (Runtime.swift:547-552): BF16 logits widened to FP32."""

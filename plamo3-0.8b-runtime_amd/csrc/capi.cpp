@@ -592,9 +592,109 @@ FlashWorkspace flash_workspace(int tokens) {
     }
     return w;
 }
+
+// Workspace of the kernel-level decode attention, per device, grown on demand: the step
+// state, the attention tickets [ROWS][4 head groups] and the partition statistics and
+// outputs [ROWS][parts][16] (x128 for the outputs), the layout the runtime's engine uses.
+struct AttnWorkspace {
+    void* base = nullptr;
+    uint32_t parts = 0;
+};
+std::mutex g_attn_ws_mu;
+std::map<int, AttnWorkspace> g_attn_ws;
+
+size_t attn_workspace_bytes(uint32_t parts) {
+    const size_t stats = size_t(plamo::ROWS) * parts * plamo::HEADS;
+    return 256 + 256 + 2 * stats * 4 + stats * plamo::HEAD_DIM * 4;
+}
+
+// Carves a workspace at `base` (256-byte aligned) into the attention parameter pointers.
+void attn_workspace_bind(void* base, uint32_t parts, plamo::AttnParams& a, plamo::StepState*& st) {
+    uint8_t* b = static_cast<uint8_t*>(base);
+    const size_t stats = size_t(plamo::ROWS) * parts * plamo::HEADS;
+    st = reinterpret_cast<plamo::StepState*>(b);
+    a.tickets = reinterpret_cast<uint32_t*>(b + 256);
+    a.part_m = reinterpret_cast<float*>(b + 512);
+    a.part_l = a.part_m + stats;
+    a.part_o = a.part_l + stats;
+}
+
+void* attn_workspace(uint32_t parts) {
+    std::lock_guard<std::mutex> lk(g_attn_ws_mu);
+    int dev = 0;
+    PLAMO_HIP(hipGetDevice(&dev));
+    AttnWorkspace& w = g_attn_ws[dev];
+    if (w.parts < parts) {
+        if (w.base) {
+            PLAMO_HIP(hipDeviceSynchronize());
+            (void)hipFree(w.base);
+            w = AttnWorkspace{};
+        }
+        PLAMO_HIP(hipMalloc(&w.base, attn_workspace_bytes(parts)));
+        w.parts = parts;
+    }
+    return w.base;
+}
+
+static_assert(sizeof(plamo::StepState) <= 256, "step state fits its workspace slot");
+
+// Validates a kernel-level decode attention call and fills every parameter except the
+// workspace pointers; returns the partition count (grid width).
+uint32_t attn_decode_params(uint64_t qkv, uint64_t q_norm, uint64_t k_norm, uint64_t keys, uint64_t values,
+                            int32_t capacity, const int32_t* positions, int32_t rows, int32_t full,
+                            uint64_t local_rope, uint64_t global_rope, uint64_t out16, plamo::AttnParams& a) {
+    if (rows < 1 || rows > plamo::ROWS || !positions || !qkv || !q_norm || !k_norm || !keys || !values || !out16 ||
+        !local_rope || (full && !global_rope) || capacity < 1 || capacity > plamo::MAX_CONTEXT)
+        throw plamo::Error(plamo::E_INVAL, "bad attention arguments");
+    int64_t most = 1;
+    for (int32_t q = 0; q < rows; ++q) {
+        const int64_t pos = positions[q];
+        if (pos < 0 || pos >= plamo::MAX_CONTEXT) throw plamo::Error(plamo::E_INVAL, "bad attention position");
+        // visible keys: 0..pos (global), the 2048-key window ending at pos (local); all of
+        // them must be resident in the lane's cache at once
+        const int64_t count = full ? pos + 1 : std::min<int64_t>(pos + 1, plamo::WINDOW);
+        if (full ? pos >= capacity : count > capacity)
+            throw plamo::Error(plamo::E_INVAL, "attention keys exceed the cache capacity");
+        most = std::max(most, count);
+    }
+    a.qkv = reinterpret_cast<const float*>(qkv);
+    a.q_norm = reinterpret_cast<const uint16_t*>(q_norm);
+    a.k_norm = reinterpret_cast<const uint16_t*>(k_norm);
+    a.keys = reinterpret_cast<uint16_t*>(keys);
+    a.values = reinterpret_cast<uint16_t*>(values);
+    a.capacity = uint32_t(capacity);
+    a.local_rope = reinterpret_cast<const uint32_t*>(local_rope);
+    a.global_rope = reinterpret_cast<const uint32_t*>(global_rope);
+    a.out16 = reinterpret_cast<uint16_t*>(out16);
+    a.parts = uint32_t((most + plamo::KEYS_PER_PART - 1) / plamo::KEYS_PER_PART);
+    a.defer = full && a.parts > plamo::ATTN_MERGE_INLINE ? plamo::ATTN_MERGE_INLINE : 0;
+    return a.parts;
+}
+
+void attn_decode_launch(plamo::AttnParams& a, plamo::StepState* st, const int32_t* positions, int32_t rows,
+                        bool full, hipStream_t s) {
+    a.state = st;
+    plamo::launch_attn_state(st, a.tickets, positions, rows, s);
+    plamo::launch_attention(full, a, rows, s);
+    if (a.defer) plamo::launch_attention_merge(a, rows, s);
+}
 }  // namespace
 
 extern "C" {
+
+int plamo_kernel_attention_decode(uint64_t qkv, uint64_t q_norm, uint64_t k_norm, uint64_t keys, uint64_t values,
+                                  int32_t capacity, const int32_t* positions, int32_t rows, int32_t full,
+                                  uint64_t local_rope, uint64_t global_rope, uint64_t out16, uint64_t stream) {
+    return guard(nullptr, 0, [&] {
+        plamo::AttnParams a{};
+        const uint32_t parts = attn_decode_params(qkv, q_norm, k_norm, keys, values, capacity, positions, rows, full,
+                                                  local_rope, global_rope, out16, a);
+        plamo::StepState* st = nullptr;
+        attn_workspace_bind(attn_workspace(parts), parts, a, st);
+        attn_decode_launch(a, st, positions, rows, full != 0, reinterpret_cast<hipStream_t>(stream));
+        PLAMO_HIP(hipGetLastError());
+    });
+}
 
 int plamo_rope_table(const double* freqs, int32_t rows, int32_t global, uint32_t* out, char* err, size_t errlen) {
     return guard(err, errlen, [&] {

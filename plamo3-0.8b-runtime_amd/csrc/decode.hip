@@ -1437,6 +1437,26 @@ __global__ void unpack_kernel(const uint8_t* payload, const uint32_t* table, uin
     out[i] = uint16_t(p12_word(blk[k], code, tag + 107u));
 }
 
+struct AttnStateArgs {
+    int32_t pos[ROWS];
+    int32_t rows;
+};
+__global__ __launch_bounds__(64) void attn_state_kernel(StepState* st, uint32_t* tickets, AttnStateArgs a) {
+    const int tid = threadIdx.x;
+    uint32_t* w = reinterpret_cast<uint32_t*>(st);
+    for (int i = tid; i < STATE_WORDS; i += 64) w[i] = 0;
+    if (tid < ROWS * HEADS / HG) tickets[tid] = 0;
+    __syncthreads();
+    if (tid == 0) {
+        st->rows = uint32_t(a.rows);
+        st->penalty = 1.0f;
+        for (int q = 0; q < ROWS; ++q) {
+            st->lane[q] = uint32_t(q);
+            st->pos[q] = q < a.rows ? uint32_t(a.pos[q]) : 0u;
+        }
+    }
+}
+
 __global__ void fill_u32_kernel(uint32_t* p, uint32_t v, size_t n) {
     const size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
     if (i < n) p[i] = v;
@@ -1544,6 +1564,13 @@ void launch_select(float* logits, int n, const int32_t* history, int hist, float
 void launch_unpack(const uint8_t* payload, const uint32_t* table, uint16_t* out, int64_t count, hipStream_t s) {
     if (count <= 0) return;
     hipLaunchKernelGGL(unpack_kernel, dim3(unsigned((count + 255) / 256)), dim3(256), 0, s, payload, table, out, count);
+}
+
+void launch_attn_state(StepState* st, uint32_t* tickets, const int32_t* pos, int rows, hipStream_t s) {
+    AttnStateArgs a{};
+    for (int q = 0; q < ROWS; ++q) a.pos[q] = q < rows ? pos[q] : 0;
+    a.rows = rows;
+    hipLaunchKernelGGL(attn_state_kernel, dim3(1), dim3(64), 0, s, st, tickets, a);
 }
 
 void launch_fill_u32(uint32_t* p, uint32_t value, size_t count, hipStream_t s) {

@@ -125,6 +125,10 @@ void launch_select(float* logits, int n, const int32_t* history, int hist, float
                    float presence, int32_t* out, hipStream_t s);
 void launch_unpack(const uint8_t* payload, const uint32_t* table, uint16_t* out, int64_t count, hipStream_t s);
 void launch_fill_u32(uint32_t* p, uint32_t value, size_t count, hipStream_t s);
+// Step state of a kernel-level decode attention call: `rows` rows at `pos` (row q reads and
+// writes KV slice q), every other field zero; clears the rows' attention tickets.  Written by
+// a kernel from its arguments, so the call needs no host copy.
+void launch_attn_state(StepState* st, uint32_t* tickets, const int32_t* pos, int rows, hipStream_t s);
 
 // prefill.hip
 struct PrefillParams;

@@ -1,13 +1,22 @@
-"""End-to-end parity of the HIP token loop against the CPU oracle (config 1 and friends).
+"""End-to-end parity of the HIP token loop against the CPU oracle (configs 1 and 3).
 
 The decode step is compared bit for bit with the order-exact oracle (test_gpu_exact.py).
 Paths whose summation order the oracle does not restate (the MFMA prefill GEMMs) are
 compared with the semantic oracle.  The task's tolerance (max-abs 2e-2, RMSE 5e-3 against
 the FP32 head output) lies below the noise floor of this random-init model: two CPU oracles
-that differ only in dot-product summation order (torch FP32 vs exactly rounded) disagree by
-max-abs 0.0564 and RMSE 0.0134 (measured on config 1's prefill).  Such comparisons therefore
-use that floor with a 1.5x margin, and record the north-star figures next to it.
+that differ only in dot-product summation order (torch FP32 vs correctly rounded) disagree
+by the floors recorded in tests/golden/manifest.json (config 1: max-abs 0.0564, RMSE 0.0134;
+config 3: 0.0476, 0.0114), which tests/test_noise_floor.py re-measures.  Such comparisons use
+1.5x that floor and print the north-star figures next to it.
+
+Greedy choices: where the oracle's top two logits are more than one BF16 ulp apart the GPU
+must pick the oracle's token; within one ulp (a near-tie a different summation order may
+legitimately resolve the other way) the choice must be one of the near-tied tokens, and the
+gap is printed.
 """
+import json
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -20,18 +29,33 @@ from oracle.bf16 import bf_np
 pytestmark = pytest.mark.gpu
 
 NORTH_STAR = (2e-2, 5e-3)          # max-abs, RMSE
-NOISE_FLOOR = (0.0564, 0.0134)     # two summation orders of the same BF16 algorithm
+with open(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "manifest.json")) as _f:
+    _FLOORS = json.load(_f)["noise_floor"]
+NOISE_FLOOR = tuple(_FLOORS["config1"])   # two summation orders of the same BF16 algorithm
 MAX_ABS, RMSE = 1.5 * NOISE_FLOOR[0], 1.5 * NOISE_FLOOR[1]
 
 
-def check_logits(gpu_bits, oracle, label):
+def bf16_ulp(v):
+    return float(2.0 ** (np.floor(np.log2(abs(v))) - 7))
+
+
+def check_choice(choice, ref, label):
+    """The GPU's choice is the oracle's best, or within one BF16 ulp of it (a near-tie)."""
+    top = float(ref.max())
+    deficit = top - float(ref[choice])
+    if deficit > 0:
+        print(f"    {label}: near-tie, chose {choice} {deficit:.4f} below the oracle's best "
+              f"{int(np.argmax(ref))} (1 ulp = {bf16_ulp(top):.4f})", flush=True)
+    assert deficit <= bf16_ulp(top), (label, choice, int(np.argmax(ref)), deficit)
+
+
+def check_logits(gpu_bits, oracle, label, floor=NOISE_FLOOR):
     ref = oracle.logits_fp32.numpy().astype(np.float64)
     got = bf_np(gpu_bits).astype(np.float64)
     err = np.abs(got - ref)
     rmse = float(np.sqrt(np.mean(err ** 2)))
-    assert err.max() <= MAX_ABS and rmse <= RMSE, (label, float(err.max()), rmse)
-    # near-tie rule: the GPU's choice is the oracle's best or within the noise envelope of it
-    assert ref[int(np.argmax(got))] >= ref.max() - MAX_ABS, label
+    assert err.max() <= 1.5 * floor[0] and rmse <= 1.5 * floor[1], (label, float(err.max()), rmse)
+    check_choice(int(np.argmax(got)), ref, label)
     return float(err.max()), rmse
 
 
@@ -165,7 +189,7 @@ def test_sampling_device_loop_matches_host_loop(runtimes, oracle_weights, golden
     # controls on the device in both loops; bitwise against the restated select in
     # test_gpu_exact.py::test_sampling_controls_bit_exact.  Against the semantic oracle
     # (teacher-forced on the GPU's choices) every controlled choice is the oracle's best or
-    # within the noise envelope of it, x1.1 for the repetition penalty's scaling.
+    # within one BF16 ulp of it (a near-tie).
     gs = golden["config1_sampling"]
     for rt in runtimes:
         rt.set_sampling(gs["penalty"], gs["frequency"], 0.0, gs["ngram"])
@@ -190,7 +214,94 @@ def test_sampling_device_loop_matches_host_loop(runtimes, oracle_weights, golden
     for i, t in enumerate(ids):
         adj = o.logits().copy()
         sampler.select(adj, hist, gs["penalty"], gs["ngram"], gs["frequency"])
-        assert adj[t] >= adj.max() - 1.1 * MAX_ABS, (i, t, float(adj[t]), float(adj.max()))
+        deficit = float(adj.max() - adj[t])
+        assert deficit <= bf16_ulp(float(adj.max())), (i, t, float(adj[t]), float(adj.max()))
         hist.append(t)
         if i + 1 < len(ids):
             o.forward([t])
+
+
+def first_divergence(got, want):
+    for i, (a, b) in enumerate(zip(got, want)):
+        if a != b:
+            return i
+    return None
+
+
+def test_greedy_ids_to_the_first_near_tie(runtimes, golden):
+    # generate() against the oracle's own greedy trajectory (golden greedy_ids): equal up to
+    # the first step whose oracle top-2 gap is under one BF16 ulp; a divergence there is a
+    # near-tie resolved the other way (its gap is asserted and printed), anywhere else a bug
+    g = golden["config1"]
+    for rt, name in zip(runtimes, ("plain", ".p12")):
+        ids, reason = rt.generate(g["prompt"], 32)
+        i = first_divergence(ids, g["greedy_ids"])
+        if i is None:
+            assert len(ids) == len(g["greedy_ids"])
+            print(f"  {name}: all {len(ids)} greedy ids equal the oracle's", flush=True)
+            continue
+        gap, ulp = g["top2_gaps"][i], g["top_ulps"][i]
+        print(f"  {name}: ids equal for {i} steps; step {i}: {ids[i]} vs oracle {g['greedy_ids'][i]}, "
+              f"oracle top-2 gap {gap:.4f} < 1 ulp {ulp:.4f}", flush=True)
+        assert gap < ulp, (name, i, gap, ulp)
+
+
+def test_sampled_ids_to_the_first_near_tie(runtimes, golden):
+    # the same with Sampler.select controls on the device (gaps of the adjusted logits)
+    gs = golden["config1_sampling"]
+    for rt, name in zip(runtimes, ("plain", ".p12")):
+        rt.set_sampling(gs["penalty"], gs["frequency"], 0.0, gs["ngram"])
+        try:
+            ids, _ = rt.generate(golden["config1"]["prompt"], gs["max_tokens"])
+        finally:
+            rt.set_sampling()
+        i = first_divergence(ids, gs["ids"])
+        if i is None:
+            assert len(ids) == len(gs["ids"])
+            print(f"  {name}: all {len(ids)} sampled ids equal the oracle's", flush=True)
+            continue
+        gap, ulp = gs["top2_gaps"][i], gs["top_ulps"][i]
+        print(f"  {name}: sampled ids equal for {i} steps; step {i}: {ids[i]} vs oracle {gs['ids'][i]}, "
+              f"adjusted top-2 gap {gap:.4f} < 1 ulp {ulp:.4f}", flush=True)
+        assert gap < ulp, (name, i, gap, ulp)
+
+
+def test_config3_prefill_2048_matches_oracle(model_dir, oracle_weights, golden):
+    # one 2048-token random prompt through all 16 layers (MFMA GEMMs, flash
+    # attention with the window on local layers and full causal on the global ones);
+    # last-position logits and every layer's populated ring/global KV against the oracle
+    g = golden["config3"]
+    prompt = np.random.default_rng(g["prompt_seed"]).integers(1024, 107520, g["length"]).tolist()
+    floor = tuple(_FLOORS["config3"])
+    d, _ = model_dir
+    rt = plamo_hip.Runtime(d, 2048)
+    try:
+        nxt = rt.prefill(prompt)
+        bits = rt.logit_bits().copy()
+        kv = [rt.kv(layer) for layer in range(16)]
+        assert rt.position == 2048
+    finally:
+        rt.close()
+    torch.set_num_threads(max(1, min(16, len(os.sched_getaffinity(0)))))
+    o = om.Oracle(oracle_weights, 2048)
+    want = o.fill(prompt)
+    assert want == g["next"]   # the oracle itself is pinned to the golden vector
+    mx, rmse = check_logits(bits, o, "config3 prefill", floor)
+    check_choice(nxt, o.logits_fp32.numpy().astype(np.float64), "config3 next token")
+    print(f"  config3 logits max-abs {mx:.4f} RMSE {rmse:.4f} (floor {floor[0]:.4f}/{floor[1]:.4f}, "
+          f"north star {NORTH_STAR[0]}/{NORTH_STAR[1]})", flush=True)
+    worst = 0.0
+    for layer in range(16):
+        k, v = kv[layer]
+        ko = o.keys[layer].numpy().astype(np.uint16)
+        vo = o.values[layer].numpy().astype(np.uint16)
+        assert k.shape[0] >= 2048 and ko.shape[0] >= 2048
+        for got, ref in ((k, ko), (v, vo)):
+            gf, wf = bf_np(got[:2048]).astype(np.float64), bf_np(ref[:2048]).astype(np.float64)
+            rel = np.sqrt(np.mean((gf - wf) ** 2)) / np.sqrt(np.mean(wf ** 2))
+            worst = max(worst, rel)
+            assert rel < 0.03, (layer, rel)   # RMS difference under 3% of the RMS value
+        # layer 0 sees no prior noise: its keys and values are bit-identical or 1-ulp off
+        if layer == 0:
+            assert np.mean(k[:2048] != ko[:2048]) < 0.01 and np.mean(v[:2048] != vo[:2048]) < 0.01
+    print(f"  config3 KV: worst layer RMS difference {worst:.4f} of RMS", flush=True)

@@ -217,3 +217,18 @@ def test_native_decode_batch_finish_order():
         plamo_hip.decode_batch([5], [8192], lambda t: t)
     with pytest.raises(native.PlamoError, match="Invalid quad predictions"):
         plamo_hip.decode_batch([5], [3], lambda t: [107520])
+
+
+def test_attention_decode_rejects_bad_geometry():
+    # plamo_kernel_attention_decode validates its geometry on the host before any device work
+    import ctypes
+    from plamo_hip import native
+    lib = native.load()
+    pos = (ctypes.c_int32 * 1)(100)
+    # global position past the capacity; local window larger than the ring; five rows
+    assert lib.plamo_kernel_attention_decode(1, 1, 1, 1, 1, 100, pos, 1, 1, 1, 1, 1, 0) != 0
+    assert lib.plamo_kernel_attention_decode(1, 1, 1, 1, 1, 50, pos, 1, 0, 1, 1, 1, 0) != 0
+    pos5 = (ctypes.c_int32 * 5)(1, 1, 1, 1, 1)
+    assert lib.plamo_kernel_attention_decode(1, 1, 1, 1, 1, 100, pos5, 5, 1, 1, 1, 1, 0) != 0
+    neg = (ctypes.c_int32 * 1)(-1)
+    assert lib.plamo_kernel_attention_decode(1, 1, 1, 1, 1, 100, neg, 1, 1, 1, 1, 1, 0) != 0

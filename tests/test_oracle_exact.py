@@ -56,3 +56,83 @@ def test_exact_decoder_tracks_semantic_oracle(oracle_weights, golden):
     got = bf_np(bits).astype(np.float64)
     rmse = float(np.sqrt(np.mean((got - ref) ** 2)))
     assert rmse < 0.03 and np.argmax(got) == np.argmax(ref)
+
+
+def _attention_pair(context, cap_local, seed):
+    """An ExactDecoder and a semantic Oracle that share only attention state (keys, values,
+    norm gains, RoPE tables): no model weights are needed for `attention`/`_attention`."""
+    from oracle import rope
+    rng = np.random.default_rng(seed)
+    f_local, f_full = rope.synthetic_frequencies()
+    ex = exact.ExactDecoder.__new__(exact.ExactDecoder)
+    ex.context = context
+    ex.cap = [context if i % 8 == 7 else cap_local for i in range(16)]
+    qn = exact.bits_np((rng.standard_normal(128) * 0.1).astype(np.float32))
+    kn = exact.bits_np((rng.standard_normal(128) * 0.1).astype(np.float32))
+    ex.layers = [{"q_norm": qn, "k_norm": kn} for _ in range(16)]
+    ex.lc, ex.ls = rope.local_table(f_local, 2064)
+    ex.gc, ex.gs = rope.global_table(f_full, context)
+    ex.keys = [exact.bits_np(rng.standard_normal((c, 128)).astype(np.float32)) for c in ex.cap]
+    ex.values = [exact.bits_np(rng.standard_normal((c, 128)).astype(np.float32)) for c in ex.cap]
+    o = om.Oracle.__new__(om.Oracle)
+    o.context = context
+    o.capacity = list(ex.cap)
+    o.local = (torch.from_numpy(ex.lc), torch.from_numpy(ex.ls))
+    o.glob = (torch.from_numpy(ex.gc), torch.from_numpy(ex.gs))
+    return ex, o, qn, kn, rng
+
+
+def _semantic_row(ex, o, layer, qkv, pos, qn):
+    """The semantic oracle's attention for the same row after the twin wrote the new key."""
+    full = layer % 8 == 7
+    o.keys = [torch.from_numpy(k.astype(np.int32)) for k in ex.keys]
+    o.values = [torch.from_numpy(v.astype(np.int32)) for v in ex.values]
+    z = om.norm(torch.from_numpy(qkv[:2048].reshape(16, 128)), torch.from_numpy(qn.astype(np.int32)), 1.0)
+    base = 0 if full else max(0, pos - 2047)
+    c, s = (o.glob[0][pos], o.glob[1][pos]) if full else (o.local[0][pos - base], o.local[1][pos - base])
+    q = om.rotate(z, c, s)
+    return o._attention(layer, q[None], 1, pos)[0].numpy()
+
+
+@pytest.mark.parametrize("layer,pos,context,cap_local", [
+    (0, 4090, 8192, 2064),    # local: window base 2043, the 2064-slot ring wrapped, 32 partitions
+    (3, 2047, 4096, 2064),    # local: the window exactly fills from key 0
+    (7, 5000, 8192, 2064),    # global: 79 partitions (> 64: the attn_merge_kernel order)
+    (15, 32767, 32768, 2064), # global at the context cap: 512 partitions
+])
+def test_exact_attention_tracks_semantic_past_the_window(layer, pos, context, cap_local):
+    # ExactDecoder.attention (the GPU's order-exact twin) against the semantic oracle's
+    # _attention (pinned by closed forms) where the twin's window, ring, RoPE base and
+    # partition-merge logic matter: same BF16 result but for summation-order rounding.
+    ex, o, qn, kn, rng = _attention_pair(context, cap_local, layer + pos)
+    qkv = exact.bf_np(exact.bits_np(rng.standard_normal(2304).astype(np.float32)))
+    got = ex.attention(layer, qkv, pos)
+    want = _semantic_row(ex, o, layer, qkv, pos, qn)
+    ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(want), 1e-30))) - 7)
+    diff = np.abs(got - want)
+    assert np.all(diff <= ulp * 1.001 + 2.0 ** -20), float(diff.max())
+    assert np.mean(diff > 0) < 0.02, float(np.mean(diff > 0))
+    # a dropped key or a wrong window would move far more than an ulp: the same row with the
+    # window shifted by one key disagrees grossly
+    if layer % 8 != 7:
+        o2 = om.Oracle.__new__(om.Oracle)
+        o2.__dict__.update(o.__dict__)
+        shifted = _semantic_row(ex, o2, layer, qkv, pos - 1, qn) if pos > 2047 else None
+        if shifted is not None:
+            assert np.abs(shifted - got).max() > 16 * np.abs(got - want).max()
+
+
+@pytest.mark.parametrize("layer,start,base,cap", [(0, 4090, 2043, 2064), (7, 65, 0, 67)])
+def test_exact_attention_window_mean(layer, start, base, cap):
+    # PlamoTests.swift:156-194 restated on the twin: zero queries score every visible key 0,
+    # so each output is the mean of the visible values (value of position p: p % 17 - 8)
+    ex, o, qn, kn, rng = _attention_pair(cap if layer % 8 == 7 else 8192, cap, 5)
+    for p in range(base, start + 2):
+        ex.values[layer][p % cap] = exact.bits_np(np.float32(p % 17 - 8))
+    for pos in (start, start + 1):
+        qkv = np.zeros(2304, np.float32)
+        qkv[2176:] = np.float32(pos % 17 - 8)
+        got = ex.attention(layer, qkv, pos)
+        begin = 0 if layer % 8 == 7 else pos - 2047
+        want = sum(k % 17 - 8 for k in range(begin, pos + 1)) / (pos - begin + 1)
+        assert np.all(np.abs(got - want) <= 3e-4), (pos, want, got[0])
