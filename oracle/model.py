@@ -119,17 +119,19 @@ def rotate(z, c, s):
 class Oracle:
     """Runtime (Runtime.swift:128-553) on the CPU for one sequence.
 
-    ``dots="fp32"`` (default) takes every dot product of the linear layers in torch's FP32
-    order; ``dots="exact"`` computes them in FP64 and rounds once to FP32 (BF16 x BF16
-    products are exact in FP64 and sums of at most 6144 of them carry ~2^-40 relative error,
-    so each dot is the correctly rounded FP32 value).  The two modes differ only in the
-    rounding of those sums; the difference of their logits is the summation-order noise
-    floor of the model (tests/test_noise_floor.py)."""
+    ``dots="fp32"`` (default) takes every dot product and sum (linear layers, norms,
+    attention scores, softmax denominators, P.V) in torch's FP32 order and exp in torch FP32;
+    ``dots="exact"`` computes each of them in FP64 and rounds once to FP32 (BF16 x BF16
+    products are exact in FP64 and sums of at most 32768 terms carry ~2^-38 relative error,
+    so each is the correctly rounded FP32 value; exp likewise).  The exact mode therefore
+    gives the same bits on every machine, while torch's FP32 order changes with the host's
+    thread count and vector width.  The two modes differ only in those roundings; the
+    difference of their logits is the summation-order noise floor of the model
+    (tests/test_noise_floor.py)."""
 
     def __init__(self, weights, context, local_capacity=None, dots="fp32"):
         assert dots in ("fp32", "exact")
         self.dots = dots
-        self._w64 = {}
         self.w = weights
         self.context = context
         self.batch_limit = min(context, 16)
@@ -153,10 +155,42 @@ class Oracle:
         """x @ w.T with the dot products of the selected mode."""
         if self.dots == "fp32":
             return x @ w.T
+        # FP64 copies are kept on the weights object, shared by every oracle over it
+        cache = self.w.__dict__.setdefault("_w64", {})
         key = id(w)
-        if key not in self._w64:
-            self._w64[key] = (w, w.double())
-        return (x.double() @ self._w64[key][1].T).float()
+        if key not in cache:
+            cache[key] = (w, w.double())
+        return (x.double() @ cache[key][1].T).float()
+
+    # Reductions and exponentials of the selected mode: torch FP32, or FP64 rounded once to
+    # FP32 (sums and exp), which no thread count, vector width or CPU changes.
+    def _sum(self, t):
+        if self.dots == "fp32":
+            return t.sum(-1, keepdim=True)
+        return t.double().sum(-1, keepdim=True).float()
+
+    def _exp(self, t):
+        if self.dots == "fp32":
+            return torch.exp(t)
+        return torch.exp(t.double()).float()
+
+    def _einsum(self, eq, a, b):
+        if self.dots == "fp32":
+            return torch.einsum(eq, a, b)
+        return torch.einsum(eq, a.double(), b.double()).float()
+
+    def _norm(self, x, w_bits, offset):
+        """``norm`` with this mode's sum of squares."""
+        n = x.shape[-1]
+        r = 1.0 / torch.sqrt(self._sum(x * x) / n + torch.tensor(1e-6, dtype=torch.float32))
+        return roundbf_t(roundbf_t(x * r) * gain(w_bits, offset))
+
+    def _softmax_pv(self, s, values):
+        """softmax over the last axis of the scaled, masked scores, then roundbf(P.V)."""
+        m = s.max(-1, keepdim=True).values
+        e = self._exp(s - m)
+        p = e / self._sum(e)
+        return roundbf_t(self._einsum("thk,kd->thd", p, values))
 
     def _attention(self, layer, q_heads, T, p0):
         """Runtime.swift:389-444 for a chunk of T tokens starting at p0."""
@@ -168,17 +202,14 @@ class Oracle:
         keys = bf_t(self.keys[layer][phys])
         if not full:
             keys = rotate(keys, self.local[0][r], self.local[1][r])
-        scores = torch.einsum("thd,kd->thk", q_heads, keys)
+        scores = self._einsum("thd,kd->thk", q_heads, keys)
         end = torch.arange(T) + p0 - base + 1
         begin = torch.zeros(T, dtype=torch.long) if full else torch.clamp(end - WINDOW, min=0)
         kk = torch.arange(count)[None, :]
         visible = (kk >= begin[:, None]) & (kk < end[:, None])
         s = torch.where(visible[:, None, :], scores * torch.tensor(SCALE), torch.tensor(-np.inf))
-        m = s.max(-1, keepdim=True).values
-        e = torch.exp(s - m)
-        p = e / e.sum(-1, keepdim=True)
         values = bf_t(self.values[layer][phys])
-        return roundbf_t(torch.einsum("thk,kd->thd", p, values)).reshape(T, HEADS * HEAD_DIM)
+        return self._softmax_pv(s, values).reshape(T, HEADS * HEAD_DIM)
 
     def forward(self, tokens, output=True):
         """Runtime.forward (Runtime.swift:327-467) for 1..16 tokens."""
@@ -187,14 +218,14 @@ class Oracle:
                 p0 + T > self.context:
             raise ValueError("Invalid tokens or context exhausted")
         x = self.w.embed(tokens)
-        xn = norm(x, self.w.layers[0]["pre"], 1.0)
+        xn = self._norm(x, self.w.layers[0]["pre"], 1.0)
         pos = torch.arange(T) + p0
         for i, L in enumerate(self.w.layers):
             full, cap = is_global(i), self.capacity[i]
             base = 0 if full else max(0, p0 - (WINDOW - 1))
             qkv = roundbf_t(self._mm(xn, L["qkv"]))
             heads = qkv[:, :17 * HEAD_DIM].reshape(T, 17, HEAD_DIM)
-            r = 1.0 / torch.sqrt((heads * heads).sum(-1, keepdim=True) / 128.0 + torch.tensor(1e-6))
+            r = 1.0 / torch.sqrt(self._sum(heads * heads) / 128.0 + torch.tensor(1e-6))
             g = torch.cat([gain(L["q_norm"], 1.0)[None].expand(16, -1), gain(L["k_norm"], 1.0)[None]], 0)
             z = roundbf_t(roundbf_t(heads * r) * g)
             if full:
@@ -207,19 +238,19 @@ class Oracle:
             self.values[i][pos % cap] = bits_t(qkv[:, 17 * HEAD_DIM:])
             att = self._attention(i, q, T, p0)
             o = roundbf_t(self._mm(att, L["o"]))
-            x = roundbf_t(x + norm(o, L["post"], 0.2))
-            xn = norm(x, L["pre_mlp"], 1.0)
+            x = roundbf_t(x + self._norm(o, L["post"], 0.2))
+            xn = self._norm(x, L["pre_mlp"], 1.0)
             gu = roundbf_t(self._mm(xn, L["up"]))
             gate = gu[:, :INTER]
-            act = roundbf_t(roundbf_t(gate / (1.0 + torch.exp(-gate))) * gu[:, INTER:])
+            act = roundbf_t(roundbf_t(gate / (1.0 + self._exp(-gate))) * gu[:, INTER:])
             d = roundbf_t(self._mm(act, L["down"]))
-            x = roundbf_t(x + norm(d, L["post_mlp"], POST_MLP_OFFSET))
+            x = roundbf_t(x + self._norm(d, L["post_mlp"], POST_MLP_OFFSET))
             if i + 1 < LAYERS:
-                xn = norm(x, self.w.layers[i + 1]["pre"], 1.0)
+                xn = self._norm(x, self.w.layers[i + 1]["pre"], 1.0)
         self.position += T
         if not output:
             return -1
-        h = norm(x[-1:], self.w.final, 1.0)
+        h = self._norm(x[-1:], self.w.final, 1.0)
         self.hidden = h[0]
         self.logits_fp32 = self._mm(h, self.w.head)[0]
         self.logit_bits = bits_t(self.logits_fp32)
@@ -250,14 +281,14 @@ class Oracle:
         if p0 + T > max(0, p0 - (WINDOW - 1)) + min(self.capacity):
             raise ValueError("prompt does not fit the ring at once")
         x = self.w.embed(tokens)
-        xn = norm(x, self.w.layers[0]["pre"], 1.0)
+        xn = self._norm(x, self.w.layers[0]["pre"], 1.0)
         pos = torch.arange(T) + p0
         chunk_base = torch.clamp(p0 + (torch.arange(T) // self.batch_limit) * self.batch_limit - (WINDOW - 1), min=0)
         for i, L in enumerate(self.w.layers):
             full, cap = is_global(i), self.capacity[i]
             qkv = roundbf_t(self._mm(xn, L["qkv"]))
             heads = qkv[:, :17 * HEAD_DIM].reshape(T, 17, HEAD_DIM)
-            r = 1.0 / torch.sqrt((heads * heads).sum(-1, keepdim=True) / 128.0 + torch.tensor(1e-6))
+            r = 1.0 / torch.sqrt(self._sum(heads * heads) / 128.0 + torch.tensor(1e-6))
             g = torch.cat([gain(L["q_norm"], 1.0)[None].expand(16, -1), gain(L["k_norm"], 1.0)[None]], 0)
             z = roundbf_t(roundbf_t(heads * r) * g)
             if full:
@@ -274,17 +305,17 @@ class Oracle:
                 rows = torch.arange(T) if full else torch.nonzero(chunk_base == b)[:, 0]
                 att[rows] = self._attend_rows(i, q[rows], pos[rows], b)
             o = roundbf_t(self._mm(att, L["o"]))
-            x = roundbf_t(x + norm(o, L["post"], 0.2))
-            xn = norm(x, L["pre_mlp"], 1.0)
+            x = roundbf_t(x + self._norm(o, L["post"], 0.2))
+            xn = self._norm(x, L["pre_mlp"], 1.0)
             gu = roundbf_t(self._mm(xn, L["up"]))
             gate = gu[:, :INTER]
-            act = roundbf_t(roundbf_t(gate / (1.0 + torch.exp(-gate))) * gu[:, INTER:])
+            act = roundbf_t(roundbf_t(gate / (1.0 + self._exp(-gate))) * gu[:, INTER:])
             d = roundbf_t(self._mm(act, L["down"]))
-            x = roundbf_t(x + norm(d, L["post_mlp"], POST_MLP_OFFSET))
+            x = roundbf_t(x + self._norm(d, L["post_mlp"], POST_MLP_OFFSET))
             if i + 1 < LAYERS:
-                xn = norm(x, self.w.layers[i + 1]["pre"], 1.0)
+                xn = self._norm(x, self.w.layers[i + 1]["pre"], 1.0)
         self.position += T
-        h = norm(x[-1:], self.w.final, 1.0)
+        h = self._norm(x[-1:], self.w.final, 1.0)
         self.hidden = h[0]
         self.logits_fp32 = self._mm(h, self.w.head)[0]
         self.logit_bits = bits_t(self.logits_fp32)
@@ -307,14 +338,11 @@ class Oracle:
         out = torch.empty(q.shape[0], HEADS * HEAD_DIM)
         for s in range(0, q.shape[0], block):
             qq, pp = q[s:s + block], pos[s:s + block]
-            scores = torch.einsum("thd,kd->thk", qq, keys)
+            scores = self._einsum("thd,kd->thk", qq, keys)
             lo = torch.zeros_like(pp) if full else torch.clamp(pp - (WINDOW - 1), min=0)
             visible = (kabs[None, :] >= lo[:, None]) & (kabs[None, :] <= pp[:, None])
             sc = torch.where(visible[:, None, :], scores * torch.tensor(SCALE), torch.tensor(-np.inf))
-            m = sc.max(-1, keepdim=True).values
-            e = torch.exp(sc - m)
-            p = e / e.sum(-1, keepdim=True)
-            out[s:s + block] = roundbf_t(torch.einsum("thk,kd->thd", p, values)).reshape(-1, HEADS * HEAD_DIM)
+            out[s:s + block] = self._softmax_pv(sc, values).reshape(-1, HEADS * HEAD_DIM)
         return out
 
     def logits(self):

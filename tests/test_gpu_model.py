@@ -9,10 +9,19 @@ by the floors recorded in tests/golden/manifest.json (config 1: max-abs 0.0564, 
 config 3: 0.0476, 0.0114), which tests/test_noise_floor.py re-measures.  Such comparisons use
 1.5x that floor and print the north-star figures next to it.
 
-Greedy choices: where the oracle's top two logits are more than one BF16 ulp apart the GPU
-must pick the oracle's token; within one ulp (a near-tie a different summation order may
-legitimately resolve the other way) the choice must be one of the near-tied tokens, and the
-gap is printed.
+The oracle here takes its dot products correctly rounded (``dots="exact"``): torch's FP32
+sums change with the host's thread count and CPU (on the GPU box they moved one sampled
+top-2 gap from 0.0108 to 0.0225), while correctly rounded sums do not, so the reference
+trajectories in the manifest (``exact``) hold on any machine.
+
+Greedy choices: a near-tie is a margin that a different valid summation order can reverse.
+Between the FP32-dot and the exact-dot oracles, teacher-forced along config 1, the gap
+between the best and any of the next seven logits moves by up to 0.052 (about 3 BF16 ulps;
+`pair_gap` in the manifest, re-measured by tests/test_noise_floor.py), so one ulp is below
+what the oracle itself resolves.  Where the oracle's best leads by more than that bound the
+GPU must pick it; within it the GPU's choice must be one of the tokens within the bound, and
+every such choice is printed with its deficit.  (Decode steps are additionally pinned bit
+for bit against the order-exact twin in test_gpu_exact.py, where no tolerance applies.)
 """
 import json
 import os
@@ -32,6 +41,7 @@ NORTH_STAR = (2e-2, 5e-3)          # max-abs, RMSE
 with open(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "manifest.json")) as _f:
     _FLOORS = json.load(_f)["noise_floor"]
 NOISE_FLOOR = tuple(_FLOORS["config1"])   # two summation orders of the same BF16 algorithm
+PAIR_GAP = _FLOORS["pair_gap"]            # how far two valid orders move a choice's margin
 MAX_ABS, RMSE = 1.5 * NOISE_FLOOR[0], 1.5 * NOISE_FLOOR[1]
 
 
@@ -39,14 +49,18 @@ def bf16_ulp(v):
     return float(2.0 ** (np.floor(np.log2(abs(v))) - 7))
 
 
+def near_tie(top):
+    return max(bf16_ulp(top), PAIR_GAP)
+
+
 def check_choice(choice, ref, label):
-    """The GPU's choice is the oracle's best, or within one BF16 ulp of it (a near-tie)."""
+    """The GPU's choice is the oracle's best, or a near-tie of it (within PAIR_GAP)."""
     top = float(ref.max())
     deficit = top - float(ref[choice])
     if deficit > 0:
         print(f"    {label}: near-tie, chose {choice} {deficit:.4f} below the oracle's best "
-              f"{int(np.argmax(ref))} (1 ulp = {bf16_ulp(top):.4f})", flush=True)
-    assert deficit <= bf16_ulp(top), (label, choice, int(np.argmax(ref)), deficit)
+              f"{int(np.argmax(ref))} (bound {near_tie(top):.4f}, 1 ulp {bf16_ulp(top):.4f})", flush=True)
+    assert deficit <= near_tie(top), (label, choice, int(np.argmax(ref)), deficit)
 
 
 def check_logits(gpu_bits, oracle, label, floor=NOISE_FLOOR):
@@ -75,7 +89,7 @@ def test_config1_prefill_then_decode_tracks_oracle(runtimes, oracle_weights, gol
     g = golden["config1"]
     plain, _ = runtimes
     plain.reset()
-    o = om.Oracle(oracle_weights, 96)
+    o = om.Oracle(oracle_weights, 96, dots="exact")
     nxt = plain.prefill(g["prompt"])
     o.prefill(g["prompt"])
     check_logits(plain.logit_bits(), o, "prefill")
@@ -127,7 +141,7 @@ def test_kv_cache_matches_oracle(runtimes, oracle_weights, golden):
     g = golden["config1"]
     plain, _ = runtimes
     plain.reset()
-    o = om.Oracle(oracle_weights, 96, local_capacity=plain.stats()["local_capacity"])
+    o = om.Oracle(oracle_weights, 96, local_capacity=plain.stats()["local_capacity"], dots="exact")
     nxt = plain.prefill(g["prompt"])
     o.prefill(g["prompt"])
     for _ in range(3):
@@ -178,7 +192,7 @@ def test_chunked_forward_matches_oracle(runtimes, oracle_weights, golden):
     plain, _ = runtimes
     p = golden["config1"]["prompt"]
     plain.reset()
-    o = om.Oracle(oracle_weights, 96)
+    o = om.Oracle(oracle_weights, 96, dots="exact")
     for chunk in (p[:5], p[5:21], p[21:22], p[22:30]):
         plain.forward(chunk)
         o.forward(chunk)
@@ -189,7 +203,7 @@ def test_sampling_device_loop_matches_host_loop(runtimes, oracle_weights, golden
     # controls on the device in both loops; bitwise against the restated select in
     # test_gpu_exact.py::test_sampling_controls_bit_exact.  Against the semantic oracle
     # (teacher-forced on the GPU's choices) every controlled choice is the oracle's best or
-    # within one BF16 ulp of it (a near-tie).
+    # a near-tie of it.
     gs = golden["config1_sampling"]
     for rt in runtimes:
         rt.set_sampling(gs["penalty"], gs["frequency"], 0.0, gs["ngram"])
@@ -208,17 +222,31 @@ def test_sampling_device_loop_matches_host_loop(runtimes, oracle_weights, golden
         finally:
             rt.set_sampling()
         assert ids == host
-    o = om.Oracle(oracle_weights, 96)
+    o = om.Oracle(oracle_weights, 96, dots="exact")
     o.prefill(golden["config1"]["prompt"])
     hist = []
     for i, t in enumerate(ids):
-        adj = o.logits().copy()
+        # the adjustments on the oracle's FP32 logits: a near-tie is judged on the values the
+        # BF16 rounding quantises (rounding alone can turn a sub-ulp gap into a 2-ulp one)
+        adj = o.logits_fp32.numpy().astype(np.float32).copy()
         sampler.select(adj, hist, gs["penalty"], gs["ngram"], gs["frequency"])
-        deficit = float(adj.max() - adj[t])
-        assert deficit <= bf16_ulp(float(adj.max())), (i, t, float(adj[t]), float(adj.max()))
+        check_choice(int(t), adj, f"sampled step {i}")
         hist.append(t)
         if i + 1 < len(ids):
             o.forward([t])
+
+
+def check_divergence(name, i, got, g):
+    """The first step where the GPU left the oracle's trajectory must be a near-tie: the
+    GPU's token is among the oracle's eight best there, within the near-tie bound."""
+    top8 = dict((k, v) for k, v in g["top8"][i])
+    best = g["top8"][i][0][1]
+    assert got in top8, (name, i, got, "not among the oracle's eight best")
+    deficit = best - top8[got]
+    print(f"  {name}: ids equal for {i} steps; step {i}: {got} vs oracle {g['top8'][i][0][0]}, "
+          f"{deficit:.4f} below it (top-2 gap {g['top2_gaps'][i]:.4f}, bound {near_tie(best):.4f}, "
+          f"1 ulp {g['top_ulps'][i]:.4f})", flush=True)
+    assert deficit <= near_tie(best), (name, i, deficit)
 
 
 def first_divergence(got, want):
@@ -229,10 +257,10 @@ def first_divergence(got, want):
 
 
 def test_greedy_ids_to_the_first_near_tie(runtimes, golden):
-    # generate() against the oracle's own greedy trajectory (golden greedy_ids): equal up to
+    # generate() against the oracle's own greedy trajectory (golden exact greedy_ids): equal up to
     # the first step whose oracle top-2 gap is under one BF16 ulp; a divergence there is a
     # near-tie resolved the other way (its gap is asserted and printed), anywhere else a bug
-    g = golden["config1"]
+    g = dict(golden["config1"]["exact"], prompt=golden["config1"]["prompt"])
     for rt, name in zip(runtimes, ("plain", ".p12")):
         ids, reason = rt.generate(g["prompt"], 32)
         i = first_divergence(ids, g["greedy_ids"])
@@ -240,15 +268,13 @@ def test_greedy_ids_to_the_first_near_tie(runtimes, golden):
             assert len(ids) == len(g["greedy_ids"])
             print(f"  {name}: all {len(ids)} greedy ids equal the oracle's", flush=True)
             continue
-        gap, ulp = g["top2_gaps"][i], g["top_ulps"][i]
-        print(f"  {name}: ids equal for {i} steps; step {i}: {ids[i]} vs oracle {g['greedy_ids'][i]}, "
-              f"oracle top-2 gap {gap:.4f} < 1 ulp {ulp:.4f}", flush=True)
-        assert gap < ulp, (name, i, gap, ulp)
+        check_divergence(name, i, ids[i], g)
 
 
 def test_sampled_ids_to_the_first_near_tie(runtimes, golden):
     # the same with Sampler.select controls on the device (gaps of the adjusted logits)
-    gs = golden["config1_sampling"]
+    gs = dict(golden["config1_sampling"]["exact"], **{k: golden["config1_sampling"][k]
+                                                      for k in ("penalty", "frequency", "ngram", "max_tokens")})
     for rt, name in zip(runtimes, ("plain", ".p12")):
         rt.set_sampling(gs["penalty"], gs["frequency"], 0.0, gs["ngram"])
         try:
@@ -260,10 +286,7 @@ def test_sampled_ids_to_the_first_near_tie(runtimes, golden):
             assert len(ids) == len(gs["ids"])
             print(f"  {name}: all {len(ids)} sampled ids equal the oracle's", flush=True)
             continue
-        gap, ulp = gs["top2_gaps"][i], gs["top_ulps"][i]
-        print(f"  {name}: sampled ids equal for {i} steps; step {i}: {ids[i]} vs oracle {gs['ids'][i]}, "
-              f"adjusted top-2 gap {gap:.4f} < 1 ulp {ulp:.4f}", flush=True)
-        assert gap < ulp, (name, i, gap, ulp)
+        check_divergence(name, i, ids[i], gs)
 
 
 def test_config3_prefill_2048_matches_oracle(model_dir, oracle_weights, golden):
@@ -283,9 +306,9 @@ def test_config3_prefill_2048_matches_oracle(model_dir, oracle_weights, golden):
     finally:
         rt.close()
     torch.set_num_threads(max(1, min(16, len(os.sched_getaffinity(0)))))
-    o = om.Oracle(oracle_weights, 2048)
+    o = om.Oracle(oracle_weights, 2048, dots="exact")
     want = o.fill(prompt)
-    assert want == g["next"]   # the oracle itself is pinned to the golden vector
+    assert want == g["exact"]["next"]   # the oracle itself is pinned to the golden vector
     mx, rmse = check_logits(bits, o, "config3 prefill", floor)
     check_choice(nxt, o.logits_fp32.numpy().astype(np.float64), "config3 next token")
     print(f"  config3 logits max-abs {mx:.4f} RMSE {rmse:.4f} (floor {floor[0]:.4f}/{floor[1]:.4f}, "

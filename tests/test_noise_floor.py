@@ -6,7 +6,8 @@ the dot products of the linear layers are summed -- torch's FP32 order vs correc
 last-bit differences of its BF16 roundings.  That disagreement is the floor under any
 comparison of an implementation with a different summation order (the MFMA prefill) against
 the FP32 oracle; the north-star tolerance (max-abs 2e-2, RMSE 5e-3) lies below it on this
-random-init model.  The GPU tests use 1.5x the floors recorded in tests/golden/manifest.json;
+random-init model.  The GPU tests use 1.5x the floors recorded in tests/golden/manifest.json,
+and the largest move of a top-8 logit margin between the two orders as their near-tie bound;
 these tests re-measure them, and pin the oracle's whole-prompt `fill` (used for the
 2048-token config) against its 16-token-chunk `prefill`.
 """
@@ -23,16 +24,32 @@ def _floor(w, prompt, context, mode):
         getattr(o, mode)(prompt)
         logits.append(o.logits_fp32.numpy().astype(np.float64))
     e = np.abs(logits[0] - logits[1])
-    return float(e.max()), float(np.sqrt(np.mean(e ** 2))), logits[0]
+    return float(e.max()), float(np.sqrt(np.mean(e ** 2))), logits[0], logits[1]
 
 
 def test_config1_noise_floor(oracle_weights, golden):
-    mx, rmse, _ = _floor(oracle_weights, golden["config1"]["prompt"], 96, "prefill")
+    mx, rmse, _, _ = _floor(oracle_weights, golden["config1"]["prompt"], 96, "prefill")
     want = golden["noise_floor"]["config1"]
     print(f"config 1 prefill: FP32 vs exact dots max-abs {mx:.4f} RMSE {rmse:.4f}")
     assert np.allclose([mx, rmse], want, rtol=0.01), (mx, rmse, want)
     # the floor is far above the north-star tolerance on this model
     assert mx > 2e-2 and rmse > 5e-3
+
+
+def test_config1_pair_gap_noise(oracle_weights, golden):
+    # how far the two summation orders move the margin between the best logit and each of
+    # the next seven, teacher-forced along the exact oracle's greedy trajectory: the
+    # near-tie bound of the GPU choice checks (several BF16 ulps, not one)
+    import importlib.util
+    import os
+    spec = importlib.util.spec_from_file_location(
+        "make_golden", os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "make_golden.py"))
+    mg = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mg)
+    got = mg.pair_gap_noise(oracle_weights, golden["config1"]["prompt"], golden["config1"]["exact"]["greedy_ids"])
+    print(f"config 1 trajectory: top-8 margins move by up to {got:.4f} between the two orders")
+    assert np.isclose(got, golden["noise_floor"]["pair_gap"], rtol=0.01)
+    assert got > 2.0 ** -6   # more than one BF16 ulp at the logits' magnitude (2..4)
 
 
 def test_fill_agrees_with_chunked_prefill(oracle_weights, golden):
@@ -59,10 +76,13 @@ def test_fill_agrees_with_chunked_prefill(oracle_weights, golden):
 def test_config3_noise_floor_and_oracle_vector(oracle_weights, golden):
     g = golden["config3"]
     prompt = np.random.default_rng(g["prompt_seed"]).integers(1024, 107520, g["length"]).tolist()
-    mx, rmse, lg = _floor(oracle_weights, prompt, 2048, "fill")
+    mx, rmse, lg, le = _floor(oracle_weights, prompt, 2048, "fill")
     want = golden["noise_floor"]["config3"]
     print(f"config 3 fill (2048 tokens): FP32 vs exact dots max-abs {mx:.4f} RMSE {rmse:.4f}")
     assert np.allclose([mx, rmse], want, rtol=0.01), (mx, rmse, want)
     top = np.argsort(-lg, kind="stable")[:8]
     assert top.tolist() == g["top8_ids"] and int(top[0]) == g["next"]
     assert np.allclose(lg[top], g["top8_logits"], rtol=0, atol=1e-6)
+    # the exact-dot oracle (the GPU tests' reference) is machine-independent: same bits
+    assert int(np.argmax(le)) == g["exact"]["next"]
+    assert le[g["exact"]["top8_ids"]].astype(np.float32).tolist() == g["exact"]["top8_logits"]
