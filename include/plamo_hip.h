@@ -277,6 +277,20 @@ int plamo_kernel_attention_decode(uint64_t qkv, uint64_t q_norm, uint64_t k_norm
                                   int32_t capacity, const int32_t* positions, int32_t rows, int32_t full,
                                   uint64_t local_rope, uint64_t global_rope, uint64_t out16, uint64_t stream);
 
+/* plamo_kernel_attention_decode without any device allocation.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Same kernels and results;
+ * the step state, tickets and partition buffers live in a static device array of
+ * 4,260,352 bytes per GPU (held until the process ends), which limits every row to 8192
+ * visible keys (global layers: pos < 8192): larger calls fail with PLAMO_EINVAL.  All calls
+ * on one GPU share that array and every call rewrites the state and clears the tickets it
+ * uses, so calls that overlap on one GPU (several streams or threads) race: serialise them.
+ * The caller passes every input and output, as for plamo_kernel_attention_decode. */
+int plamo_kernel_attention_decode_static(uint64_t qkv, uint64_t q_norm, uint64_t k_norm, uint64_t keys,
+                                         uint64_t values, int32_t capacity, const int32_t* positions, int32_t rows,
+                                         int32_t full, uint64_t local_rope, uint64_t global_rope, uint64_t out16,
+                                         uint64_t stream, char* err, size_t errlen);
+
 /* The host RoPE table builder the runtime uploads (`init_rope`, Kernels.metal:212-219; global
  * factors of `rotated`, Kernels.metal:264-267): `rows` x 64 entries of BF16 cos | sin << 16
  * from 64 inverse frequencies (config-mlx.json plamo_rope_inv_freq, Runtime.swift:268-274).

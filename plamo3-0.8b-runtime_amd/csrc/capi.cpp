@@ -603,10 +603,6 @@ struct AttnWorkspace {
 std::mutex g_attn_ws_mu;
 std::map<int, AttnWorkspace> g_attn_ws;
 
-size_t attn_workspace_bytes(uint32_t parts) {
-    const size_t stats = size_t(plamo::ROWS) * parts * plamo::HEADS;
-    return 256 + 256 + 2 * stats * 4 + stats * plamo::HEAD_DIM * 4;
-}
 
 // Carves a workspace at `base` (256-byte aligned) into the attention parameter pointers.
 void attn_workspace_bind(void* base, uint32_t parts, plamo::AttnParams& a, plamo::StepState*& st) {
@@ -630,13 +626,12 @@ void* attn_workspace(uint32_t parts) {
             (void)hipFree(w.base);
             w = AttnWorkspace{};
         }
-        PLAMO_HIP(hipMalloc(&w.base, attn_workspace_bytes(parts)));
+        PLAMO_HIP(hipMalloc(&w.base, plamo::attn_workspace_bytes(parts)));
         w.parts = parts;
     }
     return w.base;
 }
 
-static_assert(sizeof(plamo::StepState) <= 256, "step state fits its workspace slot");
 
 // Validates a kernel-level decode attention call and fills every parameter except the
 // workspace pointers; returns the partition count (grid width).
@@ -691,6 +686,25 @@ int plamo_kernel_attention_decode(uint64_t qkv, uint64_t q_norm, uint64_t k_norm
                                                   local_rope, global_rope, out16, a);
         plamo::StepState* st = nullptr;
         attn_workspace_bind(attn_workspace(parts), parts, a, st);
+        attn_decode_launch(a, st, positions, rows, full != 0, reinterpret_cast<hipStream_t>(stream));
+        PLAMO_HIP(hipGetLastError());
+    });
+}
+
+int plamo_kernel_attention_decode_static(uint64_t qkv, uint64_t q_norm, uint64_t k_norm, uint64_t keys,
+                                         uint64_t values, int32_t capacity, const int32_t* positions, int32_t rows,
+                                         int32_t full, uint64_t local_rope, uint64_t global_rope, uint64_t out16,
+                                         uint64_t stream, char* err, size_t errlen) {
+    return guard(err, errlen, [&] {
+        plamo::AttnParams a{};
+        const uint32_t parts = attn_decode_params(qkv, q_norm, k_norm, keys, values, capacity, positions, rows, full,
+                                                  local_rope, global_rope, out16, a);
+        if (parts > plamo::STATIC_ATTN_PARTS)
+            throw plamo::Error(plamo::E_INVAL, "attention exceeds the static scratch: at most " +
+                                                   std::to_string(plamo::STATIC_ATTN_PARTS * plamo::KEYS_PER_PART) +
+                                                   " visible keys per row");
+        plamo::StepState* st = nullptr;
+        attn_workspace_bind(plamo::static_attn_scratch(), parts, a, st);
         attn_decode_launch(a, st, positions, rows, full != 0, reinterpret_cast<hipStream_t>(stream));
         PLAMO_HIP(hipGetLastError());
     });

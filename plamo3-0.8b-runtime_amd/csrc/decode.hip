@@ -15,6 +15,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 
 #include "common.h"
@@ -1436,6 +1437,32 @@ __global__ void unpack_kernel(const uint8_t* payload, const uint32_t* table, uin
     const uint32_t code = (blk[128 + k / 2] >> ((k % 2) * 4)) & 15u;
     out[i] = uint16_t(p12_word(blk[k], code, tag + 107u));
 }
+
+// Scratch of the allocation-free decode attention entry point: a file-scope device array, one
+// copy per GPU, held until the process ends.  Host code uses the address hipGetSymbolAddress
+// returns for the current device (the array's name is not a device address on the host).
+static __device__ __align__(256) uint8_t scratch[attn_workspace_bytes(STATIC_ATTN_PARTS)];
+static_assert(sizeof(StepState) <= 256, "step state fits its workspace slot");
+
+}  // namespace
+
+void* static_attn_scratch() {
+    constexpr int MAX_DEVICES = 64;
+    static std::mutex mu;
+    static void* ptr[MAX_DEVICES] = {};
+    int dev = 0;
+    PLAMO_HIP(hipGetDevice(&dev));
+    if (dev < 0 || dev >= MAX_DEVICES) throw Error(E_DEVICE, "device index out of range");
+    std::lock_guard<std::mutex> lk(mu);
+    if (!ptr[dev]) {
+        void* p = nullptr;
+        PLAMO_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        ptr[dev] = p;
+    }
+    return ptr[dev];
+}
+
+namespace {
 
 struct AttnStateArgs {
     int32_t pos[ROWS];

@@ -125,6 +125,19 @@ void launch_select(float* logits, int n, const int32_t* history, int hist, float
                    float presence, int32_t* out, hipStream_t s);
 void launch_unpack(const uint8_t* payload, const uint32_t* table, uint16_t* out, int64_t count, hipStream_t s);
 void launch_fill_u32(uint32_t* p, uint32_t value, size_t count, hipStream_t s);
+// Device workspace of a kernel-level decode attention call, 256-byte aligned: the step state
+// (256 B), the attention tickets [ROWS][4 head groups] (256 B), then the partition
+// statistics m, l [ROWS][parts][16] and outputs [ROWS][parts][16][128] (FP32), the layout the
+// runtime's engine uses.
+constexpr size_t attn_workspace_bytes(uint32_t parts) {
+    return 512 + size_t(ROWS) * parts * 16 * (2 + 128) * 4;
+}
+// Partitions (64 keys each) the allocation-free entry point's static scratch holds: 8192 keys.
+constexpr uint32_t STATIC_ATTN_PARTS = 128;
+// Device address of this device's static scratch (attn_workspace_bytes(STATIC_ATTN_PARTS)
+// bytes), looked up once per device; every call on a device shares it.
+void* static_attn_scratch();
+
 // Step state of a kernel-level decode attention call: `rows` rows at `pos` (row q reads and
 // writes KV slice q), every other field zero; clears the rows' attention tickets.  Written by
 // a kernel from its arguments, so the call needs no host copy.

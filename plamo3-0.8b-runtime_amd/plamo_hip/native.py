@@ -103,6 +103,9 @@ _SIGNATURES = {
     "plamo_kernel_attention_decode": (ctypes.c_int, [ctypes.c_uint64] * 5 + [ctypes.c_int32, c_i32p,
                                                                            ctypes.c_int32, ctypes.c_int32] +
                                       [ctypes.c_uint64] * 4),
+    "plamo_kernel_attention_decode_static": (ctypes.c_int, [ctypes.c_uint64] * 5 +
+                                             [ctypes.c_int32, c_i32p, ctypes.c_int32, ctypes.c_int32] +
+                                             [ctypes.c_uint64] * 4 + [ctypes.c_char_p, ctypes.c_size_t]),
     "plamo_rope_table": (ctypes.c_int, [ctypes.POINTER(ctypes.c_double), ctypes.c_int32, ctypes.c_int32,
                                         ctypes.c_void_p, ctypes.c_char_p, ctypes.c_size_t]),
     "plamo_version": (ctypes.c_char_p, []),
