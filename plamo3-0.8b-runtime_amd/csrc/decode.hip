@@ -698,10 +698,13 @@ __device__ __forceinline__ void state_out(StepState* st, const StepState& ls) {
         reinterpret_cast<uint32_t*>(st)[threadIdx.x] = reinterpret_cast<const uint32_t*>(&ls)[threadIdx.x];
 }
 
-__global__ __launch_bounds__(256) void head_merge_kernel(DecodeBuffers b, int blocks) {
+__device__ void begin_step(StepState& ls, const DecodeBuffers& b, int* s_stop);
+
+__global__ __launch_bounds__(256) void head_merge_kernel(DecodeBuffers b, int blocks, int begin_next) {
     __shared__ float cv[ROWS * 4];
     __shared__ uint32_t ci[ROWS * 4];
     __shared__ StepState ls;
+    __shared__ int s_stop;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar)
     // every row's partials requested together with the state (rows past the step's are not used)
@@ -752,6 +755,8 @@ __global__ __launch_bounds__(256) void head_merge_kernel(DecodeBuffers b, int bl
         }
     }
     __syncthreads();
+    // device loops: the next step's bookkeeping (emit, stop, lane pass, sampler history)
+    if (begin_next && (ls.loop || ls.quad) && !ls.stopped) begin_step(ls, b, &s_stop);
     state_out(b.state, ls);
 }
 
@@ -1254,16 +1259,15 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const AttnParams p) {
 
 // ------------------------------------------------------------------------- step begin
 // Device side of the token loop (Main.swift:278-287) and of the sampler history
-// (Main.swift:237-244; Sampler.swift:11-24,54-70).
-__global__ __launch_bounds__(256) void step_begin_kernel(DecodeBuffers b) {
-    __shared__ StepState ls;
-    __shared__ int s_stop;
-    state_in(ls, b.state);
-    __syncthreads();
-    if (ls.stopped) return;
+// (Main.swift:237-244; Sampler.swift:11-24,54-70), on the state copy `ls` in LDS; every
+// thread of the 256-thread workgroup calls it.  A device loop runs it before each step's
+// layers: once before the first replay (step_begin_kernel) and then at the end of every
+// step, after the head merge fed the prediction back (head_merge_kernel), so the replayed
+// loop graph has no separate bookkeeping kernel.
+__device__ void begin_step(StepState& ls, const DecodeBuffers& b, int* s_stop) {
     const int tid = threadIdx.x;
     if (tid == 0) {
-        s_stop = 0;
+        *s_stop = 0;
         if (ls.quad) {
             // decodeBatch's lane pass (BatchDecode.swift:16-31): a lane stops at its limit or
             // on token 1 / 16, otherwise emits its prediction and, below the limit, feeds it
@@ -1294,13 +1298,13 @@ __global__ __launch_bounds__(256) void step_begin_kernel(DecodeBuffers b) {
             }
             ls.last = last;
             ls.rows = rows;
-            if (!rows) { ls.stopped = 1; s_stop = 1; }
+            if (!rows) { ls.stopped = 1; *s_stop = 1; }
         } else if (ls.loop) {
             const int32_t tok = ls.token[0];
             if (ls.stop_enabled && (tok == 1 || tok == 16)) {
-                ls.stopped = 1; ls.reason = 1; s_stop = 1;
+                ls.stopped = 1; ls.reason = 1; *s_stop = 1;
             } else if (tok < 0 || tok >= VOCAB) {
-                ls.stopped = 1; ls.reason = 3; s_stop = 1;
+                ls.stopped = 1; ls.reason = 3; *s_stop = 1;
             } else {
                 b.out_ids[ls.produced] = tok;
                 ls.produced += 1;
@@ -1308,12 +1312,12 @@ __global__ __launch_bounds__(256) void step_begin_kernel(DecodeBuffers b) {
                     b.history[ls.hist_len[0]] = tok;
                     ls.hist_len[0] += 1;
                 }
-                if (ls.produced >= ls.max_tokens) { ls.stopped = 1; ls.reason = 2; s_stop = 1; }
+                if (ls.produced >= ls.max_tokens) { ls.stopped = 1; ls.reason = 2; *s_stop = 1; }
             }
         }
     }
     __syncthreads();
-    if (!s_stop && ls.sampling) {
+    if (!*s_stop && ls.sampling) {
         for (uint32_t q = 0; q < ls.rows; ++q) {
             const int32_t* hist = b.history + size_t(q) * b.hist_cap;
             const uint32_t len = ls.hist_len[q];
@@ -1345,6 +1349,15 @@ __global__ __launch_bounds__(256) void step_begin_kernel(DecodeBuffers b) {
         }
     }
     __syncthreads();
+}
+
+__global__ __launch_bounds__(256) void step_begin_kernel(DecodeBuffers b) {
+    __shared__ StepState ls;
+    __shared__ int s_stop;
+    state_in(ls, b.state);
+    __syncthreads();
+    if (ls.stopped) return;
+    begin_step(ls, b, &s_stop);
     state_out(b.state, ls);
 }
 
@@ -1570,8 +1583,8 @@ void launch_attention_merge(const AttnParams& p, int rows, hipStream_t s) {
     hipLaunchKernelGGL(attn_merge_kernel, dim3(HEAD_DIM / 32, HEADS, rows), dim3(256), 0, s, p);
 }
 
-void launch_head_merge(const DecodeBuffers& b, int blocks, hipStream_t s) {
-    hipLaunchKernelGGL(head_merge_kernel, dim3(1), dim3(256), 0, s, b, blocks);
+void launch_head_merge(const DecodeBuffers& b, int blocks, bool begin_next, hipStream_t s) {
+    hipLaunchKernelGGL(head_merge_kernel, dim3(1), dim3(256), 0, s, b, blocks, begin_next ? 1 : 0);
 }
 
 void launch_step_begin(const DecodeBuffers& b, hipStream_t s) {

@@ -119,7 +119,8 @@ void launch_gemv(int n, bool packed, int maxr, Prologue pro, Epilogue epi, const
 void launch_attention(bool full, const AttnParams& p, int rows, hipStream_t s);
 void launch_attention_merge(const AttnParams& p, int rows, hipStream_t s);  // global layers
 void launch_step_begin(const DecodeBuffers& b, hipStream_t s);
-void launch_head_merge(const DecodeBuffers& b, int blocks, hipStream_t s);
+// begin_next: device loops run the next step's bookkeeping (step_begin) in the same kernel
+void launch_head_merge(const DecodeBuffers& b, int blocks, bool begin_next, hipStream_t s);
 void launch_argmax(const void* x, uint32_t* out, int n, int rows, bool bf16, hipStream_t s);
 void launch_select(float* logits, int n, const int32_t* history, int hist, float penalty, int ngram, float frequency,
                    float presence, int32_t* out, hipStream_t s);

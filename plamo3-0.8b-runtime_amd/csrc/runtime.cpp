@@ -286,6 +286,7 @@ Engine::Engine(std::shared_ptr<Model> mdl, int ctx, int nl, hipStream_t s)
 
 Engine::~Engine() {
     if (graph) (void)hipGraphExecDestroy(graph);
+    if (graph_loop) (void)hipGraphExecDestroy(graph_loop);
     if (graph16) (void)hipGraphExecDestroy(graph16);
 
     (void)hipEventDestroy(ev0);
@@ -316,10 +317,10 @@ void Engine::enqueue_head(const uint16_t* in, const uint16_t* resid_in, int in_r
     g.out16 = logits;
     g.bufs = bufs;
     launch_gemv(HIDDEN, m.packed, maxr, PRO_RESID16, EPI_LOGITS, g, head_blocks(maxr), stream);
-    launch_head_merge(bufs, head_blocks(maxr), stream);
+    launch_head_merge(bufs, head_blocks(maxr), false, stream);
 }
 
-void Engine::enqueue_head16() {
+void Engine::enqueue_head16(bool loop) {
     const Model& m = *model;
     const int maxr = lanes == 1 ? 1 : ROWS;
     GemvParams g{};
@@ -338,15 +339,17 @@ void Engine::enqueue_head16() {
     g.out16 = logits;
     g.bufs = bufs;
     launch_gemv(HIDDEN, m.packed, maxr, PRO_RESID16, EPI_LOGITS, g, head_blocks(maxr), stream);
-    launch_head_merge(bufs, head_blocks(maxr), stream);
+    launch_head_merge(bufs, head_blocks(maxr), loop, stream);
 }
 
-// One decode step (Runtime.swift:376-458 for one token per row; Batch.swift:147-165).
-void Engine::enqueue_step(bool head) {
+// One decode step (Runtime.swift:376-458 for one token per row; Batch.swift:147-165).  A host
+// step starts with the bookkeeping kernel; a device-loop step finds its bookkeeping done by the
+// previous step's head merge (or by begin_loop before the first replay).
+void Engine::enqueue_step(bool head, bool loop) {
     const Model& m = *model;
     const bool pk = m.packed;
     const int maxr = lanes == 1 ? 1 : ROWS;
-    launch_step_begin(bufs, stream);
+    if (!loop) launch_step_begin(bufs, stream);
     for (int l = 0; l < LAYERS; ++l) {
         const LayerWeights& L = m.layers[l];
         const bool full = is_global_layer(l);
@@ -423,7 +426,7 @@ void Engine::enqueue_step(bool head) {
         d.out16 = proj;
         launch_gemv(INTER, pk, maxr, PRO_PLAIN16, EPI_BF16, d, gemv_blocks(INTER, maxr, EPI_BF16, HIDDEN), stream);
     }
-    if (head) enqueue_head16();
+    if (head) enqueue_head16(loop);
 }
 
 void Engine::run_step() {
@@ -448,29 +451,38 @@ void Engine::run_step() {
     PLAMO_HIP(hipGraphLaunch(graph, stream));
 }
 
-// Captures (without running) the graph of LOOP_GRAPH_STEPS consecutive steps.
-void Engine::prepare_loop_graph() {
-    if (!use_graph || graph16) return;
+// Captures (without running) `steps` consecutive device-loop steps into `out`.
+void Engine::capture_loop(int steps, hipGraphExec_t* out) {
     hipGraph_t g = nullptr;
     PLAMO_HIP(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal));
     try {
-        for (int k = 0; k < LOOP_GRAPH_STEPS; ++k) enqueue_step();
+        for (int k = 0; k < steps; ++k) enqueue_step(true, true);
     } catch (...) {
         (void)hipStreamEndCapture(stream, &g);
         if (g) (void)hipGraphDestroy(g);
         throw;
     }
     PLAMO_HIP(hipStreamEndCapture(stream, &g));
-    PLAMO_HIP(hipGraphInstantiate(&graph16, g, nullptr, nullptr, 0));
+    PLAMO_HIP(hipGraphInstantiate(out, g, nullptr, nullptr, 0));
     PLAMO_HIP(hipGraphDestroy(g));
 }
 
+void Engine::prepare_loop_graph() {
+    if (!use_graph) return;
+    if (!graph_loop) capture_loop(1, &graph_loop);
+    if (!graph16) capture_loop(LOOP_GRAPH_STEPS, &graph16);
+}
+
+void Engine::begin_loop() { launch_step_begin(bufs, stream); }
+
 void Engine::run_steps(int n) {
-    if (use_graph && n >= LOOP_GRAPH_STEPS) {
-        prepare_loop_graph();
-        for (; n >= LOOP_GRAPH_STEPS; n -= LOOP_GRAPH_STEPS) PLAMO_HIP(hipGraphLaunch(graph16, stream));
+    if (!use_graph) {
+        for (; n > 0; --n) enqueue_step(true, true);
+        return;
     }
-    for (; n > 0; --n) run_step();
+    prepare_loop_graph();
+    for (; n >= LOOP_GRAPH_STEPS; n -= LOOP_GRAPH_STEPS) PLAMO_HIP(hipGraphLaunch(graph16, stream));
+    for (; n > 0; --n) PLAMO_HIP(hipGraphLaunch(graph_loop, stream));
 }
 
 // A prefill chunk of n tokens at p0 for one lane: every layer as MFMA GEMMs, K/V written
@@ -808,6 +820,7 @@ BatchImpl::Decoded BatchImpl::decode(const std::vector<int32_t>& first, const st
     // every step with running lanes emits a token on each of them, so the lane pass stops
     // the loop after at most max(limit) + 1 steps
     int launched = 0;
+    e.begin_loop();
     while (true) {
         e.run_steps(16);
         launched += 16;
@@ -876,6 +889,7 @@ std::vector<int32_t> RuntimeImpl::generate(const int32_t* prompt, int n, int max
     sync_sampler(e, 0);
     PLAMO_HIP(hipMemcpyAsync(e.state, &hs, sizeof(StepState), hipMemcpyHostToDevice, stream));
     begin_timing();
+    e.begin_loop();
     int launched = 0;
     while (launched < max_tokens) {
         const int batch = std::min(16, max_tokens - launched);
@@ -919,8 +933,9 @@ double RuntimeImpl::bench_decode(int steps) {
     hs.stopped = 0;
     sync_sampler(e, 0);
     PLAMO_HIP(hipMemcpyAsync(e.state, &hs, sizeof(StepState), hipMemcpyHostToDevice, stream));
-    e.run_step();            // capture outside the timed region
-    e.prepare_loop_graph();  // (captured, not run)
+    e.prepare_loop_graph();  // captured outside the timed region (not run)
+    e.begin_loop();
+    e.run_steps(1);
     PLAMO_HIP(hipStreamSynchronize(stream));
     PLAMO_HIP(hipEventRecord(e.ev0, stream));
     e.run_steps(steps - 1);

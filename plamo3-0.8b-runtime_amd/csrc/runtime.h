@@ -85,17 +85,21 @@ class Engine {
     int32_t* p_tokens;
     size_t part_rows_cap;    // rows x parts the partial buffers hold
     // graph
-    hipGraphExec_t graph = nullptr;
-    hipGraphExec_t graph16 = nullptr;  // LOOP_GRAPH_STEPS consecutive steps
+    hipGraphExec_t graph = nullptr;       // one host step (bookkeeping kernel first)
+    hipGraphExec_t graph_loop = nullptr;  // one device-loop step (bookkeeping in its head merge)
+    hipGraphExec_t graph16 = nullptr;     // LOOP_GRAPH_STEPS consecutive device-loop steps
     bool use_graph = true;
 
     hipEvent_t ev0, ev1;
 
-    void enqueue_step(bool head = true);    // one decode step for state->rows rows
-    void run_step();                        // graph replay (or direct launches)
-    // n device-loop steps: replays of a LOOP_GRAPH_STEPS-step graph, then single steps (one
-    // graph launch per 16 steps instead of per step)
+    // one decode step for state->rows rows; `loop`: a device-loop step (no bookkeeping kernel,
+    // the head merge prepares the next step)
+    void enqueue_step(bool head = true, bool loop = false);
+    void run_step();                        // host step: graph replay (or direct launches)
+    // Device loops: begin_loop once (the first step's bookkeeping), then n steps as replays of
+    // a LOOP_GRAPH_STEPS-step graph and single-step graphs (one launch per 16 steps)
     static constexpr int LOOP_GRAPH_STEPS = 16;
+    void begin_loop();
     void run_steps(int n);
     void prepare_loop_graph();
     // prefill of `n` tokens of one lane at position p0 (n > 1); head on the last token.
@@ -105,7 +109,8 @@ class Engine {
   private:
     void enqueue_prefill_chunk(int n, int p0, int lane, bool last_chunk, bool output);
     void enqueue_head(const uint16_t* in, const uint16_t* resid_in, int in_rows);  // prefill rows
-    void enqueue_head16();                                                    // decode: BF16 stream
+    void enqueue_head16(bool loop);                                           // decode: BF16 stream
+    void capture_loop(int steps, hipGraphExec_t* out);
 };
 
 // RoPE table of `rows` positions, one uint32 per (position, pair): BF16 cos | sin << 16.
