@@ -343,42 +343,58 @@ __device__ __forceinline__ uint4 stream_load16(const void* p) {
 __device__ __forceinline__ uint32_t stream_load4(const void* p) {
     return __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p));
 }
+__device__ __forceinline__ uint2 stream_load8(const void* p) {
+    typedef uint32_t v2 __attribute__((ext_vector_type(2)));
+    const v2 v = __builtin_nontemporal_load(reinterpret_cast<const v2*>(p));
+    return make_uint2(v[0], v[1]);
+}
 template <>
 struct WRaw<true> {
-    uint4 v;            // raw: 8 weights; packed: .x/.y = 8 sign/mantissa bytes
-    uint32_t nib, tag;  // packed: 8 exponent codes, block minimum - 107 (0: raw block)
+    uint2 a;       // raw: weights 0..3; packed: the 8 sign/mantissa bytes
+    uint2 b;       // raw: weights 4..7; packed: the exponent codes of this lane and its pair
+    uint32_t tag;  // block minimum - 107 (0: raw block)
 };
 
-// Requests for U rows x IT column steps: every .p12 table entry first, then the payload.
-template <int N, bool PACKED, int U, int IT>
-__device__ __forceinline__ void request_w(const GemvParams& p, const int (&wrow)[U], int lane,
-                                          WRaw<PACKED> (&r)[U][IT]) {
-    if constexpr (!PACKED) {
+// Plain weight requests for U rows x IT column steps.
+template <int N, int U, int IT>
+__device__ __forceinline__ void request_plain(const GemvParams& p, const int (&wrow)[U], int lane,
+                                              WRaw<false> (&r)[U][IT]) {
 #pragma unroll
-        for (int u = 0; u < U; ++u)
+    for (int u = 0; u < U; ++u)
 #pragma unroll
-            for (int it = 0; it < IT; ++it)
-                r[u][it].v = stream_load16(p.w + size_t(wrow[u]) * N + it * 512 + lane * 8);
-    } else {
-        uint32_t e[U][IT];
+        for (int it = 0; it < IT; ++it)
+            r[u][it].v = stream_load16(p.w + size_t(wrow[u]) * N + it * 512 + lane * 8);
+}
+
+// .p12 requests come in two halves: the block-table entries of U rows x IT column steps,
+// then (once they arrived) the payload at the offsets they hold.  The kernel issues the
+// table half one group ahead, so only a wave's first group waits for two round trips.
+template <int N, int U, int IT>
+__device__ __forceinline__ void request_table(const GemvParams& p, const int (&wrow)[U], int lane,
+                                              uint32_t (&e)[U][IT]) {
 #pragma unroll
-        for (int u = 0; u < U; ++u)
+    for (int u = 0; u < U; ++u)
 #pragma unroll
-            for (int it = 0; it < IT; ++it) e[u][it] = p.table[size_t(wrow[u]) * (N / 128) + it * 4 + (lane >> 4)];
-        const int sub = lane & 15;
+        for (int it = 0; it < IT; ++it) e[u][it] = p.table[size_t(wrow[u]) * (N / 128) + it * 4 + (lane >> 4)];
+}
+
+template <int U, int IT>
+__device__ __forceinline__ void request_payload(const GemvParams& p, const uint32_t (&e)[U][IT], int lane,
+                                                WRaw<true> (&r)[U][IT]) {
+    const int sub = lane & 15;
 #pragma unroll
-        for (int u = 0; u < U; ++u)
+    for (int u = 0; u < U; ++u)
 #pragma unroll
-            for (int it = 0; it < IT; ++it) {
-                const uint8_t* blk = reinterpret_cast<const uint8_t*>(p.w) + (e[u][it] & ~63u);
-                const uint32_t tag = e[u][it] & 63u;
-                // one 16-byte load: a raw block's 8 weights, or (packed) this lane's 8
-                // sign/mantissa bytes in .x/.y (the rest is the next lane's, unused)
-                r[u][it].v = stream_load16(blk + (tag ? sub * 8 : sub * 16));
-                r[u][it].nib = stream_load4(blk + 128 + sub * 4);
-                r[u][it].tag = tag;
-            }
-    }
+        for (int it = 0; it < IT; ++it) {
+            const uint8_t* blk = reinterpret_cast<const uint8_t*>(p.w) + (e[u][it] & ~63u);
+            const uint32_t tag = e[u][it] & 63u;
+            // two naturally aligned 8-byte loads, branch-free: a raw block's 16 bytes, or
+            // (packed) this lane's 8 sign/mantissa bytes and the 8 exponent-code bytes of its
+            // lane pair (the two lanes of a pair read the same word)
+            r[u][it].a = stream_load8(blk + (tag ? sub * 8 : sub * 16));
+            r[u][it].b = stream_load8(blk + (tag ? 128 + (sub & ~1) * 4 : sub * 16 + 8));
+            r[u][it].tag = tag;
+        }
 }
 
 // Lane `lane` owns columns it*512 + lane*8 .. +8 of a row: inside .p12 block it*4+lane/16
@@ -387,7 +403,11 @@ __device__ __forceinline__ void request_w(const GemvParams& p, const int (&wrow)
 template <bool PACKED>
 __device__ __forceinline__ uint4 decode_w(const WRaw<PACKED>& r) {
     if constexpr (!PACKED) return r.v;
-    else return r.tag ? p12_decode8(make_uint2(r.v.x, r.v.y), r.nib, r.tag) : r.v;
+    else {
+        if (!r.tag) return make_uint4(r.a.x, r.a.y, r.b.x, r.b.y);
+        const uint32_t nib = (threadIdx.x & 1u) ? r.b.y : r.b.x;  // lane parity = sub parity
+        return p12_decode8(r.a, nib, r.tag);
+    }
 }
 
 __device__ __forceinline__ bool better(float v, uint32_t i, float bv, uint32_t bi) {
@@ -455,19 +475,6 @@ __global__ __launch_bounds__(64 * gemv_waves(N, MAXR, EPI)) void gemv_kernel(con
     // the same words): that makes it a vector load, first in the in-order vector-memory
     // queue, instead of a scalar load whose wait would also cover the kernel arguments the
     // weight addresses need.
-    uint32_t stopped = 0, srows = 0;
-    if constexpr (STATE) {
-        const StepState* sv = st + (threadIdx.x & p.lane_mask);
-        stopped = sv->stopped;
-        srows = sv->rows;
-    }
-    Staged<N, RQ, PRO> S;
-    stage_load<N, RQ, PRO>(p, p.rows < MAXR ? p.rows : MAXR, q0, S);
-    float best_v[MAXR];
-    uint32_t best_i[MAXR];
-#pragma unroll
-    for (int q = 0; q < MAXR; ++q) { best_v[q] = NEG_INF; best_i[q] = 0xffffffffu; }
-
     auto rows_of = [&](int g, int (&wrow)[U]) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
@@ -492,13 +499,46 @@ __global__ __launch_bounds__(64 * gemv_waves(N, MAXR, EPI)) void gemv_kernel(con
         stride = int(gridDim.x) * NWV;
         g = int(blockIdx.x) * NWV + wave;
     }
-    WRaw<PACKED> wr[U][IT];
-    {
-        // unconditional (a wave without a group re-reads the last one) so the compiler
-        // can count the requests in flight exactly
+    // .p12: the first group's block-table entries go out before anything else, so their
+    // round trip overlaps the state and prologue loads (unconditional: a wave without a
+    // group re-reads the last one, and the compiler counts the requests in flight exactly)
+    uint32_t tab[PACKED ? U : 1][PACKED ? IT : 1];
+    if constexpr (PACKED) {
         int wrow[U];
-        rows_of(g < groups ? g : groups - 1, wrow);  // (past its run: any valid rows)
-        request_w<N, PACKED, U, IT>(p, wrow, lane, wr);
+        rows_of(g < groups ? g : groups - 1, wrow);
+        request_table<N, U, IT>(p, wrow, lane, tab);
+    }
+    uint32_t stopped = 0, srows = 0;
+    if constexpr (STATE) {
+        const StepState* sv = st + (threadIdx.x & p.lane_mask);
+        stopped = sv->stopped;
+        srows = sv->rows;
+    }
+    Staged<N, RQ, PRO> S;
+    stage_load<N, RQ, PRO>(p, p.rows < MAXR ? p.rows : MAXR, q0, S);
+    float best_v[MAXR];
+    uint32_t best_i[MAXR];
+#pragma unroll
+    for (int q = 0; q < MAXR; ++q) { best_v[q] = NEG_INF; best_i[q] = 0xffffffffu; }
+
+    // Waves of the LM head and of the four-row kernels walk several groups: their next
+    // group's table words are requested one group ahead.  The other launches give every wave
+    // one group (gemv_blocks), and keep no table registers live past the first payload.
+    constexpr bool PIPE_TABLE = MAXR > 1 || EPI == EPI_LOGITS;
+    WRaw<PACKED> wr[U][IT];
+    if constexpr (PACKED) {
+        // the payload as soon as the table arrived (the prologue loads issued after the table
+        // may still be in flight), then the next group's table
+        request_payload<U, IT>(p, tab, lane, wr);
+        if (PIPE_TABLE && g + stride < gend) {
+            int wrow[U];
+            rows_of(g + stride, wrow);
+            request_table<N, U, IT>(p, wrow, lane, tab);
+        }
+    } else {
+        int wrow[U];
+        rows_of(g < groups ? g : groups - 1, wrow);
+        request_plain<N, U, IT>(p, wrow, lane, wr);
     }
     // A stopped device loop runs the kernel with no rows (an early return here would let
     // the compiler sink every request above below a wait for the state).
@@ -621,7 +661,7 @@ __global__ __launch_bounds__(64 * gemv_waves(N, MAXR, EPI)) void gemv_kernel(con
             int nrow[U];
             if (g1 < gend) {
                 rows_of(g1, nrow);
-                request_w<N, PACKED, U, IT>(p, nrow, lane, wb);
+                request_plain<N, U, IT>(p, nrow, lane, wb);
             }
             uint4 w[U][IT];
             decode_all(wr, w);
@@ -629,22 +669,31 @@ __global__ __launch_bounds__(64 * gemv_waves(N, MAXR, EPI)) void gemv_kernel(con
             if (g1 >= gend) break;
             if (g2 < gend) {
                 rows_of(g2, nrow);
-                request_w<N, PACKED, U, IT>(p, nrow, lane, wr);
+                request_plain<N, U, IT>(p, nrow, lane, wr);
             }
             decode_all(wb, w);
             group(g1, w);
         }
     } else {
-        // .p12: decode, then request the next group into the same buffer (fewer registers
-        // than two buffers of payload, table words and tags)
+        // .p12: decode, then request the next group's payload into the same buffer (fewer
+        // registers than two buffers of payload, table words and tags) from the table words
+        // requested one group earlier, and the table of the group after it
         for (; g < gend; g += stride) {
             uint4 w[U][IT];
             decode_all(wr, w);
             const int gn = g + stride;
             if (gn < gend) {
-                int nrow[U];
-                rows_of(gn, nrow);
-                request_w<N, PACKED, U, IT>(p, nrow, lane, wr);
+                if constexpr (!PIPE_TABLE) {
+                    int nrow[U];
+                    rows_of(gn, nrow);
+                    request_table<N, U, IT>(p, nrow, lane, tab);
+                }
+                request_payload<U, IT>(p, tab, lane, wr);
+                if (PIPE_TABLE && gn + stride < gend) {
+                    int nrow[U];
+                    rows_of(gn + stride, nrow);
+                    request_table<N, U, IT>(p, nrow, lane, tab);
+                }
             }
             group(g, w);
         }
@@ -1440,15 +1489,18 @@ __global__ __launch_bounds__(256) void select_kernel(float* logits, int n, const
     }
 }
 
+// One thread per 8 weights (count is a whole number of 128-weight blocks), decoded by the
+// same p12_decode8 as the GEMV and GEMM loads.
 __global__ void unpack_kernel(const uint8_t* payload, const uint32_t* table, uint16_t* out, int64_t count) {
-    const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int64_t i = (int64_t(blockIdx.x) * blockDim.x + threadIdx.x) * 8;
     if (i >= count) return;
     const uint32_t entry = table[i / 128];
     const uint8_t* blk = payload + (entry & ~63u);
-    const uint32_t tag = entry & 63u, k = uint32_t(i % 128);
-    if (tag == 0) { out[i] = uint16_t(blk[2 * k] | (blk[2 * k + 1] << 8)); return; }
-    const uint32_t code = (blk[128 + k / 2] >> ((k % 2) * 4)) & 15u;
-    out[i] = uint16_t(p12_word(blk[k], code, tag + 107u));
+    const uint32_t tag = entry & 63u, sub = uint32_t(i % 128) / 8;
+    const uint4 w = tag == 0 ? *reinterpret_cast<const uint4*>(blk + sub * 16)
+                             : p12_decode8(*reinterpret_cast<const uint2*>(blk + sub * 8),
+                                           *reinterpret_cast<const uint32_t*>(blk + 128 + sub * 4), tag);
+    *reinterpret_cast<uint4*>(out + i) = w;
 }
 
 // Scratch of the allocation-free decode attention entry point: a file-scope device array, one
@@ -1603,7 +1655,8 @@ void launch_select(float* logits, int n, const int32_t* history, int hist, float
 
 void launch_unpack(const uint8_t* payload, const uint32_t* table, uint16_t* out, int64_t count, hipStream_t s) {
     if (count <= 0) return;
-    hipLaunchKernelGGL(unpack_kernel, dim3(unsigned((count + 255) / 256)), dim3(256), 0, s, payload, table, out, count);
+    if (count % 128) throw Error(E_INVAL, "unpack: count must be a whole number of 128-weight blocks");
+    hipLaunchKernelGGL(unpack_kernel, dim3(unsigned((count / 8 + 255) / 256)), dim3(256), 0, s, payload, table, out, count);
 }
 
 void launch_attn_state(StepState* st, uint32_t* tickets, const int32_t* pos, int rows, hipStream_t s) {

@@ -142,13 +142,31 @@ __device__ __forceinline__ uint32_t p12_word(uint32_t s, uint32_t code, uint32_t
     const uint32_t e = code == 15u ? 0u : minimum + code;
     return (s & 127u) | ((s & 128u) << 8) | (e << 7);
 }
+// p12_word for all eight weights at once, byte-parallel (about 3 VALU operations per weight
+// instead of 8): the exponent bytes are code + minimum (at most 184: no carry between
+// bytes), cleared where the code is 15 by a v_perm_b32 mask (with all-ones sources a
+// selector byte yields 0x00 only for selector 12 = 15 ^ 3, and 0xFF for 0..11 and 13..15);
+// then each BF16 is assembled from its low byte (exponent bit 0 | 7 mantissa bits) and its
+// high byte (sign | exponent bits 7..1), pairs interleaved by v_perm_b32.
 __device__ __forceinline__ uint4 p12_decode8(uint2 sm, uint32_t nib, uint32_t tag) {
-    const uint32_t m = tag + 107u;
+    const uint32_t mrep = tag * 0x01010101u + 0x6b6b6b6bu;  // (tag + 107) in every byte
+    const uint32_t ce = nib & 0x0f0f0f0fu;                  // codes of weights 0, 2, 4, 6
+    const uint32_t co = (nib >> 4) & 0x0f0f0f0fu;           // codes of weights 1, 3, 5, 7
+    const uint32_t ee = (ce + mrep) & __builtin_amdgcn_perm(~0u, ~0u, ce ^ 0x03030303u);
+    const uint32_t eo = (co + mrep) & __builtin_amdgcn_perm(~0u, ~0u, co ^ 0x03030303u);
+    // exponents in weight order: ea = weights 0..3, eb = weights 4..7 (selector bytes 0..3
+    // take the second operand's bytes, 4..7 the first's)
+    const uint32_t ea = __builtin_amdgcn_perm(eo, ee, 0x05010400u);
+    const uint32_t eb = __builtin_amdgcn_perm(eo, ee, 0x07030602u);
+    const uint32_t la = (sm.x & 0x7f7f7f7fu) | ((ea << 7) & 0x80808080u);
+    const uint32_t ha = (sm.x & 0x80808080u) | ((ea >> 1) & 0x7f7f7f7fu);
+    const uint32_t lb = (sm.y & 0x7f7f7f7fu) | ((eb << 7) & 0x80808080u);
+    const uint32_t hb = (sm.y & 0x80808080u) | ((eb >> 1) & 0x7f7f7f7fu);
     uint4 r;
-    r.x = p12_word(sm.x & 255u, nib & 15u, m) | (p12_word((sm.x >> 8) & 255u, (nib >> 4) & 15u, m) << 16);
-    r.y = p12_word((sm.x >> 16) & 255u, (nib >> 8) & 15u, m) | (p12_word(sm.x >> 24, (nib >> 12) & 15u, m) << 16);
-    r.z = p12_word(sm.y & 255u, (nib >> 16) & 15u, m) | (p12_word((sm.y >> 8) & 255u, (nib >> 20) & 15u, m) << 16);
-    r.w = p12_word((sm.y >> 16) & 255u, (nib >> 24) & 15u, m) | (p12_word(sm.y >> 24, nib >> 28, m) << 16);
+    r.x = __builtin_amdgcn_perm(ha, la, 0x05010400u);  // (low, high) bytes of weights 0, 1
+    r.y = __builtin_amdgcn_perm(ha, la, 0x07030602u);  // weights 2, 3
+    r.z = __builtin_amdgcn_perm(hb, lb, 0x05010400u);
+    r.w = __builtin_amdgcn_perm(hb, lb, 0x07030602u);
     return r;
 }
 
