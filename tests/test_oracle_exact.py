@@ -75,6 +75,7 @@ def _attention_pair(context, cap_local, seed):
     ex.keys = [exact.bits_np(rng.standard_normal((c, 128)).astype(np.float32)) for c in ex.cap]
     ex.values = [exact.bits_np(rng.standard_normal((c, 128)).astype(np.float32)) for c in ex.cap]
     o = om.Oracle.__new__(om.Oracle)
+    o.dots = "exact"  # correctly rounded dot products: the same on every machine
     o.context = context
     o.capacity = list(ex.cap)
     o.local = (torch.from_numpy(ex.lc), torch.from_numpy(ex.ls))
