@@ -32,6 +32,7 @@ SHAPES = {"qkv": (2304, 1536), "o": (1536, 2048), "gate_up": (12288, 1536), "dow
           "head": (107520, 1536)}
 DOMINANT = "gate_up"  # largest share of the decode step's kernel time (profiles/)
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemv_gate_up_hbm_traffic.md")
+STEP_PROFILE = os.path.join(ROOT, "profiles", "decode_step_bs1_plain_and_p12.md")
 
 
 def log(*a):
@@ -111,23 +112,80 @@ def traffic_from_profile():
         return None
 
 
-def cpu_baseline(model_dir, prompt, decode_tokens):
-    """The CPU oracle (PyTorch FP32, BF16 rounding) on the host cores: bounded sample."""
+def in_step_from_profile():
+    """The dominant GEMV's average duration inside the decode step, from the committed
+    rocprofv3 kernel trace of the step (the isolated launch above has no norm prologue and no
+    previous kernel to wait for)."""
+    try:
+        with open(STEP_PROFILE) as f:
+            m = re.search(r"in_step_gate_up_us:\s*([0-9.]+)", f.read())
+    except OSError:
+        return None
+    if not m:
+        return None
+    us = float(m.group(1))
+    return {"us": us, "GBps": round(37748736 / us / 1e3, 1), "frac": round(37748736 / us / 1e3 / HBM_PEAK_GBS, 4),
+            "source": os.path.relpath(STEP_PROFILE, ROOT)}
+
+
+def cpu_model_name():
+    """The host CPU's model name (what `lscpu` prints as "Model name")."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
+def cpu_baseline(model_dir, prompt, decode_tokens, runs=3):
+    """The CPU oracle (PyTorch FP32, BF16 rounding) on the host cores, bounded: configs[0]'s
+    64-token prefill and `decode_tokens` batch-1 decode steps, `runs` warm runs each (median),
+    and configs[1]'s GEMV shapes as FP32 matrix-vector products of the BF16-valued weights."""
+    import statistics
+    import numpy as np
     import torch
     from oracle import model as om
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
     w = om.Weights(model_dir)
     o = om.Oracle(w, context=len(prompt) + decode_tokens + 1)
-    t0 = time.perf_counter()
-    nxt = o.prefill(prompt)
-    t1 = time.perf_counter()
-    for _ in range(decode_tokens):
-        nxt = o.forward([nxt])
-    t2 = time.perf_counter()
-    return {"value": round(decode_tokens / (t2 - t1), 3), "unit": "tok/s", "cores": cores, "kind": "port",
-            "sample": f"oracle/model.py FP32 CPU: {len(prompt)}-token prefill ({t1 - t0:.2f} s) then "
-                      f"{decode_tokens} batch-1 decode steps of the full model"}
+    o.prefill(prompt)  # warm-up
+    pre, dec = [], []
+    for _ in range(runs):
+        o.reset()
+        t0 = time.perf_counter()
+        nxt = o.prefill(prompt)
+        t1 = time.perf_counter()
+        for _ in range(decode_tokens):
+            nxt = o.forward([nxt])
+        t2 = time.perf_counter()
+        pre.append(t1 - t0)
+        dec.append((t2 - t1) / decode_tokens)
+    gemv = {}
+    rng = np.random.default_rng(0)
+    for name, (m, n) in SHAPES.items():
+        wt = torch.from_numpy((rng.standard_normal((m, n), dtype=np.float32) * np.float32(0.02)))
+        wt = wt.to(torch.bfloat16).float()
+        x = torch.randn(n).to(torch.bfloat16).float()
+        torch.mv(wt, x)
+        ts = []
+        for _ in range(runs):
+            t0 = time.perf_counter()
+            torch.mv(wt, x)
+            ts.append(time.perf_counter() - t0)
+        gemv[name] = round(statistics.median(ts) * 1e6, 1)
+        del wt
+    step = statistics.median(dec)
+    return {"value": round(1.0 / step, 3), "unit": "tok/s", "cores": cores, "kind": "port",
+            "cpu_model": cpu_model_name(),
+            "prefill_s": round(statistics.median(pre), 3), "decode_step_s": round(step, 4),
+            "gemv_us": gemv, "runs": runs,
+            "sample": f"oracle/model.py FP32 CPU, median of {runs} warm runs: {len(prompt)}-token prefill "
+                      f"then {decode_tokens} batch-1 decode steps of the full model (configs[0]); "
+                      "configs[1] GEMV shapes as FP32 torch.mv of BF16-valued weights"}
 
 
 def bench_batch4(plamo_hip, np, model_dir):
@@ -161,25 +219,22 @@ def bench_batch4(plamo_hip, np, model_dir):
 
 def bench_long(plamo_hip, np, model_dir, sha):
     """.p12 weights, 30,720-token prefill, then sampled decode (repetition 1.1,
-    frequency 0.2, no-repeat-ngram 4, on the GPU) to the 32,768-token cap."""
+    frequency 0.2, no-repeat-ngram 4, on the GPU) to the 32,768-token cap.  Both phases are
+    timed inside the one generate call (the runtime's prefill / decode wall seconds, as
+    Main.swift:245-287 times them)."""
     rt = plamo_hip.Runtime(model_dir, 32768, packed=True, source_sha256=sha)
     prompt = np.random.default_rng(5).integers(1024, 107520, 30720).tolist()
     rt.prefill(prompt[:2048])  # warm-up
     rt.reset()
-    t0 = time.perf_counter()
-    rt.prefill(prompt)
-    t_pre = time.perf_counter() - t0
-    rt.reset()
     rt.set_sampling(1.1, 0.2, 0.0, 4)
-    t0 = time.perf_counter()
     ids, reason = rt.generate(prompt, 32768 - 30720)
-    t_all = time.perf_counter() - t0
+    st = rt.stats()
     rt.set_sampling()
     rt.close()
-    t_dec = max(t_all - t_pre, 1e-9)
+    t_pre, t_dec = st["last_prefill_seconds"], max(st["last_decode_seconds"], 1e-9)
     return {"prefill_tokens": 30720, "prefill_s": round(t_pre, 4), "prefill_tok_s": round(30720 / t_pre, 1),
             "decode_tokens": len(ids), "stop": reason, "decode_s": round(t_dec, 4),
-            "decode_tok_s": round(len(ids) / t_dec, 1)}
+            "decode_tok_s": round(len(ids) / t_dec, 1), "gpu_s": round(st["gpu_seconds"], 4)}
 
 
 def bench_tokenizer(plamo_hip, synth):
@@ -311,7 +366,7 @@ def main():
     cpu = None
     if not args.no_cpu:
         log("cpu baseline: oracle on host cores")
-        cpu = cpu_baseline(model_dir, prompt, 8)
+        cpu = cpu_baseline(model_dir, prompt, 6)
 
     plain = results["plain"]
     line = {
@@ -328,7 +383,9 @@ def main():
         "roofline": {"bound": "hbm", "achieved": dom["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(dom["GBps"] / HBM_PEAK_GBS, 4), "traffic": traffic_from_profile(),
                      "kernel": f"gemv {DOMINANT} 12288x1536 BF16, one row, weights streamed from HBM "
-                               "(37,748,736 B per launch)"},
+                               "(37,748,736 B per launch)",
+                     "scope": "isolated launch (configs[1] shape, plain activation prologue), HIP events",
+                     "in_step": in_step_from_profile()},
         "cpu_baseline": cpu,
         "details": results,
     }

@@ -48,6 +48,10 @@ typedef struct plamo_stats {
     int32_t packed;           /* 1 when the .p12 archive is used (Runtime.swift:148) */
     int32_t last_output_rows; /* Runtime.lastOutputRows (Runtime.swift:153) */
     int32_t local_capacity;   /* ring slots of a sliding-window layer */
+    /* wall seconds of the last plamo_generate's two phases, timed as Main.swift:245-247,287
+     * times them for prefill_seconds / decode_seconds (0 before the first call) */
+    double last_prefill_seconds;
+    double last_decode_seconds;
 } plamo_stats;
 
 /* ---- Runtime (Runtime.swift:128-553) ------------------------------------------- */

@@ -228,6 +228,8 @@ int plamo_get_stats(plamo_runtime* rt, plamo_stats* s) {
     s->packed = r.model->packed ? 1 : 0;
     s->last_output_rows = r.last_output_rows;
     s->local_capacity = r.eng->local_capacity;
+    s->last_prefill_seconds = r.last_prefill_seconds;
+    s->last_decode_seconds = r.last_decode_seconds;
     return PLAMO_OK;
 }
 

@@ -134,11 +134,11 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, const floatx1
 #pragma unroll
                 for (int j = 0; j < TW; j += 2) {  // LDS rows of tile j are gate rows, of j + 1 the matching up rows
                     const uint32_t m = uint32_t(n0 + ((ww * TW + j) >> 1) * 32 + jc);
-                    // hardware exp2 and reciprocal: the prefill is checked against a tolerance
-                    // (decode keeps the exact sequence of `exp_det` and IEEE division)
+                    // g / (1 + exp(-g)) with IEEE division (Kernels.metal:202-210), the exp of
+                    // the decode epilogue (`exp_det`): decode and prefill round alike
                     const float gt = roundbf(acc[i][j][r]);
                     const float up = roundbf(acc[i][j + 1][r]);
-                    const float silu = gt * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-gt * 1.4426950408889634f));
+                    const float silu = gt / (1.0f + exp_det(-gt));
                     buffer_store2(yv, (t * INTER + m) * 2u, uint16_t(bits(roundbf(silu) * up)));
                 }
             } else {

@@ -2,6 +2,7 @@
 #include "runtime.h"
 
 #include <algorithm>
+#include <chrono>
 #include <cmath>
 #include <cstdlib>
 #include <fstream>
@@ -871,7 +872,11 @@ std::vector<int32_t> RuntimeImpl::generate(const int32_t* prompt, int n, int max
     for (int i = 0; i < n; ++i)
         if (prompt[i] < 0 || prompt[i] >= VOCAB) throw Error(E_INVAL, "Input exceeds context");
     reset();
-    const int first = prefill(prompt, n);
+    const auto t0 = std::chrono::steady_clock::now();
+    const int first = prefill(prompt, n);  // returns after the stream synchronised
+    const auto t1 = std::chrono::steady_clock::now();
+    last_prefill_seconds = std::chrono::duration<double>(t1 - t0).count();
+    last_decode_seconds = 0;
     *reason = 0;
     if (max_tokens == 0) return {};
     Engine& e = *eng;
@@ -900,6 +905,7 @@ std::vector<int32_t> RuntimeImpl::generate(const int32_t* prompt, int n, int max
         if (hs.stopped) break;
     }
     end_timing();
+    last_decode_seconds = std::chrono::duration<double>(std::chrono::steady_clock::now() - t1).count();
     PLAMO_HIP(hipGetLastError());
     std::vector<int32_t> out(hs.produced);
     if (hs.produced)

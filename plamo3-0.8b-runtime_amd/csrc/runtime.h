@@ -127,6 +127,7 @@ struct RuntimeImpl {
     int64_t position = 0;
     int last_output_rows = 0;
     double gpu_seconds = 0;
+    double last_prefill_seconds = 0, last_decode_seconds = 0;  // phases of the last generate
     std::vector<int32_t> predictions;
     // sampler
     bool sampling = false;

@@ -21,7 +21,8 @@ class Stats(ctypes.Structure):
                 ("device_bytes", ctypes.c_int64), ("weight_bytes", ctypes.c_int64),
                 ("linear_bytes", ctypes.c_int64), ("context", ctypes.c_int32),
                 ("packed", ctypes.c_int32), ("last_output_rows", ctypes.c_int32),
-                ("local_capacity", ctypes.c_int32)]
+                ("local_capacity", ctypes.c_int32), ("last_prefill_seconds", ctypes.c_double),
+                ("last_decode_seconds", ctypes.c_double)]
 
 
 class PackReport(ctypes.Structure):
