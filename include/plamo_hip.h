@@ -159,6 +159,10 @@ int plamo_batch_hidden(plamo_batch* b, int32_t lane, float* values, char* err, s
 int plamo_batch_kv(plamo_batch* b, int32_t lane, int32_t layer, uint16_t* keys, uint16_t* values,
                    int32_t* capacity, char* err, size_t errlen);
 int plamo_batch_positions(plamo_batch* b, int32_t* out, int32_t capacity, int32_t* count);
+/* Fills every lane's K and V of every layer with the BF16 pattern `bits`.  No API
+ * counterpart: the reference's test writes its Metal buffers directly
+ * (BatchMapTests.swift:15-18 fills them with 0xff bytes, NaN) to show unused KV is never read. */
+int plamo_batch_fill_kv(plamo_batch* b, uint16_t bits);
 
 /* ---- Lane scheduler (BatchDecode.swift:8-47) --------------------------------------- */
 

@@ -352,6 +352,19 @@ int plamo_batch_kv(plamo_batch* b, int32_t lane, int32_t layer, uint16_t* keys, 
     });
 }
 
+int plamo_batch_fill_kv(plamo_batch* b, uint16_t bits) {
+    return guard(nullptr, 0, [&] {
+        if (!b) throw plamo::Error(plamo::E_INVAL, "Invalid batch");
+        auto& e = *b->impl->eng;
+        for (int l = 0; l < plamo::LAYERS; ++l) {
+            const size_t n = size_t(e.lanes) * size_t(e.capacity[l]) * plamo::HEAD_DIM;
+            PLAMO_HIP(hipMemsetD16Async(e.keys[l], bits, n, e.stream));
+            PLAMO_HIP(hipMemsetD16Async(e.values[l], bits, n, e.stream));
+        }
+        PLAMO_HIP(hipStreamSynchronize(e.stream));
+    });
+}
+
 int plamo_batch_positions(plamo_batch* b, int32_t* out, int32_t capacity, int32_t* count) {
     if (!b) return PLAMO_EINVAL;
     const auto& p = b->impl->positions;

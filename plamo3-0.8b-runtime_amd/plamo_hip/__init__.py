@@ -183,6 +183,12 @@ class Batch:
     def reset(self):
         self._lib.plamo_batch_reset(self._h)
 
+    def fill_kv(self, bits):
+        """Fills every lane's KV with the BF16 pattern `bits` (the reference test's memset of
+        its Metal KV buffers, BatchMapTests.swift:15-18)."""
+        if self._lib.plamo_batch_fill_kv(self._h, int(bits) & 0xFFFF) != 0:
+            raise native.PlamoError(1, "fill_kv failed")
+
     def positions(self):
         buf, n = (ctypes.c_int32 * 4)(), ctypes.c_int32()
         self._lib.plamo_batch_positions(self._h, buf, 4, ctypes.byref(n))

@@ -73,6 +73,7 @@ _SIGNATURES = {
                                           ctypes.c_size_t]),
     "plamo_batch_kv": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, c_u16p, c_u16p, c_i32p,
                                       ctypes.c_char_p, ctypes.c_size_t]),
+    "plamo_batch_fill_kv": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint16]),
     "plamo_batch_positions": (ctypes.c_int, [ctypes.c_void_p, c_i32p, ctypes.c_int32, c_i32p]),
     "plamo_decode_batch": (ctypes.c_int, [c_i32p, c_i32p, ctypes.c_int32, STEP_FN, EMIT_FN, FINISH_FN,
                                           ctypes.c_void_p, ctypes.c_int32, c_i32p, ctypes.c_int32, c_i32p, c_i32p,

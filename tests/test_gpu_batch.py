@@ -118,3 +118,54 @@ def test_batch_validation(engines, model_dir):
             plamo_hip.Batch(big)
     finally:
         big.close()
+
+
+def _tails(b, lengths):
+    """Every lane's KV rows past its prompt (all rows of lanes without a prompt)."""
+    out = []
+    for lane in range(4):
+        for layer in range(16):
+            k, v = b.kv(lane, layer)
+            used = min(lengths[lane], len(k)) if lane < len(lengths) else 0
+            out.append((k[used:].copy(), v[used:].copy()))
+    return out
+
+
+@pytest.mark.parametrize("packed", [False, True])
+@pytest.mark.parametrize("ring", [False, True])
+def test_poisoned_unused_kv_is_never_read(model_dir, packed, ring):
+    """BatchMapTests.swift:6-73: the batch KV filled with NaN (BF16 0xffff); prefill leaves the
+    rows past each prompt untouched, and after the steps every lane's logits, hidden row and
+    written KV rows equal scalar decode of its prompt (a NaN that reached attention would
+    show in all of them).  The reference's second configuration (context 2100, a 2063-token
+    prompt) is kept; this build's local ring holds 2100 slots there, so it does not wrap."""
+    d, sha = model_dir
+    context, steps = (2100, 2) if ring else (128, 1)
+    layouts = [[2063, 3], [3, 4]] if ring else [[63, 3, 7, 5], [3, 63], [1, 4, 2], [2]]
+    rt = plamo_hip.Runtime(d, context, packed=packed, source_sha256=sha)
+    b = plamo_hip.Batch(rt)
+    try:
+        b.fill_kv(0xFFFF)
+        for lengths in layouts:
+            prompts = prompts_for(lengths)
+            expected = [scalar_state(rt, p, steps) for p in prompts]
+            before = _tails(b, lengths)
+            tokens = b.prefill(prompts)
+            after = _tails(b, lengths)
+            assert all(np.array_equal(x[0], y[0]) and np.array_equal(x[1], y[1]) for x, y in zip(before, after)), \
+                ("unused KV overwritten", packed, lengths)
+            for _ in range(steps):
+                tokens = b.step(tokens)
+            for lane, p in enumerate(prompts):
+                nxt, logits, hidden, kv = expected[lane]
+                assert tokens[lane] == nxt, (packed, lengths, lane)
+                assert np.array_equal(b.logit_bits(lane), logits), (packed, lengths, lane)
+                assert np.array_equal(b.hidden(lane).view(np.uint32), hidden.view(np.uint32))
+                n = len(p) + steps
+                for layer in range(16):
+                    k, v = b.kv(lane, layer)
+                    m = min(n, len(k))
+                    assert np.array_equal(k[:m], kv[layer][0][:m]) and np.array_equal(v[:m], kv[layer][1][:m]), layer
+    finally:
+        b.close()
+        rt.close()
