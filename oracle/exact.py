@@ -258,7 +258,12 @@ class ExactDecoder:
             g, u = roundbf_np(gu[:6144]), roundbf_np(gu[6144:])
             act = roundbf_np(roundbf_np(g / (F(1) + exp_det(-g))) * u)
             d = roundbf_np(gemv(L["down"], act))
-        z = norm_rows(d, self._bits(Ls[15]["post_mlp"]), post_mlp)
+        return self.head_step(d, x)
+
+    def head_step(self, d, x):
+        """The head of a step: last layer's post-norm and residual, final norm, LM head GEMV
+        -> (logit_bits, hidden, next)."""
+        z = norm_rows(d, self._bits(self.layers[15]["post_mlp"]), F(1 / 5.0 ** 1.5))
         x = roundbf_np(x + z)
         h = norm_rows(x, self._bits(self.final), 1.0)
         logits = gemv(self.head, h)

@@ -245,6 +245,27 @@ __device__ __forceinline__ void buffer_store2(__amdgpu_buffer_rsrc_t r, uint32_t
     __builtin_amdgcn_raw_buffer_store_b16(v, r, off, 0, 0);
 }
 
+// 2^x for the softmax weights of flash attention (x <= 0 or -inf), with a fixed operation
+// sequence the CPU oracle reproduces bit for bit: x = k + f with k = rint(x) and f = x - k
+// exact (|f| <= 1/2), the degree-6 Taylor polynomial of 2^f = e^(f ln 2) in Horner form with
+// fused multiply-adds, then an exact 2^k scale.  Arguments below -64 give 0 (a weight under
+// 2^-64 of the running maximum's moves nothing), so every result is a normal number.
+// Accuracy: about 3 ulp.
+__device__ __forceinline__ float exp2_det(float x) {
+#pragma clang fp contract(off)
+    if (!(x >= -64.0f)) return 0.0f;
+    const float k = rintf(x);
+    const float f = x - k;
+    float p = 1.54035304e-04f;                 // ln2^6 / 6!
+    p = __builtin_fmaf(p, f, 1.33335581e-03f); // ln2^5 / 5!
+    p = __builtin_fmaf(p, f, 9.61812911e-03f); // ln2^4 / 4!
+    p = __builtin_fmaf(p, f, 5.55041087e-02f); // ln2^3 / 3!
+    p = __builtin_fmaf(p, f, 2.40226507e-01f); // ln2^2 / 2!
+    p = __builtin_fmaf(p, f, 6.93147182e-01f); // ln2
+    p = __builtin_fmaf(p, f, 1.0f);
+    return ldexpf(p, int(k));
+}
+
 // exp(x) with a fixed operation sequence the CPU oracle reproduces bit for bit:
 // Cody-Waite reduction x = k*ln2 + r (ln2 split in a 16-bit head, so k*LN2_HI is exact for
 // |k| <= 128), degree-7 Taylor polynomial of e^r in Horner form, then an exact 2^k scale.

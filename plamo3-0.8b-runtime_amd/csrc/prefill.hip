@@ -526,7 +526,9 @@ __global__ __launch_bounds__(256) void qk_prep_kernel(const QkPrepParams p) {
 // a query's 64 scores of a tile sit in one lane column (two halves of 32 lanes), so the
 // online-softmax statistics need a single cross-half exchange, and the S^T accumulator is
 // already the B operand layout of the P.V product.  P is split as hi + lo BF16 so the
-// P.V product keeps ~16 significant bits of the FP32 probabilities.
+// P.V product keeps ~16 significant bits of the FP32 probabilities.  The softmax weights come
+// from `exp2_det` and nothing is contracted, so every output is a fixed function of the
+// inputs that a CPU restatement reproduces bit for bit.
 //
 // Keys of local layers are rotated while staged, with coordinate key_pos - base of the
 // workgroup's 16-token chunk (base = max(0, chunk_start - 2047)).
@@ -631,6 +633,7 @@ __device__ __forceinline__ void split_bf16(float a, float b, uint32_t& hw, uint3
 }
 
 __global__ __launch_bounds__(256, 2) void flash_prefill_kernel(const FlashParams p) {
+#pragma clang fp contract(off)  // fixed rounding sequence, reproduced by the CPU oracle
     __shared__ __align__(16) uint16_t Ks[2][FK * KST];
     __shared__ __align__(16) uint16_t Vt[2][HEAD_DIM * VST];
     __shared__ int s_last;
@@ -723,13 +726,13 @@ __global__ __launch_bounds__(256, 2) void flash_prefill_kernel(const FlashParams
         mt = fmaxf(mt, xor_lane<32>(mt));
         const float mn = fmaxf(m, mt);
         const float ms = mn == NEG_INF ? 0.0f : mn;  // nothing visible yet: every p is 0
-        const float alpha = __builtin_amdgcn_exp2f(m - ms);
+        const float alpha = exp2_det(m - ms);
         ls *= alpha;
 #pragma unroll
         for (int r = 0; r < 2; ++r)
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-                const float e = __builtin_amdgcn_exp2f(sacc[r][i] - ms);
+                const float e = exp2_det(sacc[r][i] - ms);
                 sacc[r][i] = e;
                 ls += e;
             }
@@ -808,7 +811,7 @@ __global__ __launch_bounds__(256, 2) void flash_prefill_kernel(const FlashParams
 #pragma unroll
         for (int q = 0; q < FLASH_PARTS; ++q) {
             if (q < parts) {
-                const float w = __builtin_amdgcn_exp2f(mq[q] - M);
+                const float w = exp2_det(mq[q] - M);
                 lt += lq[q] * w;
 #pragma unroll
                 for (int dt = 0; dt < 4; ++dt)
