@@ -28,10 +28,11 @@ using namespace dev;
 namespace {
 
 // Weight rows per wave group: four for one activation row; with four rows the
-// arithmetic per weight byte quadruples, so groups shrink to spread it over more waves.
+// arithmetic per weight byte quadruples, so groups shrink to spread it over more waves
+// (SwiGLU: one gate and one up row, three groups for each of a CU's eight waves).
 template <int N, int MAXR, int EPI>
 constexpr int gemv_u() {
-    if constexpr (EPI == EPI_SWIGLU) return 4;
+    if constexpr (EPI == EPI_SWIGLU) return MAXR == 1 ? 4 : 2;
     else if constexpr (N >= 6144) return MAXR == 1 ? 2 : 1;
     else return MAXR == 1 ? (N == ATTN ? 2 : 4) : 2;
 }
@@ -1601,7 +1602,7 @@ void gemv_dispatch_n(bool packed, int maxr, Prologue pro, Epilogue epi, const Ge
 }  // namespace
 
 int gemv_group_rows(int n, int maxr, Epilogue epi) {
-    if (epi == EPI_SWIGLU) return 4;
+    if (epi == EPI_SWIGLU) return maxr == 1 ? 4 : 2;
     if (n >= 6144) return maxr == 1 ? 2 : 1;
     return maxr == 1 ? (n == ATTN ? 2 : 4) : 2;
 }
