@@ -354,6 +354,42 @@ int plamo_ordered_append(plamo_ordered* o, int32_t lane, int32_t id, char* err, 
 int plamo_ordered_finish(plamo_ordered* o, int32_t lane, const char* reason, char* err, size_t errlen);
 void plamo_ordered_close(plamo_ordered* o);
 
+/* DocumentPlan (OrderedOutput.swift:3-21) of `count` segments (Segments.swift:4-7): segment i
+ * is `texts[i]` (`text_lens[i]` UTF-8 bytes) with `tokens[i]` (`token_counts[i]` prompt ids;
+ * none: a whitespace run kept verbatim).  Document d has input tokens and a prefix (the
+ * whitespace since the previous document, or "\n" between adjacent documents); prefix index
+ * `documents` is the tail.  Error "No documents to translate". */
+typedef struct plamo_plan plamo_plan;
+int plamo_document_plan(const char* const* texts, const size_t* text_lens, const int32_t* const* tokens,
+                        const int32_t* token_counts, int32_t count, plamo_plan** out, char* err, size_t errlen);
+int32_t plamo_plan_documents(const plamo_plan* p);
+int plamo_plan_input(const plamo_plan* p, int32_t document, const int32_t** tokens, int32_t* count);
+int plamo_plan_prefix(const plamo_plan* p, int32_t document, const char** text, size_t* len);
+void plamo_plan_close(plamo_plan* p);
+
+/* DocumentOutput (OrderedOutput.swift:69-76). */
+typedef struct plamo_document_output {
+    int32_t sequences;               /* documents reported in ids / lengths / reasons */
+    double gpu_seconds;              /* Batch.gpuSeconds summed over the groups */
+    int64_t discarded_tokens;        /* emitted by lanes past a truncation, not reported */
+    int64_t prefilled_input_tokens;
+    double prefill_seconds, decode_seconds;
+} plamo_document_output;
+
+/* Batch.translateOrdered (OrderedOutput.swift:79-115): the DocumentPlan of the segments,
+ * then groups of up to four documents: Batch.prefill, decodeBatch with Batch.step and
+ * stopOnTruncation, every token streamed through an OrderedOutput in document order
+ * (`emit` as for plamo_ordered_open; the last group also emits the tail); a group whose
+ * last reported lane did not stop ends the document.  Errors "No documents to translate",
+ * "Invalid document tokens or context budget" (limit 0..8191, every input + limit within
+ * the context, ids below 107520); on any error the batch is reset.  Outputs: `ids`
+ * [documents][ids_stride], `lengths`, `reasons` (PLAMO_REASON_*) of the reported documents. */
+int plamo_batch_translate_ordered(plamo_batch* b, const plamo_tokenizer* t, const char* const* texts,
+                                  const size_t* text_lens, const int32_t* const* tokens, const int32_t* token_counts,
+                                  int32_t count, int32_t limit, plamo_text_fn emit, void* user, int32_t* ids,
+                                  int32_t ids_stride, int32_t* lengths, int32_t* reasons, plamo_document_output* out,
+                                  char* err, size_t errlen);
+
 /* Tokenizer.prompt(_:target:) (Tokenizer.swift:272-281): errors "Unsupported target
  * language", "Source must be nonempty and contain no reserved PLaMo delimiters". */
 int plamo_translation_prompt(const char* text, size_t len, const char* target, char* out, size_t cap,

@@ -1,4 +1,5 @@
 // extern "C" boundary (include/plamo_hip.h).  No C++ exception crosses it.
+#include <chrono>
 #include <cstdio>
 #include <cstring>
 #include <map>
@@ -891,6 +892,118 @@ int plamo_translation_prompt(const char* text, size_t len, const char* target, c
     return guard(err, errlen, [&] {
         if ((!text && len) || !target) throw plamo::Error(plamo::E_INVAL, "bad prompt arguments");
         put_bytes(plamo::translation_prompt(std::string(text ? text : "", len), target), out, cap, n_out);
+    });
+}
+
+struct plamo_plan {
+    plamo::DocumentPlan plan;
+};
+
+static std::vector<plamo::Segment> segments_of(const char* const* texts, const size_t* text_lens,
+                                               const int32_t* const* tokens, const int32_t* token_counts, int32_t count) {
+    if (count < 0 || (count > 0 && (!texts || !text_lens || !tokens || !token_counts)))
+        throw plamo::Error(plamo::E_INVAL, "bad segment arguments");
+    std::vector<plamo::Segment> parts(static_cast<size_t>(count));
+    for (int32_t i = 0; i < count; ++i) {
+        if ((!texts[i] && text_lens[i]) || token_counts[i] < 0 || (!tokens[i] && token_counts[i]))
+            throw plamo::Error(plamo::E_INVAL, "bad segment arguments");
+        if (text_lens[i]) parts[size_t(i)].text.assign(texts[i], text_lens[i]);
+        if (token_counts[i]) parts[size_t(i)].tokens.assign(tokens[i], tokens[i] + token_counts[i]);
+    }
+    return parts;
+}
+
+int plamo_document_plan(const char* const* texts, const size_t* text_lens, const int32_t* const* tokens,
+                        const int32_t* token_counts, int32_t count, plamo_plan** out, char* err, size_t errlen) {
+    return guard(err, errlen, [&] {
+        if (!out) throw plamo::Error(plamo::E_INVAL, "bad segment arguments");
+        *out = nullptr;
+        *out = new plamo_plan{plamo::DocumentPlan(segments_of(texts, text_lens, tokens, token_counts, count))};
+    });
+}
+
+int32_t plamo_plan_documents(const plamo_plan* p) { return p ? int32_t(p->plan.inputs.size()) : 0; }
+
+int plamo_plan_input(const plamo_plan* p, int32_t document, const int32_t** tokens, int32_t* count) {
+    if (!p || document < 0 || size_t(document) >= p->plan.inputs.size() || !tokens || !count) return PLAMO_EINVAL;
+    *tokens = p->plan.inputs[size_t(document)].data();
+    *count = int32_t(p->plan.inputs[size_t(document)].size());
+    return PLAMO_OK;
+}
+
+int plamo_plan_prefix(const plamo_plan* p, int32_t document, const char** text, size_t* len) {
+    if (!p || document < 0 || size_t(document) > p->plan.prefixes.size() || !text || !len) return PLAMO_EINVAL;
+    const std::string& s = size_t(document) == p->plan.prefixes.size() ? p->plan.tail : p->plan.prefixes[size_t(document)];
+    *text = s.data();
+    *len = s.size();
+    return PLAMO_OK;
+}
+
+void plamo_plan_close(plamo_plan* p) { delete p; }
+
+int plamo_batch_translate_ordered(plamo_batch* b, const plamo_tokenizer* t, const char* const* texts,
+                                  const size_t* text_lens, const int32_t* const* tokens, const int32_t* token_counts,
+                                  int32_t count, int32_t limit, plamo_text_fn emit, void* user, int32_t* ids,
+                                  int32_t ids_stride, int32_t* lengths, int32_t* reasons, plamo_document_output* out,
+                                  char* err, size_t errlen) {
+    return guard(err, errlen, [&] {
+        if (!b || !t) throw plamo::Error(plamo::E_INVAL, "bad segment arguments");
+        const plamo::DocumentPlan plan(segments_of(texts, text_lens, tokens, token_counts, count));
+        bool ok = limit >= 0 && limit <= 8191;
+        for (const auto& in : plan.inputs) {
+            ok = ok && int64_t(in.size()) + limit <= int64_t(b->rt->impl.context);
+            for (int32_t id : in) ok = ok && id >= 0 && id < plamo::VOCAB;
+        }
+        if (!ok) throw plamo::Error(plamo::E_INVAL, "Invalid document tokens or context budget");
+        using clock = std::chrono::steady_clock;
+        std::vector<LaneOutput> outputs;
+        double gpu = 0, prefill_s = 0, decode_s = 0;
+        int64_t discarded = 0, prefilled = 0;
+        const size_t n = plan.inputs.size();
+        try {
+            for (size_t start = 0; start < n; start += plamo::ROWS) {
+                const size_t end = std::min(start + plamo::ROWS, n);
+                plamo::OrderedOutput sink(t->tok, std::vector<std::string>(plan.prefixes.begin() + long(start),
+                                                                           plan.prefixes.begin() + long(end)),
+                                          end == n ? plan.tail : std::string(), text_emitter(emit, user));
+                int64_t generated = 0;
+                const std::vector<std::vector<int32_t>> inputs(plan.inputs.begin() + long(start), plan.inputs.begin() + long(end));
+                const auto t0 = clock::now();
+                const std::vector<int32_t> next = b->impl->prefill(inputs);
+                const auto t1 = clock::now();
+                auto batch = decode_batch(
+                    next, std::vector<int32_t>(end - start, limit),
+                    [&](const std::vector<int32_t>& tk) { return b->impl->step(tk); },
+                    [&](int lane, int id) {
+                        ++generated;
+                        sink.append(lane, id);
+                    },
+                    [&](int lane, const LaneOutput& o) { sink.finish(lane, o.reason == PLAMO_REASON_STOP ? "stop" : "length"); },
+                    true);
+                prefill_s += std::chrono::duration<double>(t1 - t0).count();
+                decode_s += std::chrono::duration<double>(clock::now() - t1).count();
+                for (const auto& in : inputs) prefilled += int64_t(in.size());
+                gpu += b->impl->gpu_seconds;
+                int64_t reported = 0;
+                for (const auto& o : batch) reported += int64_t(o.ids.size());
+                discarded += generated - reported;
+                const bool stopped = batch.back().reason == PLAMO_REASON_STOP;
+                for (auto& o : batch) outputs.push_back(std::move(o));
+                if (!stopped) break;
+            }
+        } catch (...) {
+            b->impl->reset();
+            throw;
+        }
+        write_outputs(outputs, ids, ids_stride, lengths, reasons, nullptr);
+        if (out) {
+            out->sequences = int32_t(outputs.size());
+            out->gpu_seconds = gpu;
+            out->discarded_tokens = discarded;
+            out->prefilled_input_tokens = prefilled;
+            out->prefill_seconds = prefill_s;
+            out->decode_seconds = decode_s;
+        }
     });
 }
 

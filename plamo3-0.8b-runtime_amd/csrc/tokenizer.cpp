@@ -314,6 +314,21 @@ std::string utf8_repair(const std::string& b) {
     return out;
 }
 
+DocumentPlan::DocumentPlan(const std::vector<Segment>& parts) {
+    std::string pending;
+    for (const Segment& part : parts) {
+        if (part.tokens.empty()) {
+            pending += part.text;
+            continue;
+        }
+        prefixes.push_back(!inputs.empty() && pending.empty() ? std::string("\n") : pending);
+        inputs.push_back(part.tokens);
+        pending.clear();
+    }
+    if (inputs.empty()) throw Error(E_INVAL, "No documents to translate");
+    tail = pending;
+}
+
 OrderedOutput::OrderedOutput(const Tokenizer& t, std::vector<std::string> prefixes, std::string tail, Emit emit)
     : prefixes_(std::move(prefixes)), tail_(std::move(tail)), emit_(std::move(emit)) {
     if (prefixes_.empty() || prefixes_.size() > 4) throw Error(E_INVAL, "Expected one to four output prefixes");

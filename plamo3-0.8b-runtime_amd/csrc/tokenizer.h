@@ -82,6 +82,24 @@ class OrderedOutput {
     void push(int lane, const std::string& text);
 };
 
+// One piece of a source document (Segments.swift:4-7): text to translate with its prompt
+// tokens, or a whitespace run kept verbatim (no tokens).
+struct Segment {
+    std::string text;
+    std::vector<int32_t> tokens;
+};
+
+// DocumentPlan (OrderedOutput.swift:3-21): the documents to translate (segments with tokens)
+// and the text emitted before each of them: the whitespace runs since the previous document,
+// or "\n" between two adjacent documents; the trailing run is the tail.  No document at all
+// is an error ("No documents to translate").
+struct DocumentPlan {
+    std::vector<std::vector<int32_t>> inputs;
+    std::vector<std::string> prefixes;
+    std::string tail;
+    explicit DocumentPlan(const std::vector<Segment>& parts);
+};
+
 // UTF-8 with every ill-formed sequence replaced by U+FFFD, one per maximal subpart.
 std::string utf8_repair(const std::string& bytes);
 

@@ -12,6 +12,7 @@ Names, argument meaning and error behaviour follow the reference:
 
 Every call goes to ``lib/libplamo_hip.so``; there is no CPU fallback.
 """
+import collections
 import ctypes
 
 import numpy as np
@@ -224,6 +225,40 @@ class Batch:
                     reasons, ctypes.byref(lanes))
         return [([ids[i * stride + k] for k in range(lengths[i])], REASONS[reasons[i]]) for i in range(lanes.value)]
 
+    def translate_ordered(self, parts, tokenizer, limit, emit):
+        """Batch.translateOrdered (OrderedOutput.swift:79-115): `emit(text)` receives the
+        document's text in order; an exception from `emit` cancels and is re-raised ->
+        DocumentOutput as a dict with `sequences` [(ids, reason)]."""
+        seg = native.Segments(parts)
+        failure = []
+
+        def _cb(_, data, n):
+            try:
+                emit(ctypes.string_at(data, n).decode("utf-8"))
+                return 0
+            except Exception as e:  # re-raised below
+                failure.append(e)
+                return 1
+
+        cb = native.TEXT_FN(_cb)
+        docs = max(1, sum(1 for p in parts if p.tokens))
+        stride = max(1, int(limit))
+        ids = (ctypes.c_int32 * (docs * stride))()
+        lengths, reasons = (ctypes.c_int32 * docs)(), (ctypes.c_int32 * docs)()
+        out = native.DocumentOutput()
+        err = ctypes.create_string_buffer(512)
+        rc = self._lib.plamo_batch_translate_ordered(self._h, tokenizer._h, *seg.args(), int(limit),
+                                                     ctypes.cast(cb, ctypes.c_void_p), None, ids, stride, lengths,
+                                                     reasons, ctypes.byref(out), err, 512)
+        if failure:
+            raise failure[0]
+        if rc != 0:
+            raise PlamoError(rc, err.value.decode(errors="replace"))
+        seqs = [([ids[i * stride + k] for k in range(lengths[i])], REASONS[reasons[i]]) for i in range(out.sequences)]
+        return {"sequences": seqs, "gpu_seconds": out.gpu_seconds, "discarded_tokens": out.discarded_tokens,
+                "prefilled_input_tokens": out.prefilled_input_tokens, "prefill_seconds": out.prefill_seconds,
+                "decode_seconds": out.decode_seconds}
+
     def decode(self, initial, limits, stop_on_truncation=False):
         """decodeBatch(initial, limits, step: self.step) (BatchDecode.swift:8-37) as a device loop
         after prefill -> [(ids, reason)]."""
@@ -372,6 +407,33 @@ class TokenStream:
             self.close()
         except Exception:
             pass
+
+
+Segment = collections.namedtuple("Segment", "text tokens")
+Segment.__doc__ = "A source piece (Segments.swift:4-7): text with prompt tokens, or a whitespace run (no tokens)."
+
+
+def document_plan(parts):
+    """DocumentPlan (OrderedOutput.swift:3-21) -> (inputs, prefixes, tail)."""
+    lib = native.load()
+    seg = native.Segments(parts)
+    h = ctypes.c_void_p()
+    native.call(lib.plamo_document_plan, *seg.args(), ctypes.byref(h))
+    try:
+        n = lib.plamo_plan_documents(h)
+        inputs, prefixes = [], []
+        for d in range(n + 1):
+            ptr, length = ctypes.c_void_p(), ctypes.c_size_t()
+            lib.plamo_plan_prefix(h, d, ctypes.byref(ptr), ctypes.byref(length))
+            prefixes.append(ctypes.string_at(ptr, length.value).decode("utf-8") if length.value else "")
+            if d < n:
+                tp, cnt = ctypes.c_void_p(), ctypes.c_int32()
+                lib.plamo_plan_input(h, d, ctypes.byref(tp), ctypes.byref(cnt))
+                arr = ctypes.cast(tp, ctypes.POINTER(ctypes.c_int32))
+                inputs.append([arr[i] for i in range(cnt.value)])
+        return inputs, prefixes[:-1], prefixes[-1]
+    finally:
+        lib.plamo_plan_close(h)
 
 
 class OrderedOutput:

@@ -139,7 +139,45 @@ _SIGNATURES = {
     "plamo_translation_prompt": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_size_t, ctypes.c_char_p, ctypes.c_char_p,
                                                 ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t), ctypes.c_char_p,
                                                 ctypes.c_size_t]),
+    "plamo_document_plan": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                           ctypes.c_int32, ctypes.POINTER(ctypes.c_void_p), ctypes.c_char_p,
+                                           ctypes.c_size_t]),
+    "plamo_plan_documents": (ctypes.c_int32, [ctypes.c_void_p]),
+    "plamo_plan_input": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, ctypes.POINTER(ctypes.c_void_p),
+                                        ctypes.POINTER(ctypes.c_int32)]),
+    "plamo_plan_prefix": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, ctypes.POINTER(ctypes.c_void_p),
+                                         ctypes.POINTER(ctypes.c_size_t)]),
+    "plamo_plan_close": (None, [ctypes.c_void_p]),
+    "plamo_batch_translate_ordered": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                                     ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32,
+                                                     ctypes.c_void_p, ctypes.c_void_p, c_i32p, ctypes.c_int32, c_i32p,
+                                                     c_i32p, ctypes.c_void_p, ctypes.c_char_p, ctypes.c_size_t]),
 }
+
+
+class DocumentOutput(ctypes.Structure):
+    _fields_ = [("sequences", ctypes.c_int32), ("gpu_seconds", ctypes.c_double),
+                ("discarded_tokens", ctypes.c_int64), ("prefilled_input_tokens", ctypes.c_int64),
+                ("prefill_seconds", ctypes.c_double), ("decode_seconds", ctypes.c_double)]
+
+
+class Segments:
+    """Segment arrays for the C ABI (texts, lengths, token arrays, counts); keeps the
+    buffers alive for the duration of a call."""
+
+    def __init__(self, parts):
+        self.enc = [p.text.encode("utf-8") for p in parts]
+        self.tok = [i32([int(t) for t in p.tokens]) for p in parts]
+        n = max(1, len(parts))
+        self.texts = (ctypes.c_char_p * n)(*self.enc)
+        self.lens = (ctypes.c_size_t * n)(*[len(e) for e in self.enc])
+        self.tokens = (ctypes.c_void_p * n)(*[ctypes.cast(t, ctypes.c_void_p) for t in self.tok])
+        self.counts = i32([len(p.tokens) for p in parts])
+        self.count = len(parts)
+
+    def args(self):
+        return (ctypes.cast(self.texts, ctypes.c_void_p), ctypes.cast(self.lens, ctypes.c_void_p),
+                ctypes.cast(self.tokens, ctypes.c_void_p), ctypes.cast(self.counts, ctypes.c_void_p), self.count)
 
 TEXT_FN = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t)
 

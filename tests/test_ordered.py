@@ -144,3 +144,46 @@ def test_emitted_text_is_the_repaired_decode(tok):
             sink.append(0, i)
         sink.finish(0, (ids, "stop"))
         assert "".join(out) == tok.decode_bytes(ids).decode("utf-8", errors="replace"), ids
+
+
+def test_plan_preserves_whitespace_and_adjacent_chunk_boundaries():
+    # OrderedTests.swift:52-63
+    import plamo_hip
+    S = plamo_hip.Segment
+    parts = [S("\t", []), S("source A", [449]), S("\r\n", []), S(" \n", []), S("source B", [450]),
+             S("source C", [451]), S("\n\t", [])]
+    inputs, prefixes, tail = plamo_hip.document_plan(parts)
+    assert inputs == [[449], [450], [451]]
+    assert prefixes == ["\t", "\r\n \n", "\n"]
+    assert tail == "\n\t"
+    for bad in ([], [S(" \n", [])]):
+        with pytest.raises(plamo_hip.PlamoError, match="No documents to translate"):
+            plamo_hip.document_plan(bad)
+
+
+def test_plan_against_restatement():
+    # DocumentPlan (OrderedOutput.swift:3-21) restated in a few lines, on random segment lists:
+    # documents keep their order and tokens, every whitespace run lands in exactly one prefix
+    # or the tail, and adjacent documents are separated by "\n"
+    import plamo_hip
+    rng = random.Random(3)
+    for _ in range(300):
+        parts = []
+        for _ in range(rng.randint(1, 9)):
+            if rng.random() < 0.5:
+                parts.append(plamo_hip.Segment(rng.choice(["", " ", "\n", "\r\n", "\t \n", "あ"]), []))
+            else:
+                parts.append(plamo_hip.Segment("doc", [rng.randint(0, 107519) for _ in range(rng.randint(1, 4))]))
+        want_inputs, want_prefixes, pending = [], [], ""
+        for p in parts:
+            if not p.tokens:
+                pending += p.text
+            else:
+                want_prefixes.append("\n" if want_inputs and not pending else pending)
+                want_inputs.append(list(p.tokens))
+                pending = ""
+        if not want_inputs:
+            with pytest.raises(plamo_hip.PlamoError):
+                plamo_hip.document_plan(parts)
+            continue
+        assert plamo_hip.document_plan(parts) == (want_inputs, want_prefixes, pending)
