@@ -893,12 +893,17 @@ void launch_gemm(bool packed, GemmEpilogue epi, const GemmParams& p, hipStream_t
         if (wide) launch_gemm_packed<256, 128, 4, 512>(epi, p, s);
         else launch_gemm_packed<128, 128, 2, 256>(epi, p, s);
     } else {
-        // wide projections (gate_up, qkv): 256 x 128 tiles on eight waves, three 64-deep stages
-        // (48 KB each): twice the MFMAs per barrier of 32-deep stages (gate_up 100 -> 72-77 us)
+        // gate_up: 256 x 128 tiles on eight waves, three 64-deep stages (48 KB each): twice the
+        // MFMAs per barrier of 32-deep stages (gate_up 100 -> 72-77 us); 2048 tokens make 768
+        // tiles, three per CU
+        // qkv (2304 rows): 128 x 192 tiles on eight waves (192 tiles; 256 x 128 makes 144 and
+        // leaves 112 CUs idle): 22.3 -> 19.7-20.2 us at 2048 tokens
         // 128 x 128 fallback (SwiGLU below 129 tokens): six 32-deep stages, five in flight
         // 1536-row projections (o, down): 128 x 96 tiles with four waves, 64-deep stages, so
         // 2048 tokens make exactly 256 tiles (128 x 128 left a quarter of the CUs idle)
-        if (wide) launch_gemm_dma<256, 128, 4, 512, 64, 3>(epi, p, s);
+        if (wide && epi == GEMM_SWIGLU) launch_gemm_dma<256, 128, 4, 512, 64, 3>(epi, p, s);
+        else if (wide && p.m % 192 == 0) launch_gemm_dma<128, 192, 4, 512, 64, 3>(epi, p, s);
+        else if (wide) launch_gemm_dma<256, 128, 4, 512, 64, 3>(epi, p, s);
         else if (epi != GEMM_SWIGLU && p.m % 96 == 0) launch_gemm_dma<128, 96, 4, 256, 64, 4>(epi, p, s);
         else launch_gemm_dma<128, 128, 4, 512, 32, 6>(epi, p, s);
     }
