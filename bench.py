@@ -15,6 +15,8 @@ each, stop on EOS) against batch-1 on the same segment; configs[4] .p12 long con
     python bench.py --kernels-only     # GEMV shapes + copy calibration (for rocprofv3 --pmc)
     python bench.py --prefill-only     # three 2048-token prefills (for rocprofv3 kernel traces)
     python bench.py --batch4-only      # the configs[3] batch4 measurement alone
+    python bench.py --timeline [--packed]  # in-step kernel durations of replayed decode steps
+                                           # (needs lib/libplamo_hip_timeline.so: make timeline)
 """
 import argparse
 import json
@@ -32,7 +34,6 @@ SHAPES = {"qkv": (2304, 1536), "o": (1536, 2048), "gate_up": (12288, 1536), "dow
           "head": (107520, 1536)}
 DOMINANT = "gate_up"  # largest share of the decode step's kernel time (profiles/)
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemv_gate_up_hbm_traffic.md")
-STEP_PROFILE = os.path.join(ROOT, "profiles", "decode_step_bs1_plain_and_p12.md")
 
 
 def log(*a):
@@ -112,156 +113,59 @@ def traffic_from_profile():
         return None
 
 
-def in_step_from_profile():
-    """The dominant GEMV's average duration inside the decode step, from the committed
-    rocprofv3 kernel trace of the step (the isolated launch above has no norm prologue and no
-    previous kernel to wait for)."""
-    try:
-        with open(STEP_PROFILE) as f:
-            m = re.search(r"in_step_gate_up_us:\s*([0-9.]+)", f.read())
-    except OSError:
-        return None
-    if not m:
-        return None
-    us = float(m.group(1))
-    return {"us": us, "GBps": round(37748736 / us / 1e3, 1), "frac": round(37748736 / us / 1e3 / HBM_PEAK_GBS, 4),
-            "source": os.path.relpath(STEP_PROFILE, ROOT)}
-
-
-def cpu_model_name():
-    """The host CPU's model name (what `lscpu` prints as "Model name")."""
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
-    except OSError:
-        pass
-    return None
-
-
-def cpu_baseline(model_dir, prompt, decode_tokens, runs=3):
-    """The CPU oracle (PyTorch FP32, BF16 rounding) on the host cores, bounded: configs[0]'s
-    64-token prefill and `decode_tokens` batch-1 decode steps, `runs` warm runs each (median),
-    and configs[1]'s GEMV shapes as FP32 matrix-vector products of the BF16-valued weights."""
-    import statistics
-    import numpy as np
-    import torch
-    from oracle import model as om
-    cores = len(os.sched_getaffinity(0))
-    torch.set_num_threads(cores)
-    w = om.Weights(model_dir)
-    o = om.Oracle(w, context=len(prompt) + decode_tokens + 1)
-    o.prefill(prompt)  # warm-up
-    pre, dec = [], []
-    for _ in range(runs):
-        o.reset()
-        t0 = time.perf_counter()
-        nxt = o.prefill(prompt)
-        t1 = time.perf_counter()
-        for _ in range(decode_tokens):
-            nxt = o.forward([nxt])
-        t2 = time.perf_counter()
-        pre.append(t1 - t0)
-        dec.append((t2 - t1) / decode_tokens)
-    gemv = {}
-    rng = np.random.default_rng(0)
-    for name, (m, n) in SHAPES.items():
-        wt = torch.from_numpy((rng.standard_normal((m, n), dtype=np.float32) * np.float32(0.02)))
-        wt = wt.to(torch.bfloat16).float()
-        x = torch.randn(n).to(torch.bfloat16).float()
-        torch.mv(wt, x)
-        ts = []
-        for _ in range(runs):
-            t0 = time.perf_counter()
-            torch.mv(wt, x)
-            ts.append(time.perf_counter() - t0)
-        gemv[name] = round(statistics.median(ts) * 1e6, 1)
-        del wt
-    step = statistics.median(dec)
-    return {"value": round(1.0 / step, 3), "unit": "tok/s", "cores": cores, "kind": "port",
-            "cpu_model": cpu_model_name(),
-            "prefill_s": round(statistics.median(pre), 3), "decode_step_s": round(step, 4),
-            "gemv_us": gemv, "runs": runs,
-            "sample": f"oracle/model.py FP32 CPU, median of {runs} warm runs: {len(prompt)}-token prefill "
-                      f"then {decode_tokens} batch-1 decode steps of the full model (configs[0]); "
-                      "configs[1] GEMV shapes as FP32 torch.mv of BF16-valued weights"}
-
-
-def bench_batch4(plamo_hip, np, model_dir):
-    """four segments, prompts of 512/384/256/128 random tokens, each decoding up to
-    2048 tokens (stop on EOS ids 1 / 16), one weight pass per step for all active lanes."""
-    lengths, limit = (512, 384, 256, 128), 2048
-    prompts = [np.random.default_rng(20 + i).integers(1024, 107520, n).tolist() for i, n in enumerate(lengths)]
-    rt = plamo_hip.Runtime(model_dir, 512 + limit + 8)
-    b = plamo_hip.Batch(rt)
-    b.generate([p[:16] for p in prompts], [8] * 4)  # warm-up (graph capture)
-    b.reset()
-    t0 = time.perf_counter()
-    outs = b.generate(prompts, [limit] * 4)
-    dt = time.perf_counter() - t0
-    produced = sum(len(ids) for ids, _ in outs)
-    # batch 1 on segment 0 with the same device loop, same limit
-    rt.reset()
-    rt.generate(prompts[0][:16], 8)
-    rt.reset()
-    t0 = time.perf_counter()
-    ids1, _ = rt.generate(prompts[0], limit)
-    dt1 = time.perf_counter() - t0
-    b.close()
+def step_timeline(plamo_hip, np, model_dir, sha, packed, steps=24):
+    """In-step kernel durations of graph-replayed decode steps (positions 80-128 after a
+    64-token prompt), from the device timestamps of the timeline library: each kernel's span
+    (first workgroup start to last workgroup end), the gaps between consecutive kernels, and
+    the step span, averaged over `steps` single-step replays."""
+    rt = plamo_hip.Runtime(model_dir, 64 + 16 + 2 * steps + 8, packed=packed, source_sha256=sha)
+    rt.prefill(np.random.default_rng(1).integers(1024, 107520, 64).tolist())
+    rt.bench_decode(16)
+    plamo_hip.timeline(clear=True)
+    spans, gaps, steps_us, event_ms = {}, [], [], []
+    for _ in range(steps):
+        # two replays: the first (untimed, with the loop's step_begin) sets up, the second is
+        # timed with HIP events and rewrites every slot but step_begin's, which is skipped
+        event_ms.append(rt.bench_decode(2))
+        t = plamo_hip.timeline(clear=True).astype(np.int64)
+        ran = []
+        for tag in range(plamo_hip.TIMELINE_TAGS):
+            if tag == 251:
+                continue
+            blk = t[tag][t[tag][:, 0] > 0]
+            if len(blk):
+                ran.append((int(blk[:, 0].min()), int(blk[:, 1].max()), tag))
+        ran.sort()
+        for (s0, e0, tag) in ran:
+            name = plamo_hip.timeline_name(tag)
+            kind = name.split(".")[-1]
+            spans.setdefault(kind, []).append((e0 - s0) / 100.0)  # 100 MHz ticks -> us
+        gaps += [(ran[i + 1][0] - ran[i][1]) / 100.0 for i in range(len(ran) - 1)]
+        steps_us.append((ran[-1][1] - ran[0][0]) / 100.0)
     rt.close()
-    res = {"segments": [len(ids) for ids, _ in outs], "reasons": [r for _, r in outs], "tokens": produced,
-           "s": round(dt, 4), "aggregate_tok_s": round(produced / dt, 1),
-           "bs1_same_segment_tok_s": round(len(ids1) / dt1, 1), "bs1_tokens": len(ids1)}
-    res["ratio_vs_bs1"] = round(res["aggregate_tok_s"] / res["bs1_same_segment_tok_s"], 3)
-    return res
+    res = {k: {"mean_us": round(float(np.mean(v)), 3), "launches_per_step": len(v) // steps}
+           for k, v in sorted(spans.items())}
+    return {"packed": packed, "steps": steps, "kernels": res,
+            "kernels_per_step": sum(r["launches_per_step"] for r in res.values()),
+            "kernel_us_per_step": round(sum(float(np.sum(v)) for v in spans.values()) / steps, 2),
+            "gap_mean_us": round(float(np.mean(gaps)), 3), "gap_min_us": round(float(np.min(gaps)), 3),
+            "step_span_us": round(float(np.mean(steps_us)), 2),
+            "event_ms_per_step": round(float(np.mean(event_ms)), 4)}
 
 
-def bench_long(plamo_hip, np, model_dir, sha):
-    """.p12 weights, 30,720-token prefill, then sampled decode (repetition 1.1,
-    frequency 0.2, no-repeat-ngram 4, on the GPU) to the 32,768-token cap.  Both phases are
-    timed inside the one generate call (the runtime's prefill / decode wall seconds, as
-    Main.swift:245-287 times them)."""
-    rt = plamo_hip.Runtime(model_dir, 32768, packed=True, source_sha256=sha)
-    prompt = np.random.default_rng(5).integers(1024, 107520, 30720).tolist()
-    rt.prefill(prompt[:2048])  # warm-up
-    rt.reset()
-    rt.set_sampling(1.1, 0.2, 0.0, 4)
-    ids, reason = rt.generate(prompt, 32768 - 30720)
-    st = rt.stats()
-    rt.set_sampling()
-    rt.close()
-    t_pre, t_dec = st["last_prefill_seconds"], max(st["last_decode_seconds"], 1e-9)
-    return {"prefill_tokens": 30720, "prefill_s": round(t_pre, 4), "prefill_tok_s": round(30720 / t_pre, 1),
-            "decode_tokens": len(ids), "stop": reason, "decode_s": round(t_dec, 4),
-            "decode_tok_s": round(len(ids) / t_dec, 1), "gpu_s": round(st["gpu_seconds"], 4)}
-
-
-def bench_tokenizer(plamo_hip, synth):
-    """Host-side tokenizer (Tokenizer.swift): load, encode and decode throughput of the native
-    library on ~1 MB of seeded text over the synthetic vocabulary's alphabet (no GPU work)."""
-    import random
-    path, alphabet = synth.ensure_tokenizer()
-    t0 = time.perf_counter()
-    tok = plamo_hip.Tokenizer(path)
-    load = time.perf_counter() - t0
-    rng = random.Random(7)
-    words = ["".join(rng.choice(alphabet) for _ in range(rng.randint(1, 9))) for _ in range(4096)]
-    text = " ".join(rng.choice(words) for _ in range(160000))[:1 << 20]
-    nbytes = len(text.encode())
-    enc, dec = [], []
-    for _ in range(3):
-        t0 = time.perf_counter()
-        ids = tok.encode(text)
-        enc.append(time.perf_counter() - t0)
-        t0 = time.perf_counter()
-        out = tok.decode_bytes(ids)
-        dec.append(time.perf_counter() - t0)
-    assert out == text.encode(), "tokenizer round trip"
-    tok.close()
-    return {"load_s": round(load, 3), "text_bytes": nbytes, "tokens": len(ids),
-            "encode_MBps": round(nbytes / min(enc) / 1e6, 2), "encode_tok_s": round(len(ids) / min(enc)),
-            "decode_MBps": round(nbytes / min(dec) / 1e6, 2), "cores": 1}
+def timeline_child(packed):
+    """step_timeline in a child process that loads lib/libplamo_hip_timeline.so (this process
+    holds the normal library); None when that library is not built."""
+    import subprocess
+    from plamo_hip import native
+    if not os.path.exists(native.TIMELINE_LIB_PATH):
+        return None
+    cmd = [sys.executable, os.path.abspath(__file__), "--timeline"] + (["--packed"] if packed else [])
+    out = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
+    if out.returncode != 0:
+        log(out.stderr[-2000:])
+        return None
+    return json.loads(out.stdout.strip().splitlines()[-1])
 
 
 def main():
@@ -274,6 +178,9 @@ def main():
     ap.add_argument("--kernels-only", action="store_true", help="GEMV shapes and a copy calibration only")
     ap.add_argument("--prefill-only", action="store_true", help="three 2048-token prefills only")
     ap.add_argument("--batch4-only", action="store_true", help="the configs[3] batch4 measurement only")
+    ap.add_argument("--timeline", action="store_true",
+                    help="in-step kernel durations from the timeline library (make timeline)")
+    ap.add_argument("--packed", action="store_true", help="with --timeline: .p12 weights")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one MI355X; multi-GPU runs are not part of it",
@@ -284,7 +191,13 @@ def main():
     import plamo_hip
     from plamo_hip import native, synth
 
+    if args.timeline:
+        native.LIB_PATH = native.TIMELINE_LIB_PATH
     native.load()
+    if args.timeline:
+        model_dir, sha = synth.ensure_model(packed=True)
+        print(json.dumps(step_timeline(plamo_hip, np, model_dir, sha, args.packed)), flush=True)
+        return
     if args.kernels_only:
         gemv = gemv_microbench(torch, native)
         cal = copy_calibration(torch)
@@ -363,6 +276,16 @@ def main():
     log(f"gemv: {json.dumps(gemv)}")
     dom = gemv[DOMINANT]["plain"]
 
+    timeline = {"plain": timeline_child(False), "p12": timeline_child(True)}
+    results["timeline"] = timeline
+    log(f"timeline: {json.dumps(timeline)}")
+    in_step = None
+    if timeline["plain"] and DOMINANT in timeline["plain"]["kernels"]:
+        us = timeline["plain"]["kernels"][DOMINANT]["mean_us"]
+        in_step = {"us": us, "GBps": round(37748736 / us / 1e3, 1), "frac": round(37748736 / us / 1e3 / HBM_PEAK_GBS, 4),
+                   "source": "device timestamps of graph-replayed steps (lib/libplamo_hip_timeline.so, "
+                             "bench.py --timeline)"}
+
     cpu = None
     if not args.no_cpu:
         log("cpu baseline: oracle on host cores")
@@ -385,7 +308,7 @@ def main():
                      "kernel": f"gemv {DOMINANT} 12288x1536 BF16, one row, weights streamed from HBM "
                                "(37,748,736 B per launch)",
                      "scope": "isolated launch (configs[1] shape, plain activation prologue), HIP events",
-                     "in_step": in_step_from_profile()},
+                     "in_step": in_step},
         "cpu_baseline": cpu,
         "details": results,
     }

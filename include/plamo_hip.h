@@ -164,6 +164,17 @@ int plamo_batch_positions(plamo_batch* b, int32_t* out, int32_t capacity, int32_
  * (BatchMapTests.swift:15-18 fills them with 0xff bytes, NaN) to show unused KV is never read. */
 int plamo_batch_fill_kv(plamo_batch* b, uint16_t bits);
 
+/* Step timeline, for profiling the replayed decode graph (no counterpart in the reference,
+ * whose ProfileTests.swift times kernels one dispatch at a time).  Libraries built with
+ * `make timeline` (lib/libplamo_hip_timeline.so) record every decode-step kernel's
+ * per-workgroup start and end in s_memrealtime ticks (100 MHz): `out` receives
+ * PLAMO_TIMELINE_WORDS words, [tag][block][start, end], tag = layer * 8 + (0 qkv,
+ * 1 attention, 2 attention merge, 3 o, 4 gate_up, 5 down), 200 LM head, 250 head merge,
+ * 251 step begin, block < 1024; each launch rewrites its tag's slots, zero = not run.
+ * `clear` zeroes the table after the copy.  The normal library returns PLAMO_EINVAL. */
+#define PLAMO_TIMELINE_WORDS (256 * 1024 * 2)
+int plamo_timeline(uint64_t* out, size_t words, int32_t clear, char* err, size_t errlen);
+
 /* ---- Lane scheduler (BatchDecode.swift:8-47) --------------------------------------- */
 
 /* step: receives `count` tokens (<0 = nil) and writes `count` predictions; returns 0 to

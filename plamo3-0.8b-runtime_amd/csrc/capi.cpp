@@ -887,6 +887,10 @@ int plamo_ordered_finish(plamo_ordered* o, int32_t lane, const char* reason, cha
 
 void plamo_ordered_close(plamo_ordered* o) { delete o; }
 
+int plamo_timeline(uint64_t* out, size_t words, int32_t clear, char* err, size_t errlen) {
+    return guard(err, errlen, [&] { plamo::timeline_copy(out, words, clear != 0); });
+}
+
 int plamo_translation_prompt(const char* text, size_t len, const char* target, char* out, size_t cap,
                              size_t* n_out, char* err, size_t errlen) {
     return guard(err, errlen, [&] {

@@ -27,6 +27,28 @@ using namespace dev;
 
 namespace {
 
+// ------------------------------------------------------------------------ step timeline
+#ifdef PLAMO_TIMELINE
+__device__ uint64_t g_timeline[TIMELINE_TAGS * TIMELINE_BLOCKS * 2];
+// Thread 0 of each workgroup stores the workgroup's first and last stamp when it ends.
+struct TimelineScope {
+    uint64_t t0;
+    uint32_t tag;
+    __device__ explicit TimelineScope(uint32_t t) : t0(__builtin_amdgcn_s_memrealtime()), tag(t) {}
+    __device__ ~TimelineScope() {
+        if (threadIdx.x != 0 || tag >= uint32_t(TIMELINE_TAGS)) return;
+        const uint32_t b = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+        if (b >= uint32_t(TIMELINE_BLOCKS)) return;
+        const size_t i = (size_t(tag) * TIMELINE_BLOCKS + b) * 2;
+        g_timeline[i] = t0;
+        g_timeline[i + 1] = __builtin_amdgcn_s_memrealtime();
+    }
+};
+#define PLAMO_TIMELINE_SCOPE(tag) TimelineScope timeline_scope_(tag)
+#else
+#define PLAMO_TIMELINE_SCOPE(tag) (void)0
+#endif
+
 // Weight rows per wave group: four for one activation row; with four rows the
 // arithmetic per weight byte quadruples, so groups shrink to spread it over more waves
 // (SwiGLU: one gate and one up row, three groups for each of a CU's eight waves).
@@ -454,6 +476,7 @@ __device__ __forceinline__ float sampled(float l, int32_t count, bool banned, co
 // ------------------------------------------------------------------------------- GEMV
 template <int N, bool PACKED, int MAXR, int PRO, int EPI, bool STATE>
 __global__ __launch_bounds__(64 * gemv_waves(N, MAXR, EPI)) void gemv_kernel(const GemvParams p) {
+    PLAMO_TIMELINE_SCOPE(p.tag);
     constexpr int NWV = gemv_waves(N, MAXR, EPI);
     constexpr int IT = N / 512;
     constexpr int U = gemv_u<N, MAXR, EPI>();
@@ -751,6 +774,7 @@ __device__ __forceinline__ void state_out(StepState* st, const StepState& ls) {
 __device__ void begin_step(StepState& ls, const DecodeBuffers& b, int* s_stop);
 
 __global__ __launch_bounds__(256) void head_merge_kernel(DecodeBuffers b, int blocks, int begin_next) {
+    PLAMO_TIMELINE_SCOPE(TL_HEAD_MERGE);
     __shared__ float cv[ROWS * 4];
     __shared__ uint32_t ci[ROWS * 4];
     __shared__ StepState ls;
@@ -821,6 +845,7 @@ constexpr int KS = 132;              // padded LDS row of rotated keys (16-byte 
 template <bool FULL>
 __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
 #pragma clang fp contract(off)  // fixed rounding sequence, reproduced by the CPU oracle
+    PLAMO_TIMELINE_SCOPE(p.tag);
     __shared__ __align__(16) float qs[HG * HEAD_DIM];
     __shared__ __align__(16) float ks[KP * KS];
     __shared__ __align__(16) uint16_t vs[KP * HEAD_DIM];
@@ -1233,6 +1258,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
 // kernel's own merge: M = max_p m_p, w_p = exp(m_p - M), den = sum l_p w_p, num = sum o_p w_p.
 __global__ __launch_bounds__(256) void attn_merge_kernel(const AttnParams p) {
 #pragma clang fp contract(off)  // fixed rounding sequence, reproduced by the CPU oracle
+    PLAMO_TIMELINE_SCOPE(p.tag + 1);
     constexpr uint32_t MAXP = uint32_t(MAX_CONTEXT / KP);
     static_assert(MAXP <= 512, "two statistics per thread");
     __shared__ __align__(16) float os[MAXP * 32];
@@ -1402,6 +1428,7 @@ __device__ void begin_step(StepState& ls, const DecodeBuffers& b, int* s_stop) {
 }
 
 __global__ __launch_bounds__(256) void step_begin_kernel(DecodeBuffers b) {
+    PLAMO_TIMELINE_SCOPE(TL_STEP_BEGIN);
     __shared__ StepState ls;
     __shared__ int s_stop;
     state_in(ls, b.state);
@@ -1670,6 +1697,22 @@ void launch_attn_state(StepState* st, uint32_t* tickets, const int32_t* pos, int
 void launch_fill_u32(uint32_t* p, uint32_t value, size_t count, hipStream_t s) {
     if (!count) return;
     hipLaunchKernelGGL(fill_u32_kernel, dim3(unsigned((count + 255) / 256)), dim3(256), 0, s, p, value, count);
+}
+
+void timeline_copy(uint64_t* out, size_t words, bool clear) {
+#ifdef PLAMO_TIMELINE
+    const size_t n = size_t(TIMELINE_TAGS) * TIMELINE_BLOCKS * 2;
+    if (out && words < n) throw Error(E_INVAL, "timeline buffer too small");
+    void* dev = nullptr;
+    PLAMO_HIP(hipGetSymbolAddress(&dev, HIP_SYMBOL(g_timeline)));
+    if (out) PLAMO_HIP(hipMemcpy(out, dev, n * sizeof(uint64_t), hipMemcpyDeviceToHost));
+    if (clear) PLAMO_HIP(hipMemset(dev, 0, n * sizeof(uint64_t)));
+#else
+    (void)out;
+    (void)words;
+    (void)clear;
+    throw Error(E_INVAL, "this library was built without the step timeline (make timeline)");
+#endif
 }
 
 }  // namespace plamo

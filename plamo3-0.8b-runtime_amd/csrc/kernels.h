@@ -84,6 +84,7 @@ struct GemvParams {
     float* out;               // ROUND: FP32 [rows][m]
     uint16_t* out16;          // LOGITS/BF16: [rows][m]; SWIGLU: BF16 [rows][m/2]
     DecodeBuffers bufs;       // LOGITS: sampler + argmax partials + state update
+    uint32_t tag;             // step-timeline slot of this launch (timeline builds only)
 };
 
 struct AttnParams {
@@ -104,9 +105,21 @@ struct AttnParams {
     uint16_t* out16;          // BF16 [rows][2048]
     uint32_t defer;           // rows with more partitions than this (0: none) are merged by
                               // attn_merge_kernel instead of the attention kernel's last workgroup
+    uint32_t tag;             // step-timeline slot (the merge kernel uses tag + 1)
 };
 // Partitions a global-layer row may have before its merge moves to attn_merge_kernel.
 constexpr uint32_t ATTN_MERGE_INLINE = 64;
+
+// Step timeline (builds with -DPLAMO_TIMELINE): per-workgroup start/end stamps of the
+// decode-step kernels in a [TIMELINE_TAGS][TIMELINE_BLOCKS][2] table of s_memrealtime
+// ticks (100 MHz), rewritten by every launch with the same tag.  Tags: layer * 8 + 0 qkv,
+// 1 attention, 2 attention merge, 3 o, 4 gate_up, 5 down; 200 LM head, 250 head merge,
+// 251 step begin.
+constexpr int TIMELINE_TAGS = 256, TIMELINE_BLOCKS = 1024;
+constexpr uint32_t TL_HEAD = 200, TL_HEAD_MERGE = 250, TL_STEP_BEGIN = 251;
+// Copies the table out (`out` non-null, `words` = TIMELINE_TAGS * TIMELINE_BLOCKS * 2) and/or
+// clears it; throws E_INVAL in builds without the timeline.
+void timeline_copy(uint64_t* out, size_t words, bool clear);
 
 // decode.hip
 int gemv_group_rows(int n, int maxr, Epilogue epi);     // weight rows per wave group

@@ -308,6 +308,7 @@ void Engine::enqueue_head(const uint16_t* in, const uint16_t* resid_in, int in_r
     g.m = VOCAB;
     g.w = m.head.w;
     g.table = m.head.table;
+    g.tag = TL_HEAD;
     g.in16 = in;
     g.resid16_in = resid_in;
     g.resid16_out = resid_scratch;
@@ -330,6 +331,7 @@ void Engine::enqueue_head16(bool loop) {
     g.m = VOCAB;
     g.w = m.head.w;
     g.table = m.head.table;
+    g.tag = TL_HEAD;
     g.in16 = proj;
     g.resid16_in = x1;
     g.resid16_out = x0;  // final residual, not read again
@@ -361,6 +363,7 @@ void Engine::enqueue_step(bool head, bool loop) {
         g.m = QKV;
         g.w = L.qkv.w;
         g.table = L.qkv.table;
+        g.tag = uint32_t(l) * 8;
         g.resid16_out = x0;
         g.g_next = L.pre;
         g.out = qkv;
@@ -390,6 +393,7 @@ void Engine::enqueue_step(bool head, bool loop) {
         a.parts = full ? decode_parts_global : decode_parts_local;
         a.tickets = attn_tickets;
         a.out16 = att;
+        a.tag = uint32_t(l) * 8 + 1;
         // long global-layer rings: rows past ATTN_MERGE_INLINE partitions merge in their own kernel
         a.defer = full && a.parts > ATTN_MERGE_INLINE ? ATTN_MERGE_INLINE : 0;
         launch_attention(full, a, ROWS, stream);
@@ -400,6 +404,7 @@ void Engine::enqueue_step(bool head, bool loop) {
         o.m = HIDDEN;
         o.w = L.o.w;
         o.table = L.o.table;
+        o.tag = uint32_t(l) * 8 + 3;
         o.in16 = att;
         o.out16 = proj;
         launch_gemv(ATTN, pk, maxr, PRO_PLAIN16, EPI_BF16, o, gemv_blocks(ATTN, maxr, EPI_BF16, HIDDEN), stream);
@@ -409,6 +414,7 @@ void Engine::enqueue_step(bool head, bool loop) {
         u.m = 2 * INTER;
         u.w = L.up.w;
         u.table = L.up.table;
+        u.tag = uint32_t(l) * 8 + 4;
         u.in16 = proj;
         u.resid16_in = x0;
         u.resid16_out = x1;
@@ -423,6 +429,7 @@ void Engine::enqueue_step(bool head, bool loop) {
         d.m = HIDDEN;
         d.w = L.down.w;
         d.table = L.down.table;
+        d.tag = uint32_t(l) * 8 + 5;
         d.in16 = act;
         d.out16 = proj;
         launch_gemv(INTER, pk, maxr, PRO_PLAIN16, EPI_BF16, d, gemv_blocks(INTER, maxr, EPI_BF16, HIDDEN), stream);

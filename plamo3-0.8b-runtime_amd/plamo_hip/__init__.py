@@ -409,6 +409,24 @@ class TokenStream:
             pass
 
 
+TIMELINE_TAGS, TIMELINE_BLOCKS = 256, 1024
+TIMELINE_KINDS = {0: "qkv", 1: "attention", 2: "attention_merge", 3: "o", 4: "gate_up", 5: "down"}
+
+
+def timeline(clear=True):
+    """The step timeline of a library built with `make timeline` (plamo_timeline):
+    uint64 [256 tags][1024 blocks][start, end] s_memrealtime ticks (100 MHz), zero where a
+    block did not run; `clear` zeroes the device table after the copy."""
+    out = np.zeros(TIMELINE_TAGS * TIMELINE_BLOCKS * 2, dtype=np.uint64)
+    native.call(native.load().plamo_timeline, out.ctypes.data, out.size, 1 if clear else 0)
+    return out.reshape(TIMELINE_TAGS, TIMELINE_BLOCKS, 2)
+
+
+def timeline_name(tag):
+    return {200: "head", 250: "head_merge", 251: "step_begin"}.get(
+        tag, f"L{tag // 8}.{TIMELINE_KINDS.get(tag % 8, tag % 8)}")
+
+
 Segment = collections.namedtuple("Segment", "text tokens")
 Segment.__doc__ = "A source piece (Segments.swift:4-7): text with prompt tokens, or a whitespace run (no tokens)."
 

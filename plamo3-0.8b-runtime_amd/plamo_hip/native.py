@@ -8,6 +8,8 @@ import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(os.path.dirname(_HERE), "lib", "libplamo_hip.so")
+# the same library with the step timeline compiled in (make timeline)
+TIMELINE_LIB_PATH = os.path.join(os.path.dirname(_HERE), "lib", "libplamo_hip_timeline.so")
 HEADER_PATH = os.path.join(os.path.dirname(os.path.dirname(_HERE)), "include", "plamo_hip.h")
 
 VOCAB, HIDDEN = 107520, 1536
@@ -139,6 +141,8 @@ _SIGNATURES = {
     "plamo_translation_prompt": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_size_t, ctypes.c_char_p, ctypes.c_char_p,
                                                 ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t), ctypes.c_char_p,
                                                 ctypes.c_size_t]),
+    "plamo_timeline": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int32, ctypes.c_char_p,
+                                      ctypes.c_size_t]),
     "plamo_document_plan": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                            ctypes.c_int32, ctypes.POINTER(ctypes.c_void_p), ctypes.c_char_p,
                                            ctypes.c_size_t]),
