@@ -91,7 +91,10 @@ struct Staged {
     static constexpr int V16 = (N + 2047) / 2048; // PLAIN16: 8 BF16 per thread and row
     static constexpr int E = HIDDEN / 256;       // norm prologues: elements per thread (6t .. 6t+5)
     float4 v[PRO == PRO_PLAIN ? RQ : 1][V];
-    uint4 h[PRO == PRO_PLAIN16 ? RQ : 1][V16];
+    uint4 h[PRO == PRO_PLAIN16 || PRO == PRO_MERGE ? RQ : 1][V16];
+    float4 mo[PRO == PRO_MERGE ? int(MERGE_IN_O) : 1][2];  // MERGE: partition outputs, 8 dims
+    float2 ml[PRO == PRO_MERGE ? int(MERGE_IN_O) : 1];     // MERGE: partition (m, l) of the head
+    uint32_t pos;                                          // MERGE: the row's position
     float2 a[PRO == PRO_RESID ? RQ : 1][E / 2];   // RESID: projection output
     float2 r[PRO == PRO_RESID ? RQ : 1][E / 2];   // RESID: residual stream
     uint32_t a16[PRO == PRO_RESID16 ? RQ : 1][E / 2];  // RESID16: projection output (BF16 pairs)
@@ -126,6 +129,22 @@ __device__ __forceinline__ void stage_load(const GemvParams& p, int rb, int q0, 
                 const int e = (tid + 256 * k) * 8;
                 S.h[qi][k] = *reinterpret_cast<const uint4*>(p.in16 + qq * N + (e < N ? e : N - 8));
             }
+        }
+    } else if constexpr (PRO == PRO_MERGE) {
+        // thread t: dims 8t .. 8t+7 = dims 8(t % 16) .. of head t / 16.  Both sources are
+        // requested: the attention output, and the first MERGE_IN_O partitions of the head
+        // (indices past the buffer's partitions re-read the last one); which one is used
+        // depends on the row's position, known only when the step state arrives.
+        static_assert(N == ATTN && RQ == 1 && V16 == 1, "one-row o projection");
+        S.h[0][0] = *reinterpret_cast<const uint4*>(p.in16 + tid * 8);
+        const uint32_t h = uint32_t(tid) >> 4, d0 = (uint32_t(tid) & 15u) * 8;
+#pragma unroll
+        for (uint32_t k = 0; k < MERGE_IN_O; ++k) {
+            const uint32_t kk = k < p.parts ? k : p.parts - 1;
+            const float* o = p.part_o + (size_t(kk) * HEADS + h) * HEAD_DIM + d0;
+            S.mo[k][0] = *reinterpret_cast<const float4*>(o);
+            S.mo[k][1] = *reinterpret_cast<const float4*>(o + 4);
+            S.ml[k] = make_float2(p.part_m[kk * HEADS + h], p.part_l[kk * HEADS + h]);
         }
     } else {
         static_assert(N == HIDDEN && E == 6, "norm prologue is 1536 wide");
@@ -210,6 +229,43 @@ __device__ __forceinline__ void stage_finish(const GemvParams& p, int rows, int 
                 }
             }
         }
+    } else if constexpr (PRO == PRO_MERGE) {
+        // The attention kernel's merge (same operations, same partition order): M = max m_p,
+        // w_p = exp(m_p - M), den = sum l_p w_p, num = sum o_p w_p, out = bf16(num / den).
+#pragma clang fp contract(off)
+        const uint32_t count = p.merge_full ? S.pos + 1 : (S.pos > uint32_t(WINDOW - 1) ? uint32_t(WINDOW) : S.pos + 1);
+        const uint32_t nparts = (count + KEYS_PER_PART - 1) / KEYS_PER_PART;
+        float v[8];
+        if (nparts >= 2 && nparts <= MERGE_IN_O) {
+            float M = NEG_INF;
+#pragma unroll
+            for (uint32_t k = 0; k < MERGE_IN_O; ++k)
+                if (k < nparts) M = fmaxf(M, S.ml[k].x);
+            float num[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, den = 0.f;
+#pragma unroll
+            for (uint32_t k = 0; k < MERGE_IN_O; ++k) {
+                if (k >= nparts) break;
+                const float w = exp_det(S.ml[k].x - M);
+                den = den + S.ml[k].y * w;
+                const float o[8] = {S.mo[k][0].x, S.mo[k][0].y, S.mo[k][0].z, S.mo[k][0].w,
+                                    S.mo[k][1].x, S.mo[k][1].y, S.mo[k][1].z, S.mo[k][1].w};
+#pragma unroll
+                for (int j = 0; j < 8; ++j) num[j] = num[j] + o[j] * w;
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = roundbf(num[j] / den);
+        } else {
+            const uint4 hw = S.h[0][0];
+            const uint32_t w4[4] = {hw.x, hw.y, hw.z, hw.w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                v[2 * j] = lo(w4[j]);
+                v[2 * j + 1] = hi(w4[j]);
+            }
+        }
+        float* d = reinterpret_cast<float*>(xs) + xpos(tid * 8);
+        *reinterpret_cast<float4*>(d) = make_float4(v[0], v[1], v[2], v[3]);
+        *reinterpret_cast<float4*>(d + 256) = make_float4(v[4], v[5], v[6], v[7]);
     } else if constexpr (PRO == PRO_PLAIN16) {
 #pragma unroll
         for (int qi = 0; qi < RQ; ++qi) {
@@ -532,11 +588,12 @@ __global__ __launch_bounds__(64 * gemv_waves(N, MAXR, EPI)) void gemv_kernel(con
         rows_of(g < groups ? g : groups - 1, wrow);
         request_table<N, U, IT>(p, wrow, lane, tab);
     }
-    uint32_t stopped = 0, srows = 0;
+    uint32_t stopped = 0, srows = 0, spos = 0;
     if constexpr (STATE) {
         const StepState* sv = st + (threadIdx.x & p.lane_mask);
         stopped = sv->stopped;
         srows = sv->rows;
+        if constexpr (PRO == PRO_MERGE) spos = sv->pos[0];
     }
     Staged<N, RQ, PRO> S;
     stage_load<N, RQ, PRO>(p, p.rows < MAXR ? p.rows : MAXR, q0, S);
@@ -581,6 +638,7 @@ __global__ __launch_bounds__(64 * gemv_waves(N, MAXR, EPI)) void gemv_kernel(con
     uint32_t orow_packed = 0;  // lanes are below 4: one byte each
 #pragma unroll
     for (int q = 0; q < MAXR; ++q) orow_packed |= (orow[q] & 0xffu) << (8 * q);
+    S.pos = spos;
     stage_finish<N, MAXR, RQ, PRO>(p, rows, q0, S, xs, red);
     __syncthreads();
     auto decode_all = [&](const WRaw<PACKED> (&cur)[U][IT], uint4 (&w)[U][IT]) {
@@ -1086,6 +1144,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
         }
     }
     if (nparts == 1) return;
+    if (p.merge_in_o && nparts <= MERGE_IN_O) return;  // the o projection's prologue merges
     if (p.defer != 0 && nparts > p.defer) return;  // attn_merge_kernel merges this row
     // ticket: the last workgroup of this (row, head group) merges the partitions; every
     // wave's partition stores have completed before the ticket is taken
@@ -1597,6 +1656,15 @@ void gemv_dispatch_epi(Prologue pro, Epilogue epi, const GemvParams& p, int bloc
     if (pro == PRO_PLAIN16) {
         if (epi == EPI_BF16) PLAMO_GEMV(PRO_PLAIN16, EPI_BF16);
         else throw Error(E_INVAL, "unsupported GEMV variant");
+        return;
+    }
+    if (pro == PRO_MERGE) {
+        if constexpr (N == ATTN && MAXR == 1) {
+            if (epi == EPI_BF16) PLAMO_GEMV(PRO_MERGE, EPI_BF16);
+            else throw Error(E_INVAL, "unsupported GEMV variant");
+        } else {
+            throw Error(E_INVAL, "the merging prologue is the one-row o projection's");
+        }
         return;
     }
     if constexpr (N == HIDDEN) {

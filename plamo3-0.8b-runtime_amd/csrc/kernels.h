@@ -56,7 +56,11 @@ struct DecodeBuffers {
     uint32_t* tickets;        // [1] spare ticket, zero between launches
 };
 
-enum Prologue { PRO_PLAIN = 0, PRO_EMBED = 1, PRO_RESID = 2, PRO_PLAIN16 = 3, PRO_RESID16 = 4 };
+// PRO_MERGE: the one-row o projection whose prologue merges the attention partitions of a
+// row with 2..MERGE_IN_O of them (the attention kernel then skips its own merge), else reads
+// the attention output as PRO_PLAIN16 does.
+enum Prologue { PRO_PLAIN = 0, PRO_EMBED = 1, PRO_RESID = 2, PRO_PLAIN16 = 3, PRO_RESID16 = 4, PRO_MERGE = 5 };
+constexpr uint32_t MERGE_IN_O = 6;  // partitions (64 keys each) the o prologue merges
 enum Epilogue { EPI_ROUND = 0, EPI_SWIGLU = 1, EPI_LOGITS = 2, EPI_BF16 = 3 };
 
 struct GemvParams {
@@ -85,6 +89,12 @@ struct GemvParams {
     uint16_t* out16;          // LOGITS/BF16: [rows][m]; SWIGLU: BF16 [rows][m/2]
     DecodeBuffers bufs;       // LOGITS: sampler + argmax partials + state update
     uint32_t tag;             // step-timeline slot of this launch (timeline builds only)
+    // MERGE: the attention partition buffers of the layer and its geometry
+    const float* part_m;
+    const float* part_l;
+    const float* part_o;
+    uint32_t parts;           // partitions per row in the buffers
+    uint32_t merge_full;      // global layer (all keys visible), else the 2048-key window
 };
 
 struct AttnParams {
@@ -106,6 +116,8 @@ struct AttnParams {
     uint32_t defer;           // rows with more partitions than this (0: none) are merged by
                               // attn_merge_kernel instead of the attention kernel's last workgroup
     uint32_t tag;             // step-timeline slot (the merge kernel uses tag + 1)
+    uint32_t merge_in_o;      // rows with 2..MERGE_IN_O partitions are merged by the next
+                              // kernel (the o GEMV's PRO_MERGE prologue): no ticket, no merge
 };
 // Partitions a global-layer row may have before its merge moves to attn_merge_kernel.
 constexpr uint32_t ATTN_MERGE_INLINE = 64;

@@ -394,6 +394,8 @@ void Engine::enqueue_step(bool head, bool loop) {
         a.tickets = attn_tickets;
         a.out16 = att;
         a.tag = uint32_t(l) * 8 + 1;
+        // batch 1: rows of 2..MERGE_IN_O partitions are merged by the o projection's prologue
+        a.merge_in_o = maxr == 1 ? 1u : 0u;
         // long global-layer rings: rows past ATTN_MERGE_INLINE partitions merge in their own kernel
         a.defer = full && a.parts > ATTN_MERGE_INLINE ? ATTN_MERGE_INLINE : 0;
         launch_attention(full, a, ROWS, stream);
@@ -407,7 +409,13 @@ void Engine::enqueue_step(bool head, bool loop) {
         o.tag = uint32_t(l) * 8 + 3;
         o.in16 = att;
         o.out16 = proj;
-        launch_gemv(ATTN, pk, maxr, PRO_PLAIN16, EPI_BF16, o, gemv_blocks(ATTN, maxr, EPI_BF16, HIDDEN), stream);
+        o.part_m = part_m;
+        o.part_l = part_l;
+        o.part_o = part_o;
+        o.parts = a.parts;
+        o.merge_full = full ? 1u : 0u;
+        launch_gemv(ATTN, pk, maxr, maxr == 1 ? PRO_MERGE : PRO_PLAIN16, EPI_BF16, o,
+                    gemv_blocks(ATTN, maxr, EPI_BF16, HIDDEN), stream);
         GemvParams u{};
         u.state = state;
         u.rows = ROWS;

@@ -82,3 +82,33 @@ def test_sampling_controls_bit_exact(model_dir, oracle_weights, golden):
         assert np.array_equal(rt.logit_bits(), bits)
         assert nxt == sampler.select(bf_np(bits).copy(), generated, penalty, ngram, frequency)
     rt.close()
+
+
+@pytest.mark.parametrize("prompt_len", [128, 190, 320])
+def test_decode_merges_in_the_o_projection_bit_exact(model_dir, oracle_weights, prompt_len):
+    # rows of 2..6 attention partitions (129..384 keys) are merged by the o projection's
+    # prologue instead of the attention kernel: the twin (which merges in partition order,
+    # oracle/exact.py) must still match bit for bit.  The GPU's KV after a plain prefill is
+    # handed to the twin, as in the long-context test; 3-6 partitions are crossed on the way.
+    d, _ = model_dir
+    rt = plamo_hip.Runtime(d, prompt_len + 80)
+    prompt = np.random.default_rng(prompt_len).integers(1024, 107520, prompt_len).tolist()
+    t = rt.prefill(prompt)
+    ex = exact.ExactDecoder(oracle_weights, prompt_len + 80, rt.stats()["local_capacity"])
+    for layer in range(16):
+        k, v = rt.kv(layer)
+        ex.keys[layer][:] = k
+        ex.values[layer][:] = v
+    for pos in range(prompt_len, prompt_len + 6):
+        got = rt.forward([t])
+        bits, hidden, want = ex.step(t, pos)
+        assert np.array_equal(rt.logit_bits(), bits), pos
+        assert np.array_equal(rt.hidden().view(np.uint32), hidden.view(np.uint32)), pos
+        assert got == want, pos
+        t = got
+    for layer in range(16):
+        k, v = rt.kv(layer)
+        n = prompt_len + 6
+        assert np.array_equal(k[:n], ex.keys[layer][:n]) and np.array_equal(v[:n], ex.values[layer][:n]), layer
+    print(f"  positions {prompt_len}..{prompt_len + 5}: bit-exact", flush=True)
+    rt.close()
