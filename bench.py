@@ -113,6 +113,142 @@ def traffic_from_profile():
         return None
 
 
+def cpu_model_name():
+    """The host CPU's model name (what `lscpu` prints as "Model name")."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
+def cpu_baseline(model_dir, prompt, decode_tokens, runs=3):
+    """The CPU oracle (PyTorch FP32, BF16 rounding) on the host cores, bounded: configs[0]'s
+    64-token prefill and `decode_tokens` batch-1 decode steps, `runs` warm runs each (median),
+    and configs[1]'s GEMV shapes as FP32 matrix-vector products of the BF16-valued weights."""
+    import statistics
+    import numpy as np
+    import torch
+    from oracle import model as om
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    w = om.Weights(model_dir)
+    o = om.Oracle(w, context=len(prompt) + decode_tokens + 1)
+    o.prefill(prompt)  # warm-up
+    pre, dec = [], []
+    for _ in range(runs):
+        o.reset()
+        t0 = time.perf_counter()
+        nxt = o.prefill(prompt)
+        t1 = time.perf_counter()
+        for _ in range(decode_tokens):
+            nxt = o.forward([nxt])
+        t2 = time.perf_counter()
+        pre.append(t1 - t0)
+        dec.append((t2 - t1) / decode_tokens)
+    gemv = {}
+    rng = np.random.default_rng(0)
+    for name, (m, n) in SHAPES.items():
+        wt = torch.from_numpy((rng.standard_normal((m, n), dtype=np.float32) * np.float32(0.02)))
+        wt = wt.to(torch.bfloat16).float()
+        x = torch.randn(n).to(torch.bfloat16).float()
+        torch.mv(wt, x)
+        ts = []
+        for _ in range(runs):
+            t0 = time.perf_counter()
+            torch.mv(wt, x)
+            ts.append(time.perf_counter() - t0)
+        gemv[name] = round(statistics.median(ts) * 1e6, 1)
+        del wt
+    step = statistics.median(dec)
+    return {"value": round(1.0 / step, 3), "unit": "tok/s", "cores": cores, "kind": "port",
+            "cpu_model": cpu_model_name(),
+            "prefill_s": round(statistics.median(pre), 3), "decode_step_s": round(step, 4),
+            "gemv_us": gemv, "runs": runs,
+            "sample": f"oracle/model.py FP32 CPU, median of {runs} warm runs: {len(prompt)}-token prefill "
+                      f"then {decode_tokens} batch-1 decode steps of the full model (configs[0]); "
+                      "configs[1] GEMV shapes as FP32 torch.mv of BF16-valued weights"}
+
+
+def bench_batch4(plamo_hip, np, model_dir):
+    """four segments, prompts of 512/384/256/128 random tokens, each decoding up to
+    2048 tokens (stop on EOS ids 1 / 16), one weight pass per step for all active lanes."""
+    lengths, limit = (512, 384, 256, 128), 2048
+    prompts = [np.random.default_rng(20 + i).integers(1024, 107520, n).tolist() for i, n in enumerate(lengths)]
+    rt = plamo_hip.Runtime(model_dir, 512 + limit + 8)
+    b = plamo_hip.Batch(rt)
+    b.generate([p[:16] for p in prompts], [8] * 4)  # warm-up (graph capture)
+    b.reset()
+    t0 = time.perf_counter()
+    outs = b.generate(prompts, [limit] * 4)
+    dt = time.perf_counter() - t0
+    produced = sum(len(ids) for ids, _ in outs)
+    # batch 1 on segment 0 with the same device loop, same limit
+    rt.reset()
+    rt.generate(prompts[0][:16], 8)
+    rt.reset()
+    t0 = time.perf_counter()
+    ids1, _ = rt.generate(prompts[0], limit)
+    dt1 = time.perf_counter() - t0
+    b.close()
+    rt.close()
+    res = {"segments": [len(ids) for ids, _ in outs], "reasons": [r for _, r in outs], "tokens": produced,
+           "s": round(dt, 4), "aggregate_tok_s": round(produced / dt, 1),
+           "bs1_same_segment_tok_s": round(len(ids1) / dt1, 1), "bs1_tokens": len(ids1)}
+    res["ratio_vs_bs1"] = round(res["aggregate_tok_s"] / res["bs1_same_segment_tok_s"], 3)
+    return res
+
+
+def bench_long(plamo_hip, np, model_dir, sha):
+    """.p12 weights, 30,720-token prefill, then sampled decode (repetition 1.1,
+    frequency 0.2, no-repeat-ngram 4, on the GPU) to the 32,768-token cap.  Both phases are
+    timed inside the one generate call (the runtime's prefill / decode wall seconds, as
+    Main.swift:245-287 times them)."""
+    rt = plamo_hip.Runtime(model_dir, 32768, packed=True, source_sha256=sha)
+    prompt = np.random.default_rng(5).integers(1024, 107520, 30720).tolist()
+    rt.prefill(prompt[:2048])  # warm-up
+    rt.reset()
+    rt.set_sampling(1.1, 0.2, 0.0, 4)
+    ids, reason = rt.generate(prompt, 32768 - 30720)
+    st = rt.stats()
+    rt.set_sampling()
+    rt.close()
+    t_pre, t_dec = st["last_prefill_seconds"], max(st["last_decode_seconds"], 1e-9)
+    return {"prefill_tokens": 30720, "prefill_s": round(t_pre, 4), "prefill_tok_s": round(30720 / t_pre, 1),
+            "decode_tokens": len(ids), "stop": reason, "decode_s": round(t_dec, 4),
+            "decode_tok_s": round(len(ids) / t_dec, 1), "gpu_s": round(st["gpu_seconds"], 4)}
+
+
+def bench_tokenizer(plamo_hip, synth):
+    """Host-side tokenizer (Tokenizer.swift): load, encode and decode throughput of the native
+    library on ~1 MB of seeded text over the synthetic vocabulary's alphabet (no GPU work)."""
+    import random
+    path, alphabet = synth.ensure_tokenizer()
+    t0 = time.perf_counter()
+    tok = plamo_hip.Tokenizer(path)
+    load = time.perf_counter() - t0
+    rng = random.Random(7)
+    words = ["".join(rng.choice(alphabet) for _ in range(rng.randint(1, 9))) for _ in range(4096)]
+    text = " ".join(rng.choice(words) for _ in range(160000))[:1 << 20]
+    nbytes = len(text.encode())
+    enc, dec = [], []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        ids = tok.encode(text)
+        enc.append(time.perf_counter() - t0)
+        t0 = time.perf_counter()
+        out = tok.decode_bytes(ids)
+        dec.append(time.perf_counter() - t0)
+    assert out == text.encode(), "tokenizer round trip"
+    tok.close()
+    return {"load_s": round(load, 3), "text_bytes": nbytes, "tokens": len(ids),
+            "encode_MBps": round(nbytes / min(enc) / 1e6, 2), "encode_tok_s": round(len(ids) / min(enc)),
+            "decode_MBps": round(nbytes / min(dec) / 1e6, 2), "cores": 1}
+
+
 def step_timeline(plamo_hip, np, model_dir, sha, packed, steps=24):
     """In-step kernel durations of graph-replayed decode steps (positions 80-128 after a
     64-token prompt), from the device timestamps of the timeline library: each kernel's span
