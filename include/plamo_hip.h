@@ -245,7 +245,8 @@ int plamo_check_packed(const char* path, const char* source_sha256, const char* 
 
 /* `linear` (Kernels.metal:92-114) / `project{2,3,4}` (Batch.metal:171-221): y = W.x for
  * `rows` activation rows.  `table` != 0 selects the .p12 decode (`w` = payload).  mode 0:
- * y FP32 roundbf; mode 2: y BF16 bits (LM head).  n in {1536, 2048, 6144}. */
+ * y FP32 roundbf; mode 1: y the FP32 sums unrounded; mode 2: y BF16 bits (LM head).
+ * n in {1536, 2048, 6144}. */
 int plamo_kernel_linear(uint64_t w, uint64_t table, uint64_t x, uint64_t y, int32_t n, int32_t m, int32_t rows,
                         int32_t mode, uint64_t stream);
 

@@ -1,14 +1,27 @@
 /* Order-exact GEMV restatement for the CPU oracle (test infrastructure only).
  *
  * y[r] = sum over the 64 lanes of a wave: lane l accumulates w[r][c]*x[c] for its columns
- * c = it*512 + l*8 + j (it ascending, j = 0..7) in that order, then the 64 lane sums are
- * combined by an XOR butterfly with offsets 32,16,8,4,2,1 -- the reduction tree of the
- * decode GEMV kernel.  BF16 x BF16 products are exact in FP32, so each step is one
- * correctly rounded FP32 addition.  Compiled with -ffp-contract=off. */
+ * c = it*512 + l*8 + j (it ascending, j = 0..7) as four v_dot2_f32_bf16 steps per column
+ * block (pairs j = 0-1, 2-3, 4-5, 6-7, in that order; each step folds its two exact
+ * products into the accumulator as mfma_model.h states), then the 64 lane sums are combined
+ * by an XOR butterfly with offsets 32,16,8,4,2,1 (correctly rounded FP32 additions) -- the
+ * reduction tree of the decode GEMV kernel.  w and x hold BF16 values in FP32.
+ * Compiled with -ffp-contract=off. */
 #include <stdint.h>
+#include <string.h>
+
+#include "mfma_model.h"
+
+static inline uint16_t hi16(float v) {
+    uint32_t u;
+    memcpy(&u, &v, 4);
+    return (uint16_t)(u >> 16);
+}
 
 void plamo_oracle_gemv(const float* w, const float* x, float* y, int64_t m, int64_t n) {
     const int64_t its = n / 512;
+    uint16_t* xb = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)n);
+    for (int64_t c = 0; c < n; ++c) xb[c] = hi16(x[c]);
 #pragma omp parallel for schedule(static)
     for (int64_t r = 0; r < m; ++r) {
         float acc[64];
@@ -18,10 +31,8 @@ void plamo_oracle_gemv(const float* w, const float* x, float* y, int64_t m, int6
             for (int l = 0; l < 64; ++l) {
                 const int64_t c = it * 512 + l * 8;
                 float a = acc[l];
-                for (int j = 0; j < 8; ++j) {
-                    const float p = row[c + j] * x[c + j];
-                    a = a + p;
-                }
+                for (int j = 0; j < 8; j += 2)
+                    a = dot2_bits(hi16(row[c + j]), hi16(row[c + j + 1]), xb[c + j], xb[c + j + 1], a);
                 acc[l] = a;
             }
         for (int o = 32; o > 0; o >>= 1) {
@@ -30,5 +41,30 @@ void plamo_oracle_gemv(const float* w, const float* x, float* y, int64_t m, int6
             for (int l = 0; l < 64; ++l) acc[l] = next[l];
         }
         y[r] = acc[0];
+    }
+    free(xb);
+}
+
+/* One v_dot2_f32_bf16 chain per output: acc_i <- dot2(a[s][i], b[s][i], acc_i) for s = 0 ..
+ * steps-1, a and b BF16 pairs (low half first) laid out [steps][n]; every intermediate
+ * accumulator is written to out [steps][n].  fast = 0: the general fold (dot2_group);
+ * fast = 1: dot2_bits, the form plamo_oracle_gemv uses. */
+void plamo_oracle_dot2_chain(const uint32_t* a, const uint32_t* b, const float* c, float* out, int64_t n,
+                             int64_t steps, int32_t fast) {
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; ++i) {
+        float acc = c[i];
+        for (int64_t s = 0; s < steps; ++s) {
+            const uint32_t u = a[s * n + i], v = b[s * n + i];
+            if (fast) {
+                acc = dot2_bits((uint16_t)(u & 0xffffu), (uint16_t)(u >> 16), (uint16_t)(v & 0xffffu),
+                                (uint16_t)(v >> 16), acc);
+            } else {
+                const bfdec wd[2] = {bf_decode((uint16_t)(u & 0xffffu)), bf_decode((uint16_t)(u >> 16))};
+                const bfdec xd[2] = {bf_decode((uint16_t)(v & 0xffffu)), bf_decode((uint16_t)(v >> 16))};
+                acc = dot2_group(wd, xd, acc);
+            }
+            out[s * n + i] = acc;
+        }
     }
 }

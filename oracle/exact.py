@@ -5,12 +5,14 @@ network amplifies BF16 rounding-path differences: two CPU oracles that differ on
 dot-product summation order disagree by RMSE ~0.013 on the logits, above the 5e-3 the task
 sets.  Bitwise comparison is therefore the meaningful check, and it needs the exact
 reduction trees of the GPU kernels, restated here in numpy FP32 (every operation is a
-correctly rounded IEEE FP32 operation, exactly as on the device):
+correctly rounded IEEE FP32 operation, exactly as on the device, except the GEMV steps):
 
 * GEMV (decode `linear`, Kernels.metal:92-114): lane l of a 64-wide wave owns columns
-  it*512 + l*8 .. +8; it accumulates products in column order (BF16 x BF16 products are exact
-  in FP32, so fma == add of the product); the 64 lane sums are combined by an XOR
-  butterfly (offsets 32,16,8,4,2,1).
+  it*512 + l*8 .. +8; it accumulates them as v_dot2_f32_bf16 steps over the column pairs in
+  order (each step folds two exact BF16 x BF16 products into the FP32 accumulator by the
+  MFMA accumulation rule with a group of two: csrc/mfma_model.h, pinned by device vectors in
+  tests/golden/dot2_accumulate.npz); the 64 lane sums are combined by an XOR butterfly
+  (offsets 32,16,8,4,2,1).  Restated in C (csrc/exact_gemv.c); the library must be built.
 * RMSNorm (`norm`, Kernels.metal:46-90): thread t of 256 sums squares of elements 6t..6t+5
   in order; wave butterfly; then (w0+w1)+(w2+w3).  r = 1/sqrt(sum/n + 1e-6).
 * q/k norm (`qkv`, Kernels.metal:236-246): 16 lanes x 8 elements (the RoPE pairs d, d+64
@@ -82,34 +84,41 @@ def _c_lib():
         if os.path.exists(path):
             lib = ctypes.CDLL(path)
             lib.plamo_oracle_gemv.argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_int64] * 2
+            lib.plamo_oracle_dot2_chain.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_int64] * 2 + [ctypes.c_int32]
             _C = lib
     return _C or None
 
 
-def gemv(w, x):
-    """W [m, n] FP32 (BF16 values), x [n] -> FP32 [m] in the kernel's order (the C
-    restatement in csrc/exact_gemv.c when built, else the numpy one below; identical)."""
-    m, n = w.shape
+def _lib():
     lib = _c_lib()
-    if lib is not None:
-        w = np.ascontiguousarray(w, dtype=F)
-        x = np.ascontiguousarray(x, dtype=F)
-        y = np.empty(m, F)
-        lib.plamo_oracle_gemv(w.ctypes.data, x.ctypes.data, y.ctypes.data, m, n)
-        return y
-    return gemv_numpy(w, x)
+    if lib is None:
+        raise RuntimeError("oracle C restatement not built (make -C oracle)")
+    return lib
 
 
-def gemv_numpy(w, x):
+def gemv(w, x):
+    """W [m, n] FP32 (BF16 values), x [n] -> FP32 [m] in the kernel's order
+    (csrc/exact_gemv.c)."""
     m, n = w.shape
-    it = n // 512
-    wr = w.reshape(m, it, 64, 8)
-    xr = x.astype(F).reshape(it, 64, 8)
-    acc = np.zeros((m, 64), F)
-    for i in range(it):
-        for j in range(8):
-            acc += wr[:, i, :, j] * xr[i, :, j]
-    return butterfly(acc)
+    assert n % 512 == 0
+    w = np.ascontiguousarray(w, dtype=F)
+    x = np.ascontiguousarray(x, dtype=F)
+    y = np.empty(m, F)
+    _lib().plamo_oracle_gemv(w.ctypes.data, x.ctypes.data, y.ctypes.data, m, n)
+    return y
+
+
+def dot2_chain(a_pairs, b_pairs, acc, fast=True):
+    """v_dot2_f32_bf16 chains: a, b uint32 BF16 pairs (low half first) [steps][n], acc [n]
+    -> every intermediate accumulator [steps][n].  fast=False uses the general fold."""
+    a = np.ascontiguousarray(a_pairs, dtype=np.uint32)
+    b = np.ascontiguousarray(b_pairs, dtype=np.uint32)
+    c = np.ascontiguousarray(acc, dtype=F)
+    steps, n = a.shape
+    out = np.empty((steps, n), F)
+    _lib().plamo_oracle_dot2_chain(a.ctypes.data, b.ctypes.data, c.ctypes.data, out.ctypes.data, n, steps,
+                                   1 if fast else 0)
+    return out
 
 
 def block_sumsq(v):

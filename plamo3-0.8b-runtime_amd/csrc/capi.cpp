@@ -498,7 +498,7 @@ int plamo_kernel_linear(uint64_t w, uint64_t table, uint64_t x, uint64_t y, int3
                         int32_t mode, uint64_t stream) {
     return guard(nullptr, 0, [&] {
         if (rows < 1 || rows > plamo::ROWS || m < 4 || (n != 1536 && n != 2048 && n != 6144) ||
-            m % (n >= 6144 ? 2 : 4) != 0 || (mode != 0 && mode != 2))
+            m % (n >= 6144 ? 2 : 4) != 0 || mode < 0 || mode > 2)
             throw plamo::Error(plamo::E_INVAL, "unsupported linear shape");
         plamo::GemvParams g{};
         g.w = reinterpret_cast<const uint16_t*>(w);
@@ -509,7 +509,7 @@ int plamo_kernel_linear(uint64_t w, uint64_t table, uint64_t x, uint64_t y, int3
         g.out = reinterpret_cast<float*>(y);
         g.out16 = reinterpret_cast<uint16_t*>(y);
         const int maxr = rows == 1 ? 1 : plamo::ROWS;
-        const plamo::Epilogue epi = mode == 2 ? plamo::EPI_BF16 : plamo::EPI_ROUND;
+        const plamo::Epilogue epi = mode == 2 ? plamo::EPI_BF16 : mode == 1 ? plamo::EPI_RAW : plamo::EPI_ROUND;
         if (m % plamo::gemv_group_rows(n, maxr, epi) != 0)
             throw plamo::Error(plamo::E_INVAL, "GEMV rows must be a multiple of the rows per wave group");
         const int blocks = std::max(1, std::min(4096, plamo::gemv_blocks(n, maxr, epi, m)));

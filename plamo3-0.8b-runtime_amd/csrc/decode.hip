@@ -69,15 +69,9 @@ __host__ __device__ constexpr int gemv_waves(int n, int maxr, int epi) {
 }
 
 // ---------------------------------------------------------------------------- prologues
-// Staged activation rows in LDS.  FP32 form: column c of a 512-column block sits at
-// (c & 4 ? 256 : 0) + 4 * ((c >> 3) & 63) + (c & 3), so the 8 columns a lane owns are two
-// float4 reads at 16-byte lane strides (no bank conflicts) and need no unpacking.  (Four
-// 6144-wide rows take 96 KB: their eight-wave workgroups run one per CU anyway.)
-template <int N, int MAXR>
-constexpr bool xs_f32() { return true; }
-template <int N, int MAXR>
-using xs_t = typename std::conditional<xs_f32<N, MAXR>(), float, uint16_t>::type;
-__device__ __forceinline__ int xpos(int c) { return (c & ~511) | ((c & 4) << 6) | (((c >> 3) & 63) << 2) | (c & 3); }
+// Staged activation rows in LDS: BF16, row-major, so the 8 columns a lane owns are one
+// 16-byte read at 16-byte lane strides (no bank conflicts), in the pair form v_dot2 takes.
+// (Four 6144-wide rows take 48 KB.)
 
 // Stage the BF16 activation rows into LDS.  Values are BF16-exact FP32 (every producer
 // rounds), so the BF16 copy is lossless.  The prologue is split into its loads
@@ -207,8 +201,7 @@ __device__ __forceinline__ void row_scales(const float* red, int q0, float (&rs)
 // main loop can run all MAXR rows without branches (their results are never stored).
 template <int N, int MAXR, int RQ, int PRO>
 __device__ __forceinline__ void stage_finish(const GemvParams& p, int rows, int q0, const Staged<N, RQ, PRO>& S,
-                                             xs_t<N, MAXR>* xs, float* red) {
-    constexpr bool XF = xs_f32<N, MAXR>();
+                                             uint16_t* xs, float* red) {
     const int tid = threadIdx.x & 255;
     constexpr int V = Staged<N, RQ, PRO>::V, V16 = Staged<N, RQ, PRO>::V16, E = Staged<N, RQ, PRO>::E;
     if constexpr (PRO == PRO_PLAIN) {
@@ -219,14 +212,9 @@ __device__ __forceinline__ void stage_finish(const GemvParams& p, int rows, int 
             for (int k = 0; k < V; ++k) {
                 const int e = (tid + 256 * k) * 4;
                 if (e >= N) continue;
-                if constexpr (XF) {
-                    *reinterpret_cast<float4*>(&xs[q * N + xpos(e)]) = make_float4(
-                        roundbf(S.v[qi][k].x), roundbf(S.v[qi][k].y), roundbf(S.v[qi][k].z), roundbf(S.v[qi][k].w));
-                } else {
-                    const uint32_t lo2 = (bits(S.v[qi][k].x) & 0xffffu) | (bits(S.v[qi][k].y) << 16);
-                    const uint32_t hi2 = (bits(S.v[qi][k].z) & 0xffffu) | (bits(S.v[qi][k].w) << 16);
-                    *reinterpret_cast<uint2*>(&xs[q * N + e]) = make_uint2(lo2, hi2);
-                }
+                const uint32_t lo2 = (bits(S.v[qi][k].x) & 0xffffu) | (bits(S.v[qi][k].y) << 16);
+                const uint32_t hi2 = (bits(S.v[qi][k].z) & 0xffffu) | (bits(S.v[qi][k].w) << 16);
+                *reinterpret_cast<uint2*>(&xs[q * N + e]) = make_uint2(lo2, hi2);
             }
         }
     } else if constexpr (PRO == PRO_MERGE) {
@@ -263,9 +251,8 @@ __device__ __forceinline__ void stage_finish(const GemvParams& p, int rows, int 
                 v[2 * j + 1] = hi(w4[j]);
             }
         }
-        float* d = reinterpret_cast<float*>(xs) + xpos(tid * 8);
-        *reinterpret_cast<float4*>(d) = make_float4(v[0], v[1], v[2], v[3]);
-        *reinterpret_cast<float4*>(d + 256) = make_float4(v[4], v[5], v[6], v[7]);
+        *reinterpret_cast<uint4*>(&xs[tid * 8]) = make_uint4(pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]),
+                                                            pack_bf16(v[4], v[5]), pack_bf16(v[6], v[7]));
     } else if constexpr (PRO == PRO_PLAIN16) {
 #pragma unroll
         for (int qi = 0; qi < RQ; ++qi) {
@@ -274,14 +261,7 @@ __device__ __forceinline__ void stage_finish(const GemvParams& p, int rows, int 
             for (int k = 0; k < V16; ++k) {
                 const int e = (tid + 256 * k) * 8;
                 if (e >= N) continue;
-                const uint4 h = S.h[qi][k];
-                if constexpr (XF) {
-                    float* d = reinterpret_cast<float*>(xs) + q * N + xpos(e);
-                    *reinterpret_cast<float4*>(d) = make_float4(lo(h.x), hi(h.x), lo(h.y), hi(h.y));
-                    *reinterpret_cast<float4*>(d + 256) = make_float4(lo(h.z), hi(h.z), lo(h.w), hi(h.w));
-                } else {
-                    *reinterpret_cast<uint4*>(&xs[q * N + e]) = h;
-                }
+                *reinterpret_cast<uint4*>(&xs[q * N + e]) = S.h[qi][k];
             }
         }
     } else {
@@ -380,8 +360,7 @@ __device__ __forceinline__ void stage_finish(const GemvParams& p, int rows, int 
                 float t0, t1;
                 round_bf16x2(xv[qi][k] * r, xv[qi][k + 1] * r, t0, t1);
                 const uint32_t xn2 = pack_bf16(t0 * gn[k], t1 * gn[k + 1]);  // the two BF16 results
-                if constexpr (XF) *reinterpret_cast<float2*>(&xs[q * HIDDEN + xpos(i)]) = make_float2(lo(xn2), hi(xn2));
-                else *reinterpret_cast<uint32_t*>(&xs[q * HIDDEN + i]) = xn2;
+                *reinterpret_cast<uint32_t*>(&xs[q * HIDDEN + i]) = xn2;
                 if (blockIdx.x == 0 && q < rows) {
                     if constexpr (PRO == PRO_RESID) {
                         p.resid_out[q * HIDDEN + i] = xv[qi][k];
@@ -537,7 +516,7 @@ __global__ __launch_bounds__(64 * gemv_waves(N, MAXR, EPI)) void gemv_kernel(con
     constexpr int IT = N / 512;
     constexpr int U = gemv_u<N, MAXR, EPI>();
     constexpr int H = U / 2;  // SwiGLU: gate rows (and up rows) per group
-    __shared__ __align__(16) xs_t<N, MAXR> xs[MAXR * N];
+    __shared__ __align__(16) uint16_t xs[MAXR * N];
     __shared__ float red[MAXR * 4 * 2];  // norm partials: post-norm half, next-norm half
     __shared__ float cand_v[MAXR * NWV];
     __shared__ uint32_t cand_i[MAXR * NWV];
@@ -661,20 +640,12 @@ __global__ __launch_bounds__(64 * gemv_waves(N, MAXR, EPI)) void gemv_kernel(con
 #pragma unroll
             for (int q = 0; q < MAXR; ++q) {
                 if (MAXR > 1 && q >= rows) break;
-                if constexpr (xs_f32<N, MAXR>()) {
-                    const float* xr = reinterpret_cast<const float*>(xs) + q * N + it * 512 + lane * 4;
-                    const float4 xa = *reinterpret_cast<const float4*>(xr);
-                    const float4 xb = *reinterpret_cast<const float4*>(xr + 256);
+                const uint4 xv = *reinterpret_cast<const uint4*>(&xs[q * N + it * 512 + lane * 8]);
 #pragma unroll
-                    for (int u = 0; u < U; ++u) acc[u][q] = dot8f(w[u][it], xa, xb, acc[u][q]);
-                } else {
-                    const uint4 xv = *reinterpret_cast<const uint4*>(&xs[q * N + it * 512 + lane * 8]);
-#pragma unroll
-                    for (int u = 0; u < U; ++u) acc[u][q] = dot8(w[u][it], xv, acc[u][q]);
-                }
+                for (int u = 0; u < U; ++u) acc[u][q] = dot8(w[u][it], xv, acc[u][q]);
             }
         }
-        if constexpr (EPI == EPI_ROUND || EPI == EPI_BF16 || EPI == EPI_SWIGLU) {
+        if constexpr (EPI == EPI_ROUND || EPI == EPI_BF16 || EPI == EPI_SWIGLU || EPI == EPI_RAW) {
             // Reduce-scatter: lane holds the sum of value idx = u * MAXR + q, idx = lane >> S
             // (the gate/up split is the top bit of idx, so a SwiGLU gate lane finds its up
             // sum 32 lanes away).  Lane (idx << S) writes output (row q, weight row u).
@@ -703,6 +674,7 @@ __global__ __launch_bounds__(64 * gemv_waves(N, MAXR, EPI)) void gemv_kernel(con
                     if (uu == u) r = wrow[uu];
                 if (writer) {
                     if constexpr (EPI == EPI_ROUND) p.out[size_t(q) * p.m + r] = roundbf(t);
+                    else if constexpr (EPI == EPI_RAW) p.out[size_t(q) * p.m + r] = t;
                     else p.out16[size_t(q) * p.m + r] = uint16_t(bits(t));
                 }
             }
@@ -1650,6 +1622,7 @@ void gemv_dispatch_epi(Prologue pro, Epilogue epi, const GemvParams& p, int bloc
     if (!p.state) {  // kernel-level entry points: plain rows, no step state
         if (pro == PRO_PLAIN && epi == EPI_ROUND) PLAMO_GEMV_NOSTATE(PRO_PLAIN, EPI_ROUND);
         else if (pro == PRO_PLAIN && epi == EPI_BF16) PLAMO_GEMV_NOSTATE(PRO_PLAIN, EPI_BF16);
+        else if (pro == PRO_PLAIN && epi == EPI_RAW) PLAMO_GEMV_NOSTATE(PRO_PLAIN, EPI_RAW);
         else throw Error(E_INVAL, "unsupported GEMV variant");
         return;
     }

@@ -61,7 +61,7 @@ struct DecodeBuffers {
 // the attention output as PRO_PLAIN16 does.
 enum Prologue { PRO_PLAIN = 0, PRO_EMBED = 1, PRO_RESID = 2, PRO_PLAIN16 = 3, PRO_RESID16 = 4, PRO_MERGE = 5 };
 constexpr uint32_t MERGE_IN_O = 6;  // partitions (64 keys each) the o prologue merges
-enum Epilogue { EPI_ROUND = 0, EPI_SWIGLU = 1, EPI_LOGITS = 2, EPI_BF16 = 3 };
+enum Epilogue { EPI_ROUND = 0, EPI_SWIGLU = 1, EPI_LOGITS = 2, EPI_BF16 = 3, EPI_RAW = 4 };  // RAW: FP32 sums, unrounded
 
 struct GemvParams {
     const uint16_t* w;        // plain BF16 [m][n] or .p12 payload

@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 import torch
 
-from oracle import p12, sampler
+from oracle import exact, p12, sampler
 from oracle.bf16 import bf_np, bits_np, roundbf_np
 from plamo_hip import native
 
@@ -107,13 +107,12 @@ def _linear(lib, w_bits, x, rows, mode=0, table=None, payload=None):
     else:
         wd, td = dev(payload), dev(table.view(np.int32))
     xd = dev(x.astype(np.float32))
-    y = torch.empty(rows * m * (1 if mode == 0 else 1), dtype=torch.float32 if mode == 0 else torch.int16,
-                    device="cuda")
+    y = torch.empty(rows * m, dtype=torch.int16 if mode == 2 else torch.float32, device="cuda")
     rc = lib.plamo_kernel_linear(ptr(wd), ptr(td) if td is not None else 0, ptr(xd), ptr(y), n, m, rows, mode, 0)
     assert rc == 0
     torch.cuda.synchronize()
     out = y.cpu().numpy()
-    return out.reshape(rows, m) if mode == 0 else out.view(np.uint16).reshape(rows, m)
+    return out.view(np.uint16).reshape(rows, m) if mode == 2 else out.reshape(rows, m)
 
 
 def test_linear_brute_force(lib):
@@ -158,6 +157,28 @@ def test_linear_packed_equals_plain_and_fp32(lib, name):
             single = _linear(lib, w, x[2:3], 1, mode)
             assert np.array_equal(single.view(np.uint32) if mode == 0 else single,
                                   (plain[2:3].view(np.uint32) if mode == 0 else plain[2:3]))
+
+
+@pytest.mark.parametrize("name", list(SHAPES))
+def test_linear_raw_sums_equal_the_twin(lib, name):
+    # mode 1 returns the FP32 sums before any rounding: every bit of every lane chain
+    # (v_dot2_f32_bf16 steps) and of the butterfly, against csrc/exact_gemv.c, plain and
+    # .p12, one and four rows
+    m, n = SHAPES[name]
+    rng = np.random.default_rng(11)
+    w = bits_np(rng.standard_normal((m, n)).astype(np.float32) * 0.02)
+    w[3, 128:256] = bits_np(np.full(128, 1e-30, np.float32))  # a raw .p12 block
+    data, offsets, minima = p12.pack(w)
+    table = p12.tag(offsets, minima)
+    wf = bf_np(w)
+    x = roundbf_np(rng.standard_normal((4, n)).astype(np.float32))
+    x[1, ::7] = roundbf_np(x[1, ::7] * 40)  # outliers (activations are BF16 values)
+    want = np.stack([exact.gemv(wf, x[r]) for r in range(4)])
+    for rows in (1, 4):
+        for packed in (False, True):
+            got = _linear(lib, w, x[:rows], rows, 1, table=table if packed else None, payload=data if packed else None)
+            bad = int(np.sum(got.view(np.uint32) != want[:rows].view(np.uint32)))
+            assert bad == 0, (name, rows, packed, bad)
 
 
 @pytest.mark.parametrize("m,n,tokens", [(2304, 1536, 130), (1536, 2048, 64), (1536, 6144, 257), (64, 1536, 17),

@@ -1,10 +1,14 @@
 """Pins of the order-exact decode restatement (oracle/exact.py) on the CPU."""
+import os
+
 import numpy as np
 import pytest
 import torch
 
 from oracle import exact, model as om
-from oracle.bf16 import bf_np
+from oracle.bf16 import bf_np, bits_np, roundbf_np
+
+FIXTURE_DOT2 = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "dot2_accumulate.npz")
 
 
 def test_exp_det_accuracy():
@@ -27,13 +31,68 @@ def test_gemv_order_is_a_valid_fp32_sum():
     assert np.all(np.abs(got - want) <= bound)
 
 
-def test_c_and_numpy_gemv_agree():
-    if exact._c_lib() is None:
-        pytest.skip("oracle C restatement not built (make -C oracle)")
-    rng = np.random.default_rng(2)
-    w = bf_np(np.float32(rng.standard_normal((300, 6144)) * 0.02).view(np.uint32) >> 16)
-    x = bf_np(np.float32(rng.standard_normal(6144)).view(np.uint32) >> 16)
-    assert np.array_equal(exact.gemv(w, x).view(np.uint32), exact.gemv_numpy(w, x).view(np.uint32))
+def _pairs(lo, hi):
+    return (bits_np(np.asarray(lo, np.float32)).astype(np.uint32)
+            | (bits_np(np.asarray(hi, np.float32)).astype(np.uint32) << 16))
+
+
+def test_dot2_model_reproduces_device_accumulators():
+    # the device is the authority for v_dot2_f32_bf16 rounding: every recorded accumulator,
+    # bit for bit, by the general fold and by the fast form the GEMV restatement uses
+    from golden import make_dot2_fixture as mk
+    rec = np.load(FIXTURE_DOT2)
+    for name, (a, b, c) in mk.cases().items():
+        for fast in (True, False):
+            got = mk.stored(name, exact.dot2_chain(a, b, c, fast=fast))
+            for key, want in got.items():
+                bad = int(np.sum(want.view(np.uint32) != rec[key].view(np.uint32)))
+                assert bad == 0, (key, fast, bad)
+
+
+def test_dot2_rules():
+    one = np.float32(1.0)
+    # a product below the 24-bit window of the larger one is truncated toward zero
+    assert exact.dot2_chain(_pairs([[1.0]], [[2.0 ** -30]]), _pairs([[1.0]], [[1.0]]), [0.0])[0, 0] == one
+    # the window is set by the products, not by the accumulator: 1 - 1 + 2^-30 = 0
+    assert exact.dot2_chain(_pairs([[1.0]], [[-1.0]]), _pairs([[1.0]], [[1.0]]), [2.0 ** -30])[0, 0] == 0.0
+    # the sum is floored 31 bits below its leading bit before the rounding: a tie with a
+    # sticky bit below that window rounds to even, 1 + 2^-24 + 2^-40 -> 1
+    assert exact.dot2_chain(_pairs([[2.0 ** -12]], [[2.0 ** -20]]), _pairs([[2.0 ** -12]], [[2.0 ** -20]]),
+                            [1.0])[0, 0] == one
+    # ... while a sticky bit inside it rounds up: 1 + 2^-24 + 2^-30 -> 1 + 2^-23
+    assert exact.dot2_chain(_pairs([[2.0 ** -12]], [[2.0 ** -15]]), _pairs([[2.0 ** -12]], [[2.0 ** -15]]),
+                            [1.0])[0, 0] == np.float32(1 + 2.0 ** -23)
+    # zero products leave the accumulator and its low bits unchanged
+    acc = np.float32(1 + 2.0 ** -23)
+    assert exact.dot2_chain(_pairs([[0.0]], [[0.0]]), _pairs([[3.0]], [[5.0]]), [acc])[0, 0] == acc
+    # products inside one window and a zero accumulator: the exact sum, rounded once
+    rng = np.random.default_rng(4)
+    a = roundbf_np(rng.standard_normal((1, 2000, 2)).astype(np.float32))
+    b = roundbf_np(rng.standard_normal((1, 2000, 2)).astype(np.float32))
+    got = exact.dot2_chain(_pairs(a[..., 0], a[..., 1]), _pairs(b[..., 0], b[..., 1]), np.zeros(2000, np.float32))
+    want = (a[..., 0].astype(np.float64) * b[..., 0] + a[..., 1].astype(np.float64) * b[..., 1]).astype(np.float32)
+    close = np.abs(np.log2(np.abs(a[..., 0] * b[..., 0]) + 1e-30) - np.log2(np.abs(a[..., 1] * b[..., 1]) + 1e-30)) < 8
+    assert np.array_equal(got[close], want[close])
+
+
+def test_gemv_is_lane_chains_of_dot2():
+    # a row whose only nonzero columns are lane l's (it * 512 + 8 l .. +8) returns lane l's
+    # chain: four dot2 steps per column block, pairs in column order, blocks in order
+    rng = np.random.default_rng(3)
+    n = 1536
+    x = roundbf_np(rng.standard_normal(n).astype(np.float32))
+    w = np.zeros((64, n), np.float32)
+    for l in range(64):
+        for it in range(3):
+            w[l, it * 512 + 8 * l:it * 512 + 8 * l + 8] = roundbf_np(
+                rng.standard_normal(8).astype(np.float32) * 2.0 ** rng.integers(-12, 4))
+    got = exact.gemv(w, x)
+    for l in (0, 1, 31, 63):
+        cols = np.concatenate([np.arange(it * 512 + 8 * l, it * 512 + 8 * l + 8) for it in range(3)])
+        a = _pairs(w[l, cols[0::2]], w[l, cols[1::2]])[:, None]
+        b = _pairs(x[cols[0::2]], x[cols[1::2]])[:, None]
+        chain = exact.dot2_chain(a, b, [0.0], fast=False)[-1, 0]
+        assert got[l] == chain, l
 
 
 def test_block_sumsq_and_norm():
