@@ -361,6 +361,8 @@ int plamo_batch_fill_kv(plamo_batch* b, uint16_t bits) {
             const size_t n = size_t(e.lanes) * size_t(e.capacity[l]) * plamo::HEAD_DIM;
             PLAMO_HIP(hipMemsetD16Async(e.keys[l], bits, n, e.stream));
             PLAMO_HIP(hipMemsetD16Async(e.values[l], bits, n, e.stream));
+            if (e.keys_rot[l])
+                PLAMO_HIP(hipMemsetD16Async(e.keys_rot[l], bits, size_t(e.lanes) * e.rot_rows[l] * plamo::HEAD_DIM, e.stream));
         }
         PLAMO_HIP(hipStreamSynchronize(e.stream));
     });

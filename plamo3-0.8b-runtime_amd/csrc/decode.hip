@@ -957,6 +957,11 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
     const uint32_t start = first % cap;
     uint16_t* K = p.keys + size_t(lanei) * cap * HEAD_DIM;
     uint16_t* V = p.values + size_t(lanei) * cap * HEAD_DIM;
+    // A local-layer row whose window starts at 0 rotates every key with its own position:
+    // those rotations are cached (keys_rot, written with each key), so the keys are read
+    // rotated and only the newest one is rotated here.
+    const bool prerot = !FULL && p.keys_rot != nullptr && first == 0;
+    uint16_t* KR = prerot ? p.keys_rot + size_t(lanei) * p.rot_rows * HEAD_DIM : nullptr;
     const size_t pslot = size_t(q) * p.parts + blockIdx.x;
     // partition results travel between workgroups with sc1 stores and loads (no cache fences)
     const uint32_t pstats = uint32_t(ROWS) * p.parts * HEADS;
@@ -981,7 +986,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
     if (kr < count && kr != newest) {
         uint32_t phys = start + kr;
         phys = phys >= cap ? phys - cap : phys;  // visible keys (<= capacity) wrap at most once
-        const uint16_t* krow = K + size_t(phys) * HEAD_DIM;
+        const uint16_t* krow = (prerot ? KR : K) + size_t(phys) * HEAD_DIM;  // phys == kr when prerot
         ka[0] = *reinterpret_cast<const uint4*>(krow + ksub * 16);
         ka[1] = *reinterpret_cast<const uint4*>(krow + ksub * 16 + 8);
         kb[0] = *reinterpret_cast<const uint4*>(krow + 64 + ksub * 16);
@@ -990,7 +995,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) vv[i] = *reinterpret_cast<const uint4*>(vrow + 8 * i);
     }
-    if (!FULL && kr < count) {
+    if (!FULL && !prerot && kr < count) {
         const uint4* rrow = reinterpret_cast<const uint4*>(p.local_rope + size_t(kr) * 64 + ksub * 16);
 #pragma unroll
         for (int i = 0; i < 4; ++i) rr[i] = rrow[i];
@@ -1020,14 +1025,28 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) rope_pair(z[j], z[4 + j], c4[j], z[j], z[4 + j]);
         }
+        float zr[8];
+        if (prerot) {  // the newest key at its own position (coordinate pos - first = pos)
+            const uint4 lr = *reinterpret_cast<const uint4*>(p.local_rope + size_t(pos) * 64 + t * 4);
+            const uint32_t c4[4] = {lr.x, lr.y, lr.z, lr.w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) rope_pair(z[j], z[4 + j], c4[j], zr[j], zr[4 + j]);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) zr[j] = z[j];
+        }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             if (hg == 0) {
                 K[slot + t * 4 + j] = uint16_t(bits(z[j]));
                 K[slot + 64 + t * 4 + j] = uint16_t(bits(z[4 + j]));
+                if (prerot) {
+                    KR[size_t(pos) * HEAD_DIM + t * 4 + j] = uint16_t(bits(zr[j]));
+                    KR[size_t(pos) * HEAD_DIM + 64 + t * 4 + j] = uint16_t(bits(zr[4 + j]));
+                }
             }
-            knew[t * 4 + j] = z[j];
-            knew[64 + t * 4 + j] = z[4 + j];
+            knew[t * 4 + j] = zr[j];
+            knew[64 + t * 4 + j] = zr[4 + j];
         }
     }
     if (has_new && tid >= 128) {
@@ -1053,7 +1072,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
 #pragma unroll
             for (int i = 0; i < 16; ++i) { a[i] = knew[ksub * 16 + i]; b[i] = knew[64 + ksub * 16 + i]; }
         }
-        if (!FULL && kr < count) {
+        if (!FULL && !prerot && kr < count) {
             const uint32_t rw[16] = {rr[0].x, rr[0].y, rr[0].z, rr[0].w, rr[1].x, rr[1].y, rr[1].z, rr[1].w,
                                      rr[2].x, rr[2].y, rr[2].z, rr[2].w, rr[3].x, rr[3].y, rr[3].z, rr[3].w};
 #pragma unroll

@@ -104,6 +104,9 @@ struct AttnParams {
     const uint16_t* k_norm;
     uint16_t* keys;           // [lanes][capacity][128]
     uint16_t* values;
+    uint16_t* keys_rot;       // local layers: [lanes][rot_rows][128] keys rotated at their own
+                              // position, for rows whose window starts at 0 (null: rotate)
+    uint32_t rot_rows;
     uint32_t capacity;
     const uint32_t* local_rope;  // [2064][64] BF16 (cos | sin << 16)
     const uint32_t* global_rope; // [context][64]

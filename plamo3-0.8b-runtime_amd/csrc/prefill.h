@@ -38,6 +38,8 @@ struct QkPrepParams {
     uint16_t* q16;             // out: [T][16][128] BF16, normalised and rotated queries
     uint16_t* keys;            // lane slice [capacity][128]
     uint16_t* values;
+    uint16_t* keys_rot;        // local layers: lane slice [rot_rows][128] (null: none)
+    uint32_t rot_rows;
     uint32_t capacity, p0;
     int tokens;
     int full;

@@ -502,6 +502,18 @@ __global__ __launch_bounds__(256) void qk_prep_kernel(const QkPrepParams p) {
             const uint32_t c4[4] = {gr.x, gr.y, gr.z, gr.w};
 #pragma unroll
             for (int j = 0; j < 4; ++j) rope_pair(z[j], z[4 + j], c4[j], z[j], z[4 + j]);
+        } else if (p.keys_rot && pos < p.rot_rows) {
+            // the copy rotated at the key's own position (decode inside the first window)
+            const uint4 lr = *reinterpret_cast<const uint4*>(p.local_rope + size_t(pos) * 64 + tid * 4);
+            const uint32_t c4[4] = {lr.x, lr.y, lr.z, lr.w};
+            uint16_t* kr = p.keys_rot + size_t(pos) * HEAD_DIM;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                float ra, rb;
+                rope_pair(z[j], z[4 + j], c4[j], ra, rb);
+                kr[tid * 4 + j] = uint16_t(bits(ra));
+                kr[64 + tid * 4 + j] = uint16_t(bits(rb));
+            }
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {

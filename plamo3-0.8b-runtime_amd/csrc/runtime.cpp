@@ -232,6 +232,13 @@ Engine::Engine(std::shared_ptr<Model> mdl, int ctx, int nl, hipStream_t s)
         values[l] = arena.alloc_n<uint16_t>(n);
         PLAMO_HIP(hipMemsetAsync(keys[l], 0, n * 2, stream));
         PLAMO_HIP(hipMemsetAsync(values[l], 0, n * 2, stream));
+        rot_rows[l] = is_global_layer(l) ? 0 : std::min(capacity[l], WINDOW);
+        keys_rot[l] = nullptr;
+        if (rot_rows[l]) {
+            const size_t nr = size_t(lanes) * rot_rows[l] * HEAD_DIM;
+            keys_rot[l] = arena.alloc_n<uint16_t>(nr);
+            PLAMO_HIP(hipMemsetAsync(keys_rot[l], 0, nr * 2, stream));
+        }
     }
     qkv = arena.alloc_n<float>(ROWS * QKV);
     att = arena.alloc_n<uint16_t>(ROWS * ATTN);
@@ -384,6 +391,8 @@ void Engine::enqueue_step(bool head, bool loop) {
         a.k_norm = L.k_norm;
         a.keys = keys[l];
         a.values = values[l];
+        a.keys_rot = keys_rot[l];
+        a.rot_rows = uint32_t(rot_rows[l]);
         a.capacity = uint32_t(capacity[l]);
         a.local_rope = m.local_rope;
         a.global_rope = m.global_rope;
@@ -526,6 +535,8 @@ void Engine::enqueue_prefill_chunk(int n, int p0, int lane, bool last_chunk, boo
         qp.q16 = p_q16;
         qp.keys = keys[l] + size_t(lane) * capacity[l] * HEAD_DIM;
         qp.values = values[l] + size_t(lane) * capacity[l] * HEAD_DIM;
+        qp.keys_rot = keys_rot[l] ? keys_rot[l] + size_t(lane) * rot_rows[l] * HEAD_DIM : nullptr;
+        qp.rot_rows = uint32_t(rot_rows[l]);
         qp.capacity = uint32_t(capacity[l]);
         qp.p0 = uint32_t(p0);
         qp.tokens = n;

@@ -64,6 +64,11 @@ class Engine {
     hipStream_t stream;
     DeviceArena arena;
     uint16_t *keys[LAYERS], *values[LAYERS];
+    // Local layers: every lane's keys rotated at their own position for positions below
+    // rot_rows[l] = min(capacity, 2048), where a row's window starts at 0 and the rotation
+    // coordinate of a key is its position; decode attention reads them instead of rotating.
+    uint16_t* keys_rot[LAYERS];
+    int rot_rows[LAYERS];
     int capacity[LAYERS];
     // decode scratch (ROWS rows)
     float *qkv, *hidden;

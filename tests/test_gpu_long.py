@@ -75,6 +75,38 @@ def test_long_context_decode_bit_exact(long_runtime, oracle_weights):
         rt.set_sampling()
 
 
+def test_decode_crosses_the_first_window_bit_exact(model_dir, oracle_weights):
+    # Inside the first window (positions < 2048) local-layer attention reads keys rotated at
+    # their own position, cached when each key was written (by the prefill and by decode);
+    # from 2048 on it rotates the unrotated keys by position - (pos - 2047).  Decode across
+    # the switch, from a GPU prefill handed to the CPU decoder, bit for bit.
+    d, _ = model_dir
+    rt = plamo_hip.Runtime(d, 2112)
+    try:
+        nxt = rt.prefill(np.random.default_rng(9).integers(1024, 107520, 2030).tolist())
+        ex = exact.ExactDecoder(oracle_weights, 2112, rt.stats()["local_capacity"])
+        for layer in range(16):
+            k, v = rt.kv(layer)
+            ex.keys[layer][:] = k
+            ex.values[layer][:] = v
+        t, pos = nxt, 2030
+        for step in range(30):
+            got = rt.forward([t])
+            bits, hidden, want = ex.step(t, pos)
+            assert np.array_equal(rt.logit_bits(), bits), pos
+            assert np.array_equal(rt.hidden().view(np.uint32), hidden.view(np.uint32)), pos
+            assert got == want, pos
+            if pos in (2047, 2048, 2059):
+                print(f"  position {pos}: bit-exact", flush=True)
+            t, pos = got, pos + 1
+        for layer in range(16):
+            k, v = rt.kv(layer)
+            slots = [p % k.shape[0] for p in range(2030, pos)]
+            assert np.array_equal(k[slots], ex.keys[layer][slots]), layer
+    finally:
+        rt.close()
+
+
 def test_long_context_device_loop_matches_host_loop(long_runtime):
     rt = long_runtime
     rt.set_sampling(PENALTY, FREQUENCY, 0.0, NGRAM)
