@@ -61,6 +61,9 @@ struct FlashParams {
     const uint16_t* keys;      // lane slice [capacity][128]
     const uint16_t* values;
     const uint32_t* local_rope;   // local layers: keys rotate with chunk-relative coordinates
+    const uint16_t* keys_rot;  // local layers: lane slice [rot_rows][128] of keys rotated at their
+                               // own position (null: rotate every key)
+    uint32_t rot_rows;
     uint16_t* out;             // [T][2048] BF16
     uint32_t capacity, p0;
     int tokens;

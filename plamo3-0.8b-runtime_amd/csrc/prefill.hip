@@ -543,7 +543,9 @@ __global__ __launch_bounds__(256) void qk_prep_kernel(const QkPrepParams p) {
 // inputs that a CPU restatement reproduces bit for bit.
 //
 // Keys of local layers are rotated while staged, with coordinate key_pos - base of the
-// workgroup's 16-token chunk (base = max(0, chunk_start - 2047)).
+// workgroup's 16-token chunk (base = max(0, chunk_start - 2047)); where base is 0 and every
+// key of the block lies in the rotated-key cache, that coordinate is the key's position and
+// the cached rotations (written by qk_prep_kernel) are staged as they are.
 constexpr int FT = 8;                 // tokens per query block (workgroup)
 constexpr int FK = 64;                // keys per tile
 constexpr int KST = HEAD_DIM + 8;     // K tile row stride (BF16), 16-byte aligned rows
@@ -554,11 +556,17 @@ constexpr float SCALE_LOG2E = 0.08838834764831845f * 1.4426950408889634f;
 struct KvStage {
     uint4 ka[2], kb[2], rr[4], v[4];
 };
+// Where a tile's keys come from: unrotated (rotate while staged), rotated (global layers, or
+// the rotated-key cache of a local layer).
+struct KvSource {
+    const uint16_t* keys;
+    bool rotate;
+};
 
 // Global loads of one tile: thread -> key tid/4 with RoPE pairs (d, d+64), d = 16*(tid%4)
 // .. +16; and values of keys 4*(tid%16) .. +4 at dims 8*(tid/16) .. +8.
-__device__ __forceinline__ void flash_load(const FlashParams& p, uint32_t k0, uint32_t khi, uint32_t base,
-                                           KvStage& s) {
+__device__ __forceinline__ void flash_load(const FlashParams& p, const KvSource& src, uint32_t k0, uint32_t khi,
+                                           uint32_t base, KvStage& s) {
     const int tid = threadIdx.x;
     const int part = tid & 3;
     const uint32_t kp = k0 + uint32_t(tid >> 2);
@@ -576,12 +584,13 @@ __device__ __forceinline__ void flash_load(const FlashParams& p, uint32_t k0, ui
         return slot;
     };
     if (kp <= khi) {
-        const uint16_t* row = p.keys + size_t(ring(uint32_t(tid >> 2))) * HEAD_DIM;
+        // the rotated-key cache is indexed by position (kp < rot_rows), the ring by slot
+        const uint16_t* row = src.keys + size_t(src.rotate || p.full ? ring(uint32_t(tid >> 2)) : kp) * HEAD_DIM;
         s.ka[0] = *reinterpret_cast<const uint4*>(row + part * 16);
         s.ka[1] = *reinterpret_cast<const uint4*>(row + part * 16 + 8);
         s.kb[0] = *reinterpret_cast<const uint4*>(row + 64 + part * 16);
         s.kb[1] = *reinterpret_cast<const uint4*>(row + 64 + part * 16 + 8);
-        if (!p.full) {
+        if (src.rotate) {
             const uint4* rr = reinterpret_cast<const uint4*>(p.local_rope + size_t(kp - base) * 64 + part * 16);
 #pragma unroll
             for (int i = 0; i < 4; ++i) s.rr[i] = rr[i];
@@ -601,11 +610,11 @@ __device__ __forceinline__ uint32_t u16_of(const uint4& v, int k) {
     return (k & 1) ? (w >> 16) : (w & 0xffffu);
 }
 
-__device__ __forceinline__ void flash_store(const FlashParams& p, const KvStage& s, uint16_t* Ks, uint16_t* Vt) {
+__device__ __forceinline__ void flash_store(const KvSource& src, const KvStage& s, uint16_t* Ks, uint16_t* Vt) {
     const int tid = threadIdx.x;
     const int part = tid & 3, key = tid >> 2;
     uint16_t* krow = Ks + key * KST;
-    if (p.full) {
+    if (!src.rotate) {
         *reinterpret_cast<uint4*>(krow + part * 16) = s.ka[0];
         *reinterpret_cast<uint4*>(krow + part * 16 + 8) = s.ka[1];
         *reinterpret_cast<uint4*>(krow + 64 + part * 16) = s.kb[0];
@@ -687,14 +696,16 @@ __global__ __launch_bounds__(256, 2) void flash_prefill_kernel(const FlashParams
         for (int r = 0; r < 16; ++r) oacc[dt][r] = 0.f;
     float m = NEG_INF, ls = 0.f;
 
+    const bool cached = !p.full && p.keys_rot != nullptr && base == 0 && khi < p.rot_rows;
+    const KvSource src{cached ? p.keys_rot : p.keys, !p.full && !cached};
     KvStage st;
-    flash_load(p, klo + uint32_t(j0 * FK), khi, base, st);
-    flash_store(p, st, Ks[0], Vt[0]);
+    flash_load(p, src, klo + uint32_t(j0 * FK), khi, base, st);
+    flash_store(src, st, Ks[0], Vt[0]);
     __syncthreads();
     for (int j = j0; j < j1; ++j) {
         const int buf = (j - j0) & 1;
         const uint32_t k0 = klo + uint32_t(j * FK);
-        if (j + 1 < j1) flash_load(p, k0 + FK, khi, base, st);
+        if (j + 1 < j1) flash_load(p, src, k0 + FK, khi, base, st);
         // S^T = K Q^T for 64 keys (two 32-row tiles)
         floatx16 sacc[2];
 #pragma unroll
@@ -776,7 +787,7 @@ __global__ __launch_bounds__(256, 2) void flash_prefill_kernel(const FlashParams
                 oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pl, oacc[dt], 0, 0, 0);
             }
         }
-        if (j + 1 < j1) flash_store(p, st, Ks[buf ^ 1], Vt[buf ^ 1]);
+        if (j + 1 < j1) flash_store(src, st, Ks[buf ^ 1], Vt[buf ^ 1]);
         __syncthreads();
     }
     // O = O^T / l; element i of d-tile dt is dim 32dt + 8(i/4) + 4*half + i%4

@@ -549,6 +549,8 @@ void Engine::enqueue_prefill_chunk(int n, int p0, int lane, bool last_chunk, boo
         fa.keys = qp.keys;
         fa.values = qp.values;
         fa.local_rope = m.local_rope;
+        fa.keys_rot = qp.keys_rot;
+        fa.rot_rows = qp.rot_rows;
         fa.out = p_att;
         fa.capacity = qp.capacity;
         fa.p0 = uint32_t(p0);
