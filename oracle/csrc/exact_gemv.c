@@ -68,3 +68,27 @@ void plamo_oracle_dot2_chain(const uint32_t* a, const uint32_t* b, const float* 
         }
     }
 }
+
+/* Decode attention scores (before the scale): q [16][128] and k [n][128] BF16 bits ->
+ * out [16][n].  Each score is four chains over dims 32c .. 32c+31, each a v_dot2_f32_bf16
+ * chain over the dim pairs (32c + 2i, 32c + 2i + 1) in order from 0, summed as
+ * (c0 + c1) + (c2 + c3) -- the decode attention kernel's order. */
+void plamo_oracle_attn_scores(const uint16_t* q, const uint16_t* k, int64_t n, float* out) {
+#pragma omp parallel for schedule(static)
+    for (int64_t j = 0; j < n; ++j) {
+        const uint16_t* kr = k + j * 128;
+        for (int h = 0; h < 16; ++h) {
+            const uint16_t* qr = q + h * 128;
+            float c[4];
+            for (int cc = 0; cc < 4; ++cc) {
+                float a = 0.0f;
+                for (int i = 0; i < 16; ++i) {
+                    const int d = 32 * cc + 2 * i;
+                    a = dot2_bits(qr[d], qr[d + 1], kr[d], kr[d + 1], a);
+                }
+                c[cc] = a;
+            }
+            out[h * n + j] = (c[0] + c[1]) + (c[2] + c[3]);
+        }
+    }
+}

@@ -18,7 +18,8 @@ correctly rounded IEEE FP32 operation, exactly as on the device, except the GEMV
 * q/k norm (`qkv`, Kernels.metal:236-246): 16 lanes x 8 elements (the RoPE pairs d, d+64
   of 4 consecutive d), 16-lane butterfly.
 * decode attention (Kernels.metal:440-562 split form): 64-key partitions; score = four
-  ordered 32-dim chains of q*k summed as (c0 + c1) + (c2 + c3); softmax statistics per
+  32-dim chains of q*k (v_dot2_f32_bf16 steps over the dim pairs in order) summed as
+  (c0 + c1) + (c2 + c3); softmax statistics per
   partition with `exp_det`; P.V as two ordered chains over keys 0..31 and 32..63 (no
   contraction) added at the end; merge over partitions in order.
 * `exp_det`: Cody-Waite reduction with a 16-bit ln2 head, degree-7 Taylor polynomial, exact
@@ -85,6 +86,7 @@ def _c_lib():
             lib = ctypes.CDLL(path)
             lib.plamo_oracle_gemv.argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_int64] * 2
             lib.plamo_oracle_dot2_chain.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_int64] * 2 + [ctypes.c_int32]
+            lib.plamo_oracle_attn_scores.argtypes = [ctypes.c_void_p] * 2 + [ctypes.c_int64, ctypes.c_void_p]
             _C = lib
     return _C or None
 
@@ -106,6 +108,18 @@ def gemv(w, x):
     y = np.empty(m, F)
     _lib().plamo_oracle_gemv(w.ctypes.data, x.ctypes.data, y.ctypes.data, m, n)
     return y
+
+
+def attn_scores(q, keys):
+    """q [16][128], keys [n][128] (BF16-valued FP32) -> raw scores [16][n] in the decode
+    attention kernel's order (csrc/exact_gemv.c)."""
+    qb = bits_np(np.ascontiguousarray(q, dtype=F))
+    kb = bits_np(np.ascontiguousarray(keys, dtype=F))
+    assert np.array_equal(bf_np(qb), q) and np.array_equal(bf_np(kb), keys), "BF16 values expected"
+    n = kb.shape[0]
+    out = np.empty((16, n), F)
+    _lib().plamo_oracle_attn_scores(qb.ctypes.data, kb.ctypes.data, n, out.ctypes.data)
+    return out
 
 
 def dot2_chain(a_pairs, b_pairs, acc, fast=True):
@@ -205,6 +219,7 @@ class ExactDecoder:
         if not full:
             keys = rope_pair(keys, self.lc[r], self.ls[r])
         vals = bf_np(self.values[layer][phys])
+        scores = attn_scores(q, keys)
         parts = (count + KP - 1) // KP
         pm = np.zeros((parts, 16), F)
         pl = np.zeros((parts, 16), F)
@@ -214,14 +229,7 @@ class ExactDecoder:
             kk = keys[k0:k0 + KP]
             vv = vals[k0:k0 + KP]
             nk = kk.shape[0]
-            quarters = []
-            for c in range(4):
-                part = np.zeros((16, nk), F)
-                for d in range(32 * c, 32 * c + 32):
-                    part += q[:, d:d + 1] * kk[None, :, d]
-                quarters.append(part)
-            sc = ((quarters[0] + quarters[1]) + (quarters[2] + quarters[3])).astype(F)
-            sc = (sc * SCALE).astype(F)
+            sc = (scores[:, k0:k0 + nk] * SCALE).astype(F)
             full_sc = np.full((16, 64), -np.inf, F)
             full_sc[:, :nk] = sc
             m = full_sc.max(1)

@@ -896,7 +896,7 @@ __global__ __launch_bounds__(256) void head_merge_kernel(DecodeBuffers b, int bl
 // ---------------------------------------------------------------------- decode attention
 constexpr int KP = KEYS_PER_PART;
 constexpr int HG = 4;                // heads per workgroup (grid.y = HEADS / HG head groups)
-constexpr int KS = 132;              // padded LDS row of rotated keys (16-byte aligned rows)
+constexpr int KS = 68;               // padded LDS row of rotated keys: 64 BF16 pairs + 4 words
 
 // Workgroup (partition x, head group y, row z): keys x*64 .. x*64+63 of the row's visible
 // keys for heads 4y .. 4y+3.  All four head groups rotate the same keys; only group 0
@@ -905,8 +905,8 @@ template <bool FULL>
 __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
 #pragma clang fp contract(off)  // fixed rounding sequence, reproduced by the CPU oracle
     PLAMO_TIMELINE_SCOPE(p.tag);
-    __shared__ __align__(16) float qs[HG * HEAD_DIM];
-    __shared__ __align__(16) float ks[KP * KS];
+    __shared__ __align__(16) uint32_t qs[HG * HEAD_DIM / 2];  // BF16 pairs (dims 2i, 2i + 1)
+    __shared__ __align__(16) uint32_t ks[KP * KS];            // BF16 pairs
     __shared__ __align__(16) uint16_t vs[KP * HEAD_DIM];
     __shared__ __align__(16) float ps[HG * KP];
     __shared__ __align__(16) float knew[HEAD_DIM];
@@ -1005,13 +1005,13 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
         float z[8];
         head_norm8(qlo, qhi, glo, ghi, z);
         const uint32_t c4[4] = {qr.x, qr.y, qr.z, qr.w};
+        float ra[4], rb[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            float ra, rb;
-            rope_pair(z[j], z[4 + j], c4[j], ra, rb);
-            qs[hl * HEAD_DIM + sq * 4 + j] = ra;
-            qs[hl * HEAD_DIM + 64 + sq * 4 + j] = rb;
-        }
+        for (int j = 0; j < 4; ++j) rope_pair(z[j], z[4 + j], c4[j], ra[j], rb[j]);
+        // BF16-exact values: the pairs are lossless
+        uint32_t* qrow = qs + hl * (HEAD_DIM / 2);
+        *reinterpret_cast<uint2*>(qrow + sq * 2) = make_uint2(pack_bf16(ra[0], ra[1]), pack_bf16(ra[2], ra[3]));
+        *reinterpret_cast<uint2*>(qrow + 32 + sq * 2) = make_uint2(pack_bf16(rb[0], rb[1]), pack_bf16(rb[2], rb[3]));
     }
     // ---- the newest key: k norm, RoPE at pos for global layers, KV write (Kernels.metal:253-257)
     if (has_new && tid >= 64 && tid < 80) {
@@ -1058,32 +1058,29 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
     // the newest key and value rows are read by other threads below; the queries only after
     // the next barrier (has_new is the same for the whole workgroup)
     if (has_new) __syncthreads();
-    // ---- keys: (newest from LDS) rotate with coordinate r, stage FP32 in LDS
+    // ---- keys: (newest from LDS) rotate with coordinate r, stage BF16 pairs in LDS: thread
+    //      (kj, ksub) holds dims ksub*16 .. +16 (words aw) and 64 + ksub*16 .. +16 (words bw)
     {
-        float a[16], b[16];
-        const uint32_t aw[8] = {ka[0].x, ka[0].y, ka[0].z, ka[0].w, ka[1].x, ka[1].y, ka[1].z, ka[1].w};
-        const uint32_t bw[8] = {kb[0].x, kb[0].y, kb[0].z, kb[0].w, kb[1].x, kb[1].y, kb[1].z, kb[1].w};
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            a[2 * i] = lo(aw[i]); a[2 * i + 1] = hi(aw[i]);
-            b[2 * i] = lo(bw[i]); b[2 * i + 1] = hi(bw[i]);
-        }
+        uint32_t aw[8] = {ka[0].x, ka[0].y, ka[0].z, ka[0].w, ka[1].x, ka[1].y, ka[1].z, ka[1].w};
+        uint32_t bw[8] = {kb[0].x, kb[0].y, kb[0].z, kb[0].w, kb[1].x, kb[1].y, kb[1].z, kb[1].w};
         if (kr == newest) {
 #pragma unroll
-            for (int i = 0; i < 16; ++i) { a[i] = knew[ksub * 16 + i]; b[i] = knew[64 + ksub * 16 + i]; }
+            for (int i = 0; i < 8; ++i) {
+                aw[i] = pack_bf16(knew[ksub * 16 + 2 * i], knew[ksub * 16 + 2 * i + 1]);
+                bw[i] = pack_bf16(knew[64 + ksub * 16 + 2 * i], knew[64 + ksub * 16 + 2 * i + 1]);
+            }
         }
         if (!FULL && !prerot && kr < count) {
             const uint32_t rw[16] = {rr[0].x, rr[0].y, rr[0].z, rr[0].w, rr[1].x, rr[1].y, rr[1].z, rr[1].w,
                                      rr[2].x, rr[2].y, rr[2].z, rr[2].w, rr[3].x, rr[3].y, rr[3].z, rr[3].w};
 #pragma unroll
-            for (int i = 0; i < 16; i += 2) rope_pair_x2f(a[i], b[i], rw[i], a[i + 1], b[i + 1], rw[i + 1]);
+            for (int i = 0; i < 8; ++i) rope_pair_x2(aw[i], bw[i], rw[2 * i], rw[2 * i + 1], aw[i], bw[i]);
         }
-        float* krow = ks + kj * KS;
-#pragma unroll
-        for (int i = 0; i < 16; i += 4) {
-            *reinterpret_cast<float4*>(krow + ksub * 16 + i) = make_float4(a[i], a[i + 1], a[i + 2], a[i + 3]);
-            *reinterpret_cast<float4*>(krow + 64 + ksub * 16 + i) = make_float4(b[i], b[i + 1], b[i + 2], b[i + 3]);
-        }
+        uint32_t* krow = ks + kj * KS;
+        *reinterpret_cast<uint4*>(krow + ksub * 8) = make_uint4(aw[0], aw[1], aw[2], aw[3]);
+        *reinterpret_cast<uint4*>(krow + ksub * 8 + 4) = make_uint4(aw[4], aw[5], aw[6], aw[7]);
+        *reinterpret_cast<uint4*>(krow + 32 + ksub * 8) = make_uint4(bw[0], bw[1], bw[2], bw[3]);
+        *reinterpret_cast<uint4*>(krow + 32 + ksub * 8 + 4) = make_uint4(bw[4], bw[5], bw[6], bw[7]);
         if (kr != newest) {  // the newest V row was staged before the barrier
 #pragma unroll
             for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(vs + kj * HEAD_DIM + ksub * 32 + 8 * i) = vv[i];
@@ -1091,22 +1088,23 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
     }
     __syncthreads();
     // ---- scores: wave w = local head w, lane = key.  Each score is four ordered 32-dim
-    //      chains (dims 32c .. 32c+31) summed as (c0 + c1) + (c2 + c3).
+    //      chains (dims 32c .. 32c+31, v_dot2_f32_bf16 over the dim pairs in order) summed as
+    //      (c0 + c1) + (c2 + c3).
     {
         const int j = lane, w = wave;
         float sc[4] = {0.f, 0.f, 0.f, 0.f};
-        const float* krow = ks + j * KS;
-        const float* qrow = qs + w * HEAD_DIM;
-#pragma unroll 4
-        for (int d = 0; d < 32; d += 4) {
+        const uint32_t* krow = ks + j * KS;
+        const uint32_t* qrow = qs + w * (HEAD_DIM / 2);
+#pragma unroll
+        for (int i = 0; i < 16; i += 4) {
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
-                const float4 kd = *reinterpret_cast<const float4*>(krow + 32 * c + d);
-                const float4 qd = *reinterpret_cast<const float4*>(qrow + 32 * c + d);
-                sc[c] = fmaf(qd.x, kd.x, sc[c]);
-                sc[c] = fmaf(qd.y, kd.y, sc[c]);
-                sc[c] = fmaf(qd.z, kd.z, sc[c]);
-                sc[c] = fmaf(qd.w, kd.w, sc[c]);
+                const uint4 kd = *reinterpret_cast<const uint4*>(krow + 16 * c + i);
+                const uint4 qd = *reinterpret_cast<const uint4*>(qrow + 16 * c + i);
+                sc[c] = dot2bf(qd.x, kd.x, sc[c]);
+                sc[c] = dot2bf(qd.y, kd.y, sc[c]);
+                sc[c] = dot2bf(qd.z, kd.z, sc[c]);
+                sc[c] = dot2bf(qd.w, kd.w, sc[c]);
             }
         }
         const bool valid = k0 + j < count;
@@ -1181,8 +1179,8 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
     // per head: M = max_p m_p, w_p = exp(m_p - M), den = sum_p l_p w_p (partition order);
     // then each (h, d) sums o_p w_p in partition order.  Partition statistics are staged in
     // LDS (the key tile is free now) with all loads in flight together.
-    float* mm = ks;                                    // [np][HG]
-    float* wl = ks + (KP * KS) / 2;                    // [np][HG]: l, then the weights
+    float* mm = reinterpret_cast<float*>(ks);          // [np][HG]
+    float* wl = mm + (KP * KS) / 2;                    // [np][HG]: l, then the weights
     const uint32_t np = nparts <= uint32_t(KP * KS / 2 / HG) ? nparts : uint32_t(KP * KS / 2 / HG);
     // up to 64 partitions one entry per thread; more: eight entries per thread in flight
     if (np * HG <= 256) {

@@ -95,6 +95,27 @@ def test_gemv_is_lane_chains_of_dot2():
         assert got[l] == chain, l
 
 
+def test_attention_scores_are_dot2_chains():
+    # each raw score: four 32-dim chains of dot2 steps over the dim pairs in order, summed as
+    # (c0 + c1) + (c2 + c3); checked against the general fold one chain at a time
+    rng = np.random.default_rng(6)
+    q = roundbf_np(rng.standard_normal((16, 128)).astype(np.float32))
+    k = roundbf_np((rng.standard_normal((70, 128)) * 2.0 ** rng.integers(-6, 6, (70, 1))).astype(np.float32))
+    got = exact.attn_scores(q, k)
+    for h, j in ((0, 0), (5, 17), (15, 69)):
+        chains = []
+        for c in range(4):
+            d = np.arange(32 * c, 32 * c + 32)
+            a = _pairs(q[h, d[0::2]], q[h, d[1::2]])[:, None]
+            b = _pairs(k[j, d[0::2]], k[j, d[1::2]])[:, None]
+            chains.append(exact.dot2_chain(a, b, [0.0], fast=False)[-1, 0])
+        assert got[h, j] == (chains[0] + chains[1]) + (chains[2] + chains[3]), (h, j)
+    # small integers: every sum exact, whatever the order
+    qi = rng.integers(-8, 9, (16, 128)).astype(np.float32)
+    ki = rng.integers(-8, 9, (5, 128)).astype(np.float32)
+    assert np.array_equal(exact.attn_scores(qi, ki), (qi.astype(np.float64) @ ki.T.astype(np.float64)).astype(np.float32))
+
+
 def test_block_sumsq_and_norm():
     v = np.full(1536, 2.0, np.float32)
     assert exact.block_sumsq(v) == np.float32(6144.0)
