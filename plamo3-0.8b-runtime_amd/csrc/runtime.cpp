@@ -284,6 +284,7 @@ Engine::Engine(std::shared_ptr<Model> mdl, int ctx, int nl, hipStream_t s)
     p_flash_o = arena.alloc_n<float>(flash_part_o_floats(chunk));
     p_flash_ml = arena.alloc_n<float>(flash_part_ml_floats(chunk));
     p_flash_tickets = arena.alloc_n<uint32_t>(size_t(flash_blocks(chunk)));
+    if (model->packed) p_wexp = arena.alloc_n<uint16_t>(size_t(2 * INTER) * HIDDEN);
     PLAMO_HIP(hipMemsetAsync(p_flash_tickets, 0, size_t(flash_blocks(chunk)) * 4, stream));
     p_act = arena.alloc_n<uint16_t>(size_t(chunk) * INTER);
     p_tokens = arena.alloc_n<int32_t>(size_t(chunk));
@@ -522,12 +523,25 @@ void Engine::enqueue_prefill_chunk(int n, int p0, int lane, bool last_chunk, boo
     rn.g_next = m.layers[0].pre;
     rn.xn = p_xn;
     launch_rows_norm(rn, n, stream);
+    // .p12 weights are expanded to BF16 rows (bit-identical to the plain tensor) right before
+    // their GEMM, which then loads them straight into LDS like plain weights: expanding each
+    // block in the GEMM's registers was up to seven times slower at short prompts
+    auto gemm = [&](const Linear& W, GemmEpilogue epi, GemmParams g) {
+        if (pk) {
+            launch_unpack(reinterpret_cast<const uint8_t*>(W.w), W.table, p_wexp, int64_t(g.m) * g.k, stream);
+            g.w = p_wexp;
+        } else {
+            g.w = W.w;
+        }
+        g.table = nullptr;
+        launch_gemm(false, epi, g, stream);
+    };
     for (int l = 0; l < LAYERS; ++l) {
         const LayerWeights& L = m.layers[l];
         const bool full = is_global_layer(l);
         GemmParams q{};
-        q.w = L.qkv.w; q.table = L.qkv.table; q.x = p_xn; q.y16 = p_qkv; q.m = QKV; q.k = HIDDEN; q.tokens = n;
-        launch_gemm(pk, GEMM_BF16, q, stream);
+        q.x = p_xn; q.y16 = p_qkv; q.m = QKV; q.k = HIDDEN; q.tokens = n;
+        gemm(L.qkv, GEMM_BF16, q);
         QkPrepParams qp{};
         qp.qkv = p_qkv;
         qp.q_norm = L.q_norm;
@@ -561,18 +575,18 @@ void Engine::enqueue_prefill_chunk(int n, int p0, int lane, bool last_chunk, boo
         fa.tickets = p_flash_tickets;
         launch_flash_prefill(fa, stream);
         GemmParams o{};
-        o.w = L.o.w; o.table = L.o.table; o.x = p_att; o.y16 = p_proj; o.m = HIDDEN; o.k = ATTN; o.tokens = n;
-        launch_gemm(pk, GEMM_BF16, o, stream);
+        o.x = p_att; o.y16 = p_proj; o.m = HIDDEN; o.k = ATTN; o.tokens = n;
+        gemm(L.o, GEMM_BF16, o);
         RowsNormParams r1{};
         r1.in = p_proj; r1.g_post = L.post; r1.post_offset = POST_MIXER_OFFSET; r1.x = p_x; r1.g_next = L.pre_mlp;
         r1.xn = p_xn;
         launch_rows_norm(r1, n, stream);
         GemmParams u{};
-        u.w = L.up.w; u.table = L.up.table; u.x = p_xn; u.y16 = p_act; u.m = 2 * INTER; u.k = HIDDEN; u.tokens = n;
-        launch_gemm(pk, GEMM_SWIGLU, u, stream);
+        u.x = p_xn; u.y16 = p_act; u.m = 2 * INTER; u.k = HIDDEN; u.tokens = n;
+        gemm(L.up, GEMM_SWIGLU, u);
         GemmParams d{};
-        d.w = L.down.w; d.table = L.down.table; d.x = p_act; d.y16 = p_proj; d.m = HIDDEN; d.k = INTER; d.tokens = n;
-        launch_gemm(pk, GEMM_BF16, d, stream);
+        d.x = p_act; d.y16 = p_proj; d.m = HIDDEN; d.k = INTER; d.tokens = n;
+        gemm(L.down, GEMM_BF16, d);
         if (l + 1 < LAYERS) {
             RowsNormParams r2{};
             r2.in = p_proj; r2.g_post = L.post_mlp; r2.post_offset = post_mlp_offset(); r2.x = p_x;

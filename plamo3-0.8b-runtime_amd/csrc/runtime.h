@@ -87,6 +87,9 @@ class Engine {
     uint16_t *p_xn, *p_att, *p_act, *p_q16;
     float *p_flash_o, *p_flash_ml;  // split flash prefill workspace
     uint32_t* p_flash_tickets;
+    // .p12 models: one projection's weights expanded to BF16 rows for the prefill GEMMs
+    // (the largest, gate_up: 37.7 MB), rewritten before each GEMM of a chunk
+    uint16_t* p_wexp = nullptr;
     int32_t* p_tokens;
     size_t part_rows_cap;    // rows x parts the partial buffers hold
     // graph
