@@ -1005,9 +1005,9 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
         float z[8];
         head_norm8(qlo, qhi, glo, ghi, z);
         const uint32_t c4[4] = {qr.x, qr.y, qr.z, qr.w};
-        float ra[4], rb[4];
+        float ra[4] = {z[0], z[1], z[2], z[3]}, rb[4] = {z[4], z[5], z[6], z[7]};
 #pragma unroll
-        for (int j = 0; j < 4; ++j) rope_pair(z[j], z[4 + j], c4[j], ra[j], rb[j]);
+        for (int j = 0; j < 4; j += 2) rope_pair_x2f(ra[j], rb[j], c4[j], ra[j + 1], rb[j + 1], c4[j + 1]);
         // BF16-exact values: the pairs are lossless
         uint32_t* qrow = qs + hl * (HEAD_DIM / 2);
         *reinterpret_cast<uint2*>(qrow + sq * 2) = make_uint2(pack_bf16(ra[0], ra[1]), pack_bf16(ra[2], ra[3]));
@@ -1023,14 +1023,16 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
             const uint4 gr = *reinterpret_cast<const uint4*>(p.global_rope + size_t(pos) * 64 + t * 4);
             const uint32_t c4[4] = {gr.x, gr.y, gr.z, gr.w};
 #pragma unroll
-            for (int j = 0; j < 4; ++j) rope_pair(z[j], z[4 + j], c4[j], z[j], z[4 + j]);
+            for (int j = 0; j < 4; j += 2) rope_pair_x2f(z[j], z[4 + j], c4[j], z[j + 1], z[4 + j + 1], c4[j + 1]);
         }
         float zr[8];
         if (prerot) {  // the newest key at its own position (coordinate pos - first = pos)
             const uint4 lr = *reinterpret_cast<const uint4*>(p.local_rope + size_t(pos) * 64 + t * 4);
             const uint32_t c4[4] = {lr.x, lr.y, lr.z, lr.w};
 #pragma unroll
-            for (int j = 0; j < 4; ++j) rope_pair(z[j], z[4 + j], c4[j], zr[j], zr[4 + j]);
+            for (int j = 0; j < 8; ++j) zr[j] = z[j];
+#pragma unroll
+            for (int j = 0; j < 4; j += 2) rope_pair_x2f(zr[j], zr[4 + j], c4[j], zr[j + 1], zr[4 + j + 1], c4[j + 1]);
         } else {
 #pragma unroll
             for (int j = 0; j < 8; ++j) zr[j] = z[j];

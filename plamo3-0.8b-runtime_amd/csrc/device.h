@@ -346,11 +346,13 @@ __device__ __forceinline__ void head_norm8(const float4 lo, const float4 hi, con
     ss = group16_sum(ss);
     const float r = 1.0f / sqrtf(ss / 128.0f + 1e-6f);
     const uint32_t g[4] = {glo.x, glo.y, ghi.x, ghi.y};
+    // z = roundbf(roundbf(v r) roundbf(w + 1)), two elements per packed RNE conversion
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const uint32_t gw = g[j >> 1];
-        const float gain = roundbf((j & 1 ? hi_bf(gw) : lo_bf(gw)) + 1.0f);
-        z[j] = roundbf(roundbf(v[j] * r) * gain);
+    for (int j = 0; j < 8; j += 2) {
+        float g0, g1, t0, t1;
+        round_bf16x2(lo_bf(g[j >> 1]) + 1.0f, hi_bf(g[j >> 1]) + 1.0f, g0, g1);
+        round_bf16x2(v[j] * r, v[j + 1] * r, t0, t1);
+        round_bf16x2(t0 * g0, t1 * g1, z[j], z[j + 1]);
     }
 }
 

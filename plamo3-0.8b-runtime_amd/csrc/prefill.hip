@@ -415,12 +415,17 @@ __global__ __launch_bounds__(256) void rows_norm_kernel(const RowsNormParams p) 
 #pragma unroll
             for (int k = 0; k < 8; ++k) ss += pv[c][k] * pv[c][k];
         const float r = 1.0f / sqrtf(wave_sum(ss) / float(HIDDEN) + 1e-6f);
+        // z = roundbf(roundbf(p r) roundbf(w + offset)), x = roundbf(x + z): the roundings two
+        // at a time with the packed RNE conversion (same bits as `roundbf`)
 #pragma unroll
         for (int c = 0; c < C; ++c)
 #pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                const float z = roundbf(roundbf(pv[c][k] * r) * roundbf(gp[c][k] + p.post_offset));
-                xv[c][k] = roundbf(rv[c][k] + z);
+            for (int k = 0; k < 8; k += 2) {
+                float t0, t1, g0, g1, z0, z1;
+                round_bf16x2(pv[c][k] * r, pv[c][k + 1] * r, t0, t1);
+                round_bf16x2(gp[c][k] + p.post_offset, gp[c][k + 1] + p.post_offset, g0, g1);
+                round_bf16x2(t0 * g0, t1 * g1, z0, z1);
+                round_bf16x2(rv[c][k] + z0, rv[c][k + 1] + z1, xv[c][k], xv[c][k + 1]);
             }
     }
     float ss = 0.f;
@@ -437,10 +442,13 @@ __global__ __launch_bounds__(256) void rows_norm_kernel(const RowsNormParams p) 
         if (p.xn) unpack(*reinterpret_cast<const uint4*>(p.g_next + i), gn);
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-            xw[k] = bits(xv[c][2 * k]) | (bits(xv[c][2 * k + 1]) << 16);
-            if (p.xn)
-                nw[k] = bits(roundbf(roundbf(xv[c][2 * k] * r) * roundbf(gn[2 * k] + 1.0f))) |
-                        (bits(roundbf(roundbf(xv[c][2 * k + 1] * r) * roundbf(gn[2 * k + 1] + 1.0f))) << 16);
+            xw[k] = pack_bf16(xv[c][2 * k], xv[c][2 * k + 1]);  // BF16 values: exact
+            if (p.xn) {
+                float t0, t1, g0, g1;
+                round_bf16x2(xv[c][2 * k] * r, xv[c][2 * k + 1] * r, t0, t1);
+                round_bf16x2(gn[2 * k] + 1.0f, gn[2 * k + 1] + 1.0f, g0, g1);
+                nw[k] = pack_bf16(t0 * g0, t1 * g1);
+            }
         }
         *reinterpret_cast<uint4*>(p.x + row + i) = make_uint4(xw[0], xw[1], xw[2], xw[3]);
         if (p.xn) *reinterpret_cast<uint4*>(p.xn + row + i) = make_uint4(nw[0], nw[1], nw[2], nw[3]);
@@ -477,17 +485,12 @@ __global__ __launch_bounds__(256) void qk_prep_kernel(const QkPrepParams p) {
         float z[8];
         head_norm8(qlo, qhi, glo, ghi, z);
         const uint32_t c4[4] = {qr.x, qr.y, qr.z, qr.w};
-        uint16_t ra[4], rb[4];
+        // rope_pair_x2f: two RoPE pairs per packed RNE conversion (same bits as rope_pair)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            float a, b;
-            rope_pair(z[j], z[4 + j], c4[j], a, b);
-            ra[j] = uint16_t(bits(a));
-            rb[j] = uint16_t(bits(b));
-        }
+        for (int j = 0; j < 4; j += 2) rope_pair_x2f(z[j], z[4 + j], c4[j], z[j + 1], z[4 + j + 1], c4[j + 1]);
         uint16_t* qo = p.q16 + (size_t(t) * HEADS + hq) * HEAD_DIM;
-        *reinterpret_cast<uint2*>(qo + sq * 4) = make_uint2(ra[0] | (uint32_t(ra[1]) << 16), ra[2] | (uint32_t(ra[3]) << 16));
-        *reinterpret_cast<uint2*>(qo + 64 + sq * 4) = make_uint2(rb[0] | (uint32_t(rb[1]) << 16), rb[2] | (uint32_t(rb[3]) << 16));
+        *reinterpret_cast<uint2*>(qo + sq * 4) = make_uint2(pack_bf16(z[0], z[1]), pack_bf16(z[2], z[3]));
+        *reinterpret_cast<uint2*>(qo + 64 + sq * 4) = make_uint2(pack_bf16(z[4], z[5]), pack_bf16(z[6], z[7]));
     }
     const size_t slot = size_t(pos % p.capacity) * HEAD_DIM;
     if (tid < 16) {
@@ -501,19 +504,17 @@ __global__ __launch_bounds__(256) void qk_prep_kernel(const QkPrepParams p) {
             const uint4 gr = *reinterpret_cast<const uint4*>(p.global_rope + size_t(pos) * 64 + tid * 4);
             const uint32_t c4[4] = {gr.x, gr.y, gr.z, gr.w};
 #pragma unroll
-            for (int j = 0; j < 4; ++j) rope_pair(z[j], z[4 + j], c4[j], z[j], z[4 + j]);
+            for (int j = 0; j < 4; j += 2) rope_pair_x2f(z[j], z[4 + j], c4[j], z[j + 1], z[4 + j + 1], c4[j + 1]);
         } else if (p.keys_rot && pos < p.rot_rows) {
             // the copy rotated at the key's own position (decode inside the first window)
             const uint4 lr = *reinterpret_cast<const uint4*>(p.local_rope + size_t(pos) * 64 + tid * 4);
             const uint32_t c4[4] = {lr.x, lr.y, lr.z, lr.w};
-            uint16_t* kr = p.keys_rot + size_t(pos) * HEAD_DIM;
+            float zr[8] = {z[0], z[1], z[2], z[3], z[4], z[5], z[6], z[7]};
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                float ra, rb;
-                rope_pair(z[j], z[4 + j], c4[j], ra, rb);
-                kr[tid * 4 + j] = uint16_t(bits(ra));
-                kr[64 + tid * 4 + j] = uint16_t(bits(rb));
-            }
+            for (int j = 0; j < 4; j += 2) rope_pair_x2f(zr[j], zr[4 + j], c4[j], zr[j + 1], zr[4 + j + 1], c4[j + 1]);
+            uint16_t* kr = p.keys_rot + size_t(pos) * HEAD_DIM;
+            *reinterpret_cast<uint2*>(kr + tid * 4) = make_uint2(pack_bf16(zr[0], zr[1]), pack_bf16(zr[2], zr[3]));
+            *reinterpret_cast<uint2*>(kr + 64 + tid * 4) = make_uint2(pack_bf16(zr[4], zr[5]), pack_bf16(zr[6], zr[7]));
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
