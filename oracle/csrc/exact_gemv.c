@@ -7,6 +7,7 @@
  * by an XOR butterfly with offsets 32,16,8,4,2,1 (correctly rounded FP32 additions) -- the
  * reduction tree of the decode GEMV kernel.  w and x hold BF16 values in FP32.
  * Compiled with -ffp-contract=off. */
+#include <math.h>
 #include <stdint.h>
 #include <string.h>
 
@@ -91,4 +92,23 @@ void plamo_oracle_attn_scores(const uint16_t* q, const uint16_t* k, int64_t n, f
             out[h * n + j] = (c[0] + c[1]) + (c[2] + c[3]);
         }
     }
+}
+
+/* Decode attention P.V of one 64-key partition: e [16][64] FP32 probabilities (unnormalised),
+ * v [nk][128] BF16 bits -> out [16][128].  Per head and dim, keys 0..31 and 32..63 are two
+ * chains of fused multiply-adds in key order from 0 (keys past nk are absent), then the two
+ * halves are added -- the decode attention kernel's order. */
+void plamo_oracle_attn_pv(const float* e, const uint16_t* v, int64_t nk, float* out) {
+    for (int h = 0; h < 16; ++h)
+        for (int d = 0; d < 128; ++d) {
+            float half[2] = {0.0f, 0.0f};
+            for (int hf = 0; hf < 2; ++hf)
+                for (int64_t j = 32 * hf; j < 32 * hf + 32 && j < nk; ++j) {
+                    const uint32_t u = (uint32_t)v[j * 128 + d] << 16;
+                    float vf;
+                    memcpy(&vf, &u, 4);
+                    half[hf] = fmaf(e[h * 64 + j], vf, half[hf]);
+                }
+            out[h * 128 + d] = half[0] + half[1];
+        }
 }

@@ -19,9 +19,9 @@ correctly rounded IEEE FP32 operation, exactly as on the device, except the GEMV
   of 4 consecutive d), 16-lane butterfly.
 * decode attention (Kernels.metal:440-562 split form): 64-key partitions; score = four
   32-dim chains of q*k (v_dot2_f32_bf16 steps over the dim pairs in order) summed as
-  (c0 + c1) + (c2 + c3); softmax statistics per
-  partition with `exp_det`; P.V as two ordered chains over keys 0..31 and 32..63 (no
-  contraction) added at the end; merge over partitions in order.
+  (c0 + c1) + (c2 + c3); softmax statistics per partition with `exp_det`; P.V as two
+  chains of fused multiply-adds over keys 0..31 and 32..63 per dim, added at the end;
+  merge over partitions in order.
 * `exp_det`: Cody-Waite reduction with a 16-bit ln2 head, degree-7 Taylor polynomial, exact
   2^k scale -- the same operation sequence as the device helper.
 
@@ -87,6 +87,7 @@ def _c_lib():
             lib.plamo_oracle_gemv.argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_int64] * 2
             lib.plamo_oracle_dot2_chain.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_int64] * 2 + [ctypes.c_int32]
             lib.plamo_oracle_attn_scores.argtypes = [ctypes.c_void_p] * 2 + [ctypes.c_int64, ctypes.c_void_p]
+            lib.plamo_oracle_attn_pv.argtypes = [ctypes.c_void_p] * 2 + [ctypes.c_int64, ctypes.c_void_p]
             _C = lib
     return _C or None
 
@@ -119,6 +120,18 @@ def attn_scores(q, keys):
     n = kb.shape[0]
     out = np.empty((16, n), F)
     _lib().plamo_oracle_attn_scores(qb.ctypes.data, kb.ctypes.data, n, out.ctypes.data)
+    return out
+
+
+def attn_pv(e, v_bits):
+    """One partition's P.V: e [16][64] FP32, v_bits [nk][128] BF16 bits -> [16][128] in the
+    decode attention kernel's order (two 32-key chains of fused multiply-adds per head and
+    dim, then their sum; csrc/exact_gemv.c)."""
+    e = np.ascontiguousarray(e, dtype=F)
+    assert e.shape == (16, 64)
+    vb = np.ascontiguousarray(v_bits, dtype=np.uint16)
+    out = np.empty((16, 128), F)
+    _lib().plamo_oracle_attn_pv(e.ctypes.data, vb.ctypes.data, vb.shape[0], out.ctypes.data)
     return out
 
 
@@ -218,7 +231,7 @@ class ExactDecoder:
         keys = bf_np(self.keys[layer][phys])
         if not full:
             keys = rope_pair(keys, self.lc[r], self.ls[r])
-        vals = bf_np(self.values[layer][phys])
+        vbits = self.values[layer][phys]
         scores = attn_scores(q, keys)
         parts = (count + KP - 1) // KP
         pm = np.zeros((parts, 16), F)
@@ -227,7 +240,6 @@ class ExactDecoder:
         for p in range(parts):
             k0 = p * KP
             kk = keys[k0:k0 + KP]
-            vv = vals[k0:k0 + KP]
             nk = kk.shape[0]
             sc = (scores[:, k0:k0 + nk] * SCALE).astype(F)
             full_sc = np.full((16, 64), -np.inf, F)
@@ -236,13 +248,7 @@ class ExactDecoder:
             e = np.zeros((16, 64), F)
             e[:, :nk] = exp_det(sc - m[:, None])
             pm[p], pl[p] = m, butterfly(e)
-            halves = []
-            for hf in range(2):
-                o = np.zeros((16, 128), F)
-                for j in range(32 * hf, min(nk, 32 * hf + 32)):
-                    o = (o + e[:, j:j + 1] * vv[j][None, :]).astype(F)
-                halves.append(o)
-            po[p] = (halves[0] + halves[1]).astype(F)
+            po[p] = attn_pv(e, vbits[k0:k0 + KP])
         M = pm.max(0)
         num = np.zeros((16, 128), F)
         den = np.zeros(16, F)

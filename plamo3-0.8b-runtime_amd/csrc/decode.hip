@@ -1130,7 +1130,8 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     // ---- unnormalised P.V: thread -> dims 2e, 2e+1 (e = tid & 63) of local head tid >> 6;
-    //      keys 0..31 and 32..63 as two ordered chains per dim, added at the end
+    //      keys 0..31 and 32..63 as two ordered chains of fused multiply-adds per dim, added
+    //      at the end
     {
         const int e = tid & 63, hl = wave;
         const uint32_t* v32 = reinterpret_cast<const uint32_t*>(vs);
@@ -1148,8 +1149,8 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
                 const float pw[4] = {pp.x, pp.y, pp.z, pp.w};
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    o[0][hf] = o[0][hf] + pw[i] * lo(vw[hf][i]);
-                    o[1][hf] = o[1][hf] + pw[i] * hi(vw[hf][i]);
+                    o[0][hf] = fmaf(pw[i], lo(vw[hf][i]), o[0][hf]);
+                    o[1][hf] = fmaf(pw[i], hi(vw[hf][i]), o[1][hf]);
                 }
             }
         }

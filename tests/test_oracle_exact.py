@@ -116,6 +116,29 @@ def test_attention_scores_are_dot2_chains():
     assert np.array_equal(exact.attn_scores(qi, ki), (qi.astype(np.float64) @ ki.T.astype(np.float64)).astype(np.float32))
 
 
+def test_attention_pv_is_fma_chains():
+    # per head and dim: keys 0..31 and 32..nk-1 as two chains of fused multiply-adds from 0
+    # (one rounding per step: exact in float64 for these magnitudes), then the halves added
+    rng = np.random.default_rng(8)
+    nk = 45
+    e = np.zeros((16, 64), np.float32)
+    e[:, :nk] = rng.uniform(0.1, 1.0, (16, nk)).astype(np.float32)
+    v = roundbf_np(rng.uniform(-2, 2, (nk, 128)).astype(np.float32))
+    got = exact.attn_pv(e, bits_np(v))
+    fused = np.zeros((16, 128), np.float32)
+    unfused = np.zeros((16, 128), np.float32)
+    for hf, ks in enumerate((range(0, 32), range(32, nk))):
+        a = np.zeros((16, 128), np.float32)
+        b = np.zeros((16, 128), np.float32)
+        for j in ks:
+            a = (a.astype(np.float64) + e[:, j:j + 1].astype(np.float64) * v[j].astype(np.float64)).astype(np.float32)
+            b = (b + (e[:, j:j + 1] * v[j]).astype(np.float32)).astype(np.float32)
+        fused = (fused + a).astype(np.float32) if hf else a
+        unfused = (unfused + b).astype(np.float32) if hf else b
+    assert np.array_equal(got, fused)
+    assert not np.array_equal(got, unfused)
+
+
 def test_block_sumsq_and_norm():
     v = np.full(1536, 2.0, np.float32)
     assert exact.block_sumsq(v) == np.float32(6144.0)
