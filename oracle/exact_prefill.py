@@ -131,12 +131,15 @@ class ExactPrefill:
     def _bits(self, t):
         return self.ex._bits(t)
 
-    def prefill(self, tokens, p0=0):
-        """Runtime.prefill from position p0 -> (logit_bits, hidden, next) of the last token."""
+    def prefill(self, tokens, p0=0, kv_layers=None):
+        """Runtime.prefill from position p0 -> (logit_bits, hidden, next) of the last token.
+        kv_layers = L < 16 (one chunk only): stop once layer L - 1 has written its keys and
+        values (layers 0 .. L - 2 in full), return None."""
         out = None
         for c0 in range(0, len(tokens), self.chunk):
             part = tokens[c0:c0 + self.chunk]
-            out = self._chunk(part, p0 + c0, c0 + len(part) == len(tokens))
+            assert kv_layers is None or len(part) == len(tokens), "kv_layers: a single chunk"
+            out = self._chunk(part, p0 + c0, c0 + len(part) == len(tokens), kv_layers)
         return out
 
     def _qk_prep(self, layer, qkv, p0):
@@ -161,7 +164,7 @@ class ExactPrefill:
             ex.values[layer][pos % cap] = bits_np(qkv[t, 2176:2304])
         return q16
 
-    def _chunk(self, tokens, p0, last):
+    def _chunk(self, tokens, p0, last, kv_layers=None):
         ex = self.ex
         Ls = ex.layers
         emb = bf_np(ex.w.embed_bits[np.asarray(tokens, np.int64)]).astype(F)
@@ -176,6 +179,8 @@ class ExactPrefill:
                 xn = rows_norm(x, self._bits(L["pre"]), 1.0)
             qkv = roundbf_np(mfma_gemm(self.wb[i]["qkv"], bits_np(xn)))
             q16 = self._qk_prep(i, qkv, p0)
+            if kv_layers is not None and i + 1 >= kv_layers:
+                return None
             att = flash(q16, ex.keys[i], ex.values[i], self.lcb, self.lsb, ex.cap[i], p0, full)
             o = roundbf_np(mfma_gemm(self.wb[i]["o"], att))
             z = rows_norm(o, self._bits(L["post"]), POST_MIXER)

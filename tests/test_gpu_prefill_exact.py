@@ -130,6 +130,30 @@ def test_prefill_bit_exact(model_dir, twin_prefill, packed):
     rt.close()
 
 
+def test_config3_prefill_first_layers_bit_exact(model_dir, oracle_weights, golden):
+    # configs[2] itself: the 2048-token prompt in one chunk.  The twin runs layer 0 in full
+    # (qkv, flash attention over the 2048-key causal window, o, norms, gate_up, down) and
+    # layer 1 up to its KV write; every key and value of both layers equals the GPU's.
+    g = golden["config3"]
+    prompt = np.random.default_rng(g["prompt_seed"]).integers(1024, 107520, g["length"]).tolist()
+    d, _ = model_dir
+    rt = plamo_hip.Runtime(d, 2048)
+    try:
+        rt.prefill(prompt)
+        kv = [rt.kv(layer) for layer in (0, 1)]
+        cap = rt.stats()["local_capacity"]
+    finally:
+        rt.close()
+    ex = exact.ExactDecoder(oracle_weights, 2048, cap)
+    xp.ExactPrefill(ex).prefill(prompt, kv_layers=2)
+    n = len(prompt)
+    for layer, (k, v) in zip((0, 1), kv):
+        bad_k = int(np.sum(k[:n] != ex.keys[layer][:n]))
+        bad_v = int(np.sum(v[:n] != ex.values[layer][:n]))
+        print(f"  config3 layer {layer}: {bad_k} key / {bad_v} value words differ", flush=True)
+        assert bad_k == 0 and bad_v == 0, layer
+
+
 def test_decode_after_prefill_bit_exact(model_dir, oracle_weights, twin_prefill):
     # greedy decode on the prefilled KV: the GPU step equals the decode twin run on the
     # prefill twin's KV, step after step
