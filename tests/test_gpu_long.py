@@ -6,8 +6,9 @@ the prefill is handed to the order-exact CPU decoder (oracle/exact.py), and ever
 decode step must match it bit for bit: logits, final hidden state, the new KV rows and the
 controlled selection (Sampler.select over the generated history, Main.swift:237-244).  This
 covers the ring wrap of the 14 local layers, global attention over ~30K keys in 480
-partitions and the split-K merge at that size; the MFMA prefill itself is covered by the
-noise-floor tests.
+partitions and the split-K merge at that size.  The device loop then runs the whole config
+(2,048 generated tokens) to the 32,768 cap, and its last eight positions are checked the same
+way.  The MFMA prefill is held bit-exact by tests/test_gpu_prefill_exact.py.
 
 Config 4 (same shape, shorter decode): four segments with 512/384/256/128-token prompts
 decode in one batch until the longest attends over a full 2048-key window that no longer
@@ -105,6 +106,49 @@ def test_decode_crosses_the_first_window_bit_exact(model_dir, oracle_weights):
             assert np.array_equal(k[slots], ex.keys[layer][slots]), layer
     finally:
         rt.close()
+
+
+def test_long_context_runs_to_the_cap_bit_exact(long_runtime, oracle_weights):
+    # Config 5 end to end: the device loop generates from the 30,720-token prompt to within
+    # a few positions of the 32,768 cap (sampling controls over the generated history), the
+    # CPU decoder takes over the GPU's KV there, and the last forwards up to position 32,767
+    # match it bit for bit; one more forward is refused (Runtime.swift:328-330).
+    rt = long_runtime
+    tail = 7
+    rt.set_sampling(PENALTY, FREQUENCY, 0.0, NGRAM)
+    try:
+        t0 = time.time()
+        ids, reason = rt.generate(long_prompt(), 2048 - tail)
+        print(f"  device loop: {len(ids)} tokens in {time.time() - t0:.2f} s, reason {reason}", flush=True)
+        assert reason is None and len(ids) == 2048 - tail
+        pos = rt.position
+        assert pos == 30720 + len(ids) - 1, pos
+        ex = exact.ExactDecoder(oracle_weights, 32768, rt.stats()["local_capacity"])
+        for layer in range(16):
+            k, v = rt.kv(layer)
+            ex.keys[layer][:] = k
+            ex.values[layer][:] = v
+        generated, t, start = list(ids), ids[-1], pos
+        while pos < 32768:
+            got = rt.forward([t])
+            bits, hidden, _ = ex.step(t, pos)
+            assert np.array_equal(rt.logit_bits(), bits), pos
+            assert np.array_equal(rt.hidden().view(np.uint32), hidden.view(np.uint32)), pos
+            assert got == sampler.select(bf_np(bits).copy(), generated, PENALTY, NGRAM, FREQUENCY), pos
+            print(f"  position {pos}: bit-exact, token {got}", flush=True)
+            t, pos = got, pos + 1
+            generated.append(t)
+            rt.observe(t)
+        assert rt.position == 32768
+        with pytest.raises(plamo_hip.PlamoError, match="context exhausted"):
+            rt.forward([t])
+        for layer in range(16):
+            k, v = rt.kv(layer)
+            slots = [p % k.shape[0] for p in range(start, 32768)]
+            assert np.array_equal(k[slots], ex.keys[layer][slots]), layer
+            assert np.array_equal(v[slots], ex.values[layer][slots]), layer
+    finally:
+        rt.set_sampling()
 
 
 def test_long_context_device_loop_matches_host_loop(long_runtime):

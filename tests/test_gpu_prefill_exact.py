@@ -154,6 +154,45 @@ def test_config3_prefill_first_layers_bit_exact(model_dir, oracle_weights, golde
         assert bad_k == 0 and bad_v == 0, layer
 
 
+def test_config3_prefill_all_layers_match_twin_digests(model_dir, golden):
+    # configs[2] through all 16 layers and the head.  The full twin runs for minutes, so
+    # tests/golden/make_config3_digest.py ran it on the CPU and kept SHA-256 digests of its
+    # keys, values, logits and hidden row; the GPU prefill's bytes must hash to the same.
+    import hashlib
+    import json
+    import os
+    with open(os.path.join(os.path.dirname(__file__), "golden", "config3_prefill_digest.json")) as f:
+        want = json.load(f)
+    d, sha = model_dir
+    assert want["model_sha256"] == sha
+    g = golden["config3"]
+    prompt = np.random.default_rng(g["prompt_seed"]).integers(1024, 107520, g["length"]).tolist()
+    n = len(prompt)
+    assert n == want["prompt_tokens"]
+
+    def digest(a, dtype):
+        return hashlib.sha256(np.ascontiguousarray(a, dtype=dtype).tobytes()).hexdigest()
+
+    rt = plamo_hip.Runtime(d, want["context"], source_sha256=sha)
+    try:
+        nxt = rt.prefill(prompt)
+        bad = []
+        for layer in range(16):
+            k, v = rt.kv(layer)
+            for name, a in (("keys", k[:n]), ("values", v[:n])):
+                if digest(a, np.uint16) != want["layers"][layer][name]:
+                    bad.append(f"layer {layer} {name}")
+        if digest(rt.logit_bits(), np.uint16) != want["logits"]:
+            bad.append("logits")
+        if digest(rt.hidden().view(np.uint32), np.uint32) != want["hidden"]:
+            bad.append("hidden")
+    finally:
+        rt.close()
+    print(f"  config3 full prefill: next {nxt} (twin {want['next']}), differing: {bad or 'none'}", flush=True)
+    assert not bad, bad
+    assert nxt == want["next"]
+
+
 def test_decode_after_prefill_bit_exact(model_dir, oracle_weights, twin_prefill):
     # greedy decode on the prefilled KV: the GPU step equals the decode twin run on the
     # prefill twin's KV, step after step
