@@ -244,14 +244,14 @@ __device__ __forceinline__ void buffer_store2(__amdgpu_buffer_rsrc_t r, uint32_t
 // exact (|f| <= 1/2), the degree-6 Taylor polynomial of 2^f = e^(f ln 2) in Horner form with
 // fused multiply-adds, then an exact 2^k scale.  Arguments below -64 give 0 (a weight under
 // 2^-64 of the running maximum's moves nothing), so every result is a normal number.
-// Accuracy: about 3 ulp.  Branch-free: the argument is clamped to -64 and the result
-// selected afterwards (a per-element branch costs exec-mask writes and keeps the scheduler
-// from interleaving the polynomial with other work; same bits).
+// Accuracy: about 3 ulp.  Branch-free: the polynomial runs on every argument and the result
+// is selected afterwards (a per-element branch costs exec-mask writes and keeps the
+// scheduler from interleaving the polynomial with other work; same bits).  What -inf, NaN
+// or arguments below -64 produce on the way is discarded by the select.
 __device__ __forceinline__ float exp2_det(float x) {
 #pragma clang fp contract(off)
-    const float xc = fmaxf(x, -64.0f);
-    const float k = rintf(xc);
-    const float f = xc - k;
+    const float k = rintf(x);
+    const float f = x - k;
     float p = 1.54035304e-04f;                 // ln2^6 / 6!
     p = __builtin_fmaf(p, f, 1.33335581e-03f); // ln2^5 / 5!
     p = __builtin_fmaf(p, f, 9.61812911e-03f); // ln2^4 / 4!
@@ -267,12 +267,11 @@ __device__ __forceinline__ float exp2_det(float x) {
 // Cody-Waite reduction x = k*ln2 + r (ln2 split in a 16-bit head, so k*LN2_HI is exact for
 // |k| <= 128), degree-7 Taylor polynomial of e^r in Horner form, then an exact 2^k scale.
 // Every product and sum is rounded separately (no contraction).  Accuracy: about 2 ulp.
-// Branch-free like exp2_det: clamped argument, result selected at the end.
+// Branch-free like exp2_det: the result is selected at the end.
 __device__ __forceinline__ float exp_det(float x) {
 #pragma clang fp contract(off)
-    const float xc = fminf(fmaxf(x, -80.0f), 88.72283935546875f);
-    const float k = rintf(xc * 1.44269502162933349609375f);
-    const float r = (xc - k * 0.693145751953125f) - k * 1.428606765330187e-06f;
+    const float k = rintf(x * 1.44269502162933349609375f);
+    const float r = (x - k * 0.693145751953125f) - k * 1.428606765330187e-06f;
     float p = 1.98412698e-04f;                 // 1/7!
     p = p * r + 1.38888889e-03f;               // 1/6!
     p = p * r + 8.33333377e-03f;               // 1/5!

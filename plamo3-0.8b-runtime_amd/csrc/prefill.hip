@@ -565,15 +565,14 @@ struct KvSource {
 };
 
 // Global loads of one tile: thread -> key tid/4 with RoPE pairs (d, d+64), d = 16*(tid%4)
-// .. +16; and values of keys 4*(tid%16) .. +4 at dims 8*(tid/16) .. +8.
+// .. +16; and values of keys 4*(tid%16) .. +4 at dims 8*(tid/16) .. +8.  Keys past khi (the
+// last tile's tail) load key khi instead: their scores are masked and their weights are
+// exactly 0, so any finite row serves, every load stays on a written key, and no register
+// has to be cleared or load predicated.
 __device__ __forceinline__ void flash_load(const FlashParams& p, const KvSource& src, uint32_t k0, uint32_t khi,
                                            uint32_t base, KvStage& s) {
     const int tid = threadIdx.x;
     const int part = tid & 3;
-    const uint32_t kp = k0 + uint32_t(tid >> 2);
-    const uint4 z = make_uint4(0, 0, 0, 0);
-    s.ka[0] = s.ka[1] = s.kb[0] = s.kb[1] = z;
-    s.rr[0] = s.rr[1] = s.rr[2] = s.rr[3] = z;
     // ring slots: one modulo per tile, then at most one wrap per key when the ring holds a
     // whole tile (offsets are below 64); smaller rings wrap by repeated subtraction
     const uint32_t slot0 = k0 % p.capacity;
@@ -584,25 +583,22 @@ __device__ __forceinline__ void flash_load(const FlashParams& p, const KvSource&
         while (slot >= p.capacity) slot -= p.capacity;
         return slot;
     };
-    if (kp <= khi) {
-        // the rotated-key cache is indexed by position (kp < rot_rows), the ring by slot
-        const uint16_t* row = src.keys + size_t(src.rotate || p.full ? ring(uint32_t(tid >> 2)) : kp) * HEAD_DIM;
-        s.ka[0] = *reinterpret_cast<const uint4*>(row + part * 16);
-        s.ka[1] = *reinterpret_cast<const uint4*>(row + part * 16 + 8);
-        s.kb[0] = *reinterpret_cast<const uint4*>(row + 64 + part * 16);
-        s.kb[1] = *reinterpret_cast<const uint4*>(row + 64 + part * 16 + 8);
-        if (src.rotate) {
-            const uint4* rr = reinterpret_cast<const uint4*>(p.local_rope + size_t(kp - base) * 64 + part * 16);
+    const uint32_t kp = min(k0 + uint32_t(tid >> 2), khi);
+    // the rotated-key cache is indexed by position (kp < rot_rows), the ring by slot
+    const uint16_t* row = src.keys + size_t(src.rotate || p.full ? ring(kp - k0) : kp) * HEAD_DIM;
+    s.ka[0] = *reinterpret_cast<const uint4*>(row + part * 16);
+    s.ka[1] = *reinterpret_cast<const uint4*>(row + part * 16 + 8);
+    s.kb[0] = *reinterpret_cast<const uint4*>(row + 64 + part * 16);
+    s.kb[1] = *reinterpret_cast<const uint4*>(row + 64 + part * 16 + 8);
+    if (src.rotate) {
+        const uint4* rr = reinterpret_cast<const uint4*>(p.local_rope + size_t(kp - base) * 64 + part * 16);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) s.rr[i] = rr[i];
-        }
+        for (int i = 0; i < 4; ++i) s.rr[i] = rr[i];
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const uint32_t kv = k0 + uint32_t(4 * (tid & 15) + i);
-        s.v[i] = kv <= khi ? *reinterpret_cast<const uint4*>(p.values + size_t(ring(uint32_t(4 * (tid & 15) + i))) * HEAD_DIM +
-                                                             8 * (tid >> 4))
-                           : z;
+        const uint32_t kv = min(k0 + uint32_t(4 * (tid & 15) + i), khi);
+        s.v[i] = *reinterpret_cast<const uint4*>(p.values + size_t(ring(kv - k0)) * HEAD_DIM + 8 * (tid >> 4));
     }
 }
 
