@@ -512,9 +512,9 @@ int plamo_kernel_linear(uint64_t w, uint64_t table, uint64_t x, uint64_t y, int3
         g.out16 = reinterpret_cast<uint16_t*>(y);
         const int maxr = rows == 1 ? 1 : plamo::ROWS;
         const plamo::Epilogue epi = mode == 2 ? plamo::EPI_BF16 : mode == 1 ? plamo::EPI_RAW : plamo::EPI_ROUND;
-        if (m % plamo::gemv_group_rows(n, maxr, epi) != 0)
+        if (m % plamo::gemv_group_rows(n, maxr, epi, table != 0) != 0)
             throw plamo::Error(plamo::E_INVAL, "GEMV rows must be a multiple of the rows per wave group");
-        const int blocks = std::max(1, std::min(4096, plamo::gemv_blocks(n, maxr, epi, m)));
+        const int blocks = std::max(1, std::min(4096, plamo::gemv_blocks(n, maxr, epi, m, table != 0)));
         plamo::launch_gemv(n, table != 0, maxr, plamo::PRO_PLAIN, epi, g, blocks, reinterpret_cast<hipStream_t>(stream));
         PLAMO_HIP(hipGetLastError());
     });

@@ -51,11 +51,13 @@ struct TimelineScope {
 
 // Weight rows per wave group: four for one activation row; with four rows the
 // arithmetic per weight byte quadruples, so groups shrink to spread it over more waves
-// (SwiGLU: one gate and one up row, three groups for each of a CU's eight waves).
-template <int N, int MAXR, int EPI>
+// (SwiGLU: one gate and one up row, three groups for each of a CU's eight waves).  The
+// one-row .p12 down projection takes one row per group: 384 workgroups instead of 192
+// hide its block decode behind more waves (.p12 step 0.542 -> 0.524 ms; plain rows keep two).
+template <int N, int MAXR, int EPI, bool PACKED>
 constexpr int gemv_u() {
     if constexpr (EPI == EPI_SWIGLU) return MAXR == 1 ? 4 : 2;
-    else if constexpr (N >= 6144) return MAXR == 1 ? 2 : 1;
+    else if constexpr (N >= 6144) return MAXR == 1 ? (PACKED ? 1 : 2) : 1;
     else return MAXR == 1 ? (N == ATTN ? 2 : 4) : 2;
 }
 
@@ -537,7 +539,7 @@ __global__ __launch_bounds__(64 * gemv_waves(N, MAXR, EPI)) void gemv_kernel(con
     PLAMO_TIMELINE_SCOPE(p.tag);
     constexpr int NWV = gemv_waves(N, MAXR, EPI);
     constexpr int IT = N / 512;
-    constexpr int U = gemv_u<N, MAXR, EPI>();
+    constexpr int U = gemv_u<N, MAXR, EPI, PACKED>();
     constexpr int H = U / 2;  // SwiGLU: gate rows (and up rows) per group
     __shared__ __align__(16) uint16_t xs[MAXR * N];
     __shared__ float red[MAXR * 4 * 2];  // norm partials: post-norm half, next-norm half
@@ -1718,14 +1720,14 @@ void gemv_dispatch_n(bool packed, int maxr, Prologue pro, Epilogue epi, const Ge
 
 }  // namespace
 
-int gemv_group_rows(int n, int maxr, Epilogue epi) {
+int gemv_group_rows(int n, int maxr, Epilogue epi, bool packed) {
     if (epi == EPI_SWIGLU) return maxr == 1 ? 4 : 2;
-    if (n >= 6144) return maxr == 1 ? 2 : 1;
+    if (n >= 6144) return maxr == 1 ? (packed ? 1 : 2) : 1;
     return maxr == 1 ? (n == ATTN ? 2 : 4) : 2;
 }
 
-int gemv_blocks(int n, int maxr, Epilogue epi, int m) {
-    const int groups = m / gemv_group_rows(n, maxr, epi);
+int gemv_blocks(int n, int maxr, Epilogue epi, int m, bool packed) {
+    const int groups = m / gemv_group_rows(n, maxr, epi, packed);
     const int nw = gemv_waves(n, maxr, epi);
     const int b = (groups + nw - 1) / nw;  // one group per wave
     // Multi-row kernels: at most two workgroups per CU, each wave walking several groups

@@ -137,8 +137,8 @@ constexpr uint32_t TL_HEAD = 200, TL_HEAD_MERGE = 250, TL_STEP_BEGIN = 251;
 void timeline_copy(uint64_t* out, size_t words, bool clear);
 
 // decode.hip
-int gemv_group_rows(int n, int maxr, Epilogue epi);     // weight rows per wave group
-int gemv_blocks(int n, int maxr, Epilogue epi, int m);  // workgroups for one group per wave
+int gemv_group_rows(int n, int maxr, Epilogue epi, bool packed);     // weight rows per wave group
+int gemv_blocks(int n, int maxr, Epilogue epi, int m, bool packed);  // workgroups for one group per wave
 // LM-head workgroups (argmax partials, at most HEAD_BLOCKS): four waves each for one row;
 // for four rows one eight-wave workgroup per CU.
 inline int head_blocks(int maxr) { return maxr == 1 ? HEAD_BLOCKS : HEAD_BLOCKS / 4; }

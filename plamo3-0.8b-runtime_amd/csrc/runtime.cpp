@@ -377,13 +377,13 @@ void Engine::enqueue_step(bool head, bool loop) {
         g.out = qkv;
         if (l == 0) {
             g.embed = m.embed;
-            launch_gemv(HIDDEN, pk, maxr, PRO_EMBED, EPI_ROUND, g, gemv_blocks(HIDDEN, maxr, EPI_ROUND, QKV), stream);
+            launch_gemv(HIDDEN, pk, maxr, PRO_EMBED, EPI_ROUND, g, gemv_blocks(HIDDEN, maxr, EPI_ROUND, QKV, pk), stream);
         } else {
             g.in16 = proj;
             g.resid16_in = x1;
             g.g_post = m.layers[l - 1].post_mlp;
             g.post_offset = post_mlp_offset();
-            launch_gemv(HIDDEN, pk, maxr, PRO_RESID16, EPI_ROUND, g, gemv_blocks(HIDDEN, maxr, EPI_ROUND, QKV), stream);
+            launch_gemv(HIDDEN, pk, maxr, PRO_RESID16, EPI_ROUND, g, gemv_blocks(HIDDEN, maxr, EPI_ROUND, QKV, pk), stream);
         }
         AttnParams a{};
         a.state = state;
@@ -425,7 +425,7 @@ void Engine::enqueue_step(bool head, bool loop) {
         o.parts = a.parts;
         o.merge_full = full ? 1u : 0u;
         launch_gemv(ATTN, pk, maxr, maxr == 1 ? PRO_MERGE : PRO_PLAIN16, EPI_BF16, o,
-                    gemv_blocks(ATTN, maxr, EPI_BF16, HIDDEN), stream);
+                    gemv_blocks(ATTN, maxr, EPI_BF16, HIDDEN, pk), stream);
         GemvParams u{};
         u.state = state;
         u.rows = ROWS;
@@ -440,7 +440,7 @@ void Engine::enqueue_step(bool head, bool loop) {
         u.post_offset = POST_MIXER_OFFSET;
         u.g_next = L.pre_mlp;
         u.out16 = act;
-        launch_gemv(HIDDEN, pk, maxr, PRO_RESID16, EPI_SWIGLU, u, gemv_blocks(HIDDEN, maxr, EPI_SWIGLU, 2 * INTER), stream);
+        launch_gemv(HIDDEN, pk, maxr, PRO_RESID16, EPI_SWIGLU, u, gemv_blocks(HIDDEN, maxr, EPI_SWIGLU, 2 * INTER, pk), stream);
         GemvParams d{};
         d.state = state;
         d.rows = ROWS;
@@ -450,7 +450,7 @@ void Engine::enqueue_step(bool head, bool loop) {
         d.tag = uint32_t(l) * 8 + 5;
         d.in16 = act;
         d.out16 = proj;
-        launch_gemv(INTER, pk, maxr, PRO_PLAIN16, EPI_BF16, d, gemv_blocks(INTER, maxr, EPI_BF16, HIDDEN), stream);
+        launch_gemv(INTER, pk, maxr, PRO_PLAIN16, EPI_BF16, d, gemv_blocks(INTER, maxr, EPI_BF16, HIDDEN, pk), stream);
     }
     if (head) enqueue_head16(loop);
 }
