@@ -1332,7 +1332,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
     if (tid == 0) atomicExch(ticket, 0u);  // ready for the next launch
 }
 
-// Partition merge of global-layer rows with more than p.defer partitions (long contexts),
+// Partition merge of rows with more than p.defer partitions (long contexts),
 // one workgroup per (32 dims of a head, head, row).  The workgroup's slice of every partition
 // output is staged in LDS with all of its loads in flight together (one workgroup keeping a
 // few partitions in flight would take tens of microseconds at 500 partitions), then 32
@@ -1351,7 +1351,8 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const AttnParams p) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     if (st->stopped || q >= int(st->rows)) return;
-    const uint32_t count = st->pos[q] + 1;  // global layer: keys 0 .. pos
+    // keys 0 .. pos on global layers, the last WINDOW of them on local layers
+    const uint32_t count = p.window && st->pos[q] + 1 > p.window ? p.window : st->pos[q] + 1;
     const uint32_t nparts = (count + KP - 1) / KP;
     if (nparts <= p.defer || nparts > MAXP || nparts > p.parts) return;  // merged in the attention kernel
     const size_t row0 = size_t(q) * p.parts;
