@@ -125,9 +125,9 @@ struct AttnParams {
 };
 // Partitions a global-layer row may have before its merge moves to attn_merge_kernel.
 constexpr uint32_t ATTN_MERGE_INLINE = 64;
-// The same for local-layer rows at batch 1: past 8 partitions (positions from 512 on) the
-// 64 workgroups of attn_merge_kernel merge a row faster than the last workgroup of each head
-// group (long-context decode 1515 -> 1554 tok/s).
+// The same for local-layer rows: past 8 partitions (positions from 512 on) the 64
+// workgroups of attn_merge_kernel merge a row faster than the last workgroup of each head
+// group (long-context decode 1515 -> 1554 tok/s, batch 4 5848 -> 6041 tok/s).
 constexpr uint32_t ATTN_MERGE_INLINE_LOCAL = 8;
 
 // Step timeline (builds with -DPLAMO_TIMELINE): per-workgroup start/end stamps of the
