@@ -123,12 +123,10 @@ struct AttnParams {
     uint32_t merge_in_o;      // rows with 2..MERGE_IN_O partitions are merged by the next
                               // kernel (the o GEMV's PRO_MERGE prologue): no ticket, no merge
 };
-// Partitions a global-layer row may have before its merge moves to attn_merge_kernel.
-constexpr uint32_t ATTN_MERGE_INLINE = 64;
-// The same for local-layer rows: past 8 partitions (positions from 512 on) the 64
-// workgroups of attn_merge_kernel merge a row faster than the last workgroup of each head
-// group (long-context decode 1515 -> 1554 tok/s, batch 4 5848 -> 6041 tok/s).
-constexpr uint32_t ATTN_MERGE_INLINE_LOCAL = 8;
+// Partitions a row may have before its merge moves to attn_merge_kernel: past 8 partitions
+// (positions from 512 on) its 64 workgroups per row merge faster than the last workgroup of
+// each head group (long-context decode 1515 -> 1554 tok/s, batch 4 5848 -> 6077 tok/s).
+constexpr uint32_t ATTN_MERGE_INLINE = 8;
 
 // Step timeline (builds with -DPLAMO_TIMELINE): per-workgroup start/end stamps of the
 // decode-step kernels in a [TIMELINE_TAGS][TIMELINE_BLOCKS][2] table of s_memrealtime
