@@ -127,6 +127,10 @@ struct AttnParams {
 // (positions from 512 on) its 64 workgroups per row merge faster than the last workgroup of
 // each head group (long-context decode 1515 -> 1554 tok/s, batch 4 5848 -> 6077 tok/s).
 constexpr uint32_t ATTN_MERGE_INLINE = 8;
+// Four-row batches whose graph launches attn_merge_kernel anyway (contexts past 8
+// partitions) send it every row past 2 partitions as well (batch 4 6074 -> 6126 tok/s; past
+// 1 partition: the same).
+constexpr uint32_t ATTN_MERGE_INLINE_BATCH = 2;
 
 // Step timeline (builds with -DPLAMO_TIMELINE): per-workgroup start/end stamps of the
 // decode-step kernels in a [TIMELINE_TAGS][TIMELINE_BLOCKS][2] table of s_memrealtime

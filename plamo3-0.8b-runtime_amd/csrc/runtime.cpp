@@ -406,8 +406,9 @@ void Engine::enqueue_step(bool head, bool loop) {
         a.tag = uint32_t(l) * 8 + 1;
         // batch 1: rows of 2..MERGE_IN_O partitions are merged by the o projection's prologue
         a.merge_in_o = maxr == 1 ? 1u : 0u;
-        // rows past ATTN_MERGE_INLINE partitions merge in their own kernel
-        a.defer = a.parts > ATTN_MERGE_INLINE ? ATTN_MERGE_INLINE : 0u;
+        // rows past ATTN_MERGE_INLINE partitions merge in their own kernel (past
+        // ATTN_MERGE_INLINE_BATCH in four-row batches, once that kernel is launched)
+        a.defer = a.parts > ATTN_MERGE_INLINE ? (maxr > 1 ? ATTN_MERGE_INLINE_BATCH : ATTN_MERGE_INLINE) : 0u;
         a.window = full ? 0u : uint32_t(WINDOW);
         launch_attention(full, a, ROWS, stream);
         if (a.defer) launch_attention_merge(a, ROWS, stream);
