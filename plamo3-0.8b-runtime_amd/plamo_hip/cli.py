@@ -282,6 +282,11 @@ def split_segments(text, target, limit, tokenizer):
     return parts
 
 
+def _text(chunk):
+    """A token stream hands out whole UTF-8 characters as bytes."""
+    return chunk.decode("utf-8", "replace") if isinstance(chunk, bytes) else chunk
+
+
 def _device_name():
     hip = ctypes.CDLL("libamdhip64.so")
     name = ctypes.create_string_buffer(256)
@@ -402,7 +407,7 @@ def execute(arguments, stdin, stdout, stderr):
                 generated.append(nxt)
                 runtime.observe(nxt)
                 if stream is not None:
-                    s = stream.push(nxt)
+                    s = _text(stream.push(nxt))
                     if s:
                         stdout.write(s)
                         stdout.flush()
@@ -420,7 +425,7 @@ def execute(arguments, stdin, stdout, stderr):
                 "gpu_seconds": runtime.gpu_seconds,
                 "stop_reason": "prefill" if o.max_tokens == 0 else (stop or "length"), "output_ids": generated}))
             if stream is not None:
-                stdout.write(stream.finish())
+                stdout.write(_text(stream.finish()))
                 stream.close()
             else:
                 translated += tokenizer.decode(generated)
