@@ -15,6 +15,7 @@ each, stop on EOS) against batch-1 on the same segment; configs[4] .p12 long con
     python bench.py --kernels-only     # GEMV shapes + copy calibration (for rocprofv3 --pmc)
     python bench.py --prefill-only     # three 2048-token prefills (for rocprofv3 kernel traces)
     python bench.py --batch4-only      # the configs[3] batch4 measurement alone
+    python bench.py --tokenizer-only   # host C++ tokenizer throughput (no GPU work)
     python bench.py --timeline [--packed]  # in-step kernel durations of replayed decode steps
                                            # (needs lib/libplamo_hip_timeline.so: make timeline)
 """
@@ -314,6 +315,8 @@ def main():
     ap.add_argument("--kernels-only", action="store_true", help="GEMV shapes and a copy calibration only")
     ap.add_argument("--prefill-only", action="store_true", help="three 2048-token prefills only")
     ap.add_argument("--batch4-only", action="store_true", help="the configs[3] batch4 measurement only")
+    ap.add_argument("--tokenizer-only", action="store_true",
+                    help="host tokenizer throughput (no GPU work; not part of the GPU line)")
     ap.add_argument("--timeline", action="store_true",
                     help="in-step kernel durations from the timeline library (make timeline)")
     ap.add_argument("--packed", action="store_true", help="with --timeline: .p12 weights")
@@ -343,6 +346,9 @@ def main():
     model_dir, sha = synth.ensure_model(packed=True)
     if args.batch4_only:
         print(json.dumps({"batch4": bench_batch4(plamo_hip, np, model_dir)}), flush=True)
+        return
+    if args.tokenizer_only:
+        print(json.dumps({"tokenizer": bench_tokenizer(plamo_hip, synth)}), flush=True)
         return
     if args.prefill_only:
         rt = plamo_hip.Runtime(model_dir, 2048 + 64)
@@ -386,8 +392,6 @@ def main():
         log(f"batch4: {results['batch4']}")
         results["long_context"] = bench_long(plamo_hip, np, model_dir, sha)
         log(f"long_context: {results['long_context']}")
-        results["tokenizer"] = bench_tokenizer(plamo_hip, synth)
-        log(f"tokenizer: {results['tokenizer']}")
         # --- prefill of 2048 tokens
         rt = plamo_hip.Runtime(model_dir, 2048 + 64)
         p2 = np.random.default_rng(3).integers(1024, 107520, 2048).tolist()

@@ -133,12 +133,13 @@ class ExactPrefill:
 
     def prefill(self, tokens, p0=0, kv_layers=None):
         """Runtime.prefill from position p0 -> (logit_bits, hidden, next) of the last token.
-        kv_layers = L < 16 (one chunk only): stop once layer L - 1 has written its keys and
-        values (layers 0 .. L - 2 in full), return None."""
+        kv_layers = L < 16: every chunk stops once layer L - 1 has written its keys and
+        values (layers 0 .. L - 2 in full), and the call returns None.  Layer i's keys and
+        values depend only on layers 0 .. i of this and earlier chunks, so the cached rows of
+        layers 0 .. L - 1 are those of the full prefill."""
         out = None
         for c0 in range(0, len(tokens), self.chunk):
             part = tokens[c0:c0 + self.chunk]
-            assert kv_layers is None or len(part) == len(tokens), "kv_layers: a single chunk"
             out = self._chunk(part, p0 + c0, c0 + len(part) == len(tokens), kv_layers)
         return out
 

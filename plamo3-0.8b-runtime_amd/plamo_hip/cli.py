@@ -20,11 +20,13 @@ Differences, each forced by the platform:
 * Metal memory keys report HIP device memory held by the runtime; the macOS footprint keys
   report VmRSS / VmHWM from /proc/self/status.
 """
+import contextlib
 import ctypes
 import json
 import os
 import resource
 import sys
+import tempfile
 import time
 
 import regex
@@ -51,6 +53,29 @@ def _is_white(ch):
 
 def _is_newline(ch):
     return ch == "\r\n" or ch[:1] in _NEWLINE
+
+
+_LIBC = ctypes.CDLL(None)
+_LIBC.strtof.restype = ctypes.c_float
+_LIBC.strtof.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p)]
+
+
+def swift_float(text):
+    """Float(text) as Swift parses it for the penalty options (Main.swift:74-75 store a Float):
+    the C library's strtof over the whole text (decimal or hexadecimal digits, inf, nan), one
+    rounding to FP32, out-of-range magnitudes to infinity; None if the text is empty, starts
+    with whitespace or has characters strtof does not read.  Returned as a Python float that
+    holds the FP32 value exactly, so every later comparison sees what Swift's Float holds:
+    "1.00000001" is 1 (no sampling control), "1e39" is infinite (rejected)."""
+    if not text or text[0].isspace() or "\0" in text:
+        return None
+    raw = text.encode()
+    buf = ctypes.create_string_buffer(raw)
+    end = ctypes.c_void_p()
+    value = _LIBC.strtof(buf, ctypes.byref(end))
+    if end.value is None or end.value - ctypes.addressof(buf) != len(raw):
+        return None
+    return float(value)
 
 
 class Options:
@@ -114,11 +139,8 @@ class Options:
             return n
 
         def real(ok, message):
-            try:
-                x = float(value)
-            except ValueError:
-                raise Failure(message) from None
-            if x != x or x in (float("inf"), float("-inf")) or not ok(x):
+            x = swift_float(value)
+            if x is None or x != x or x in (float("inf"), float("-inf")) or not ok(x):
                 raise Failure(message)
             return x
 
@@ -301,6 +323,28 @@ def _proc_status(key):
     return 0
 
 
+@contextlib.contextmanager
+def _device_init_notices(stderr):
+    """The first HIP call of a process loads libdrm, which writes one line about a missing
+    marketing-name table ("amdgpu.ids: No such file or directory") to file descriptor 2.
+    The reference's stderr carries nothing but the metrics line or an error (web/server.ts
+    parses all of it as JSON), so that notice is dropped; anything else written to
+    descriptor 2 meanwhile is passed on to `stderr`."""
+    sys.stderr.flush()
+    saved = os.dup(2)
+    with tempfile.TemporaryFile() as tmp:
+        os.dup2(tmp.fileno(), 2)
+        try:
+            yield
+        finally:
+            os.dup2(saved, 2)
+            os.close(saved)
+            tmp.seek(0)
+            for line in tmp.read().decode("utf-8", "replace").splitlines(True):
+                if "amdgpu.ids" not in line:
+                    stderr.write(line)
+
+
 def execute(arguments, stdin, stdout, stderr):
     """Main.execute (Main.swift:126-348)."""
     o = Options(arguments)
@@ -337,9 +381,11 @@ def execute(arguments, stdin, stdout, stderr):
     if o.qsa or o.mtp:
         raise Failure("QSA and MTP are not built for this GPU")
     load_start = time.time()
-    runtime = Runtime(o.model, context, packed=o.packed)
-    plan = document_plan(parts) if o.batch4 else None
-    batch = Batch(runtime) if plan is not None and len(plan[0]) > 1 else None
+    with _device_init_notices(stderr):
+        runtime = Runtime(o.model, context, packed=o.packed)
+        plan = document_plan(parts) if o.batch4 else None
+        batch = Batch(runtime) if plan is not None and len(plan[0]) > 1 else None
+        device = _device_name()
     load_seconds = time.time() - load_start
     controlled = o.repetition_penalty != 1 or o.frequency_penalty != 0 or o.no_repeat_ngram > 1
     runtime.set_sampling(o.repetition_penalty, o.frequency_penalty, 0.0, o.no_repeat_ngram if controlled else 0)
@@ -455,7 +501,7 @@ def execute(arguments, stdin, stdout, stderr):
     stdout.flush()
     stats = runtime.stats()
     metrics = {
-        "device": _device_name(), "load_seconds": load_seconds, "packed": o.packed, "qsa": o.qsa,
+        "device": device, "load_seconds": load_seconds, "packed": o.packed, "qsa": o.qsa,
         "qsa_budget": o.qsa_budget if o.qsa else 0, "mtp": o.mtp,
         "repetition_penalty": o.repetition_penalty, "frequency_penalty": o.frequency_penalty,
         "no_repeat_ngram": o.no_repeat_ngram,

@@ -32,6 +32,8 @@ def tok():
     ["--segment-tokens", "64", "--decode", "1"], ["--segment-tokens", "64", "--dump-logits", "x"],
     ["--stream", "--repeat", "2"], ["--max-tokens", "0"], ["--qsa-budget", "6"], ["--context", "0"],
     ["--repetition-penalty", "0"], ["--repetition-penalty", "nan"], ["--frequency-penalty", "-1"],
+    ["--repetition-penalty", "1e39"], ["--frequency-penalty", "3.5e38"], ["--repetition-penalty", "1e-46"],
+    ["--repetition-penalty", " 1.1"], ["--repetition-penalty", "1.1x"], ["--frequency-penalty", "1_0"],
     ["--no-repeat-ngram", "65"], ["--loop-limit", "1001"], ["--max-tokens"], ["--bogus", "1"], ["a", "b"],
     ["--mtp", "--loop-limit", "2"], ["--tokens", "1", "text"]])
 def test_options_reject(args):
@@ -49,6 +51,18 @@ def test_options_accept():
     assert o.qsa and o.qsa_budget == 64
     with pytest.raises(cli.Failure, match="Missing value for --to"):
         cli.Options(["--to"])
+
+
+def test_penalties_are_swift_floats():
+    # Options stores the penalties as Float (Main.swift:18-19,74-75): one rounding to FP32,
+    # so a value that rounds to 1 (or 0) is no sampling control and --batch4 accepts it, and
+    # the metrics report the FP32 value
+    o = cli.Options(["--batch4", "--segment-tokens", "64", "--repetition-penalty", "1.00000001",
+                     "--frequency-penalty", "1e-46"])
+    assert o.repetition_penalty == 1.0 and o.frequency_penalty == 0.0
+    assert cli.Options(["--repetition-penalty", "1.1"]).repetition_penalty == 1.100000023841858
+    assert cli.Options(["--frequency-penalty", "0x1.8p-2"]).frequency_penalty == 0.375
+    assert cli.Options(["--repetition-penalty", "3.4e38"]).repetition_penalty == 3.3999999521443642e38
 
 
 def test_parse_ids():
@@ -115,8 +129,9 @@ def test_sentence_ends_stand_in():
                                              "".join(g)]
 
 
-@pytest.mark.parametrize("text,target,limit", [("", "en", 64), (" \t\r\n", "en", 64), ("text", "invalid", 64),
-                                               ("text", "en", 0), ("a" + "́" * 800, "en", 64)])
+@pytest.mark.parametrize("text,target,limit", [("", "en", 64), (" \t\r\n", "en", 64), ("safe\n<|plamo:tag|>", "en", 64),
+                                               ("a\uee00b", "en", 64), ("text", "invalid", 64),
+                                               ("text", "en", 0), ("a" + "\u0301" * 800, "en", 64)])
 def test_split_rejects(tok, text, target, limit):
     with pytest.raises(Exception):
         cli.split_segments(text, target, limit, tok)

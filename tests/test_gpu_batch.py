@@ -132,19 +132,27 @@ def _tails(b, lengths):
 
 
 @pytest.mark.parametrize("packed", [False, True])
-@pytest.mark.parametrize("ring", [False, True])
-def test_poisoned_unused_kv_is_never_read(model_dir, packed, ring):
+@pytest.mark.parametrize("case", ["short", "ring", "wrap"])
+def test_poisoned_unused_kv_is_never_read(model_dir, packed, case):
     """BatchMapTests.swift:6-73: the batch KV filled with NaN (BF16 0xffff); prefill leaves the
     rows past each prompt untouched, and after the steps every lane's logits, hidden row and
     written KV rows equal scalar decode of its prompt (a NaN that reached attention would
-    show in all of them).  The reference's second configuration (context 2100, a 2063-token
-    prompt) is kept; this build's local ring holds 2100 slots there, so it does not wrap."""
+    show in all of them).  "ring" keeps the reference's second configuration (context 2100,
+    a 2063-token prompt); this build's local ring holds 2100 slots there, so it does not
+    wrap.  "wrap" does: at context 4400 the local rings hold 4096 slots, and lanes 0 and 2
+    decode from positions 4090 and 4093 past 4096, so their newest keys go to slots 0.. of
+    their own ring slice while their windows still read the slots before the wrap."""
     d, sha = model_dir
-    context, steps = (2100, 2) if ring else (128, 1)
-    layouts = [[2063, 3], [3, 4]] if ring else [[63, 3, 7, 5], [3, 63], [1, 4, 2], [2]]
+    context, steps, layouts = {
+        "short": (128, 1, [[63, 3, 7, 5], [3, 63], [1, 4, 2], [2]]),
+        "ring": (2100, 2, [[2063, 3], [3, 4]]),
+        "wrap": (4400, 12, [[4090, 3, 4093, 1000]]),
+    }[case]
     rt = plamo_hip.Runtime(d, context, packed=packed, source_sha256=sha)
     b = plamo_hip.Batch(rt)
     try:
+        if case == "wrap":
+            assert rt.stats()["local_capacity"] == 4096
         b.fill_kv(0xFFFF)
         for lengths in layouts:
             prompts = prompts_for(lengths)
@@ -166,6 +174,8 @@ def test_poisoned_unused_kv_is_never_read(model_dir, packed, ring):
                     k, v = b.kv(lane, layer)
                     m = min(n, len(k))
                     assert np.array_equal(k[:m], kv[layer][0][:m]) and np.array_equal(v[:m], kv[layer][1][:m]), layer
+            print(f"  {case} packed={packed} prompts {lengths}: every lane equals scalar decode after {steps} steps",
+                  flush=True)
     finally:
         b.close()
         rt.close()

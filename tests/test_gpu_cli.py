@@ -2,12 +2,16 @@
 
 Checks the stderr metrics schema (Main.swift:331-347 top-level keys, 265-273 run keys), that
 the command's tokens equal the runtime's own greedy loop, --stream text equal to the plain
-text, --dump-logits, and the segment pipeline's stop rule (SegmentTests.swift:97-107: a
-truncated segment stops the pipeline; the synthetic model's random weights rarely stop, so
-only the first segment is translated)."""
+text, --dump-logits, the segment pipeline's stop rule (SegmentTests.swift:97-107: a
+truncated segment stops the pipeline, and segments that stop on an end id let the next one
+run, adjacent ones joined by a newline), and the command run as a fresh process: the
+translation alone on stdout and exactly one JSON line on stderr (web/server.ts:22-58 reads
+stdout as the translation and parses all of stderr)."""
 import io
 import json
 import os
+import subprocess
+import sys
 
 import numpy as np
 import pytest
@@ -80,11 +84,63 @@ def test_segment_pipeline_and_batch4(model):
     chunked, m = run(model, ["--stream", "--to", "en", "--max-tokens", "4", "--segment-tokens", "64"], UNBROKEN)
     r = m["runs"][0]
     assert r["segments_total"] == len(parts)
-    if m1["runs"][0]["stop_reason"] == "length":
-        assert chunked == first and r["stop_reason"] == "length" and r["segments_completed"] == 0
-        assert r["output_ids"] == m1["runs"][0]["output_ids"]
+    # the first segment runs to its limit (the synthetic model does not stop on these prompts),
+    # so the pipeline ends after it
+    assert m1["runs"][0]["stop_reason"] == "length"
+    assert chunked == first and r["stop_reason"] == "length" and r["segments_completed"] == 0
+    assert r["output_ids"] == m1["runs"][0]["output_ids"]
     _, b = run(model, ["--to", "en", "--max-tokens", "4", "--segment-tokens", "64", "--batch4"], UNBROKEN)
     rb = b["runs"][0]
     assert {"prefilled_input_tokens", "discarded_output_tokens", "segments", "segments_total"} <= set(rb)
     assert rb["segments"][0]["output_ids"] == m1["runs"][0]["output_ids"]
     tok.close()
+
+
+def test_segments_that_stop_let_the_next_run(model, monkeypatch):
+    # A segment whose prompt predicts an end id stops with no tokens ("stop"), and the
+    # pipeline goes on (Main.swift's segment loop): adjacent text segments are joined by a
+    # newline, literal pieces are copied, and the last segment runs to its limit.  The
+    # synthetic model stops at once only on the one-token prompt of tests/golden/eos_prompts.json,
+    # so the segmenter's output is replaced by segments made of it.
+    with open(os.path.join(os.path.dirname(__file__), "golden", "eos_prompts.json")) as f:
+        eos = json.load(f)["eos_prompts"][0][0]
+    tok = plamo_hip.Tokenizer(os.path.join(model, "tokenizer.jsonl"))
+    last = tok.encode(plamo_hip.Tokenizer.prompt("abc 日本語.", "en"), bos=True)
+    tok.close()
+    parts = [plamo_hip.Segment("x", [eos]), plamo_hip.Segment("y", [eos]), plamo_hip.Segment(" \t", []),
+             plamo_hip.Segment("z", last)]
+    monkeypatch.setattr(cli, "split_segments", lambda *a: parts)
+    _, one = run(model, ["--to", "en", "--max-tokens", "4"], "abc 日本語.")
+    assert one["runs"][0]["stop_reason"] == "length"
+    out, m = run(model, ["--to", "en", "--max-tokens", "4", "--segment-tokens", "64"], "x y z")
+    r = m["runs"][0]
+    assert [s["stop_reason"] for s in r["segments"]] == ["stop", "stop", "length"]
+    assert r["segments_completed"] == 2 and r["segments_total"] == 3 and r["stop_reason"] == "length"
+    assert r["output_ids"] == one["runs"][0]["output_ids"]
+    tok = plamo_hip.Tokenizer(os.path.join(model, "tokenizer.jsonl"))
+    assert out == "\n" + " \t" + tok.decode(r["output_ids"]) + "\n"
+    tok.close()
+    out_b, b = run(model, ["--to", "en", "--max-tokens", "4", "--segment-tokens", "64", "--batch4"], "x y z")
+    rb = b["runs"][0]
+    assert [s["stop_reason"] for s in rb["segments"]] == ["stop", "stop", "length"]
+    assert rb["segments_completed"] == 2 and rb["output_ids"] == r["output_ids"] and out_b == out
+
+
+def test_command_in_a_fresh_process(model):
+    # what web/server.ts spawns: a new process, whose first HIP call happens in it
+    env = dict(os.environ, PYTHONPATH=os.pathsep.join(
+        [os.path.join(os.path.dirname(os.path.dirname(__file__)), "plamo3-0.8b-runtime_amd"),
+         os.environ.get("PYTHONPATH", "")]))
+    p = subprocess.run([sys.executable, "-m", "plamo_hip.cli", "--model", model, "--max-tokens", "8", TEXT],
+                       capture_output=True, env=env, timeout=110)
+    assert p.returncode == 0, p.stderr.decode(errors="replace")
+    lines = p.stderr.decode().splitlines()
+    assert len(lines) == 1, lines
+    m = json.loads(lines[0])
+    want, wm = run(model, ["--max-tokens", "8"], TEXT)
+    assert m["runs"][0]["output_ids"] == wm["runs"][0]["output_ids"]
+    assert p.stdout.decode() == want
+    bad = subprocess.run([sys.executable, "-m", "plamo_hip.cli", "--model", model, "--repetition-penalty", "0", TEXT],
+                         capture_output=True, env=env, timeout=110)
+    assert bad.returncode == 1 and bad.stdout == b""
+    assert bad.stderr.decode() == "error: Repetition penalty must be a positive finite number\n"

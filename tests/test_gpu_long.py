@@ -10,11 +10,14 @@ partitions and the split-K merge at that size.  The device loop then runs the wh
 (2,048 generated tokens) to the 32,768 cap, and its last eight positions are checked the same
 way.  The MFMA prefill is held bit-exact by tests/test_gpu_prefill_exact.py.
 
-Config 4 (same shape, shorter decode): four segments with 512/384/256/128-token prompts
-decode in one batch until the longest attends over a full 2048-key window that no longer
-starts at position 0, bit-identical to scalar decode of each segment (Batch.swift:109-180
-keeps lanes independent).  (The ring wrap itself is exercised by the config-5 test: this
-build's local ring holds 2048 + one 2048-token prefill chunk.)
+Config 4 itself: four segments with 512/384/256/128-token prompts, each greedy-decoding up
+to 2048 tokens (stop ids 1 and 16) at context 2,560 in the batch device loop; every lane's
+ids equal scalar generation of its prompt and, at the end, its logits, hidden row and every
+layer's KV equal the scalar runtime's bit for bit (Batch.swift:109-180 keeps lanes
+independent).  A shorter variant steps the batch by hand until the longest lane attends over
+a 2048-key window that no longer starts at position 0.  (Lane rings wrap in
+tests/test_gpu_batch.py's "wrap" case: this build's local ring holds 2048 + one 2048-token
+prefill chunk, more than configs[3]'s context.)
 """
 import time
 
@@ -199,6 +202,42 @@ def test_batch_segments_cross_the_window(model_dir):
                 ks, vs = rt.kv(layer)
                 assert np.array_equal(kb[:n], ks[:n]) and np.array_equal(vb[:n], vs[:n]), (lane, layer)
             print(f"  lane {lane} (prompt {len(p)}): batch == scalar", flush=True)
+    finally:
+        b.close()
+        rt.close()
+
+
+def test_config4_batch_runs_to_its_horizon(model_dir):
+    d, _ = model_dir
+    lengths, limit, context = (512, 384, 256, 128), 2048, 2560
+    # the bench's configs[3] prompts
+    prompts = [np.random.default_rng(20 + i).integers(1024, 107520, n).tolist() for i, n in enumerate(lengths)]
+    rt = plamo_hip.Runtime(d, context)
+    b = plamo_hip.Batch(rt)
+    try:
+        t0 = time.time()
+        outs = b.generate(prompts, [limit] * 4)
+        print(f"  batch device loop: {[len(ids) for ids, _ in outs]} tokens, reasons "
+              f"{[r for _, r in outs]} in {time.time() - t0:.2f} s", flush=True)
+        lanes = [(b.logit_bits(lane).copy(), b.hidden(lane).copy(), [b.kv(lane, layer) for layer in range(16)])
+                 for lane in range(4)]
+        positions = b.positions()
+        for lane, p in enumerate(prompts):
+            rt.reset()
+            ids, reason = rt.generate(p, limit)
+            assert ids == outs[lane][0], lane
+            assert outs[lane][1] == ("stop" if reason == "stop" else "length"), lane
+            assert positions[lane] == rt.position, lane
+            logits, hidden, kv = lanes[lane]
+            assert np.array_equal(logits, rt.logit_bits()), lane
+            assert np.array_equal(hidden.view(np.uint32), rt.hidden().view(np.uint32)), lane
+            n = rt.position
+            for layer in range(16):
+                ks, vs = rt.kv(layer)
+                kb, vb = kv[layer]
+                assert np.array_equal(kb[:n], ks[:n]) and np.array_equal(vb[:n], vs[:n]), (lane, layer)
+            print(f"  lane {lane} (prompt {len(p)}): {len(ids)} tokens ({outs[lane][1]}), position {n}: "
+                  "batch == scalar", flush=True)
     finally:
         b.close()
         rt.close()

@@ -159,3 +159,37 @@ def test_prefill_twin_tracks_decode_twin(oracle_weights, golden):
     assert np.sqrt(np.mean((a - b) ** 2)) < 0.03 and np.abs(a - b).max() < 0.15
     assert np.mean(ex.keys[0][:8] == ex2.keys[0][:8]) > 0.99
     assert np.array_equal(ex.values[0][:8] != 0, ex2.values[0][:8] != 0)
+
+
+def test_chunked_prefill_twin_equals_one_call(oracle_weights, golden):
+    # Runtime.prefill runs a prompt chunk by chunk (Runtime.swift:469-483).  Every prefill
+    # operation acts on one token's row or on the keys that token sees, and the flash query
+    # blocks of 8 tokens start at the same positions when chunks are multiples of 8, so the
+    # twin over two 8-token chunks equals the twin over the whole prompt in every logit,
+    # hidden and cached bit (a chunk placed at the wrong position, or keys of an earlier
+    # chunk not seen, would not).  Both agree with the semantic oracle, which runs the
+    # reference's 16-token chunks in torch order, within the measured summation-order noise
+    # floor.
+    from oracle import model as om
+    prompt = golden["config1"]["prompt"][:16]
+    runs = []
+    for chunk in (2048, 8):
+        ex = exact.ExactDecoder(oracle_weights, 32, 32)
+        runs.append((xp.ExactPrefill(ex, chunk=chunk).prefill(prompt), ex))
+    ((bits, hidden, nxt), ex0), ((b, h, t), ex) = runs
+    assert np.array_equal(b, bits) and np.array_equal(h.view(np.uint32), hidden.view(np.uint32)) and t == nxt
+    for layer in range(16):
+        assert np.array_equal(ex.keys[layer], ex0.keys[layer]), layer
+        assert np.array_equal(ex.values[layer], ex0.values[layer]), layer
+    o = om.Oracle(oracle_weights, 32, dots="exact")
+    o.prefill(prompt)
+    ref = o.logits_fp32.numpy().astype(np.float64)
+    err = np.abs(bf_np(bits).astype(np.float64) - ref)
+    floor = golden["noise_floor"]["config1"]
+    assert err.max() <= 1.5 * floor[0] and np.sqrt(np.mean(err ** 2)) <= 1.5 * floor[1], float(err.max())
+    # a twin whose second chunk starts one position early caches different layer-1 keys
+    ex = exact.ExactDecoder(oracle_weights, 32, 32)
+    tw = xp.ExactPrefill(ex, chunk=8)
+    tw.prefill(prompt[:8], kv_layers=2)
+    tw.prefill(prompt[8:], p0=7, kv_layers=2)
+    assert not np.array_equal(ex.keys[1][:16], ex0.keys[1][:16])
