@@ -21,7 +21,8 @@ correctly rounded IEEE FP32 operation, exactly as on the device, except the GEMV
   32-dim chains of q*k (v_dot2_f32_bf16 steps over the dim pairs in order) summed as
   (c0 + c1) + (c2 + c3); softmax statistics per partition with `exp_det`; P.V as two
   chains of fused multiply-adds over keys 0..31 and 32..63 per dim, added at the end;
-  merge over partitions in order.
+  merge over partitions in order, in blocks of 128 partitions past 128 (each block summed in
+  partition order, the block sums added in block order).
 * `exp_det`: Cody-Waite reduction with a 16-bit ln2 head, degree-7 Taylor polynomial, exact
   2^k scale -- the same operation sequence as the device helper.
 
@@ -38,6 +39,7 @@ SCALE = F(0.08838834764831845)
 EPS = F(1e-6)
 WINDOW = 2048
 KP = 64
+MERGE_BLOCK = 128  # partitions per block of the partition merge (attn_merge_kernel)
 
 
 def exp_det(x):
@@ -249,13 +251,21 @@ class ExactDecoder:
             e[:, :nk] = exp_det(sc - m[:, None])
             pm[p], pl[p] = m, butterfly(e)
             po[p] = attn_pv(e, vbits[k0:k0 + KP])
+        # merge: M = max m_p; w_p = exp(m_p - M); num = sum o_p w_p, den = sum l_p w_p as
+        # sums of blocks of MERGE_BLOCK partitions (each in partition order, from 0), added in
+        # block order (one block: the plain partition-order sum)
         M = pm.max(0)
         num = np.zeros((16, 128), F)
         den = np.zeros(16, F)
-        for p in range(parts):
-            wgt = exp_det(pm[p] - M)
-            den = (den + pl[p] * wgt).astype(F)
-            num = (num + po[p] * wgt[:, None]).astype(F)
+        for b0 in range(0, parts, MERGE_BLOCK):
+            bnum = np.zeros((16, 128), F)
+            bden = np.zeros(16, F)
+            for p in range(b0, min(b0 + MERGE_BLOCK, parts)):
+                wgt = exp_det(pm[p] - M)
+                bden = (bden + pl[p] * wgt).astype(F)
+                bnum = (bnum + po[p] * wgt[:, None]).astype(F)
+            den = (den + bden).astype(F)
+            num = (num + bnum).astype(F)
         return roundbf_np((num / den[:, None]).astype(F)).reshape(2048)
 
     def step(self, token, pos, x_prev=None, d_prev=None):

@@ -1333,7 +1333,8 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
 }
 
 // Partition merge of rows with more than p.defer partitions (long contexts),
-// one workgroup per (32 dims of a head, head, row).  The workgroup's slice of every partition
+// one workgroup per (32 dims of a head, head, row).  Past MERGE_BLOCK partitions the sums
+// run as blocks of MERGE_BLOCK partitions in parallel, added in block order.  The workgroup's slice of every partition
 // output is staged in LDS with all of its loads in flight together (one workgroup keeping a
 // few partitions in flight would take tens of microseconds at 500 partitions), then 32
 // threads sum in partition order.  Same arithmetic in the same order as the attention
@@ -1346,6 +1347,10 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const AttnParams p) {
     __shared__ __align__(16) float os[MAXP * 32];
     __shared__ float ws[MAXP], lsh[MAXP];
     __shared__ float red[4];
+    // block sums of the merge: MERGE_BLOCK partitions per block, one block per wave
+    constexpr uint32_t MB = uint32_t(MERGE_BLOCK), NB = MAXP / MB;
+    static_assert(MAXP % MB == 0 && NB <= 4, "one wave per block");
+    __shared__ float bnum[NB * 32], bden[NB * 32];
     const StepState* st = p.state;
     const int q = blockIdx.z, h = blockIdx.y, d0 = blockIdx.x * 32;
     const int tid = threadIdx.x, lane = tid & 63;
@@ -1405,12 +1410,35 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const AttnParams p) {
         if (k < nparts) *reinterpret_cast<uint4*>(&os[k * 32 + sub4]) = ov[j];
     }
     __syncthreads();
+    // num = sum_k o_k w_k, den = sum_k l_k w_k: lanes 0..31 of wave b sum partitions
+    // b*MB .. b*MB + MB - 1 in order (a chain of at most MB dependent sums instead of one of
+    // nparts; the partition index stays wave-uniform), then 32 threads add the block sums in
+    // block order.  With one block this is the partition-order sum of the attention kernel's
+    // own merge.
+    const uint32_t nblk = (nparts + MB - 1) / MB;
+    if (uint32_t(wave) < nblk && lane < 32) {
+        float bn = 0.f, bd = 0.f;
+        const uint32_t k0 = uint32_t(wave) * MB, k1 = min(k0 + MB, nparts);
+#pragma unroll 8  // eight partitions' LDS reads per round trip
+        for (uint32_t k = k0; k < k1; ++k) {
+            const float w = ws[k];
+            bn = bn + os[k * 32 + lane] * w;
+            bd = bd + lsh[k] * w;
+        }
+        if (nblk == 1) {  // one block: 0 + bn is bn, so the block sum is the result
+            p.out16[size_t(q) * ATTN + h * HEAD_DIM + d0 + lane] = uint16_t(bits(bn / bd));
+            return;
+        }
+        bnum[wave * 32 + lane] = bn;
+        bden[wave * 32 + lane] = bd;
+    }
+    if (nblk == 1) return;
+    __syncthreads();
     if (tid < 32) {
         float num = 0.f, den = 0.f;
-        for (uint32_t k = 0; k < nparts; ++k) {
-            const float w = ws[k];
-            num = num + os[k * 32 + tid] * w;
-            den = den + lsh[k] * w;
+        for (uint32_t b = 0; b < nblk; ++b) {
+            num = num + bnum[b * 32 + tid];
+            den = den + bden[b * 32 + tid];
         }
         p.out16[size_t(q) * ATTN + h * HEAD_DIM + d0 + tid] = uint16_t(bits(num / den));
     }

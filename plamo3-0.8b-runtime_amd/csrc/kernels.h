@@ -127,6 +127,11 @@ struct AttnParams {
 // (positions from 512 on) its 64 workgroups per row merge faster than the last workgroup of
 // each head group (long-context decode 1515 -> 1554 tok/s, batch 4 5848 -> 6077 tok/s).
 constexpr uint32_t ATTN_MERGE_INLINE = 8;
+// attn_merge_kernel sums partitions in blocks of this many, one wave per block (block sums
+// in partition order, then added in block order): 480 partitions at 30,720 keys run as
+// four chains of 128 and one of 4 instead of one chain of 480 (8.5 us of the kernel's 13.6
+// us at that size); rows of up to 128 partitions (8,192 keys) keep the single chain
+constexpr uint32_t MERGE_BLOCK = 128;
 // Four-row batches whose graph launches attn_merge_kernel anyway (contexts past 8
 // partitions) send it every row past 2 partitions as well (batch 4 6074 -> 6126 tok/s; past
 // 1 partition: the same).
