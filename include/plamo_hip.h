@@ -52,6 +52,12 @@ typedef struct plamo_stats {
      * times them for prefill_seconds / decode_seconds (0 before the first call) */
     double last_prefill_seconds;
     double last_decode_seconds;
+    /* trained adapters in device memory (auxiliary_weight_bytes, Main.swift:342) and the QSA
+     * counters Runtime.sparseQueries / sparseKeys / denseKeys (Runtime.swift:160-162,409-414) */
+    int64_t auxiliary_bytes;
+    int64_t sparse_queries;
+    int64_t sparse_keys;
+    int64_t dense_keys;
 } plamo_stats;
 
 /* ---- Runtime (Runtime.swift:128-553) ------------------------------------------- */
@@ -64,6 +70,16 @@ typedef struct plamo_stats {
  * pinned checksum of the original model. */
 int plamo_open(const char* directory, int32_t context, int32_t packed, const char* source_sha256,
                plamo_runtime** out, char* err, size_t errlen);
+/* Runtime.init(directory:context:packed:qsaBudget:mtp:) (Runtime.swift:164-176,248): as
+ * plamo_open, plus the trained adapters of auxiliary.safetensors (Auxiliary.swift:14-62,
+ * format plamo-aux-v1, whose teacher_sha256 must equal `source_sha256`, NULL = the pinned
+ * checksum).  `qsa_budget` 0 = dense attention, else a multiple of four in 4..2048 ("QSA budget
+ * must be a multiple of four in 4...2048"): the global layers' block indexers select
+ * qsa_budget / 4 blocks of four keys plus the unfinished block for each query once a row sees
+ * more than the budget (Kernels.metal:564-702).  `mtp` loads the MTP head (plamo_draft,
+ * plamo_forward_ex with all/sequential, plamo_rewind). */
+int plamo_open_aux(const char* directory, int32_t context, int32_t packed, const char* source_sha256,
+                   int32_t qsa_budget, int32_t mtp, plamo_runtime** out, char* err, size_t errlen);
 /* Releases the runtime.  Batches opened on it share its stream and weights: while any is
  * open the release is deferred to the last plamo_batch_close (the handle must not be used
  * after plamo_close either way). */
@@ -78,6 +94,27 @@ void plamo_reset(plamo_runtime* rt);
  * Error "Invalid tokens or context exhausted" (Runtime.swift:330). */
 int plamo_forward(plamo_runtime* rt, const int32_t* tokens, int32_t count, int32_t output,
                   int32_t* next, char* err, size_t errlen);
+
+/* Runtime.forward(_:output:all:sequential:) (Runtime.swift:322-467).  `all`: every row's
+ * logits (slots 0 .. count-1 of plamo_logits) and prediction (plamo_predictions);
+ * `sequential`: each row takes the local RoPE coordinates of a scalar decode step
+ * (Kernels.metal:288-298), so its outputs equal count single-token forwards.  Both need an
+ * MTP runtime and count <= 2 (Runtime.verifyRows), else "Invalid tokens or context
+ * exhausted". */
+int plamo_forward_ex(plamo_runtime* rt, const int32_t* tokens, int32_t count, int32_t output, int32_t all,
+                     int32_t sequential, int32_t* next, char* err, size_t errlen);
+
+/* Runtime.draft(_:) (Runtime.swift:485-520): the MTP head's one-token draft after `first`,
+ * from the first output row's normalised hidden state and first's embedding.  Leaves the
+ * position and the logits slots alone; the draft replaces the first prediction.  Error "MTP
+ * requires a prefetched context and trained adapters". */
+int plamo_draft(plamo_runtime* rt, int32_t first, int32_t* draft, char* err, size_t errlen);
+
+/* Runtime.rewind(_:hiddenIndex:) (Runtime.swift:527-538): keeps output row `hidden_index` of
+ * the last forward (logits, hidden state, prediction) and moves the position to
+ * `new_position`, which must be position - rows + hidden_index + 1 ("Invalid verification
+ * rollback"). */
+int plamo_rewind(plamo_runtime* rt, int64_t new_position, int32_t hidden_index, char* err, size_t errlen);
 
 /* Runtime.prefill(_:) (Runtime.swift:469-483): any prompt length up to the context.
  * Processed in large MFMA chunks with the reference's 16-token chunk RoPE coordinates.
@@ -230,6 +267,12 @@ int plamo_pack(const char* safetensors, const char* output, const char* source_s
 int plamo_pack_tensor(const uint16_t* values, int64_t count, uint8_t* payload, int64_t payload_cap,
                       uint32_t* table, int64_t* payload_bytes, char* err, size_t errlen);
 
+/* Auxiliary.init + tensor checks (Auxiliary.swift:14-62) on auxiliary.safetensors without a
+ * device: the archive, then the MTP head (`mtp`) and the global layers' QSA indexers (`qsa`);
+ * the reference's messages ("Trained adapters missing; ...", "Invalid adapter size", "Invalid
+ * adapter header", "Incompatible trained adapters", "Invalid adapter tensor: NAME"). */
+int plamo_check_aux(const char* path, const char* teacher_sha256, int32_t mtp, int32_t qsa, char* err,
+                    size_t errlen);
 /* Weights(path:).tensor(name, shape) validation (Runtime.swift:33-101) without a device. */
 int plamo_check_weights(const char* path, const char* name, const int64_t* shape, int32_t ndim, char* err,
                         size_t errlen);

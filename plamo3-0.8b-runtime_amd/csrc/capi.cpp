@@ -154,6 +154,38 @@ int plamo_open(const char* directory, int32_t context, int32_t packed, const cha
     });
 }
 
+int plamo_open_aux(const char* directory, int32_t context, int32_t packed, const char* sha, int32_t qsa_budget,
+                   int32_t mtp, plamo_runtime** out, char* err, size_t errlen) {
+    return guard(err, errlen, [&] {
+        if (!out || !directory) throw plamo::Error(plamo::E_INVAL, "null argument");
+        *out = nullptr;
+        // Runtime.swift:165,171-175: context, budget, then the adapters before the model
+        if (context < 1 || context > plamo::MAX_CONTEXT) throw plamo::Error(plamo::E_INVAL, "Context must be 1...32768");
+        if (qsa_budget != 0 && (qsa_budget < 4 || qsa_budget > 2048 || qsa_budget % 4 != 0))
+            throw plamo::Error(plamo::E_INVAL, "QSA budget must be a multiple of four in 4...2048");
+        const bool indexers = qsa_budget > 0 && context > qsa_budget;  // Runtime.swift:248
+        if (indexers) throw plamo::Error(plamo::E_INVAL, "QSA indexers are not built yet");
+        std::unique_ptr<plamo::AuxArchive> ar;
+        if (qsa_budget > 0 || mtp) {
+            ar = std::make_unique<plamo::AuxArchive>(std::string(directory) + "/auxiliary.safetensors", sha ? sha : "");
+            plamo::check_aux_tensors(*ar, mtp != 0, false);  // the Predictor before the model
+        }
+        auto rt = std::make_unique<plamo_runtime>();
+        auto& r = rt->impl;
+        r.context = context;
+        int dev = 0;
+        if (hipGetDeviceCount(&dev) != hipSuccess || dev < 1)
+            throw plamo::Error(plamo::E_DEVICE, "An MI355X (gfx950) HIP device is required");
+        PLAMO_HIP(hipStreamCreateWithFlags(&r.stream, hipStreamNonBlocking));
+        r.model = plamo::load_model(directory, context, packed != 0, sha ? sha : "", r.stream);
+        r.eng = std::make_unique<plamo::Engine>(r.model, context, 1, r.stream);
+        if (ar) r.aux = plamo::load_aux(*ar, mtp != 0, indexers);  // indexers after the layers
+        r.mtp = mtp != 0;
+        r.qsa_budget = qsa_budget;
+        *out = rt.release();
+    });
+}
+
 void plamo_close(plamo_runtime* rt) {
     if (!rt) return;
     if (rt->open_batches > 0) {
@@ -176,6 +208,30 @@ int plamo_forward(plamo_runtime* rt, const int32_t* tokens, int32_t count, int32
     });
 }
 
+int plamo_forward_ex(plamo_runtime* rt, const int32_t* tokens, int32_t count, int32_t output, int32_t all,
+                     int32_t sequential, int32_t* next, char* err, size_t errlen) {
+    return guard(err, errlen, [&] {
+        if (!rt || (!tokens && count)) throw plamo::Error(plamo::E_INVAL, "Invalid tokens or context exhausted");
+        const int n = rt->impl.forward_ex(tokens, count, output != 0, all != 0, sequential != 0);
+        if (next) *next = n;
+    });
+}
+
+int plamo_draft(plamo_runtime* rt, int32_t first, int32_t* draft, char* err, size_t errlen) {
+    return guard(err, errlen, [&] {
+        if (!rt) throw plamo::Error(plamo::E_INVAL, "null argument");
+        const int d = rt->impl.draft(first);
+        if (draft) *draft = d;
+    });
+}
+
+int plamo_rewind(plamo_runtime* rt, int64_t new_position, int32_t hidden_index, char* err, size_t errlen) {
+    return guard(err, errlen, [&] {
+        if (!rt) throw plamo::Error(plamo::E_INVAL, "null argument");
+        rt->impl.rewind(new_position, hidden_index);
+    });
+}
+
 int plamo_prefill(plamo_runtime* rt, const int32_t* tokens, int32_t count, int32_t* next, char* err, size_t errlen) {
     return guard(err, errlen, [&] {
         if (!rt || (!tokens && count)) throw plamo::Error(plamo::E_INVAL, "Input exceeds context");
@@ -188,8 +244,7 @@ int plamo_logits_bf16(plamo_runtime* rt, int32_t slot, uint16_t* bits, char* err
     return guard(err, errlen, [&] {
         if (!rt || !bits || slot < 0 || slot >= std::max(1, rt->impl.last_output_rows))
             throw plamo::Error(plamo::E_INVAL, "Invalid logits slot");
-        PLAMO_HIP(hipMemcpy(bits, rt->impl.eng->logits + size_t(slot) * plamo::VOCAB, plamo::VOCAB * 2,
-                            hipMemcpyDeviceToHost));
+        PLAMO_HIP(hipMemcpy(bits, rt->impl.logits_row(slot), plamo::VOCAB * 2, hipMemcpyDeviceToHost));
     });
 }
 
@@ -205,7 +260,7 @@ int plamo_logits(plamo_runtime* rt, int32_t slot, float* values, char* err, size
 int plamo_hidden(plamo_runtime* rt, float* values, char* err, size_t errlen) {
     return guard(err, errlen, [&] {
         if (!rt || !values) throw plamo::Error(plamo::E_INVAL, "null argument");
-        PLAMO_HIP(hipMemcpy(values, rt->impl.eng->hidden, plamo::HIDDEN * 4, hipMemcpyDeviceToHost));
+        PLAMO_HIP(hipMemcpy(values, rt->impl.hidden_row(), plamo::HIDDEN * 4, hipMemcpyDeviceToHost));
     });
 }
 
@@ -231,6 +286,11 @@ int plamo_get_stats(plamo_runtime* rt, plamo_stats* s) {
     s->local_capacity = r.eng->local_capacity;
     s->last_prefill_seconds = r.last_prefill_seconds;
     s->last_decode_seconds = r.last_decode_seconds;
+    s->auxiliary_bytes = r.aux ? r.aux->bytes : 0;
+    s->sparse_queries = r.sparse_queries;
+    s->sparse_keys = r.sparse_keys;
+    s->dense_keys = r.dense_keys;
+    s->device_bytes += r.aux ? int64_t(r.aux->arena.bytes()) : 0;
     return PLAMO_OK;
 }
 
@@ -474,6 +534,15 @@ int plamo_pack_tensor(const uint16_t* values, int64_t count, uint8_t* payload, i
         std::memcpy(payload, data.data(), data.size());
         std::memcpy(table, entries.data(), entries.size() * 4);
         if (payload_bytes) *payload_bytes = int64_t(data.size());
+    });
+}
+
+int plamo_check_aux(const char* path, const char* teacher_sha256, int32_t mtp, int32_t qsa, char* err,
+                    size_t errlen) {
+    return guard(err, errlen, [&] {
+        if (!path) throw plamo::Error(plamo::E_INVAL, "null argument");
+        plamo::AuxArchive ar(path, teacher_sha256 ? teacher_sha256 : "");
+        plamo::check_aux_tensors(ar, mtp != 0, qsa != 0);
     });
 }
 

@@ -26,6 +26,13 @@ constexpr int MAX_ROWS = 4;                   // Batch lanes (Batch.swift:40)
 constexpr int LOCAL_ROPE_ROWS = WINDOW + CHUNK;  // Runtime.swift:266
 constexpr float POST_MIXER_OFFSET = 0.2f;     // Runtime.swift:446
 constexpr float NEXT_OFFSET = 1.0f;           // Runtime.swift:377,455
+// Trained adapters (Auxiliary.swift:87-111): the MTP head's rank and input width, the QSA
+// indexer's projection width (4 query heads + 1 key of 128), rows one verification pass
+// outputs (Runtime.verifyRows, Runtime.swift:130)
+constexpr int MTP_RANK = 256;
+constexpr int MTP_IN = 2 * HIDDEN;            // 3072: [hidden | embedding]
+constexpr int QSA_PROJ = 5 * HEAD_DIM;        // 640
+constexpr int VERIFY_ROWS = 2;
 
 inline bool is_global_layer(int layer) { return layer % 8 == 7; }  // Runtime.swift:239
 

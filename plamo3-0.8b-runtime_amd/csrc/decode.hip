@@ -1630,6 +1630,41 @@ __global__ __launch_bounds__(256) void select_kernel(float* logits, int n, const
 
 // One thread per 8 weights (count is a whole number of 128-weight blocks), decoded by the
 // same p12_decode8 as the GEMV and GEMM loads.
+// ------------------------------------------------------------------------------------ MTP
+// Input of the MTP adapter (Runtime.swift:493-494): the final normalised hidden row of the
+// last output, then the embedding row of the first draft token, as 3072 floats.
+__global__ __launch_bounds__(256) void mtp_input_kernel(const float* hidden, const uint16_t* embed, int token,
+                                                         float* out) {
+    for (int i = threadIdx.x; i < HIDDEN; i += 256) {
+        out[i] = hidden[i];
+        out[HIDDEN + i] = bf(embed[size_t(token) * HIDDEN + i]);
+    }
+}
+
+// The adapter's activation, down projection and residual (mtp_activate, linear, mtp_add;
+// Kernels.metal:347-356, Runtime.swift:498-501): a_j = roundbf(u_j / (1 + exp(-u_j))) of the
+// up projection's 256 outputs, then row r: y = roundbf(W_r . a), out_r = roundbf(x_r + y)
+// with x the hidden half of the input.  One wave per row; lane l owns columns 4l .. 4l+3:
+// two v_dot2_f32_bf16 steps over the column pairs in order, then the wave's XOR butterfly.
+__global__ __launch_bounds__(256) void mtp_down_kernel(const float* up, const float* x, const uint16_t* w,
+                                                        float* out) {
+#pragma clang fp contract(off)  // fixed rounding sequence, reproduced by the CPU oracle
+    __shared__ uint32_t as[MTP_RANK / 2];  // activations as BF16 pairs (BF16-exact values)
+    const int tid = threadIdx.x;
+    if (tid < MTP_RANK / 2) {
+        const float u0 = up[2 * tid], u1 = up[2 * tid + 1];
+        as[tid] = pack_bf16(roundbf(u0 / (1.0f + exp_det(-u0))), roundbf(u1 / (1.0f + exp_det(-u1))));
+    }
+    __syncthreads();
+    const int lane = tid & 63, r = int(blockIdx.x) * 4 + (tid >> 6);
+    if (r >= HIDDEN) return;
+    const uint2 wv = *reinterpret_cast<const uint2*>(w + size_t(r) * MTP_RANK + lane * 4);
+    float acc = dot2bf(wv.x, as[2 * lane], 0.f);
+    acc = dot2bf(wv.y, as[2 * lane + 1], acc);
+    const float t = wave_sum(acc);
+    if (lane == 0) out[r] = roundbf(x[r] + roundbf(t));
+}
+
 __global__ void unpack_kernel(const uint8_t* payload, const uint32_t* table, uint16_t* out, int64_t count) {
     const int64_t i = (int64_t(blockIdx.x) * blockDim.x + threadIdx.x) * 8;
     if (i >= count) return;
@@ -1770,7 +1805,11 @@ void launch_gemv(int n, bool packed, int maxr, Prologue pro, Epilogue epi, const
     if (n == HIDDEN) gemv_dispatch_n<HIDDEN>(packed, maxr, pro, epi, p, blocks, s);
     else if (n == ATTN) gemv_dispatch_n<ATTN>(packed, maxr, pro, epi, p, blocks, s);
     else if (n == INTER) gemv_dispatch_n<INTER>(packed, maxr, pro, epi, p, blocks, s);
-    else throw Error(E_INVAL, "GEMV input width must be 1536, 2048 or 6144");
+    else if (n == MTP_IN && !packed && maxr == 1 && !p.state) {  // the MTP adapter's up projection
+        const dim3 grid(blocks), block(64 * gemv_waves(MTP_IN, 1, EPI_ROUND));
+        if (pro != PRO_PLAIN || epi != EPI_ROUND) throw Error(E_INVAL, "unsupported GEMV variant");
+        hipLaunchKernelGGL((gemv_kernel<MTP_IN, false, 1, PRO_PLAIN, EPI_ROUND, false>), grid, block, 0, s, p);
+    } else throw Error(E_INVAL, "GEMV input width must be 1536, 2048, 3072 or 6144");
 }
 
 void launch_attention(bool full, const AttnParams& p, int rows, hipStream_t s) {
@@ -1800,6 +1839,14 @@ void launch_select(float* logits, int n, const int32_t* history, int hist, float
                    float presence, int32_t* out, hipStream_t s) {
     hipLaunchKernelGGL(select_kernel, dim3(1), dim3(256), 0, s, logits, n, history, hist, penalty, ngram, frequency,
                        presence, out);
+}
+
+void launch_mtp_input(const float* hidden, const uint16_t* embed, int token, float* out, hipStream_t s) {
+    hipLaunchKernelGGL(mtp_input_kernel, dim3(1), dim3(256), 0, s, hidden, embed, token, out);
+}
+
+void launch_mtp_down(const float* up, const float* x, const uint16_t* w, float* out, hipStream_t s) {
+    hipLaunchKernelGGL(mtp_down_kernel, dim3(HIDDEN / 4), dim3(256), 0, s, up, x, w, out);
 }
 
 void launch_unpack(const uint8_t* payload, const uint32_t* table, uint16_t* out, int64_t count, hipStream_t s) {

@@ -181,6 +181,65 @@ TensorView SafeTensors::tensor(const std::string& name, const std::vector<int64_
     return TensorView{file_->data() + data_start_ + a, size_t(b - a)};
 }
 
+// ------------------------------------------------------------------------------ AuxArchive
+namespace {
+// Swift's Int(String): optional sign, then decimal digits only
+bool swift_int(const std::string& s, int64_t& out) {
+    size_t i = (!s.empty() && (s[0] == '+' || s[0] == '-')) ? 1 : 0;
+    if (i >= s.size() || s.size() - i > 18) return false;
+    int64_t v = 0;
+    for (size_t k = i; k < s.size(); ++k) {
+        if (s[k] < '0' || s[k] > '9') return false;
+        v = v * 10 + (s[k] - '0');
+    }
+    out = s[0] == '-' ? -v : v;
+    return true;
+}
+}  // namespace
+
+AuxArchive::AuxArchive(const std::string& path, const std::string& teacher_sha256) {
+    // Auxiliary.swift:16-17
+    file_ = std::make_unique<MappedFile>(path, "Trained adapters missing; run scripts/train_auxiliary.py --collect");
+    const size_t size = file_->size();
+    if (size <= 8 || size >= 268435456ull) throw Error(E_FORMAT, "Invalid adapter size");  // :20-22
+    const uint64_t count = load_u64(file_->data());
+    if (count > 1048576 || count >= size - 8 || (count + 8) % 8 != 0) throw Error(E_FORMAT, "Invalid adapter header");
+    data_start_ = count + 8;
+    const std::string incompatible = "Incompatible trained adapters";
+    try {
+        header_ = json::parse(reinterpret_cast<const char*>(file_->data() + 8), count);
+    } catch (const std::exception&) {
+        throw Error(E_FORMAT, incompatible);
+    }
+    // Auxiliary.swift:33-40: the metadata strings
+    const std::string want = teacher_sha256.empty() ? REFERENCE_SOURCE_SHA : teacher_sha256;
+    const json::Value* meta = header_.kind == json::Value::Object ? header_.get("__metadata__") : nullptr;
+    auto text = [&](const char* key) -> const std::string* {
+        const json::Value* v = meta ? meta->get(key) : nullptr;
+        return v && v->kind == json::Value::String ? &v->str : nullptr;
+    };
+    int64_t qsa_steps = 0, mtp_steps = 0;
+    const std::string *fmt = text("format"), *teacher = text("teacher_sha256"), *rank = text("rank");
+    const std::string *qs = text("qsa_steps"), *ms = text("mtp_steps");
+    if (!meta || meta->kind != json::Value::Object || !fmt || *fmt != "plamo-aux-v1" || !teacher || *teacher != want ||
+        !rank || *rank != "256" || !qs || !swift_int(*qs, qsa_steps) || qsa_steps <= 0 || !ms ||
+        !swift_int(*ms, mtp_steps) || mtp_steps <= 0)
+        throw Error(E_FORMAT, incompatible);
+}
+
+TensorView AuxArchive::tensor(const std::string& name, const std::vector<int64_t>& shape) const {
+    // Auxiliary.swift:44-49
+    const json::Value* t = header_.get(name);
+    int64_t a = 0, b = 0, numel = 2;
+    for (auto s : shape) numel *= s;
+    const json::Value* dt = t ? t->get("dtype") : nullptr;
+    if (!t || t->kind != json::Value::Object || !dt || dt->kind != json::Value::String || dt->str != "BF16" ||
+        !shape_is(t->get("shape"), shape) || !int_pair(t->get("data_offsets"), a, b) || a < 0 || a % 4 != 0 ||
+        b < a || b - a != numel || b > int64_t(file_->size() - data_start_))
+        throw Error(E_FORMAT, "Invalid adapter tensor: " + name);
+    return TensorView{file_->data() + data_start_ + a, size_t(b - a)};
+}
+
 // --------------------------------------------------------------------------- PackedArchive
 PackedArchive::PackedArchive(const std::string& path, const std::string& source_sha256) {
     file_ = std::make_unique<MappedFile>(path, "Packed weights missing; run scripts/pack_weights.py first");  // :14

@@ -77,6 +77,21 @@ class PackedArchive {
     size_t payload_ = 0;
 };
 
+// auxiliary.safetensors: the trained QSA indexers and MTP adapter (Auxiliary.swift:5-62).
+class AuxArchive {
+  public:
+    // Auxiliary.init (Auxiliary.swift:14-41); `teacher_sha256` empty = the reference's pinned
+    // checksum of the model the adapters were trained against.
+    AuxArchive(const std::string& path, const std::string& teacher_sha256);
+    // Auxiliary.tensor(name, shape) (Auxiliary.swift:43-62): BF16, exact shape, 4-byte aligned.
+    TensorView tensor(const std::string& name, const std::vector<int64_t>& shape) const;
+
+  private:
+    std::unique_ptr<MappedFile> file_;
+    json::Value header_;
+    size_t data_start_ = 0;
+};
+
 extern const char* const REFERENCE_SOURCE_SHA;
 
 struct PackReport {

@@ -165,6 +165,10 @@ void launch_argmax(const void* x, uint32_t* out, int n, int rows, bool bf16, hip
 void launch_select(float* logits, int n, const int32_t* history, int hist, float penalty, int ngram, float frequency,
                    float presence, int32_t* out, hipStream_t s);
 void launch_unpack(const uint8_t* payload, const uint32_t* table, uint16_t* out, int64_t count, hipStream_t s);
+// MTP adapter (Runtime.swift:485-520): input row [hidden | embed(token)], and the
+// activation + down projection + residual after the up projection (a 3072-wide GEMV).
+void launch_mtp_input(const float* hidden, const uint16_t* embed, int token, float* out, hipStream_t s);
+void launch_mtp_down(const float* up, const float* x, const uint16_t* w, float* out, hipStream_t s);
 void launch_fill_u32(uint32_t* p, uint32_t value, size_t count, hipStream_t s);
 // Device workspace of a kernel-level decode attention call, 256-byte aligned: the step state
 // (256 B), the attention tickets [ROWS][4 head groups] (256 B), then the partition

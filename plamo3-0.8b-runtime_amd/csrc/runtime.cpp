@@ -513,6 +513,53 @@ void Engine::run_steps(int n) {
     for (; n > 0; --n) PLAMO_HIP(hipGraphLaunch(graph_loop, stream));
 }
 
+void check_aux_tensors(const AuxArchive& ar, bool mtp, bool qsa) {
+    if (mtp) {  // Predictor (Auxiliary.swift:101-102)
+        ar.tensor("mtp.heads.0.up.weight", {MTP_RANK, MTP_IN});
+        ar.tensor("mtp.heads.0.down.weight", {HIDDEN, MTP_RANK});
+    }
+    if (qsa)  // Indexer of each global layer (Auxiliary.swift:75-77)
+        for (int l = 0; l < LAYERS; ++l) {
+            if (!is_global_layer(l)) continue;
+            const std::string p = "qsa." + std::to_string(l) + ".";
+            ar.tensor(p + "proj.weight", {QSA_PROJ, HIDDEN});
+            ar.tensor(p + "q_norm.weight", {HEAD_DIM});
+            ar.tensor(p + "k_norm.weight", {HEAD_DIM});
+        }
+}
+
+std::unique_ptr<Aux> load_aux(const AuxArchive& ar, bool mtp, bool qsa) {
+    check_aux_tensors(ar, mtp, qsa);
+    auto x = std::make_unique<Aux>();
+    DeviceArena& a = x->arena;
+    auto put = [&](const std::string& name, std::vector<int64_t> shape) {
+        const TensorView t = ar.tensor(name, shape);
+        x->bytes += int64_t(t.bytes);
+        return upload<uint16_t>(a, t.data, t.bytes);
+    };
+    if (mtp) {
+        x->mtp_up = put("mtp.heads.0.up.weight", {MTP_RANK, MTP_IN});
+        x->mtp_down = put("mtp.heads.0.down.weight", {HIDDEN, MTP_RANK});
+        x->mtp_in = a.alloc_n<float>(MTP_IN);
+        x->mtp_up_out = a.alloc_n<float>(MTP_RANK);
+        x->mtp_hidden = a.alloc_n<float>(HIDDEN);
+        x->mtp_logits = a.alloc_n<uint16_t>(VOCAB);
+        x->slot_logits = a.alloc_n<uint16_t>(size_t(VERIFY_ROWS) * VOCAB);
+        x->slot_hidden = a.alloc_n<float>(size_t(VERIFY_ROWS) * HIDDEN);
+        x->slot_next = a.alloc_n<int32_t>(VERIFY_ROWS);
+    }
+    if (qsa) {
+        for (int l = 0; l < LAYERS; ++l) {
+            if (!is_global_layer(l)) continue;
+            const std::string p = "qsa." + std::to_string(l) + ".";
+            x->qsa_proj[l] = put(p + "proj.weight", {QSA_PROJ, HIDDEN});
+            x->qsa_q_norm[l] = put(p + "q_norm.weight", {HEAD_DIM});
+            x->qsa_k_norm[l] = put(p + "k_norm.weight", {HEAD_DIM});
+        }
+    }
+    return x;
+}
+
 // A prefill chunk of n tokens at p0 for one lane: every layer as MFMA GEMMs, K/V written
 // for the chunk, then MFMA flash attention of the chunk's queries over their visible keys.
 void Engine::enqueue_prefill_chunk(int n, int p0, int lane, bool last_chunk, bool output) {
@@ -610,6 +657,18 @@ void Engine::prefill(const int32_t* tokens, int n, int p0, int lane, bool output
     }
 }
 
+void Engine::prefill_heads(int n, uint16_t* slot_logits, float* slot_hidden, int32_t* slot_next) {
+    for (int i = 0; i < n; ++i) {
+        launch_step_begin(bufs, stream);
+        enqueue_head(p_proj + size_t(i) * HIDDEN, p_x + size_t(i) * HIDDEN, 1);
+        PLAMO_HIP(hipMemcpyAsync(slot_logits + size_t(i) * VOCAB, logits, size_t(VOCAB) * 2, hipMemcpyDeviceToDevice,
+                                 stream));
+        PLAMO_HIP(hipMemcpyAsync(slot_hidden + size_t(i) * HIDDEN, hidden, size_t(HIDDEN) * 4, hipMemcpyDeviceToDevice,
+                                 stream));
+        PLAMO_HIP(hipMemcpyAsync(slot_next + i, &state->next[0], 4, hipMemcpyDeviceToDevice, stream));
+    }
+}
+
 // ---------------------------------------------------------------------------- runtime
 RuntimeImpl::~RuntimeImpl() {
     eng.reset();
@@ -621,6 +680,7 @@ void RuntimeImpl::reset() {
     position = 0;
     gpu_seconds = 0;
     last_output_rows = 0;
+    sparse_queries = sparse_keys = dense_keys = 0;
     history.clear();
     uploaded = 0;
     counts_dirty = true;
@@ -727,8 +787,147 @@ int RuntimeImpl::prefill(const int32_t* tokens, int n) {
     return next;
 }
 
+int RuntimeImpl::forward_ex(const int32_t* tokens, int n, bool output, bool all, bool sequential) {
+    // Runtime.swift:328-330: validate before touching any state
+    const int limit = std::min(context, CHUNK);
+    bool ok = n > 0 && n <= limit && position + n <= context;
+    for (int i = 0; ok && i < n; ++i) ok = tokens[i] >= 0 && tokens[i] < VOCAB;
+    if (all && !(mtp && n <= VERIFY_ROWS)) ok = false;
+    if (sequential && !(mtp && n <= VERIFY_ROWS)) ok = false;
+    if (!ok) throw Error(E_INVAL, "Invalid tokens or context exhausted");
+    if (!all && !sequential) return forward(tokens, n, output);
+    Engine& e = *eng;
+    StepState& hs = *e.host_state;
+    const int rows = output ? (all ? n : 1) : 0;  // Runtime.swift:453
+    begin_timing();
+    if (sequential || n == 1) {
+        // Each row as a scalar decode step at its own position: its local keys and query take
+        // the coordinates of that step (rotate_steps, Kernels.metal:288-298), so row i's
+        // outputs are those of forward([tokens[i]]) after rows 0 .. i - 1.
+        for (int i = 0; i < n; ++i) {
+            hs.rows = 1;
+            hs.lane[0] = 0;
+            hs.pos[0] = uint32_t(position + i);
+            hs.token[0] = tokens[i];
+            hs.loop = 0;
+            hs.stopped = 0;
+            sync_sampler(e, 0);
+            PLAMO_HIP(hipMemcpyAsync(e.state, &hs, sizeof(StepState), hipMemcpyHostToDevice, stream));
+            const bool head = output && (all || i == n - 1);
+            if (head) e.run_step();
+            else e.enqueue_step(false);
+            if (head && all) {
+                PLAMO_HIP(hipMemcpyAsync(aux->slot_logits + size_t(i) * VOCAB, e.logits, size_t(VOCAB) * 2,
+                                         hipMemcpyDeviceToDevice, stream));
+                PLAMO_HIP(hipMemcpyAsync(aux->slot_hidden + size_t(i) * HIDDEN, e.hidden, size_t(HIDDEN) * 4,
+                                         hipMemcpyDeviceToDevice, stream));
+                PLAMO_HIP(hipMemcpyAsync(aux->slot_next + i, &e.state->next[0], 4, hipMemcpyDeviceToDevice, stream));
+            }
+        }
+    } else {
+        // one chunk of n rows (chunk-relative local coordinates, Runtime.swift:389), then a
+        // head per row
+        hs.rows = 1;
+        hs.lane[0] = 0;
+        hs.pos[0] = uint32_t(position);
+        hs.loop = 0;
+        hs.stopped = 0;
+        sync_sampler(e, 0);
+        PLAMO_HIP(hipMemcpyAsync(e.state, &hs, sizeof(StepState), hipMemcpyHostToDevice, stream));
+        e.prefill(tokens, n, int(position), 0, false);
+        if (output) e.prefill_heads(n, aux->slot_logits, aux->slot_hidden, aux->slot_next);
+    }
+    end_timing();
+    int32_t next[VERIFY_ROWS] = {-1, -1};
+    if (rows > 1) PLAMO_HIP(hipMemcpyAsync(next, aux->slot_next, size_t(rows) * 4, hipMemcpyDeviceToHost, stream));
+    PLAMO_HIP(hipMemcpyAsync(&hs, e.state, sizeof(StepState), hipMemcpyDeviceToHost, stream));
+    PLAMO_HIP(hipStreamSynchronize(stream));
+    PLAMO_HIP(hipGetLastError());
+    position += n;
+    last_output_rows = rows;
+    if (!output) return -1;
+    if (rows > 1) predictions.assign(next, next + rows);
+    else predictions.assign(1, int32_t(hs.next[0]));
+    return predictions.back();
+}
+
+const uint16_t* RuntimeImpl::logits_row(int slot) const {
+    return last_output_rows > 1 ? aux->slot_logits + size_t(slot) * VOCAB : eng->logits;
+}
+
+const float* RuntimeImpl::hidden_row() const { return eng->hidden; }
+
+int RuntimeImpl::draft(int first) {
+    // Runtime.swift:489-491
+    if (!mtp || !aux || position <= 0 || first < 0 || first >= VOCAB || first == 1 || first == 16)
+        throw Error(E_STATE, "MTP requires a prefetched context and trained adapters");
+    Engine& e = *eng;
+    const Model& m = *model;
+    StepState& hs = *e.host_state;
+    begin_timing();
+    // the first row's normalised hidden state (Runtime.swift:493), then the token's embedding
+    const float* h = last_output_rows > 1 ? aux->slot_hidden : e.hidden;
+    launch_mtp_input(h, m.embed, first, aux->mtp_in, stream);
+    GemvParams u{};
+    u.rows = 1;
+    u.m = MTP_RANK;
+    u.w = aux->mtp_up;
+    u.in = aux->mtp_in;
+    u.out = aux->mtp_up_out;
+    u.tag = uint32_t(TIMELINE_TAGS);
+    launch_gemv(MTP_IN, false, 1, PRO_PLAIN, EPI_ROUND, u, gemv_blocks(MTP_IN, 1, EPI_ROUND, MTP_RANK, false), stream);
+    launch_mtp_down(aux->mtp_up_out, aux->mtp_in, aux->mtp_down, aux->mtp_hidden, stream);
+    // the LM head and argmax (Runtime.swift:502-503), greedy whatever the sampler settings
+    hs.rows = 1;
+    hs.lane[0] = 0;
+    hs.loop = 0;
+    hs.stopped = 0;
+    hs.sampling = 0;
+    PLAMO_HIP(hipMemcpyAsync(e.state, &hs, sizeof(StepState), hipMemcpyHostToDevice, stream));
+    GemvParams g{};
+    g.state = e.state;
+    g.rows = 1;
+    g.m = VOCAB;
+    g.w = m.head.w;
+    g.table = m.head.table;
+    g.tag = uint32_t(TIMELINE_TAGS);
+    g.in = aux->mtp_hidden;
+    g.out16 = aux->mtp_logits;
+    g.bufs = e.bufs;
+    launch_gemv(HIDDEN, m.packed, 1, PRO_PLAIN, EPI_LOGITS, g, head_blocks(1), stream);
+    launch_head_merge(e.bufs, head_blocks(1), false, stream);
+    end_timing();
+    PLAMO_HIP(hipMemcpyAsync(&hs, e.state, sizeof(StepState), hipMemcpyDeviceToHost, stream));
+    PLAMO_HIP(hipStreamSynchronize(stream));
+    PLAMO_HIP(hipGetLastError());
+    const int32_t d = int32_t(hs.next[0]);
+    // the draft lands in the first prediction slot (Runtime.swift:503-507)
+    if (!predictions.empty()) predictions[0] = d;
+    return d;
+}
+
+void RuntimeImpl::rewind(int64_t new_position, int hidden_index) {
+    // Runtime.swift:528-531
+    if (hidden_index < 0 || hidden_index >= last_output_rows ||
+        new_position != position - last_output_rows + hidden_index + 1)
+        throw Error(E_STATE, "Invalid verification rollback");
+    Engine& e = *eng;
+    if (last_output_rows > 1 && hidden_index != last_output_rows - 1) {
+        PLAMO_HIP(hipMemcpyAsync(e.logits, aux->slot_logits + size_t(hidden_index) * VOCAB, size_t(VOCAB) * 2,
+                                 hipMemcpyDeviceToDevice, stream));
+        PLAMO_HIP(hipMemcpyAsync(e.hidden, aux->slot_hidden + size_t(hidden_index) * HIDDEN, size_t(HIDDEN) * 4,
+                                 hipMemcpyDeviceToDevice, stream));
+        PLAMO_HIP(hipStreamSynchronize(stream));
+    }
+    predictions.assign(1, predictions[size_t(hidden_index)]);
+    position = new_position;
+    last_output_rows = 1;
+}
+
 // ------------------------------------------------------------------------------ batch
 BatchImpl::BatchImpl(RuntimeImpl* r) : rt(r) {
+    if (rt->qsa_budget > 0 || rt->mtp)
+        throw Error(E_INVAL, "Batch requires dense greedy inference with context below 8192");  // Batch.swift:34-36
     if (rt->context < 1 || rt->context >= 8192)
         throw Error(E_INVAL, "Batch requires dense greedy inference with context below 8192");  // Batch.swift:34-36
     eng = std::make_unique<Engine>(rt->model, rt->context, ROWS, rt->stream);

@@ -9,6 +9,7 @@
 #include <vector>
 
 #include "common.h"
+#include "formats.h"
 #include "kernels.h"
 #include "prefill.h"
 
@@ -52,6 +53,31 @@ struct Model {
     int64_t weight_bytes = 0, linear_bytes = 0;
     DeviceArena arena;
 };
+
+// Trained adapters in HBM (Auxiliary.swift:5-111): the MTP head (Predictor) and, on the
+// global layers, the QSA block indexers (Indexer), plus the draft and verification scratch.
+struct Aux {
+    const uint16_t* mtp_up = nullptr;    // [256][3072]
+    const uint16_t* mtp_down = nullptr;  // [1536][256]
+    const uint16_t* qsa_proj[LAYERS] = {};    // [640][1536] (global layers)
+    const uint16_t* qsa_q_norm[LAYERS] = {};  // [128]
+    const uint16_t* qsa_k_norm[LAYERS] = {};
+    int64_t bytes = 0;                   // adapter bytes in HBM (auxiliary_weight_bytes)
+    // draft: input [hidden | embedding], up projection, adapter output, its logits
+    float *mtp_in = nullptr, *mtp_up_out = nullptr, *mtp_hidden = nullptr;
+    uint16_t* mtp_logits = nullptr;
+    // rows of the last verification pass (forward with all): logits, hidden, prediction
+    uint16_t* slot_logits = nullptr;     // [VERIFY_ROWS][VOCAB]
+    float* slot_hidden = nullptr;        // [VERIFY_ROWS][HIDDEN]
+    int32_t* slot_next = nullptr;        // [VERIFY_ROWS]
+    DeviceArena arena;
+};
+
+// Predictor/Indexer tensors of a validated archive (Runtime.swift:174-176,248) in HBM: `mtp`
+// the MTP head, `qsa` the indexers of the global layers.
+std::unique_ptr<Aux> load_aux(const AuxArchive& archive, bool mtp, bool qsa);
+// Names and shapes the runtime reads from auxiliary.safetensors (Auxiliary.swift:72-111).
+void check_aux_tensors(const AuxArchive& archive, bool mtp, bool qsa);
 
 // KV, scratch, step state and the captured decode graph for `lanes` sequences.
 class Engine {
@@ -112,6 +138,9 @@ class Engine {
     void prepare_loop_graph();
     // prefill of `n` tokens of one lane at position p0 (n > 1); head on the last token.
     void prefill(const int32_t* tokens, int n, int p0, int lane, bool output);
+    // after a prefill without output: the head of each of its first n rows, row i's logits,
+    // final hidden row and prediction copied to slot i (the engine keeps row n - 1's)
+    void prefill_heads(int n, uint16_t* slot_logits, float* slot_hidden, int32_t* slot_next);
     void zero_sampler();
 
   private:
@@ -145,9 +174,23 @@ struct RuntimeImpl {
     size_t uploaded = 0;            // history entries already on the device
     bool counts_dirty = true;
 
+    // trained adapters (Runtime.swift:170-176): MTP draft, QSA budget (0: dense attention)
+    std::unique_ptr<Aux> aux;
+    bool mtp = false;
+    int qsa_budget = 0;
+    int64_t sparse_queries = 0, sparse_keys = 0, dense_keys = 0;  // Runtime.swift:160-162
+
     ~RuntimeImpl();
     void reset();
     int forward(const int32_t* tokens, int n, bool output);
+    // Runtime.forward(_:output:all:sequential:) (Runtime.swift:322-467): `all` outputs every
+    // row (at most VERIFY_ROWS, MTP only); `sequential` gives each row the local RoPE
+    // coordinates of a scalar decode step (rotate_steps, Kernels.metal:288-298)
+    int forward_ex(const int32_t* tokens, int n, bool output, bool all, bool sequential);
+    int draft(int first);                                   // Runtime.draft (Runtime.swift:485-520)
+    void rewind(int64_t new_position, int hidden_index);    // Runtime.rewind (Runtime.swift:527-538)
+    const uint16_t* logits_row(int slot) const;             // device logits of output row `slot`
+    const float* hidden_row() const;                        // device final hidden of the last row
     int prefill(const int32_t* tokens, int n);
     void begin_timing();
     void end_timing();

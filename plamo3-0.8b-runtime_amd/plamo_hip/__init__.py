@@ -28,13 +28,20 @@ def _u16_to_f32(bits):
 
 
 class Runtime:
-    """Runtime(directory:context:packed:) (Runtime.swift:164)."""
+    """Runtime(directory:context:packed:qsaBudget:mtp:) (Runtime.swift:164).  `qsa_budget`
+    and `mtp` load the trained adapters of auxiliary.safetensors, whose teacher checksum must
+    equal `source_sha256` (None: the reference's pinned value)."""
 
-    def __init__(self, directory, context, packed=False, source_sha256=None):
+    def __init__(self, directory, context, packed=False, source_sha256=None, qsa_budget=None, mtp=False):
         lib = native.load()
         h = ctypes.c_void_p()
-        native.call(lib.plamo_open, str(directory).encode(), int(context), 1 if packed else 0,
-                    source_sha256.encode() if source_sha256 else None, ctypes.byref(h))
+        sha = source_sha256.encode() if source_sha256 else None
+        if qsa_budget is None and not mtp:
+            native.call(lib.plamo_open, str(directory).encode(), int(context), 1 if packed else 0, sha,
+                        ctypes.byref(h))
+        else:
+            native.call(lib.plamo_open_aux, str(directory).encode(), int(context), 1 if packed else 0, sha,
+                        int(qsa_budget or 0), 1 if mtp else 0, ctypes.byref(h))
         self._h = h
         self._lib = lib
 
@@ -58,13 +65,28 @@ class Runtime:
     def reset(self):
         self._lib.plamo_reset(self._h)
 
-    def forward(self, tokens, output=True):
-        """Runtime.forward(_:output:) (Runtime.swift:321-467) -> next token (-1 without output)."""
+    def forward(self, tokens, output=True, all=False, sequential=False):
+        """Runtime.forward(_:output:all:sequential:) (Runtime.swift:321-467) -> next token of the
+        last row (-1 without output); with `all`, predictions() holds every row's."""
         tokens = [int(t) for t in tokens]
         nxt = ctypes.c_int32(-1)
-        native.call(self._lib.plamo_forward, self._h, native.i32(tokens), len(tokens), 1 if output else 0,
-                    ctypes.byref(nxt))
+        if all or sequential:
+            native.call(self._lib.plamo_forward_ex, self._h, native.i32(tokens), len(tokens), 1 if output else 0,
+                        1 if all else 0, 1 if sequential else 0, ctypes.byref(nxt))
+        else:
+            native.call(self._lib.plamo_forward, self._h, native.i32(tokens), len(tokens), 1 if output else 0,
+                        ctypes.byref(nxt))
         return nxt.value
+
+    def draft(self, first):
+        """Runtime.draft(_:) (Runtime.swift:485-520) -> [draft token]."""
+        d = ctypes.c_int32(-1)
+        native.call(self._lib.plamo_draft, self._h, int(first), ctypes.byref(d))
+        return [d.value]
+
+    def rewind(self, new_position, hidden_index):
+        """Runtime.rewind(_:hiddenIndex:) (Runtime.swift:527-538)."""
+        native.call(self._lib.plamo_rewind, self._h, int(new_position), int(hidden_index))
 
     def prefill(self, tokens):
         """Runtime.prefill(_:) (Runtime.swift:469-483)."""

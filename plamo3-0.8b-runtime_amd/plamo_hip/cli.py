@@ -15,8 +15,9 @@ Differences, each forced by the platform:
   the line, or after '。', '！', '？', '．', '｡' (plus closing marks) whatever follows.  Every
   other step (grapheme units, the limit*4 window, halving, whitespace literals) is the
   reference's.
-* QSA and MTP (--qsa, --qsa-budget, --mtp) are not built on this GPU; the options parse with
-  the reference's rules and then fail with an error saying so.
+* The .p12 archive and auxiliary.safetensors must carry the original model's checksum; a
+  model directory of another model (the synthetic test model) names its own in the
+  environment variable PLAMO_SOURCE_SHA256.
 * Metal memory keys report HIP device memory held by the runtime; the macOS footprint keys
   report VmRSS / VmHWM from /proc/self/status.
 """
@@ -186,7 +187,7 @@ Without TEXT, reads UTF-8 from stdin. Translation goes to stdout; JSON metrics t
 and keep the source whitespace between them; --max-tokens applies per segment.
 --batch4 batches up to four segments (greedy only, context below 8192; requires --segment-tokens).
 --repetition-penalty F, --frequency-penalty F, --no-repeat-ngram N, --loop-limit N as in the reference.
---qsa/--qsa-budget/--mtp are accepted by the parser and rejected at run time (not built).
+--qsa/--qsa-budget N select sparse global attention; --mtp drafts and verifies tokens (trained adapters).
 Verification: --tokenize TEXT | --decode IDS | --tokens IDS --dump-logits FILE [--max-tokens 0]"""
 
 
@@ -378,11 +379,12 @@ def execute(arguments, stdin, stdout, stderr):
         raise Failure("Input plus output limit exceeds context")
     if o.batch4 and context >= 8192:
         raise Failure("Batch4 context must be below 8192")
-    if o.qsa or o.mtp:
-        raise Failure("QSA and MTP are not built for this GPU")
     load_start = time.time()
     with _device_init_notices(stderr):
-        runtime = Runtime(o.model, context, packed=o.packed)
+        # the .p12 archive and the adapters carry the original model's checksum; a synthetic
+        # model directory names its own in PLAMO_SOURCE_SHA256 (test and bench hook)
+        runtime = Runtime(o.model, context, packed=o.packed, source_sha256=os.environ.get("PLAMO_SOURCE_SHA256"),
+                          qsa_budget=o.qsa_budget if o.qsa else None, mtp=o.mtp)
         plan = document_plan(parts) if o.batch4 else None
         batch = Batch(runtime) if plan is not None and len(plan[0]) > 1 else None
         device = _device_name()
@@ -439,6 +441,15 @@ def execute(arguments, stdin, stdout, stderr):
             stream = TokenStream(tokenizer) if o.stream else None
             runtime.reset()
             generated, stop = [], None
+            proposed = accepted = verifications = 0
+
+            def emit(token):
+                if stream is not None:
+                    s = _text(stream.push(token))
+                    if s:
+                        stdout.write(s)
+                        stdout.flush()
+
             start = time.time()
             nxt = runtime.prefill(part.tokens)
             prefill_end = time.time()
@@ -446,25 +457,57 @@ def execute(arguments, stdin, stdout, stderr):
                 tmp = o.dump + ".tmp"
                 runtime.logits().astype("<f4").tofile(tmp)
                 os.replace(tmp, o.dump)
-            for i in range(o.max_tokens):
-                if nxt in END_IDS:
-                    stop = "stop"
-                    break
-                generated.append(nxt)
-                runtime.observe(nxt)
-                if stream is not None:
-                    s = _text(stream.push(nxt))
-                    if s:
-                        stdout.write(s)
-                        stdout.flush()
-                if o.loop_limit > 0 and repetition_period(generated, o.loop_limit) is not None:
-                    stop = "repeat"
-                    break
-                if i + 1 < o.max_tokens:
-                    nxt = runtime.forward([nxt])
+            if o.mtp:
+                # draft, verify the candidates in one sequential pass, keep the agreeing prefix
+                # (Main.swift:254-276): the output is the greedy sequence
+                while len(generated) < o.max_tokens:
+                    if nxt in END_IDS:
+                        stop = "stop"
+                        break
+                    remaining = o.max_tokens - len(generated)
+                    if remaining == 1:
+                        generated.append(nxt)
+                        emit(nxt)
+                        break
+                    candidates = [nxt]
+                    for token in runtime.draft(nxt)[:remaining - 1]:
+                        if token in END_IDS:
+                            break
+                        candidates.append(token)
+                    proposed += len(candidates) - 1
+                    start_position = runtime.position
+                    runtime.forward(candidates, all=True, sequential=True)
+                    verified = runtime.predictions()
+                    count = 1
+                    while count < len(candidates) and candidates[count] == verified[count - 1]:
+                        count += 1
+                    for token in candidates[:count]:
+                        generated.append(token)
+                        emit(token)
+                    nxt = verified[count - 1]
+                    accepted += count - 1
+                    verifications += 1
+                    runtime.rewind(start_position + count, count - 1)
+            else:
+                for i in range(o.max_tokens):
+                    if nxt in END_IDS:
+                        stop = "stop"
+                        break
+                    generated.append(nxt)
+                    runtime.observe(nxt)
+                    emit(nxt)
+                    if o.loop_limit > 0 and repetition_period(generated, o.loop_limit) is not None:
+                        stop = "repeat"
+                        break
+                    if i + 1 < o.max_tokens:
+                        nxt = runtime.forward([nxt])
             end = time.time()
+            counters = runtime.stats()
             count = max(0, len(generated) - (1 if stop is None else 0))
             seg_runs.append(dict(zero_aux, **{
+                "mtp_proposed_tokens": proposed, "mtp_accepted_tokens": accepted, "mtp_verifications": verifications,
+                "qsa_queries": counters["sparse_queries"], "qsa_selected_keys": counters["sparse_keys"],
+                "qsa_dense_keys": counters["dense_keys"],
                 "input_tokens": len(part.tokens), "output_tokens": len(generated),
                 "prefill_seconds": prefill_end - start, "decode_seconds": end - prefill_end,
                 "decode_tokens_per_second": count / max(end - prefill_end, 1e-9),
@@ -509,7 +552,7 @@ def execute(arguments, stdin, stdout, stderr):
         "physical_footprint_bytes": _proc_status("VmRSS"), "peak_physical_footprint_bytes": _proc_status("VmHWM"),
         "resident_bytes": _proc_status("VmRSS"),
         "metal_allocated_bytes": stats["device_bytes"], "peak_metal_allocated_bytes": stats["device_bytes"],
-        "gpu_weight_bytes": stats["weight_bytes"], "auxiliary_weight_bytes": 0,
+        "gpu_weight_bytes": stats["weight_bytes"], "auxiliary_weight_bytes": stats["auxiliary_bytes"],
         "context": context, "segment_tokens": o.segment_tokens, "batch4": o.batch4, "runs": runs}
     stderr.write(json.dumps(metrics, sort_keys=True, separators=(",", ":")) + "\n")
     if batch is not None:

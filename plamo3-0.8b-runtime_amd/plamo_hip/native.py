@@ -24,7 +24,8 @@ class Stats(ctypes.Structure):
                 ("linear_bytes", ctypes.c_int64), ("context", ctypes.c_int32),
                 ("packed", ctypes.c_int32), ("last_output_rows", ctypes.c_int32),
                 ("local_capacity", ctypes.c_int32), ("last_prefill_seconds", ctypes.c_double),
-                ("last_decode_seconds", ctypes.c_double)]
+                ("last_decode_seconds", ctypes.c_double), ("auxiliary_bytes", ctypes.c_int64),
+                ("sparse_queries", ctypes.c_int64), ("sparse_keys", ctypes.c_int64), ("dense_keys", ctypes.c_int64)]
 
 
 class PackReport(ctypes.Structure):
@@ -40,6 +41,14 @@ FINISH_FN = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_void_p, ctypes.c_int32, c_i3
 _SIGNATURES = {
     "plamo_open": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_char_p,
                                   ctypes.POINTER(ctypes.c_void_p), ctypes.c_char_p, ctypes.c_size_t]),
+    "plamo_open_aux": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_char_p,
+                                      ctypes.c_int32, ctypes.c_int32, ctypes.POINTER(ctypes.c_void_p), ctypes.c_char_p,
+                                      ctypes.c_size_t]),
+    "plamo_forward_ex": (ctypes.c_int, [ctypes.c_void_p, c_i32p, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
+                                        ctypes.c_int32, c_i32p, ctypes.c_char_p, ctypes.c_size_t]),
+    "plamo_draft": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, c_i32p, ctypes.c_char_p, ctypes.c_size_t]),
+    "plamo_rewind": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_char_p,
+                                    ctypes.c_size_t]),
     "plamo_close": (None, [ctypes.c_void_p]),
     "plamo_reset": (None, [ctypes.c_void_p]),
     "plamo_forward": (ctypes.c_int, [ctypes.c_void_p, c_i32p, ctypes.c_int32, ctypes.c_int32, c_i32p,
@@ -90,6 +99,8 @@ _SIGNATURES = {
     "plamo_pack_tensor": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64,
                                          ctypes.c_void_p, ctypes.POINTER(ctypes.c_int64), ctypes.c_char_p,
                                          ctypes.c_size_t]),
+    "plamo_check_aux": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_int32, ctypes.c_int32,
+                                       ctypes.c_char_p, ctypes.c_size_t]),
     "plamo_check_weights": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(ctypes.c_int64),
                                            ctypes.c_int32, ctypes.c_char_p, ctypes.c_size_t]),
     "plamo_check_packed": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p,
@@ -222,6 +233,12 @@ def call(fn, *args):
     rc = fn(*args, err, 512)
     if rc != 0:
         raise PlamoError(rc, err.value.decode(errors="replace"))
+
+
+def check_aux(path, teacher_sha256=None, mtp=True, qsa=True):
+    """Auxiliary.init and its tensor checks (Auxiliary.swift:14-62) without a device."""
+    call(load().plamo_check_aux, str(path).encode(), teacher_sha256.encode() if teacher_sha256 else None,
+         1 if mtp else 0, 1 if qsa else 0)
 
 
 def i32(values):

@@ -112,6 +112,46 @@ def write_model(directory, seed=0, std=0.02):
     return sha
 
 
+def aux_plan():
+    """[(name, shape, kind)] of auxiliary.safetensors (Auxiliary.swift:72-111): the QSA indexers
+    of the two global layers and the MTP head."""
+    plan = []
+    for layer in (7, 15):
+        p = f"qsa.{layer}."
+        plan += [(p + "proj.weight", (640, HIDDEN), "random"), (p + "q_norm.weight", (HEAD_DIM,), 0.0),
+                 (p + "k_norm.weight", (HEAD_DIM,), 0.0)]
+    plan += [("mtp.heads.0.up.weight", (256, 2 * HIDDEN), "random"),
+             ("mtp.heads.0.down.weight", (HIDDEN, 256), "random")]
+    return plan
+
+
+def write_auxiliary(directory, teacher_sha256, seed=100, std=0.02):
+    """Random-init adapters in the plamo-aux-v1 layout the loader checks (Auxiliary.swift:29-40;
+    header padded to 64 bytes as scripts/auxiliary.py:12-31 writes it), trained against the
+    model whose safetensors SHA-256 is `teacher_sha256`."""
+    plan = aux_plan()
+    header, offset = {}, 0
+    for name, shape, _ in plan:
+        size = int(np.prod(shape)) * 2
+        header[name] = {"dtype": "BF16", "shape": list(shape), "data_offsets": [offset, offset + size]}
+        offset += size
+    header["__metadata__"] = {"format": "plamo-aux-v1", "teacher_sha256": teacher_sha256, "rank": "256",
+                              "qsa_steps": "1", "mtp_steps": "1"}
+    blob = json.dumps(header, separators=(",", ":")).encode()
+    blob += b" " * ((-(8 + len(blob))) % 64)
+    rng = np.random.default_rng(seed)
+    path = os.path.join(directory, "auxiliary.safetensors")
+    with open(path + ".part", "wb") as f:
+        f.write(struct.pack("<Q", len(blob)) + blob)
+        for name, shape, kind in plan:
+            n = int(np.prod(shape))
+            a = (rng.standard_normal(n, dtype=np.float32) * np.float32(std)) if kind == "random" else \
+                np.full(n, kind, dtype=np.float32)
+            f.write(_bf16(a).tobytes())
+    os.replace(path + ".part", path)
+    return path
+
+
 def ensure_model(directory=None, seed=0, packed=True):
     """Create (once) and return a synthetic model directory with model.p12 packed by the
     native packer.  Directory defaults to $PLAMO_MODEL_DIR or <tmp>/plamo_synth_seed<seed>."""
@@ -122,6 +162,8 @@ def ensure_model(directory=None, seed=0, packed=True):
     if not os.path.exists(sha_path) or not os.path.exists(os.path.join(directory, "config-mlx.json")):
         write_model(directory, seed)
     sha = open(sha_path).read().strip()
+    if not os.path.exists(os.path.join(directory, "auxiliary.safetensors")):
+        write_auxiliary(directory, sha)
     if packed and not os.path.exists(os.path.join(directory, "model.p12")):
         from . import native
         native.pack(os.path.join(directory, "model.safetensors"), os.path.join(directory, "model.p12"), sha)

@@ -144,3 +144,22 @@ def test_command_in_a_fresh_process(model):
                          capture_output=True, env=env, timeout=110)
     assert bad.returncode == 1 and bad.stdout == b""
     assert bad.stderr.decode() == "error: Repetition penalty must be a positive finite number\n"
+
+
+def test_mtp_output_is_the_greedy_sequence(model, model_dir, monkeypatch):
+    # --mtp drafts with the adapter and keeps only what a sequential verification pass
+    # predicts (Main.swift:254-276), so the output ids are greedy decoding's; the counters
+    # follow the loop (every verification proposes at most one draft)
+    monkeypatch.setenv("PLAMO_SOURCE_SHA256", model_dir[1])
+    out, m = run(model, ["--max-tokens", "12"], TEXT)
+    out_mtp, mm = run(model, ["--max-tokens", "12", "--mtp"], TEXT)
+    r, rm = m["runs"][0], mm["runs"][0]
+    assert rm["output_ids"] == r["output_ids"] and out_mtp == out
+    assert mm["mtp"] is True and mm["auxiliary_weight_bytes"] == 2 * (256 * 3072 + 1536 * 256)
+    assert rm["mtp_verifications"] >= 1 and 0 <= rm["mtp_accepted_tokens"] <= rm["mtp_proposed_tokens"]
+    assert rm["mtp_proposed_tokens"] <= rm["mtp_verifications"]
+    # each verification keeps its first candidate plus the accepted drafts; a last single
+    # token goes out without one
+    assert len(rm["output_ids"]) - (rm["mtp_verifications"] + rm["mtp_accepted_tokens"]) in (0, 1)
+    streamed, _ = run(model, ["--max-tokens", "12", "--mtp", "--stream"], TEXT)
+    assert streamed + "\n" == out
