@@ -305,6 +305,15 @@ int plamo_kernel_argmax(uint64_t x, uint64_t out, int32_t n, int32_t rows, int32
 int plamo_kernel_select(uint64_t logits, int32_t n, uint64_t history, int32_t hist, float penalty,
                         int32_t ngram, float frequency, float presence, uint64_t out, uint64_t stream);
 
+/* `qsa_select` (Kernels.metal:618-682, QSATests.swift:6-46): for query rows t = 0 .. tokens-1 at
+ * positions start + t, the min(complete, budget / 4) blocks of largest max(score, 0) among the
+ * complete = (start + t + 1) / 4 blocks, ties to the lower index (every block when the budget
+ * covers them).  scores: FP32 [tokens][blocks]; out: uint32 [tokens][(blocks + 31) / 32], bit
+ * b of word b / 32 set for a chosen block (the reference lists the chosen keys instead; the
+ * keys of the unfinished block are always attended).  blocks <= 8192. */
+int plamo_kernel_qsa_select(uint64_t scores, int32_t blocks, int32_t tokens, int32_t start, int32_t budget,
+                            uint64_t out, uint64_t stream);
+
 /* MFMA BF16 GEMM of the prefill path: Y[t][m] = sum_k X[t][k] W[m][k] with X BF16
  * [tokens][n] and W plain BF16 or .p12 ([m][n]).  out_mode 0: Y FP32 BF16-rounded
  * (`matrix` full == 0); 1: Y BF16 bits (full == 2); 2: Y raw FP32 (full == 1,

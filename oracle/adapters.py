@@ -15,6 +15,26 @@ MTP draft after token `first`, from the first output row's normalised hidden sta
 Pinned by: bit equality with the GPU draft (tests/test_gpu_adapters.py), and agreement with
 `textbook_draft` (FP64 sums, exact exp) within the rounding of its BF16 steps
 (tests/test_oracle_adapters.py).
+
+QSA indexers (Runtime.swift:378-418, Kernels.metal:564-702), QsaTwin, on each global layer:
+  p    = roundbf(P xn)           the indexer projection [640] of the pre-attention normed row
+                                 (decode: the GEMV order; prefill: the MFMA GEMM order)
+  q_h  = rope(norm(p[128h:128h+128], q_norm), pos)   h = 0..3, global RoPE
+  raw[pos] = p[512:640]
+  block b (complete once 4b + 3 is written): mean_d = roundbf((((k0 + k1) + k2) + k3) / 4)
+         over raw[4b..4b+3], pooled[b] = rope(norm(mean, k_norm), 4b)
+  norm(v, w): lane l of a wave holds (v_l, v_l+64), ss = butterfly(v_l^2 + v_l+64^2),
+         r = 1 / sqrt(ss / 128 + 1e-6), z = roundbf(roundbf(v r) roundbf(w + 1))
+  score(b) = (sum over h in order of max(0, q_h . pooled[b])) / sqrt(128), each dot product
+         one v_dot2 chain over the 64 dimension pairs in order
+  selection: with C = (pos + 1) / 4 complete blocks and k = min(C, budget / 4), every block
+         if k == C, else the k largest max(score, 0), ties to the lower index (a sort here;
+         a radix search on the device)
+  attention then sees the selected blocks and the keys of the unfinished block.
+
+Pinned by: the reference's selection known-answer test (QSATests.swift:6-46) restated over
+`select`, a textbook FP64 indexer (`textbook_scores`) within BF16 rounding, and bit equality of
+decode and prefill with the GPU (tests/test_gpu_qsa.py).
 """
 import os
 
@@ -80,3 +100,123 @@ def textbook_draft(embed_bits, head, adapters, hidden, first):
     y = bf_np(bits_np((bf_np(adapters.mtp_down).astype(np.float64) @ a).astype(F))).astype(np.float64)
     z = bf_np(bits_np((x[:1536] + y).astype(F))).astype(np.float64)
     return np.asarray(head, np.float64) @ z
+
+
+QSA_SCALE = F(0.08838834764831845)
+
+
+def qsa_norm_rope(v, w_bits, c, s):
+    """The indexer's head RMSNorm (gain w + 1) and global RoPE with table rows c, s."""
+    v = np.asarray(v, F)
+    a, b = v[:64], v[64:]
+    ss = exact.butterfly(((a * a) + (b * b)).astype(F)[None])[0]
+    r = F(1) / np.sqrt(F(ss / F(128)) + exact.EPS)
+    z = roundbf_np(roundbf_np(v * r) * exact.gain(w_bits, 1.0))
+    return exact.rope_pair(z, c, s)
+
+
+def select(scores, complete, budget):
+    """Blocks chosen among `complete` (bool [complete]): the budget/4 largest max(score, 0),
+    ties to the lower index; all of them when the budget covers them."""
+    k = min(complete, budget // 4)
+    chosen = np.zeros(complete, bool)
+    if k == complete:
+        chosen[:] = True
+        return chosen
+    s = np.asarray(scores[:complete], F)
+    val = np.where(s > 0, s, F(0)).astype(F).view(np.uint32).astype(np.int64)
+    order = np.lexsort((np.arange(complete), -val))
+    chosen[order[:k]] = True
+    return chosen
+
+
+class QsaTwin:
+    """Indexer state of the global layers (raw and pooled keys) and the order-exact selection.
+    Attach to exact.ExactDecoder(qsa=...); the prefill twin uses the decoder's."""
+
+    def __init__(self, adapters, context, budget):
+        self.budget = budget
+        self.blocks = context // 4
+        self.words = (self.blocks + 31) // 32
+        self.a = adapters
+        self.proj = {l: bf_np(adapters.qsa[l]["proj"]).astype(F) for l in adapters.qsa}
+        self.raw = {l: np.zeros((context, 128), np.uint16) for l in adapters.qsa}
+        self.pooled = {l: np.zeros((max(self.blocks, 1), 128), np.uint16) for l in adapters.qsa}
+        self.last_scores = {}
+
+    def _rows(self, ex, layer, proj, p0):
+        """proj [T][640] BF16-valued rows of positions p0 .. p0+T-1 -> uint32 masks [T][words]
+        (bit b of word b / 32: block b selected)."""
+        A = self.a.qsa[layer]
+        qn, kn = np.asarray(A["q_norm"], np.uint16), np.asarray(A["k_norm"], np.uint16)
+        T = proj.shape[0]
+        raw, pooled = self.raw[layer], self.pooled[layer]
+        queries = np.empty((T, 4, 128), np.uint16)
+        for t in range(T):
+            pos = p0 + t
+            for h in range(4):
+                queries[t, h] = bits_np(qsa_norm_rope(proj[t, 128 * h:128 * h + 128], qn, ex.gc[pos], ex.gs[pos]))
+            raw[pos] = bits_np(proj[t, 512:640])
+        for b in range(p0 // 4, (p0 + T) // 4):
+            k = bf_np(raw[4 * b:4 * b + 4]).astype(F)
+            mean = roundbf_np(((((k[0] + k[1]) + k[2]) + k[3]) / F(4)).astype(F))
+            pooled[b] = bits_np(qsa_norm_rope(mean, kn, ex.gc[4 * b], ex.gs[4 * b]))
+        masks = np.zeros((T, max(self.words, 1)), np.uint32)
+        self.last_scores[layer] = []
+        for t in range(T):
+            complete = (p0 + t + 1) // 4
+            if complete == 0:
+                self.last_scores[layer].append(np.zeros(0, F))
+                continue
+            kp = _pairs(pooled[:complete])                                   # [C][64]
+            score = np.zeros(complete, F)
+            for h in range(4):
+                qp = _pairs(queries[t, h])                                   # [64]
+                a = np.ascontiguousarray(np.broadcast_to(qp[:, None], (64, complete)))
+                acc = exact.dot2_chain(a, np.ascontiguousarray(kp.T), np.zeros(complete, F))[-1]
+                score = (score + np.maximum(acc, F(0))).astype(F)
+            score = (score * QSA_SCALE).astype(F)
+            self.last_scores[layer].append(score)
+            chosen = np.flatnonzero(select(score, complete, self.budget))
+            np.bitwise_or.at(masks[t], chosen >> 5, (np.uint32(1) << (chosen & 31).astype(np.uint32)))
+        return masks
+
+    def decode_mask(self, ex, layer, xn, pos):
+        """One decode step: bool [complete blocks] for exact.ExactDecoder.attention."""
+        p = roundbf_np(exact.gemv(self.proj[layer], xn))
+        m = self._rows(ex, layer, p[None], pos)[0]
+        complete = (pos + 1) // 4
+        return ((m[np.arange(complete) >> 5] >> (np.arange(complete) & 31).astype(np.uint32)) & 1).astype(bool)
+
+    def prefill_masks(self, ex, layer, xn, p0):
+        """A prefill chunk's rows xn [T][1536] -> masks [T][words] for exact_prefill.flash."""
+        from .exact_prefill import mfma_gemm
+        p = roundbf_np(mfma_gemm(bits_np(self.proj[layer]), bits_np(xn)))
+        return self._rows(ex, layer, p, p0)
+
+
+def textbook_scores(adapters, layer, gcos, gsin, rows, relu=True, gain_offset=1.0, k_rope_shift=0):
+    """FP64 indexer scores of every query row against the blocks complete at its position,
+    from the projected rows of positions 0 .. T-1 (BF16-valued [T][640]): the same formula with
+    exact sums and square roots.  relu, gain_offset and k_rope_shift (block keys rotated at
+    4b + shift) exist to plant mistakes that a check against this function must catch."""
+    A = adapters.qsa[layer]
+    gq = bf_np(np.asarray(A["q_norm"], np.uint16)).astype(np.float64) + gain_offset
+    gk = bf_np(np.asarray(A["k_norm"], np.uint16)).astype(np.float64) + gain_offset
+
+    def nr(v, g, c, s):
+        v = np.asarray(v, np.float64)
+        z = v / np.sqrt(np.mean(v * v) + 1e-6) * g
+        c, s = np.asarray(c, np.float64), np.asarray(s, np.float64)
+        return np.concatenate([z[:64] * c - z[64:] * s, z[64:] * c + z[:64] * s])
+
+    rows = np.asarray(rows, np.float64)
+    blocks = len(rows) // 4
+    pk = [nr(rows[4 * b:4 * b + 4, 512:].mean(0), gk, gcos[4 * b + k_rope_shift], gsin[4 * b + k_rope_shift])
+          for b in range(blocks)]
+    out = []
+    for pos in range(len(rows)):
+        qs = [nr(rows[pos, 128 * h:128 * h + 128], gq, gcos[pos], gsin[pos]) for h in range(4)]
+        act = (lambda v: max(0.0, v)) if relu else (lambda v: v)
+        out.append(np.array([sum(act(float(q @ k)) for q in qs) / np.sqrt(128) for k in pk[:(pos + 1) // 4]]))
+    return out

@@ -18,7 +18,8 @@
  *     o_d   = o_d * alpha, then for each 16-key step s the MFMA chain over the products
  *             v_kd * hi_k (keys 16s + {0-3, 8-11}, then {4-7, 12-15}) and v_kd * lo_k (same
  *             two groups), hi = bf16(e), lo = bf16(e - hi);
- *   l = l_0 + l_1.  One part: out = bf16(o / l).  Several: M = max of the parts' m in part
+ *   l = l_0 + l_1.  One part: out = bf16(o / l).  With a QSA mask, keys of unselected complete
+ *   blocks of four are invisible like masked ones.  Several: M = max of the parts' m in part
  *   order, w = exp2_det(m_q - M), l = sum l_q * w and o = sum o_q * w in part order (every
  *   product and sum rounded), out = bf16(o / l).
  * Compiled with -ffp-contract=off. */
@@ -68,8 +69,16 @@ typedef struct {
 } part_state;
 
 /* One query (token position qpos, head vector q) over tiles j0 .. j1 of its block. */
+/* QSA: key kp is seen when its block is the query's unfinished one or selected in `mask`
+ * (bit b of word b / 32); null mask: every key. */
+static inline int qsa_seen(const uint32_t* mask, uint32_t qpos, uint32_t kp) {
+    if (!mask) return 1;
+    const uint32_t b = kp >> 2;
+    return b >= (qpos + 1) / 4 || ((mask[b >> 5] >> (b & 31)) & 1u);
+}
+
 static void flash_part(const bfdec* qd, const bfdec* kd, const uint16_t* vt, uint32_t klo, uint32_t qpos, int full,
-                       int j0, int j1, part_state* st) {
+                       const uint32_t* mask, int j0, int j1, part_state* st) {
     const float sc = 0.08838834764831845f * 1.4426950408889634f;
     float m = -INFINITY, ls[2] = {0.0f, 0.0f};
     float* o = st->o;
@@ -82,7 +91,7 @@ static void flash_part(const bfdec* qd, const bfdec* kd, const uint16_t* vt, uin
         float mt = -INFINITY;
         for (int c = 0; c < FK; ++c) {
             const uint32_t kp = k0 + (uint32_t)c;
-            const int vis = kp <= qpos && (full || kp + (uint32_t)(WINDOW - 1) >= qpos);
+            const int vis = kp <= qpos && (full || kp + (uint32_t)(WINDOW - 1) >= qpos) && qsa_seen(mask, qpos, kp);
             const float s = mfma_dot(kt + (size_t)c * HD, qd, HD, 0.0f);
             x[c] = vis ? s * sc : -INFINITY;
             mt = fmaxf(mt, x[c]);
@@ -129,7 +138,7 @@ static void flash_part(const bfdec* qd, const bfdec* kd, const uint16_t* vt, uin
  * RoPE table [rows][64] (local layers only); out: [tokens][2048].  All BF16 bits. */
 void plamo_oracle_flash(const uint16_t* q, const uint16_t* keys, const uint16_t* values, const uint16_t* lcos,
                         const uint16_t* lsin, int64_t capacity, int64_t p0, int64_t tokens, int32_t full,
-                        uint16_t* out) {
+                        uint16_t* out, const uint32_t* qsa_mask, int64_t qsa_words) {
     const int nqb = (int)((tokens + FT - 1) / FT);
     for (int qb = 0; qb < nqb; ++qb) {
         const int t0 = qb * FT;
@@ -174,8 +183,9 @@ void plamo_oracle_flash(const uint16_t* q, const uint16_t* keys, const uint16_t*
             bfdec qd[HD];
             for (int d = 0; d < HD; ++d) qd[d] = bf_decode(q[((size_t)t * HEADS + h) * HD + d]);
             part_state ps[PARTS];
+            const uint32_t* mask = qsa_mask ? qsa_mask + (size_t)t * (size_t)qsa_words : 0;
             for (int pt = 0; pt < parts; ++pt)
-                flash_part(qd, kd, vt, klo, qpos, full, pt * ntiles / parts, (pt + 1) * ntiles / parts, &ps[pt]);
+                flash_part(qd, kd, vt, klo, qpos, full, mask, pt * ntiles / parts, (pt + 1) * ntiles / parts, &ps[pt]);
             float o[HD], l;
             if (parts == 1) {
                 l = ps[0].l;

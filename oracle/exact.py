@@ -194,7 +194,9 @@ def rope_pair(z, c, s):
 class ExactDecoder:
     """Bit-exact CPU twin of the decode step (one sequence)."""
 
-    def __init__(self, weights, context, local_capacity):
+    def __init__(self, weights, context, local_capacity, qsa=None):
+        # qsa: the QSA indexers of the global layers (oracle.adapters.QsaTwin), None: dense
+        self.qsa = qsa
         self.w = weights
         self.context = context
         self.cap = [context if i % 8 == 7 else local_capacity for i in range(16)]
@@ -212,7 +214,9 @@ class ExactDecoder:
     def _bits(self, t):
         return np.asarray(t, dtype=np.int64).astype(np.uint16)
 
-    def attention(self, layer, qkv, pos):
+    def attention(self, layer, qkv, pos, mask=None):
+        """mask (global layers with QSA): bool per complete block of four keys, the selected
+        ones; keys of the unfinished block are always seen."""
         full = layer % 8 == 7
         cap = self.cap[layer]
         L = self.layers[layer]
@@ -239,6 +243,10 @@ class ExactDecoder:
         pm = np.zeros((parts, 16), F)
         pl = np.zeros((parts, 16), F)
         po = np.zeros((parts, 16, 128), F)
+        if mask is not None and len(mask) > 0:
+            seen = (r // 4 >= len(mask)) | np.asarray(mask, bool)[np.minimum(r // 4, len(mask) - 1)]
+        else:
+            mask = None
         for p in range(parts):
             k0 = p * KP
             kk = keys[k0:k0 + KP]
@@ -246,9 +254,12 @@ class ExactDecoder:
             sc = (scores[:, k0:k0 + nk] * SCALE).astype(F)
             full_sc = np.full((16, 64), -np.inf, F)
             full_sc[:, :nk] = sc
+            if mask is not None:
+                full_sc[:, :nk][:, ~seen[k0:k0 + nk]] = -np.inf
             m = full_sc.max(1)
             e = np.zeros((16, 64), F)
-            e[:, :nk] = exp_det(sc - m[:, None])
+            with np.errstate(invalid="ignore"):
+                e[:, :nk] = np.where(np.isfinite(full_sc[:, :nk]), exp_det(full_sc[:, :nk] - m[:, None]), F(0))
             pm[p], pl[p] = m, butterfly(e)
             po[p] = attn_pv(e, vbits[k0:k0 + KP])
         # merge: M = max m_p; w_p = exp(m_p - M); num = sum o_p w_p, den = sum l_p w_p as
@@ -282,7 +293,8 @@ class ExactDecoder:
                 x = roundbf_np(x + z)
                 xn = norm_rows(x, self._bits(L["pre"]), 1.0)
             qkv = roundbf_np(gemv(L["qkv"], xn))
-            att = self.attention(i, qkv, pos)
+            mask = self.qsa.decode_mask(self, i, xn, pos) if (self.qsa is not None and i % 8 == 7) else None
+            att = self.attention(i, qkv, pos, mask)
             o = roundbf_np(gemv(L["o"], att))
             z = norm_rows(o, self._bits(L["post"]), 0.2)
             x = roundbf_np(x + z)

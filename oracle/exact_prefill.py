@@ -40,7 +40,8 @@ POST_MLP = F(1 / 5.0 ** 1.5)
 _SIGS = {
     "plamo_oracle_mfma_gemm": (None, [ctypes.c_void_p] * 3 + [ctypes.c_int64] * 3),
     "plamo_oracle_mfma_chain": (ctypes.c_float, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_float]),
-    "plamo_oracle_flash": (None, [ctypes.c_void_p] * 5 + [ctypes.c_int64] * 3 + [ctypes.c_int32, ctypes.c_void_p]),
+    "plamo_oracle_flash": (None, [ctypes.c_void_p] * 5 + [ctypes.c_int64] * 3 + [ctypes.c_int32, ctypes.c_void_p,
+                                                                                  ctypes.c_void_p, ctypes.c_int64]),
     "plamo_oracle_exp2_det": (ctypes.c_float, [ctypes.c_float]),
 }
 
@@ -82,16 +83,19 @@ def exp2_det(x):
     return np.array([c.plamo_oracle_exp2_det(float(v)) for v in np.ravel(x)], F).reshape(np.shape(x))
 
 
-def flash(q_bits, keys, values, lcos_bits, lsin_bits, capacity, p0, full):
+def flash(q_bits, keys, values, lcos_bits, lsin_bits, capacity, p0, full, qsa_mask=None):
     """q [tokens][16][128], keys/values [capacity][128], local table [rows][64] (BF16 bits)
-    -> attention output BF16 bits [tokens][2048]."""
+    -> attention output BF16 bits [tokens][2048].  qsa_mask: uint32 [tokens][words] selected
+    blocks of four keys per query (global layers), None: every key."""
     q = _u16(q_bits)
     tokens = q.shape[0]
     k, v = _u16(keys), _u16(values)
     lc, ls = _u16(lcos_bits), _u16(lsin_bits)
     out = np.empty((tokens, 2048), np.uint16)
+    m = None if qsa_mask is None else np.ascontiguousarray(qsa_mask, dtype=np.uint32)
     lib().plamo_oracle_flash(q.ctypes.data, k.ctypes.data, v.ctypes.data, lc.ctypes.data, ls.ctypes.data, capacity,
-                             p0, tokens, 1 if full else 0, out.ctypes.data)
+                             p0, tokens, 1 if full else 0, out.ctypes.data, None if m is None else m.ctypes.data,
+                             0 if m is None else m.shape[1])
     return out
 
 
@@ -182,7 +186,8 @@ class ExactPrefill:
             q16 = self._qk_prep(i, qkv, p0)
             if kv_layers is not None and i + 1 >= kv_layers:
                 return None
-            att = flash(q16, ex.keys[i], ex.values[i], self.lcb, self.lsb, ex.cap[i], p0, full)
+            mask = ex.qsa.prefill_masks(ex, i, xn, p0) if (ex.qsa is not None and full) else None
+            att = flash(q16, ex.keys[i], ex.values[i], self.lcb, self.lsb, ex.cap[i], p0, full, mask)
             o = roundbf_np(mfma_gemm(self.wb[i]["o"], att))
             z = rows_norm(o, self._bits(L["post"]), POST_MIXER)
             x = roundbf_np(x + z)

@@ -164,7 +164,6 @@ int plamo_open_aux(const char* directory, int32_t context, int32_t packed, const
         if (qsa_budget != 0 && (qsa_budget < 4 || qsa_budget > 2048 || qsa_budget % 4 != 0))
             throw plamo::Error(plamo::E_INVAL, "QSA budget must be a multiple of four in 4...2048");
         const bool indexers = qsa_budget > 0 && context > qsa_budget;  // Runtime.swift:248
-        if (indexers) throw plamo::Error(plamo::E_INVAL, "QSA indexers are not built yet");
         std::unique_ptr<plamo::AuxArchive> ar;
         if (qsa_budget > 0 || mtp) {
             ar = std::make_unique<plamo::AuxArchive>(std::string(directory) + "/auxiliary.safetensors", sha ? sha : "");
@@ -180,6 +179,7 @@ int plamo_open_aux(const char* directory, int32_t context, int32_t packed, const
         r.model = plamo::load_model(directory, context, packed != 0, sha ? sha : "", r.stream);
         r.eng = std::make_unique<plamo::Engine>(r.model, context, 1, r.stream);
         if (ar) r.aux = plamo::load_aux(*ar, mtp != 0, indexers);  // indexers after the layers
+        if (indexers) r.eng->enable_qsa(r.aux.get(), qsa_budget);
         r.mtp = mtp != 0;
         r.qsa_budget = qsa_budget;
         *out = rt.release();
@@ -613,6 +613,28 @@ int plamo_kernel_select(uint64_t logits, int32_t n, uint64_t history, int32_t hi
         plamo::launch_select(reinterpret_cast<float*>(logits), n, reinterpret_cast<const int32_t*>(history), hist,
                              penalty, ngram, frequency, presence, reinterpret_cast<int32_t*>(out),
                              reinterpret_cast<hipStream_t>(stream));
+        PLAMO_HIP(hipGetLastError());
+    });
+}
+
+int plamo_kernel_qsa_select(uint64_t scores, int32_t blocks, int32_t tokens, int32_t start, int32_t budget,
+                            uint64_t out, uint64_t stream) {
+    return guard(nullptr, 0, [&] {
+        if (blocks < 1 || blocks > plamo::MAX_CONTEXT / 4 || tokens < 1 || start < 0 || budget < 0)
+            throw plamo::Error(plamo::E_INVAL, "bad QSA select shape");
+        // every row's complete blocks must lie inside its score row
+        if (int64_t(start) + tokens > 4 * int64_t(blocks) + 3)
+            throw plamo::Error(plamo::E_INVAL, "QSA select: positions past the score rows");
+        if (!scores || !out) throw plamo::Error(plamo::E_INVAL, "null QSA select operand");
+        plamo::QsaParams p{};
+        p.p0 = uint32_t(start);
+        p.tokens = tokens;
+        p.scores = reinterpret_cast<float*>(scores);
+        p.mask = reinterpret_cast<uint32_t*>(out);
+        p.blocks = uint32_t(blocks);
+        p.words = uint32_t((blocks + 31) / 32);
+        p.budget = budget;
+        plamo::launch_qsa_select(p, reinterpret_cast<hipStream_t>(stream));
         PLAMO_HIP(hipGetLastError());
     });
 }

@@ -1111,7 +1111,13 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
                 sc[c] = dot2bf(qd.w, kd.w, sc[c]);
             }
         }
-        const bool valid = k0 + j < count;
+        bool valid = k0 + j < count;
+        if (FULL && p.qsa_mask) {
+            // QSA: key k = position k; the blocks of four keys complete at this position must be
+            // selected, the unfinished block is always seen (Kernels.metal:618-700)
+            const uint32_t b = (k0 + uint32_t(j)) >> 2;
+            valid = valid && (b >= (pos + 1) / 4 || ((p.qsa_mask[size_t(q) * p.qsa_words + (b >> 5)] >> (b & 31)) & 1u));
+        }
         const float dot = (sc[0] + sc[1]) + (sc[2] + sc[3]);
         const float s = valid ? dot * SCALE : NEG_INF;
         const float m = wave_max(s);
@@ -1758,6 +1764,7 @@ void gemv_dispatch_epi(Prologue pro, Epilogue epi, const GemvParams& p, int bloc
     if constexpr (N == HIDDEN) {
         if (pro == PRO_EMBED && epi == EPI_ROUND) PLAMO_GEMV(PRO_EMBED, EPI_ROUND);
         else if (pro == PRO_RESID16 && epi == EPI_ROUND) PLAMO_GEMV(PRO_RESID16, EPI_ROUND);
+        else if (pro == PRO_RESID16 && epi == EPI_BF16) PLAMO_GEMV(PRO_RESID16, EPI_BF16);  // QSA indexer
         else if (pro == PRO_RESID16 && epi == EPI_SWIGLU) PLAMO_GEMV(PRO_RESID16, EPI_SWIGLU);
         else if (pro == PRO_RESID16 && epi == EPI_LOGITS) PLAMO_GEMV(PRO_RESID16, EPI_LOGITS);
         else if (pro == PRO_RESID && epi == EPI_LOGITS) PLAMO_GEMV(PRO_RESID, EPI_LOGITS);

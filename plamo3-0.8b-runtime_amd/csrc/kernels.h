@@ -122,7 +122,33 @@ struct AttnParams {
     uint32_t window;          // local layers: WINDOW (the keys a row sees), global layers: 0 (all)
     uint32_t merge_in_o;      // rows with 2..MERGE_IN_O partitions are merged by the next
                               // kernel (the o GEMV's PRO_MERGE prologue): no ticket, no merge
+    const uint32_t* qsa_mask; // global layers with QSA: row q's selected blocks of four keys
+                              // (bit b of word q * qsa_words + b / 32); keys of the unfinished
+                              // block are always seen; null: every key
+    uint32_t qsa_words;
 };
+
+// QSA block indexer of a global layer for `tokens` rows (qsa.hip).
+struct QsaParams {
+    const StepState* state;   // decode: one row at state->pos[0]; null: rows at p0 + t
+    uint32_t p0;
+    int tokens;
+    const uint16_t* proj;     // [tokens][640] BF16 indexer projection of the normed rows
+    const uint16_t* q_norm;   // [128]
+    const uint16_t* k_norm;
+    const uint32_t* global_rope;  // [context][64]
+    uint16_t* queries;        // [tokens][512] BF16 rotated indexer queries
+    uint16_t* raw;            // [context][128] raw keys by position
+    uint16_t* pooled;         // [context / 4][128] block keys
+    float* scores;            // [tokens][blocks]
+    uint32_t* mask;           // [tokens][words] selected blocks
+    uint32_t blocks, words;   // context / 4, its 32-bit words
+    int budget;               // keys a query may select (multiple of four)
+};
+// qsa_prep, qsa_pool, qsa_scores (max_blocks: blocks the widest row may score), qsa_select.
+void launch_qsa(const QsaParams& p, int max_blocks, hipStream_t s);
+// The selection alone, on scores the caller supplies (p.scores, p.blocks, p.mask, p.words).
+void launch_qsa_select(const QsaParams& p, hipStream_t s);
 // Partitions a row may have before its merge moves to attn_merge_kernel: past 8 partitions
 // (positions from 512 on) its 64 workgroups per row merge faster than the last workgroup of
 // each head group (long-context decode 1515 -> 1554 tok/s, batch 4 5848 -> 6077 tok/s).

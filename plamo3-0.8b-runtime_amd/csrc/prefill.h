@@ -71,6 +71,9 @@ struct FlashParams {
     float* part_o;             // flash_part_o_floats(tokens)
     float* part_ml;            // flash_part_ml_floats(tokens)
     uint32_t* tickets;         // flash_blocks(tokens), zero between launches
+    const uint32_t* qsa_mask;  // global layers with QSA: token t's selected blocks of four keys
+                               // (bit b of word t * qsa_words + b / 32); null: every key
+    uint32_t qsa_words;
 };
 
 void launch_gemm(bool packed, GemmEpilogue epi, const GemmParams& p, hipStream_t s);

@@ -693,6 +693,9 @@ __global__ __launch_bounds__(256, 2) void flash_prefill_kernel(const FlashParams
         for (int r = 0; r < 16; ++r) oacc[dt][r] = 0.f;
     float m = NEG_INF, ls = 0.f;
 
+    const bool qsa = p.full && p.qsa_mask != nullptr;
+    const uint32_t* qmask = qsa ? p.qsa_mask + size_t(tqc) * p.qsa_words : nullptr;
+    const uint32_t qcomplete = (qpos + 1) / 4;
     const bool cached = !p.full && p.keys_rot != nullptr && base == 0 && khi < p.rot_rows;
     const KvSource src{cached ? p.keys_rot : p.keys, !p.full && !cached};
     KvStage st;
@@ -720,7 +723,9 @@ __global__ __launch_bounds__(256, 2) void flash_prefill_kernel(const FlashParams
         // Online softmax in the base-2 domain: x = score * scale * log2(e), p = 2^(x - max).
         // Element i of tile r is key k0 + 32r + 8(i/4) + 4*half + i%4.  Only tiles that cross
         // a query's causal edge or window start need the mask.
-        const bool edge = !(k0 + uint32_t(FK - 1) <= plo && (p.full || k0 + uint32_t(WINDOW - 1) >= khi));
+        // QSA: every tile is masked by the query's selected blocks (its unfinished block is
+        // always seen)
+        const bool edge = qsa || !(k0 + uint32_t(FK - 1) <= plo && (p.full || k0 + uint32_t(WINDOW - 1) >= khi));
         float mt = NEG_INF;
         if (edge) {
 #pragma unroll
@@ -728,7 +733,11 @@ __global__ __launch_bounds__(256, 2) void flash_prefill_kernel(const FlashParams
 #pragma unroll
                 for (int i = 0; i < 16; ++i) {
                     const uint32_t kp = k0 + uint32_t(32 * r + 8 * (i >> 2) + 4 * half + (i & 3));
-                    const bool vis = kp <= qpos && (p.full || kp + uint32_t(WINDOW - 1) >= qpos);
+                    bool vis = kp <= qpos && (p.full || kp + uint32_t(WINDOW - 1) >= qpos);
+                    if (qsa) {
+                        const uint32_t b = kp >> 2;
+                        vis = vis && (b >= qcomplete || ((qmask[b >> 5] >> (b & 31)) & 1u));
+                    }
                     const float x = vis ? sacc[r][i] * SCALE_LOG2E : NEG_INF;
                     sacc[r][i] = x;
                     mt = fmaxf(mt, x);

@@ -307,6 +307,42 @@ void Engine::zero_sampler() {
     PLAMO_HIP(hipMemsetAsync(bufs.counts, 0, size_t(ROWS) * VOCAB * 4, stream));
 }
 
+void Engine::enable_qsa(const Aux* aux, int budget) {
+    qsa_aux = aux;
+    qsa_budget = budget;
+    qsa_blocks = uint32_t(context / 4);
+    qsa_words = (qsa_blocks + 31) / 32;
+    qsa_proj = arena.alloc_n<uint16_t>(size_t(chunk) * QSA_PROJ);
+    qsa_q = arena.alloc_n<uint16_t>(size_t(chunk) * 4 * HEAD_DIM);
+    for (int l = 0; l < LAYERS; ++l) {
+        if (!is_global_layer(l)) continue;
+        qsa_raw[l] = arena.alloc_n<uint16_t>(size_t(context) * HEAD_DIM);
+        qsa_pooled[l] = arena.alloc_n<uint16_t>(size_t(std::max<uint32_t>(qsa_blocks, 1)) * HEAD_DIM);
+    }
+    qsa_scores = arena.alloc_n<float>(size_t(chunk) * std::max<uint32_t>(qsa_blocks, 1));
+    qsa_mask = arena.alloc_n<uint32_t>(size_t(chunk) * std::max<uint32_t>(qsa_words, 1));
+}
+
+QsaParams Engine::qsa_params(int layer, int tokens, const StepState* st, uint32_t p0) const {
+    QsaParams q{};
+    q.state = st;
+    q.p0 = p0;
+    q.tokens = tokens;
+    q.proj = qsa_proj;
+    q.q_norm = qsa_aux->qsa_q_norm[layer];
+    q.k_norm = qsa_aux->qsa_k_norm[layer];
+    q.global_rope = model->global_rope;
+    q.queries = qsa_q;
+    q.raw = qsa_raw[layer];
+    q.pooled = qsa_pooled[layer];
+    q.scores = qsa_scores;
+    q.mask = qsa_mask;
+    q.blocks = qsa_blocks;
+    q.words = qsa_words;
+    q.budget = qsa_budget;
+    return q;
+}
+
 void Engine::enqueue_head(const uint16_t* in, const uint16_t* resid_in, int in_rows) {
     const Model& m = *model;
     const int maxr = lanes == 1 ? 1 : ROWS;
@@ -385,6 +421,22 @@ void Engine::enqueue_step(bool head, bool loop) {
             g.post_offset = post_mlp_offset();
             launch_gemv(HIDDEN, pk, maxr, PRO_RESID16, EPI_ROUND, g, gemv_blocks(HIDDEN, maxr, EPI_ROUND, QKV, pk), stream);
         }
+        const bool qsa = full && qsa_aux && lanes == 1;
+        if (qsa) {
+            // the indexer projection of the same normed row (same prologue, Runtime.swift:381),
+            // then queries, raw key, block key, scores and the selection (Runtime.swift:382-403)
+            GemvParams x = g;
+            x.m = QSA_PROJ;
+            x.w = qsa_aux->qsa_proj[l];
+            x.table = nullptr;
+            x.out = nullptr;
+            x.out16 = qsa_proj;
+            x.resid16_out = resid_scratch;
+            x.tag = uint32_t(TIMELINE_TAGS);
+            launch_gemv(HIDDEN, false, 1, PRO_RESID16, EPI_BF16, x, gemv_blocks(HIDDEN, 1, EPI_BF16, QSA_PROJ, false),
+                        stream);
+            launch_qsa(qsa_params(l, 1, state, 0), int(qsa_blocks), stream);
+        }
         AttnParams a{};
         a.state = state;
         a.qkv = qkv;
@@ -410,6 +462,8 @@ void Engine::enqueue_step(bool head, bool loop) {
         // ATTN_MERGE_INLINE_BATCH in four-row batches, once that kernel is launched)
         a.defer = a.parts > ATTN_MERGE_INLINE ? (maxr > 1 ? ATTN_MERGE_INLINE_BATCH : ATTN_MERGE_INLINE) : 0u;
         a.window = full ? 0u : uint32_t(WINDOW);
+        a.qsa_mask = qsa ? qsa_mask : nullptr;
+        a.qsa_words = qsa_words;
         launch_attention(full, a, ROWS, stream);
         if (a.defer) launch_attention_merge(a, ROWS, stream);
         GemvParams o{};
@@ -607,6 +661,20 @@ void Engine::enqueue_prefill_chunk(int n, int p0, int lane, bool last_chunk, boo
         qp.local_rope = m.local_rope;
         qp.global_rope = m.global_rope;
         launch_qk_prep(qp, stream);
+        const bool qsa = full && qsa_aux && lanes == 1;
+        if (qsa) {
+            // the indexer on the chunk's normed rows: every token selects its own blocks
+            GemmParams xg{};
+            xg.w = qsa_aux->qsa_proj[l];
+            xg.x = p_xn;
+            xg.y16 = qsa_proj;
+            xg.m = QSA_PROJ;
+            xg.k = HIDDEN;
+            xg.tokens = n;
+            launch_gemm(false, GEMM_BF16, xg, stream);
+            launch_qsa(qsa_params(l, n, nullptr, uint32_t(p0)), std::min<int>(int(qsa_blocks), (p0 + n) / 4 + 1),
+                       stream);
+        }
         FlashParams fa{};
         fa.q = p_q16;
         fa.keys = qp.keys;
@@ -622,6 +690,8 @@ void Engine::enqueue_prefill_chunk(int n, int p0, int lane, bool last_chunk, boo
         fa.part_o = p_flash_o;
         fa.part_ml = p_flash_ml;
         fa.tickets = p_flash_tickets;
+        fa.qsa_mask = qsa ? qsa_mask : nullptr;
+        fa.qsa_words = qsa_words;
         launch_flash_prefill(fa, stream);
         GemmParams o{};
         o.x = p_att; o.y16 = p_proj; o.m = HIDDEN; o.k = ATTN; o.tokens = n;
@@ -751,6 +821,7 @@ int RuntimeImpl::forward(const int32_t* tokens, int n, bool output) {
     PLAMO_HIP(hipMemcpyAsync(&hs, e.state, sizeof(StepState), hipMemcpyDeviceToHost, stream));
     PLAMO_HIP(hipStreamSynchronize(stream));
     PLAMO_HIP(hipGetLastError());
+    count_qsa(position, n);
     position += n;
     last_output_rows = output ? 1 : 0;
     if (!output) return -1;
@@ -780,6 +851,8 @@ int RuntimeImpl::prefill(const int32_t* tokens, int n) {
     PLAMO_HIP(hipMemcpyAsync(&hs, e.state, sizeof(StepState), hipMemcpyDeviceToHost, stream));
     PLAMO_HIP(hipStreamSynchronize(stream));
     PLAMO_HIP(hipGetLastError());
+    for (int s0 = 0; s0 < n; s0 += std::min(context, CHUNK))  // Runtime.fill's forwards (Runtime.swift:476)
+        count_qsa(position + s0, std::min(std::min(context, CHUNK), n - s0));
     position += n;
     last_output_rows = 1;
     const int next = int32_t(hs.next[0]);
@@ -843,12 +916,26 @@ int RuntimeImpl::forward_ex(const int32_t* tokens, int n, bool output, bool all,
     PLAMO_HIP(hipMemcpyAsync(&hs, e.state, sizeof(StepState), hipMemcpyDeviceToHost, stream));
     PLAMO_HIP(hipStreamSynchronize(stream));
     PLAMO_HIP(hipGetLastError());
+    count_qsa(position, n);
     position += n;
     last_output_rows = rows;
     if (!output) return -1;
     if (rows > 1) predictions.assign(next, next + rows);
     else predictions.assign(1, int32_t(hs.next[0]));
     return predictions.back();
+}
+
+void RuntimeImpl::count_qsa(int64_t p0, int n) {
+    if (!eng->qsa_aux || p0 + n <= qsa_budget) return;  // selected = position + batch > budget
+    for (int l = 0; l < LAYERS; ++l) {
+        if (!is_global_layer(l)) continue;
+        sparse_queries += n;
+        for (int t = 0; t < n; ++t) {
+            const int64_t visible = p0 + t + 1;
+            dense_keys += visible;
+            sparse_keys += std::min<int64_t>(visible / 4, qsa_budget / 4) * 4 + visible % 4;
+        }
+    }
 }
 
 const uint16_t* RuntimeImpl::logits_row(int slot) const {
@@ -1153,6 +1240,7 @@ std::vector<int32_t> RuntimeImpl::generate(const int32_t* prompt, int n, int max
     std::vector<int32_t> out(hs.produced);
     if (hs.produced)
         PLAMO_HIP(hipMemcpy(out.data(), e.bufs.out_ids, size_t(hs.produced) * 4, hipMemcpyDeviceToHost));
+    for (int64_t p = position; p < int64_t(hs.pos[0]); ++p) count_qsa(p, 1);
     position = hs.pos[0];
     *reason = int(hs.reason);
     hs.loop = 0;

@@ -126,6 +126,18 @@ class Engine {
 
     hipEvent_t ev0, ev1;
 
+    // QSA block indexers of the global layers (Runtime.swift:380-418); null: dense attention
+    const Aux* qsa_aux = nullptr;
+    int qsa_budget = 0;
+    uint16_t *qsa_proj = nullptr, *qsa_q = nullptr;  // [chunk][640], [chunk][512] BF16
+    uint16_t* qsa_raw[LAYERS] = {};                   // global layers: [context][128] raw keys
+    uint16_t* qsa_pooled[LAYERS] = {};                // global layers: [context / 4][128] block keys
+    float* qsa_scores = nullptr;                      // [chunk][context / 4]
+    uint32_t* qsa_mask = nullptr;                     // [chunk][words] selected blocks
+    uint32_t qsa_blocks = 0, qsa_words = 0;
+    void enable_qsa(const Aux* aux, int budget);
+    QsaParams qsa_params(int layer, int tokens, const StepState* st, uint32_t p0) const;
+
     // one decode step for state->rows rows; `loop`: a device-loop step (no bookkeeping kernel,
     // the head merge prepares the next step)
     void enqueue_step(bool head = true, bool loop = false);
@@ -179,6 +191,8 @@ struct RuntimeImpl {
     bool mtp = false;
     int qsa_budget = 0;
     int64_t sparse_queries = 0, sparse_keys = 0, dense_keys = 0;  // Runtime.swift:160-162
+    // the QSA counters of one reference forward of n tokens at p0 (Runtime.swift:405-414)
+    void count_qsa(int64_t p0, int n);
 
     ~RuntimeImpl();
     void reset();

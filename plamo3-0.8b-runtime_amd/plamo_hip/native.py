@@ -109,6 +109,7 @@ _SIGNATURES = {
     "plamo_kernel_linear": (ctypes.c_int, [ctypes.c_uint64] * 4 + [ctypes.c_int32] * 4 + [ctypes.c_uint64]),
     "plamo_kernel_unpack": (ctypes.c_int, [ctypes.c_uint64] * 3 + [ctypes.c_int64, ctypes.c_uint64]),
     "plamo_kernel_argmax": (ctypes.c_int, [ctypes.c_uint64] * 2 + [ctypes.c_int32] * 3 + [ctypes.c_uint64]),
+    "plamo_kernel_qsa_select": (ctypes.c_int, [ctypes.c_uint64] + [ctypes.c_int32] * 4 + [ctypes.c_uint64] * 2),
     "plamo_kernel_select": (ctypes.c_int, [ctypes.c_uint64, ctypes.c_int32, ctypes.c_uint64, ctypes.c_int32,
                                            ctypes.c_float, ctypes.c_int32, ctypes.c_float, ctypes.c_float,
                                            ctypes.c_uint64, ctypes.c_uint64]),

@@ -163,3 +163,23 @@ def test_mtp_output_is_the_greedy_sequence(model, model_dir, monkeypatch):
     assert len(rm["output_ids"]) - (rm["mtp_verifications"] + rm["mtp_accepted_tokens"]) in (0, 1)
     streamed, _ = run(model, ["--max-tokens", "12", "--mtp", "--stream"], TEXT)
     assert streamed + "\n" == out
+
+
+def test_qsa_budgets(model, model_dir, monkeypatch):
+    # --qsa-budget: a budget above the context keeps dense attention's tokens with no
+    # sparse queries; a small one selects fewer keys than dense attention would see; with
+    # --mtp the output stays that of the same budget's greedy loop (Main.swift:254-276)
+    monkeypatch.setenv("PLAMO_SOURCE_SHA256", model_dir[1])
+    out, m = run(model, ["--max-tokens", "24"], TEXT)
+    wide_out, wide = run(model, ["--max-tokens", "24", "--qsa-budget", "2048"], TEXT)
+    r, rw = m["runs"][0], wide["runs"][0]
+    assert wide["qsa"] is True and wide["qsa_budget"] == 2048
+    # no indexer is loaded for a budget the context does not exceed (Runtime.swift:248)
+    assert wide["auxiliary_weight_bytes"] == 0
+    assert rw["output_ids"] == r["output_ids"] and rw["qsa_queries"] == 0
+    small_out, small = run(model, ["--max-tokens", "24", "--qsa-budget", "16"], TEXT)
+    rs = small["runs"][0]
+    assert small["auxiliary_weight_bytes"] == 2 * 2 * (640 * 1536 + 2 * 128)
+    assert rs["qsa_queries"] > 0 and rs["qsa_selected_keys"] < rs["qsa_dense_keys"]
+    both_out, both = run(model, ["--max-tokens", "24", "--qsa-budget", "16", "--mtp"], TEXT)
+    assert both["runs"][0]["output_ids"] == rs["output_ids"] and both_out == small_out
