@@ -10,8 +10,8 @@ QsaTwin, exact_flash.c's key mask, ExactDecoder's masked attention) pinned again
   block keys rotated at 4b + 1) each outside that bound;
 * the masked prefill attention against an FP64 softmax over the selected keys, and an
   all-selected mask bit-equal to no mask;
-* the decode twin: a budget that covers every block is bit-equal to dense decoding, a small
-  budget equals it until the first query sees more blocks than the budget, and differs later.
+* the decode twin: a small budget equals a covering one until the first query sees more
+  complete blocks than the budget allows, and differs later.
 """
 import types
 
@@ -172,16 +172,16 @@ def test_masked_flash_matches_softmax():
 
 
 def test_decode_twin_budget(oracle_weights, model_dir):
+    # (dense attention equals an all-selected mask: test_masked_flash_matches_softmax here,
+    # and the GPU runtime against its dense twin)
     adapters = ad.Adapters(model_dir[0])
-    ctx, steps = 32, 18
-    dense = exact.ExactDecoder(oracle_weights, ctx, 16)
+    ctx, steps = 32, 14
     covering = exact.ExactDecoder(oracle_weights, ctx, 16, qsa=ad.QsaTwin(adapters, ctx, 32))
     small = exact.ExactDecoder(oracle_weights, ctx, 16, qsa=ad.QsaTwin(adapters, ctx, 8))
     tokens = [1] + [500 + 3 * k for k in range(steps - 1)]
     differs = []
     for pos, tok in enumerate(tokens):
-        d = dense.step(tok, pos)[0]
-        assert np.array_equal(covering.step(tok, pos)[0], d), pos
+        d = covering.step(tok, pos)[0]
         s = small.step(tok, pos)[0]
         if (pos + 1) // 4 <= 2:  # no query sees more than budget / 4 = 2 complete blocks
             assert np.array_equal(s, d), pos
