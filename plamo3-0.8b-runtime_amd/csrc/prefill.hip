@@ -650,6 +650,9 @@ __device__ __forceinline__ void split_bf16(float a, float b, uint32_t& hw, uint3
     __builtin_memcpy(&lw, &l, 4);
 }
 
+// QSA: global layers with a selection bitmap (a separate instance, so the dense kernel's
+// edge tiles carry no bitmap test).
+template <bool QSA>
 __global__ __launch_bounds__(256, 2) void flash_prefill_kernel(const FlashParams p) {
 #pragma clang fp contract(off)  // fixed rounding sequence, reproduced by the CPU oracle
     __shared__ __align__(16) uint16_t Ks[2][FK * KST];
@@ -693,8 +696,9 @@ __global__ __launch_bounds__(256, 2) void flash_prefill_kernel(const FlashParams
         for (int r = 0; r < 16; ++r) oacc[dt][r] = 0.f;
     float m = NEG_INF, ls = 0.f;
 
-    const bool qsa = p.full && p.qsa_mask != nullptr;
-    const uint32_t* qmask = qsa ? p.qsa_mask + size_t(tqc) * p.qsa_words : nullptr;
+    // QSA: the query's blocks of four keys complete at its position are seen only when
+    // selected (bit b of its bitmap word b / 32); its unfinished block always is
+    const uint32_t* qmask = QSA ? p.qsa_mask + size_t(tqc) * p.qsa_words : nullptr;
     const uint32_t qcomplete = (qpos + 1) / 4;
     const bool cached = !p.full && p.keys_rot != nullptr && base == 0 && khi < p.rot_rows;
     const KvSource src{cached ? p.keys_rot : p.keys, !p.full && !cached};
@@ -725,18 +729,24 @@ __global__ __launch_bounds__(256, 2) void flash_prefill_kernel(const FlashParams
         // a query's causal edge or window start need the mask.
         // QSA: every tile is masked by the query's selected blocks (its unfinished block is
         // always seen)
-        const bool edge = qsa || !(k0 + uint32_t(FK - 1) <= plo && (p.full || k0 + uint32_t(WINDOW - 1) >= khi));
+        const bool edge = QSA || !(k0 + uint32_t(FK - 1) <= plo && (p.full || k0 + uint32_t(WINDOW - 1) >= khi));
         float mt = NEG_INF;
         if (edge) {
+            // QSA (global layers: k0 is a multiple of 64): the tile's 16 blocks b0 .. b0 + 15
+            // are bits 0..15 of one bitmap word shifted by b0 % 32, read once per tile; blocks
+            // at or past qcomplete are not tested
+            uint32_t qbits = 0u;
+            const uint32_t b0 = k0 >> 2;
+            if (QSA && b0 < qcomplete) qbits = qmask[b0 >> 5] >> (b0 & 31);
 #pragma unroll
             for (int r = 0; r < 2; ++r)
 #pragma unroll
                 for (int i = 0; i < 16; ++i) {
                     const uint32_t kp = k0 + uint32_t(32 * r + 8 * (i >> 2) + 4 * half + (i & 3));
                     bool vis = kp <= qpos && (p.full || kp + uint32_t(WINDOW - 1) >= qpos);
-                    if (qsa) {
+                    if (QSA) {
                         const uint32_t b = kp >> 2;
-                        vis = vis && (b >= qcomplete || ((qmask[b >> 5] >> (b & 31)) & 1u));
+                        vis = vis && (b >= qcomplete || ((qbits >> (b - b0)) & 1u));
                     }
                     const float x = vis ? sacc[r][i] * SCALE_LOG2E : NEG_INF;
                     sacc[r][i] = x;
@@ -952,7 +962,9 @@ void launch_qk_prep(const QkPrepParams& p, hipStream_t s) {
 void launch_flash_prefill(const FlashParams& p, hipStream_t s) {
     if (p.tokens < 1) return;
     if (p.tokens > 65536 / FLASH_PARTS * 8) throw Error(E_INVAL, "flash prefill: too many tokens in one call");
-    hipLaunchKernelGGL(flash_prefill_kernel, dim3(flash_blocks(p.tokens) * FLASH_PARTS), dim3(256), 0, s, p);
+    const dim3 grid(flash_blocks(p.tokens) * FLASH_PARTS), block(256);
+    if (p.full && p.qsa_mask) hipLaunchKernelGGL(flash_prefill_kernel<true>, grid, block, 0, s, p);
+    else hipLaunchKernelGGL(flash_prefill_kernel<false>, grid, block, 0, s, p);
 }
 
 }  // namespace plamo
