@@ -897,7 +897,7 @@ __global__ __launch_bounds__(256) void head_merge_kernel(DecodeBuffers b, int bl
 
 // ---------------------------------------------------------------------- decode attention
 constexpr int KP = KEYS_PER_PART;
-constexpr int HG = 4;                // heads per workgroup (grid.y = HEADS / HG head groups)
+constexpr int HG = 4;                // heads per workgroup (HEADS / HG head groups per partition)
 constexpr int KS = 68;               // padded LDS row of rotated keys: 64 BF16 pairs + 4 words
 
 // Workgroup (partition x, head group y, row z): keys x*64 .. x*64+63 of the row's visible
@@ -917,7 +917,12 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
     __shared__ int s_last;
 
     const StepState* st = p.state;
-    const int q = blockIdx.z, hg = blockIdx.y;
+    // workgroup -> (partition, head group): the four head groups of a partition share
+    // id % 8, so they run on one XCD and read its keys and values through one L2 (ids of
+    // partitions past p.parts return below)
+    const uint32_t wid = blockIdx.x;
+    const uint32_t part = (wid >> 5) * 8u + (wid & 7u);
+    const int q = blockIdx.z, hg = int((wid >> 3) & 3u);
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar)
     // ---- loads that do not depend on the step state go out before it arrives: the group's
@@ -954,7 +959,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
     const uint32_t first = FULL ? 0u : (pos > uint32_t(WINDOW - 1) ? pos - uint32_t(WINDOW - 1) : 0u);
     const uint32_t qcoord = FULL ? pos : pos - first;
     const uint32_t count = pos + 1 - first;
-    const uint32_t k0 = blockIdx.x * KP;
+    const uint32_t k0 = part * KP;
     const uint32_t cap = p.capacity;
     const uint32_t start = first % cap;
     uint16_t* K = p.keys + size_t(lanei) * cap * HEAD_DIM;
@@ -964,14 +969,14 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
     // rotated and only the newest one is rotated here.
     const bool prerot = !FULL && p.keys_rot != nullptr && first == 0;
     uint16_t* KR = prerot ? p.keys_rot + size_t(lanei) * p.rot_rows * HEAD_DIM : nullptr;
-    const size_t pslot = size_t(q) * p.parts + blockIdx.x;
+    const size_t pslot = size_t(q) * p.parts + part;
     // partition results travel between workgroups with sc1 stores and loads (no cache fences)
     const uint32_t pstats = uint32_t(ROWS) * p.parts * HEADS;
     const __amdgpu_buffer_rsrc_t mview = buffer_view(p.part_m, pstats * 4u);
     const __amdgpu_buffer_rsrc_t lview = buffer_view(p.part_l, pstats * 4u);
     const __amdgpu_buffer_rsrc_t oview = buffer_view(p.part_o, pstats * HEAD_DIM * 4u);
     const uint32_t nparts = (count + KP - 1) / KP;
-    if (blockIdx.x >= nparts) return;  // partitions past the visible keys take no ticket
+    if (part >= nparts) return;  // partitions past the visible keys take no ticket
     const uint32_t newest = count - 1;
     const bool has_new = newest >= k0 && newest < k0 + KP;
 
@@ -1820,7 +1825,7 @@ void launch_gemv(int n, bool packed, int maxr, Prologue pro, Epilogue epi, const
 }
 
 void launch_attention(bool full, const AttnParams& p, int rows, hipStream_t s) {
-    const dim3 grid(p.parts, HEADS / HG, rows), block(256);
+    const dim3 grid(32 * ((p.parts + 7) / 8), 1, rows), block(256);
     if (full) hipLaunchKernelGGL(attn_decode_kernel<true>, grid, block, 0, s, p);
     else hipLaunchKernelGGL(attn_decode_kernel<false>, grid, block, 0, s, p);
 }
