@@ -223,6 +223,45 @@ def bench_long(plamo_hip, np, model_dir, sha):
             "decode_tok_s": round(len(ids) / t_dec, 1), "gpu_s": round(st["gpu_seconds"], 4)}
 
 
+def bench_adapters(plamo_hip, np, model_dir, sha):
+    """The trained-adapter options on random-init adapters (their acceptance and selection
+    quality mean nothing here; the costs do): batch-1 decode ms/step at position 8,192 with
+    QSA at budgets 2048 and 512 against dense attention (Runtime.swift:378-418), and the MTP
+    draft and a two-row sequential verification against two scalar decode steps
+    (Runtime.swift:322-538), each timed with HIP events around the call."""
+    prompt = np.random.default_rng(6).integers(1024, 107520, 8192).tolist()
+    out = {"position": 8192}
+    for name, budget in (("dense", None), ("qsa2048", 2048), ("qsa512", 512)):
+        rt = plamo_hip.Runtime(model_dir, 8192 + 96, source_sha256=sha, qsa_budget=budget)
+        rt.prefill(prompt)
+        rt.bench_decode(8)
+        out[name + "_ms_per_step"] = round(rt.bench_decode(64), 4)
+        rt.close()
+    rt = plamo_hip.Runtime(model_dir, 2048 + 64, source_sha256=sha, mtp=True)
+    nxt = rt.prefill(prompt[:2048])
+    draft, verify, scalar = [], [], []
+    gpu = lambda: rt.stats()["gpu_seconds"]
+    for _ in range(10):
+        g0 = gpu()
+        d = rt.draft(nxt)[0]
+        g1 = gpu()
+        rt.forward([nxt, d], all=True, sequential=True)
+        g2 = gpu()
+        rt.rewind(rt.position - 1, 0)  # keep the first row
+        nxt = rt.predictions()[0]
+        g3 = gpu()
+        nxt = rt.forward([rt.forward([nxt])])
+        g4 = gpu()
+        draft.append(g1 - g0)
+        verify.append(g2 - g1)
+        scalar.append(g4 - g3)
+    rt.close()
+    out.update({"mtp_draft_ms": round(1e3 * float(np.median(draft)), 4),
+                "mtp_verify_two_rows_ms": round(1e3 * float(np.median(verify)), 4),
+                "two_scalar_steps_ms": round(1e3 * float(np.median(scalar)), 4)})
+    return out
+
+
 def bench_tokenizer(plamo_hip, synth):
     """Host-side tokenizer (Tokenizer.swift): load, encode and decode throughput of the native
     library on ~1 MB of seeded text over the synthetic vocabulary's alphabet (no GPU work)."""
@@ -392,6 +431,8 @@ def main():
         log(f"batch4: {results['batch4']}")
         results["long_context"] = bench_long(plamo_hip, np, model_dir, sha)
         log(f"long_context: {results['long_context']}")
+        results["adapters"] = bench_adapters(plamo_hip, np, model_dir, sha)
+        log(f"adapters: {results['adapters']}")
         # --- prefill of 2048 tokens
         rt = plamo_hip.Runtime(model_dir, 2048 + 64)
         p2 = np.random.default_rng(3).integers(1024, 107520, 2048).tolist()

@@ -130,15 +130,43 @@ __global__ __launch_bounds__(64) void qsa_scores_kernel(const QsaParams p) {
     p.scores[size_t(t) * p.blocks + b] = score * QSA_SCALE;
 }
 
+// Inclusive prefix sum of one value per thread over a 256-thread workgroup (wave scans with
+// lane shuffles, then the wave totals through LDS); `total` gets the sum of all 256.
+// Integer sums: the order does not matter.
+__device__ __forceinline__ uint32_t block_scan(uint32_t v, uint32_t* waves, uint32_t& total) {
+    const int lane = int(threadIdx.x & 63), w = int(threadIdx.x >> 6);
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t y = __shfl_up(v, o, 64);
+        if (lane >= o) v += y;
+    }
+    if (lane == 63) waves[w] = v;
+    __syncthreads();
+    uint32_t before = 0;
+    total = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t x = waves[i];
+        before += i < w ? x : 0u;
+        total += x;
+    }
+    __syncthreads();  // waves[] is free again
+    return v + before;
+}
+
 // Token t = blockIdx.x: visible = pos + 1 keys, complete = visible / 4 blocks, chosen =
 // min(complete, budget / 4).  With chosen == complete every block is selected; otherwise
 // the chosen blocks of largest value max(score, 0) (as FP32 bits: nonnegative floats order
-// as integers), ties to the lower index: a radix search for the chosen-th largest value v,
+// as integers), ties to the lower index (Kernels.metal:618-682): a radix search, 8 bits per
+// pass from the top, for the chosen-th largest value v (each pass: a histogram of the next
+// digit among the values matching the digits found so far; thread t holds digit 255 - t,
+// and the one whose prefix sum from the top first reaches the remaining rank is the digit),
 // then every block above v and the first (chosen - above) blocks equal to v in index order
-// (Kernels.metal:618-682).  Output: bit b of mask word b / 32 (words up to p.words).
+// (thread i owns a contiguous run of blocks; its ties start after the prefix sum of the
+// earlier runs' ties).  Output: bit b of mask word b / 32 (words up to p.words).
 __global__ __launch_bounds__(256) void qsa_select_kernel(const QsaParams p) {
-    __shared__ uint32_t hist[256], eqs[256], words[MAX_CONTEXT / 4 / 32];
-    __shared__ uint32_t s_prefix, s_mask, s_rank, s_above;
+    __shared__ uint32_t hist[256], words[MAX_CONTEXT / 4 / 32], waves[4];
+    __shared__ uint32_t s_prefix, s_rank;
     const int t = int(blockIdx.x), tid = int(threadIdx.x);
     if (p.state && (p.state->stopped || p.state->rows == 0)) return;
     const uint32_t visible = row_pos(p, t) + 1, complete = visible / 4;
@@ -149,32 +177,29 @@ __global__ __launch_bounds__(256) void qsa_select_kernel(const QsaParams p) {
     __syncthreads();
     if (chosen == complete) {
         for (uint32_t b = uint32_t(tid); b < complete; b += 256) atomicOr(&words[b >> 5], 1u << (b & 31));
-    } else {
+    } else if (chosen > 0) {
         auto value = [&](uint32_t b) { const float s = sc[b]; return __float_as_uint(s > 0.f ? s : 0.f); };
-        if (tid == 0) { s_prefix = 0; s_mask = 0; s_rank = chosen; }
-        __syncthreads();
+        if (tid == 0) { s_prefix = 0; s_rank = chosen; }
         for (int shift = 24; shift >= 0; shift -= 8) {
             hist[tid] = 0;
-            __syncthreads();
-            const uint32_t prefix = s_prefix, mask = s_mask;
+            __syncthreads();  // also orders the last pass's s_prefix / s_rank before these reads
+            const uint32_t prefix = s_prefix, rank = s_rank;
+            const uint32_t mask = shift == 24 ? 0u : ~0u << (shift + 8);
             for (uint32_t b = uint32_t(tid); b < complete; b += 256) {
                 const uint32_t v = value(b);
                 if ((v & mask) == prefix) atomicAdd(&hist[(v >> shift) & 255u], 1u);
             }
             __syncthreads();
-            if (tid == 0) {
-                uint32_t remaining = s_rank;
-                for (int d = 255; d >= 0; --d) {
-                    const uint32_t c = hist[d];
-                    if (remaining > c) remaining -= c;
-                    else { s_prefix |= uint32_t(d) << shift; s_rank = remaining; break; }
-                }
-                s_mask |= 255u << shift;
+            const uint32_t c = hist[255 - tid], d = uint32_t(255 - tid);
+            uint32_t total;
+            const uint32_t incl = block_scan(c, waves, total);
+            // count above digit d: incl - c; exactly one thread sees the rank inside its bin
+            if (incl - c < rank && rank <= incl) {
+                s_prefix = prefix | (d << shift);
+                s_rank = rank - (incl - c);
             }
-            __syncthreads();
         }
-        // v = s_prefix: blocks above v, then the ties in index order (thread i owns a
-        // contiguous run of blocks)
+        __syncthreads();
         const uint32_t v = s_prefix;
         const uint32_t run = (complete + 255) / 256, b0 = uint32_t(tid) * run, b1 = min(b0 + run, complete);
         uint32_t above = 0, eq = 0;
@@ -183,22 +208,11 @@ __global__ __launch_bounds__(256) void qsa_select_kernel(const QsaParams p) {
             above += x > v;
             eq += x == v;
         }
-        hist[tid] = above;
-        eqs[tid] = eq;
-        __syncthreads();
-        if (tid == 0) {
-            uint32_t total = 0, ties = 0;
-            for (int i = 0; i < 256; ++i) {
-                total += hist[i];
-                const uint32_t e = eqs[i];
-                eqs[i] = ties;  // ties before thread i's run
-                ties += e;
-            }
-            s_above = total;
-        }
-        __syncthreads();
-        const uint32_t allowance = chosen - s_above;
-        uint32_t seen = eqs[tid];
+        uint32_t total_above, total_eq;
+        block_scan(above, waves, total_above);
+        const uint32_t eq_incl = block_scan(eq, waves, total_eq);
+        const uint32_t allowance = chosen - total_above;
+        uint32_t seen = eq_incl - eq;  // ties in the runs of threads before this one
         for (uint32_t b = b0; b < b1; ++b) {
             const uint32_t x = value(b);
             bool take = x > v;
