@@ -15,6 +15,7 @@ each, stop on EOS) against batch-1 on the same segment; configs[4] .p12 long con
     python bench.py --kernels-only     # GEMV shapes + copy calibration (for rocprofv3 --pmc)
     python bench.py --prefill-only     # three 2048-token prefills (for rocprofv3 kernel traces)
     python bench.py --batch4-only      # the configs[3] batch4 measurement alone
+    python bench.py --long-only N      # configs[4]: 30,720-token prefill, then N sampled tokens
     python bench.py --tokenizer-only   # host C++ tokenizer throughput (no GPU work)
     python bench.py --timeline [--packed]  # in-step kernel durations of replayed decode steps
                                            # (needs lib/libplamo_hip_timeline.so: make timeline)
@@ -203,17 +204,17 @@ def bench_batch4(plamo_hip, np, model_dir):
     return res
 
 
-def bench_long(plamo_hip, np, model_dir, sha):
+def bench_long(plamo_hip, np, model_dir, sha, tokens=32768 - 30720):
     """.p12 weights, 30,720-token prefill, then sampled decode (repetition 1.1,
-    frequency 0.2, no-repeat-ngram 4, on the GPU) to the 32,768-token cap.  Both phases are
-    timed inside the one generate call (the runtime's prefill / decode wall seconds, as
-    Main.swift:245-287 times them)."""
+    frequency 0.2, no-repeat-ngram 4, on the GPU) to the 32,768-token cap (or `tokens`
+    generated tokens).  Both phases are timed inside the one generate call (the runtime's
+    prefill / decode wall seconds, as Main.swift:245-287 times them)."""
     rt = plamo_hip.Runtime(model_dir, 32768, packed=True, source_sha256=sha)
     prompt = np.random.default_rng(5).integers(1024, 107520, 30720).tolist()
     rt.prefill(prompt[:2048])  # warm-up
     rt.reset()
     rt.set_sampling(1.1, 0.2, 0.0, 4)
-    ids, reason = rt.generate(prompt, 32768 - 30720)
+    ids, reason = rt.generate(prompt, tokens)
     st = rt.stats()
     rt.set_sampling()
     rt.close()
@@ -354,6 +355,8 @@ def main():
     ap.add_argument("--kernels-only", action="store_true", help="GEMV shapes and a copy calibration only")
     ap.add_argument("--prefill-only", action="store_true", help="three 2048-token prefills only")
     ap.add_argument("--batch4-only", action="store_true", help="the configs[3] batch4 measurement only")
+    ap.add_argument("--long-only", type=int, default=0, metavar="TOKENS",
+                    help="the configs[4] workload only, generating TOKENS tokens after the 30,720-token prefill")
     ap.add_argument("--tokenizer-only", action="store_true",
                     help="host tokenizer throughput (no GPU work; not part of the GPU line)")
     ap.add_argument("--timeline", action="store_true",
@@ -385,6 +388,9 @@ def main():
     model_dir, sha = synth.ensure_model(packed=True)
     if args.batch4_only:
         print(json.dumps({"batch4": bench_batch4(plamo_hip, np, model_dir)}), flush=True)
+        return
+    if args.long_only:
+        print(json.dumps({"long_context": bench_long(plamo_hip, np, model_dir, sha, args.long_only)}), flush=True)
         return
     if args.tokenizer_only:
         print(json.dumps({"tokenizer": bench_tokenizer(plamo_hip, synth)}), flush=True)
