@@ -922,7 +922,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
     // partitions past p.parts return below)
     const uint32_t wid = blockIdx.x;
     const uint32_t part = (wid >> 5) * 8u + (wid & 7u);
-    const int q = blockIdx.z, hg = int((wid >> 3) & 3u);
+    const int q = int(blockIdx.z + p.row0), hg = int((wid >> 3) & 3u);
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar)
     // ---- loads that do not depend on the step state go out before it arrives: the group's
@@ -955,7 +955,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
     // Kernels.metal:251,283-284).
     if (st->stopped || q >= int(st->rows)) return;
     const uint32_t pos = st->pos[q];
-    const uint32_t lanei = st->lane[q];
+    const uint32_t lanei = st->kv_shared ? 0u : st->lane[q];
     const uint32_t first = FULL ? 0u : (pos > uint32_t(WINDOW - 1) ? pos - uint32_t(WINDOW - 1) : 0u);
     const uint32_t qcoord = FULL ? pos : pos - first;
     const uint32_t count = pos + 1 - first;

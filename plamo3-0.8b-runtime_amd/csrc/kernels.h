@@ -41,7 +41,11 @@ struct StepState {
     uint32_t lcount[ROWS];    // tokens emitted per lane
     uint32_t llimit[ROWS];    // per-lane token limit
     uint32_t lreason[ROWS];   // 0 running, 1 stop token, 2 length
+    // Verification rows (Runtime.forward(all: sequential:) with two rows): every row reads and
+    // writes KV slice 0 at its own position; `lane` then only names its output slot.
+    uint32_t kv_shared;
 };
+static_assert(sizeof(StepState) <= 256, "the kernel-level attention workspace keeps 256 B for the state");
 
 // Buffers the decode kernels share.
 struct DecodeBuffers {
@@ -99,6 +103,7 @@ struct GemvParams {
 
 struct AttnParams {
     const StepState* state;   // rows, positions and KV slices of the step
+    uint32_t row0;            // the launch covers rows row0 .. row0 + gridDim.z - 1
     const float* qkv;         // [rows][2304] (BF16-valued FP32)
     const uint16_t* q_norm;   // [128]
     const uint16_t* k_norm;

@@ -297,6 +297,7 @@ Engine::~Engine() {
     if (graph) (void)hipGraphExecDestroy(graph);
     if (graph_loop) (void)hipGraphExecDestroy(graph_loop);
     if (graph16) (void)hipGraphExecDestroy(graph16);
+    if (graph_verify) (void)hipGraphExecDestroy(graph_verify);
 
     (void)hipEventDestroy(ev0);
     (void)hipEventDestroy(ev1);
@@ -366,9 +367,8 @@ void Engine::enqueue_head(const uint16_t* in, const uint16_t* resid_in, int in_r
     launch_head_merge(bufs, head_blocks(maxr), false, stream);
 }
 
-void Engine::enqueue_head16(bool loop) {
+void Engine::enqueue_head16(bool loop, int maxr) {
     const Model& m = *model;
-    const int maxr = lanes == 1 ? 1 : ROWS;
     GemvParams g{};
     g.state = state;
     g.rows = ROWS;
@@ -392,10 +392,10 @@ void Engine::enqueue_head16(bool loop) {
 // One decode step (Runtime.swift:376-458 for one token per row; Batch.swift:147-165).  A host
 // step starts with the bookkeeping kernel; a device-loop step finds its bookkeeping done by the
 // previous step's head merge (or by begin_loop before the first replay).
-void Engine::enqueue_step(bool head, bool loop) {
+void Engine::enqueue_step(bool head, bool loop, bool verify) {
     const Model& m = *model;
     const bool pk = m.packed;
-    const int maxr = lanes == 1 ? 1 : ROWS;
+    const int maxr = lanes == 1 && !verify ? 1 : ROWS;
     if (!loop) launch_step_begin(bufs, stream);
     for (int l = 0; l < LAYERS; ++l) {
         const LayerWeights& L = m.layers[l];
@@ -421,7 +421,7 @@ void Engine::enqueue_step(bool head, bool loop) {
             g.post_offset = post_mlp_offset();
             launch_gemv(HIDDEN, pk, maxr, PRO_RESID16, EPI_ROUND, g, gemv_blocks(HIDDEN, maxr, EPI_ROUND, QKV, pk), stream);
         }
-        const bool qsa = full && qsa_aux && lanes == 1;
+        const bool qsa = full && qsa_aux && lanes == 1 && !verify;
         if (qsa) {
             // the indexer projection of the same normed row (same prologue, Runtime.swift:381),
             // then queries, raw key, block key, scores and the selection (Runtime.swift:382-403)
@@ -464,7 +464,16 @@ void Engine::enqueue_step(bool head, bool loop) {
         a.window = full ? 0u : uint32_t(WINDOW);
         a.qsa_mask = qsa ? qsa_mask : nullptr;
         a.qsa_words = qsa_words;
-        launch_attention(full, a, ROWS, stream);
+        if (verify) {
+            // row 1 reads the key and value row 0 writes at its position: one launch per row
+            for (uint32_t r = 0; r < VERIFY_ROWS; ++r) {
+                a.row0 = r;
+                launch_attention(full, a, 1, stream);
+            }
+            a.row0 = 0;
+        } else {
+            launch_attention(full, a, ROWS, stream);
+        }
         if (a.defer) launch_attention_merge(a, ROWS, stream);
         GemvParams o{};
         o.state = state;
@@ -508,37 +517,17 @@ void Engine::enqueue_step(bool head, bool loop) {
         d.out16 = proj;
         launch_gemv(INTER, pk, maxr, PRO_PLAIN16, EPI_BF16, d, gemv_blocks(INTER, maxr, EPI_BF16, HIDDEN, pk), stream);
     }
-    if (head) enqueue_head16(loop);
+    if (head) enqueue_head16(loop, maxr);
 }
 
-void Engine::run_step() {
-    if (!use_graph) {
-        enqueue_step();
-        return;
-    }
-    if (!graph) {
-        hipGraph_t g = nullptr;
-        PLAMO_HIP(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal));
-        try {
-            enqueue_step();
-        } catch (...) {
-            (void)hipStreamEndCapture(stream, &g);
-            if (g) (void)hipGraphDestroy(g);
-            throw;
-        }
-        PLAMO_HIP(hipStreamEndCapture(stream, &g));
-        PLAMO_HIP(hipGraphInstantiate(&graph, g, nullptr, nullptr, 0));
-        PLAMO_HIP(hipGraphDestroy(g));
-    }
-    PLAMO_HIP(hipGraphLaunch(graph, stream));
-}
-
-// Captures (without running) `steps` consecutive device-loop steps into `out`.
-void Engine::capture_loop(int steps, hipGraphExec_t* out) {
+namespace {
+// Captures (without running) what `enqueue` puts on `stream` into `out`.
+template <typename F>
+void capture_graph(hipStream_t stream, hipGraphExec_t* out, F enqueue) {
     hipGraph_t g = nullptr;
     PLAMO_HIP(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal));
     try {
-        for (int k = 0; k < steps; ++k) enqueue_step(true, true);
+        enqueue();
     } catch (...) {
         (void)hipStreamEndCapture(stream, &g);
         if (g) (void)hipGraphDestroy(g);
@@ -547,6 +536,32 @@ void Engine::capture_loop(int steps, hipGraphExec_t* out) {
     PLAMO_HIP(hipStreamEndCapture(stream, &g));
     PLAMO_HIP(hipGraphInstantiate(out, g, nullptr, nullptr, 0));
     PLAMO_HIP(hipGraphDestroy(g));
+}
+}  // namespace
+
+void Engine::run_step() {
+    if (!use_graph) {
+        enqueue_step();
+        return;
+    }
+    if (!graph) capture_graph(stream, &graph, [&] { enqueue_step(); });
+    PLAMO_HIP(hipGraphLaunch(graph, stream));
+}
+
+void Engine::run_verify() {
+    if (!use_graph) {
+        enqueue_step(true, false, true);
+        return;
+    }
+    if (!graph_verify) capture_graph(stream, &graph_verify, [&] { enqueue_step(true, false, true); });
+    PLAMO_HIP(hipGraphLaunch(graph_verify, stream));
+}
+
+// Captures (without running) `steps` consecutive device-loop steps into `out`.
+void Engine::capture_loop(int steps, hipGraphExec_t* out) {
+    capture_graph(stream, out, [&] {
+        for (int k = 0; k < steps; ++k) enqueue_step(true, true);
+    });
 }
 
 void Engine::prepare_loop_graph() {
@@ -873,7 +888,36 @@ int RuntimeImpl::forward_ex(const int32_t* tokens, int n, bool output, bool all,
     StepState& hs = *e.host_state;
     const int rows = output ? (all ? n : 1) : 0;  // Runtime.swift:453
     begin_timing();
-    if (sequential || n == 1) {
+    if (sequential && n == VERIFY_ROWS && output && all && !sampling && !e.qsa_aux) {
+        // Both rows in one pass over the weights (the linear_pair pass of Runtime.swift:370-371):
+        // the multi-row kernels with each row at its own position in KV slice 0 and its outputs
+        // in slot i; row 1's attention runs after row 0's, whose key and value it reads.  Per
+        // row these are the operations of a scalar step, so the bits are those of
+        // forward([tokens[0]]) then forward([tokens[1]]).
+        hs.rows = VERIFY_ROWS;
+        for (int i = 0; i < VERIFY_ROWS; ++i) {
+            hs.lane[i] = uint32_t(i);
+            hs.pos[i] = uint32_t(position + i);
+            hs.token[i] = tokens[i];
+            sync_sampler(e, i);
+        }
+        hs.kv_shared = 1;
+        hs.loop = 0;
+        hs.stopped = 0;
+        PLAMO_HIP(hipMemcpyAsync(e.state, &hs, sizeof(StepState), hipMemcpyHostToDevice, stream));
+        e.run_verify();
+        PLAMO_HIP(hipMemcpyAsync(aux->slot_logits, e.logits, size_t(VERIFY_ROWS) * VOCAB * 2, hipMemcpyDeviceToDevice,
+                                 stream));
+        PLAMO_HIP(hipMemcpyAsync(aux->slot_hidden, e.hidden, size_t(VERIFY_ROWS) * HIDDEN * 4,
+                                 hipMemcpyDeviceToDevice, stream));
+        PLAMO_HIP(hipMemcpyAsync(aux->slot_next, &e.state->next[0], size_t(VERIFY_ROWS) * 4, hipMemcpyDeviceToDevice,
+                                 stream));
+        // slot 0 then holds the last row, as after two scalar steps (rewind to the last row)
+        PLAMO_HIP(hipMemcpyAsync(e.logits, aux->slot_logits + size_t(VERIFY_ROWS - 1) * VOCAB, size_t(VOCAB) * 2,
+                                 hipMemcpyDeviceToDevice, stream));
+        PLAMO_HIP(hipMemcpyAsync(e.hidden, aux->slot_hidden + size_t(VERIFY_ROWS - 1) * HIDDEN, size_t(HIDDEN) * 4,
+                                 hipMemcpyDeviceToDevice, stream));
+    } else if (sequential || n == 1) {
         // Each row as a scalar decode step at its own position: its local keys and query take
         // the coordinates of that step (rotate_steps, Kernels.metal:288-298), so row i's
         // outputs are those of forward([tokens[i]]) after rows 0 .. i - 1.
@@ -916,6 +960,7 @@ int RuntimeImpl::forward_ex(const int32_t* tokens, int n, bool output, bool all,
     PLAMO_HIP(hipMemcpyAsync(&hs, e.state, sizeof(StepState), hipMemcpyDeviceToHost, stream));
     PLAMO_HIP(hipStreamSynchronize(stream));
     PLAMO_HIP(hipGetLastError());
+    hs.kv_shared = 0;  // later uploads run single rows again
     count_qsa(position, n);
     position += n;
     last_output_rows = rows;

@@ -122,6 +122,7 @@ class Engine {
     hipGraphExec_t graph = nullptr;       // one host step (bookkeeping kernel first)
     hipGraphExec_t graph_loop = nullptr;  // one device-loop step (bookkeeping in its head merge)
     hipGraphExec_t graph16 = nullptr;     // LOOP_GRAPH_STEPS consecutive device-loop steps
+    hipGraphExec_t graph_verify = nullptr;  // the two-row verification step
     bool use_graph = true;
 
     hipEvent_t ev0, ev1;
@@ -140,8 +141,11 @@ class Engine {
 
     // one decode step for state->rows rows; `loop`: a device-loop step (no bookkeeping kernel,
     // the head merge prepares the next step)
-    void enqueue_step(bool head = true, bool loop = false);
-    void run_step();                        // host step: graph replay (or direct launches)
+    // verify: the two verification rows of one sequence (StepState::kv_shared) through the
+    // multi-row kernels, each row's attention launched after the previous row's
+    void enqueue_step(bool head = true, bool loop = false, bool verify = false);
+    void run_step();
+    void run_verify();  // enqueue_step(true, false, true), replayed from a captured graph                        // host step: graph replay (or direct launches)
     // Device loops: begin_loop once (the first step's bookkeeping), then n steps as replays of
     // a LOOP_GRAPH_STEPS-step graph and single-step graphs (one launch per 16 steps)
     static constexpr int LOOP_GRAPH_STEPS = 16;
@@ -158,7 +162,7 @@ class Engine {
   private:
     void enqueue_prefill_chunk(int n, int p0, int lane, bool last_chunk, bool output);
     void enqueue_head(const uint16_t* in, const uint16_t* resid_in, int in_rows);  // prefill rows
-    void enqueue_head16(bool loop);                                           // decode: BF16 stream
+    void enqueue_head16(bool loop, int maxr);                                 // decode: BF16 stream
     void capture_loop(int steps, hipGraphExec_t* out);
 };
 

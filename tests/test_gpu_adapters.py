@@ -3,9 +3,11 @@ with the synthetic seed-0 model and random-init adapters (synth.write_auxiliary)
 
 * the draft equals the order-exact CPU restatement (oracle/adapters.py) in every logit bit
   and its token, plain and .p12, also after a verification pass and a rewind;
-* VerificationTests.swift:6-53: a two-row sequential verification equals two scalar
-  forwards bit for bit (every row's logits and prediction), three rows are refused without
-  touching the state, rewind keeps the chosen row and continues like a clean runtime;
+* VerificationTests.swift:6-53: a two-row sequential verification (one pass of the
+  multi-row kernels over the weights, the reference's linear_pair pass) equals two scalar
+  forwards bit for bit (every row's logits, hidden row and prediction), pass after pass;
+  three rows are refused without touching the state, rewind keeps the chosen row and
+  continues like a clean runtime;
 * VerificationTests.swift:96-108 (draft shapes and refusals), LogitsTests.swift:49-68 (rows
   of a non-sequential two-row forward and rewind to the second row).
 """
@@ -175,3 +177,34 @@ def test_batch_refuses_adapters(model_dir):
             plamo_hip.Batch(rt)
     finally:
         rt.close()
+
+
+@pytest.mark.parametrize("packed", [False, True])
+def test_repeated_verifications_equal_scalar_steps(model_dir, packed):
+    # the two-row verification pass (one read of the weights for both rows, replayed from a
+    # captured graph) equals two scalar steps in every logit and hidden bit, replay after
+    # replay, with rewinds, host synchronisations and single steps between the replays
+    prefix = [1] + [300 + 11 * k for k in range(40)]
+    pair, scalar = _mtp(model_dir, 128, packed), _mtp(model_dir, 128, packed)
+    try:
+        assert pair.prefill(prefix) == scalar.prefill(prefix)
+        rng = np.random.default_rng(4)
+        for it in range(5):
+            cand = [int(t) for t in rng.integers(1024, 107520, 2)]
+            pair.forward(cand, all=True, sequential=True)
+            want, nxt = [], []
+            for t in cand:
+                nxt.append(scalar.forward([t]))
+                want.append((_bits(scalar), scalar.hidden().view(np.uint32).copy()))
+            assert pair.predictions() == nxt, it
+            for i in range(2):
+                assert np.array_equal(_bits(pair, i), want[i][0]), (it, i)
+            pair.rewind(pair.position, 1)
+            assert np.array_equal(pair.hidden().view(np.uint32), want[1][1]), it
+            t = int(rng.integers(1024, 107520))
+            assert pair.forward([t]) == scalar.forward([t]), it
+            assert np.array_equal(_bits(pair), _bits(scalar)), it
+        print(f"  packed={packed}: five verification passes equal scalar steps", flush=True)
+    finally:
+        pair.close()
+        scalar.close()
