@@ -187,6 +187,7 @@ int gemv_blocks(int n, int maxr, Epilogue epi, int m, bool packed);  // workgrou
 inline int head_blocks(int maxr) { return maxr == 1 ? HEAD_BLOCKS : HEAD_BLOCKS / 4; }
 void launch_gemv(int n, bool packed, int maxr, Prologue pro, Epilogue epi, const GemvParams& p, int blocks,
                  hipStream_t s);
+// Rows p.row0 .. p.row0 + rows - 1 of the step (one launch per row for verification rows).
 void launch_attention(bool full, const AttnParams& p, int rows, hipStream_t s);
 void launch_attention_merge(const AttnParams& p, int rows, hipStream_t s);  // global layers
 void launch_step_begin(const DecodeBuffers& b, hipStream_t s);
