@@ -189,7 +189,7 @@ void launch_gemv(int n, bool packed, int maxr, Prologue pro, Epilogue epi, const
                  hipStream_t s);
 // Rows p.row0 .. p.row0 + rows - 1 of the step (one launch per row for verification rows).
 void launch_attention(bool full, const AttnParams& p, int rows, hipStream_t s);
-void launch_attention_merge(const AttnParams& p, int rows, hipStream_t s);  // global layers
+void launch_attention_merge(const AttnParams& p, int rows, hipStream_t s);  // rows past the inline merge
 void launch_step_begin(const DecodeBuffers& b, hipStream_t s);
 // begin_next: device loops run the next step's bookkeeping (step_begin) in the same kernel
 void launch_head_merge(const DecodeBuffers& b, int blocks, bool begin_next, hipStream_t s);
