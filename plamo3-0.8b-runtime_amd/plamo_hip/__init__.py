@@ -40,8 +40,10 @@ class Runtime:
             native.call(lib.plamo_open, str(directory).encode(), int(context), 1 if packed else 0, sha,
                         ctypes.byref(h))
         else:
+            # None = dense attention (the C ABI's 0); an explicit 0 is a budget, and refused
+            budget = 0 if qsa_budget is None else (int(qsa_budget) if int(qsa_budget) != 0 else -1)
             native.call(lib.plamo_open_aux, str(directory).encode(), int(context), 1 if packed else 0, sha,
-                        int(qsa_budget or 0), 1 if mtp else 0, ctypes.byref(h))
+                        budget, 1 if mtp else 0, ctypes.byref(h))
         self._h = h
         self._lib = lib
 

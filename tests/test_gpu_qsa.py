@@ -6,8 +6,8 @@ the synthetic seed-0 model and random-init indexers (synth.write_auxiliary).
 * QSATests.swift:48-70 restated: a budget that still covers every complete block
   (context 19, budget 16) and one above the context (budget 128) give the dense runtime's
   tokens and logits bit for bit, with the reference's counters;
-* prefill (a chunk from position 0, then one starting inside a block) and decode at budget
-  16 equal the order-exact CPU twin (oracle/adapters.py QsaTwin on exact.ExactDecoder and
+* prefill (a chunk from position 0, then forwards starting inside blocks) and decode at
+  budget 16, plain and .p12, equal the order-exact CPU twin (oracle/adapters.py QsaTwin on exact.ExactDecoder and
   exact_prefill.ExactPrefill) in every logit bit, the hidden row and the next token, and
   differ from dense attention;
 * with MTP: a two-row sequential verification equals two scalar QSA forwards.
@@ -107,12 +107,13 @@ def _counts(calls, budget):
     return q, s, d
 
 
-def test_prefill_and_decode_bit_exact(model_dir, oracle_weights):
+@pytest.mark.parametrize("packed", [False, True])
+def test_prefill_and_decode_bit_exact(model_dir, oracle_weights, packed):
     context, budget = 160, 16
     rng = np.random.default_rng(31)
     prompt = [1] + rng.integers(1024, 107520, 69).tolist()
     adapters = ad.Adapters(model_dir[0])
-    rt, dense = _rt(model_dir, context, budget), _rt(model_dir, context)
+    rt, dense = _rt(model_dir, context, budget, packed=packed), _rt(model_dir, context, packed=packed)
     try:
         # a prompt, then forwards of 16 and 13 rows starting inside blocks 10 and 14
         rt.prefill(prompt[:41])
@@ -131,7 +132,8 @@ def test_prefill_and_decode_bit_exact(model_dir, oracle_weights):
         assert np.array_equal(rt.logit_bits(), bits)
         assert np.array_equal(rt.hidden().view(np.uint32), hidden.view(np.uint32))
         assert nxt == want
-        print(f"  QSA prefill of 41 + 16 + 13 tokens (budget {budget}): bit-exact, next {nxt}", flush=True)
+        print(f"  QSA prefill of 41 + 16 + 13 tokens (budget {budget}, packed={packed}): bit-exact, next {nxt}",
+              flush=True)
         # the prompt's counters follow Runtime.fill's 16-row forwards (Runtime.swift:476)
         calls = [(0, 16), (16, 16), (32, 9), (41, 16), (57, 13)]
         pos, t = len(prompt), nxt

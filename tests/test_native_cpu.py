@@ -167,6 +167,38 @@ def test_open_without_device_fails_loudly(model_dir):
         plamo_hip.Runtime(model_dir[0], 96)
 
 
+def test_open_with_adapters_validates_in_the_reference_order(model_dir, tmp_path):
+    # Runtime.init (Runtime.swift:166-178): the context, then the QSA budget, then
+    # auxiliary.safetensors, all before the model or a device is touched (on this CPU-only
+    # host the next step is the device check)
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("GPU present")
+    d, sha = model_dir
+    bare = tmp_path / "no_adapters"
+    bare.mkdir()
+    for name in os.listdir(d):
+        if name != "auxiliary.safetensors":
+            os.symlink(os.path.join(d, name), bare / name)
+    budget = "QSA budget must be a multiple of four in 4...2048"
+    missing = "Trained adapters missing; run scripts/train_auxiliary.py --collect"
+    for context in (0, 32769):
+        with pytest.raises(native.PlamoError, match=r"Context must be 1\.\.\.32768"):
+            plamo_hip.Runtime(bare, context, source_sha256=sha, qsa_budget=3)
+    for b in (0, 3, 6, 2052, -4):
+        with pytest.raises(native.PlamoError, match=budget):
+            plamo_hip.Runtime(bare, 64, source_sha256=sha, qsa_budget=b, mtp=True)
+    for kw in ({"qsa_budget": 16}, {"mtp": True}, {"qsa_budget": 2048, "mtp": True}):
+        with pytest.raises(native.PlamoError, match=missing):
+            plamo_hip.Runtime(bare, 64, source_sha256=sha, **kw)
+    # adapters trained against another model are refused before the device as well
+    with pytest.raises(native.PlamoError, match="Incompatible trained adapters"):
+        plamo_hip.Runtime(d, 64, qsa_budget=16)
+    # valid adapters pass: the device check comes next
+    with pytest.raises(native.PlamoError, match="HIP device"):
+        plamo_hip.Runtime(d, 64, source_sha256=sha, qsa_budget=16, mtp=True)
+
+
 # ---------------------------------------------------------- native decodeBatch (host)
 def _bytes_ids(text):
     return [b + 384 if b < 128 else b for b in text.encode()]
