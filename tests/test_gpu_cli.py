@@ -6,7 +6,8 @@ text, --dump-logits, the segment pipeline's stop rule (SegmentTests.swift:97-107
 truncated segment stops the pipeline, and segments that stop on an end id let the next one
 run, adjacent ones joined by a newline), and the command run as a fresh process: the
 translation alone on stdout and exactly one JSON line on stderr (web/server.ts:22-58 reads
-stdout as the translation and parses all of stderr)."""
+stdout as the translation and parses all of stderr), and BatchCLITests.swift:5-60's
+--batch4 against the sequential segment loop."""
 import io
 import json
 import os
@@ -183,3 +184,26 @@ def test_qsa_budgets(model, model_dir, monkeypatch):
     assert rs["qsa_queries"] > 0 and rs["qsa_selected_keys"] < rs["qsa_dense_keys"]
     both_out, both = run(model, ["--max-tokens", "24", "--qsa-budget", "16", "--mtp"], TEXT)
     assert both["runs"][0]["output_ids"] == rs["output_ids"] and both_out == small_out
+
+
+def test_batch4_matches_sequential_command(model):
+    # BatchCLITests.swift:5-60 restated on the synthetic model: the same text through the
+    # sequential segment loop and through --batch4 gives the same stdout, ids, stop reason
+    # and segment count, for plain and streamed output and a short limit; the batch adds
+    # KV and scratch, not another copy of the weights; --repeat 2 repeats the run exactly
+    source = "\tThe meeting has been moved to next Monday.\r\n\r\n Hello.\nThank you.\nYes.\nNo.\n  "
+    base = ["--segment-tokens", "64", "--to", "ja", "--max-tokens", "6"]
+    for flags in (["--stream"], [], ["--stream", "--max-tokens", "3"]):
+        s_out, s = run(model, base + flags, source)
+        b_out, b = run(model, base + flags + ["--batch4"], source)
+        sr, br = s["runs"][0], b["runs"][0]
+        assert s_out == b_out and sr["output_ids"] == br["output_ids"], flags
+        assert sr["stop_reason"] == br["stop_reason"] and sr["segments_total"] == br["segments_total"] > 1
+        assert s["batch4"] is False and b["batch4"] is True
+        assert s["gpu_weight_bytes"] == b["gpu_weight_bytes"]
+        assert b["metal_allocated_bytes"] - s["metal_allocated_bytes"] < b["gpu_weight_bytes"] // 2
+        assert b["peak_metal_allocated_bytes"] >= b["metal_allocated_bytes"]
+    expected, _ = run(model, base, source)
+    repeated, r = run(model, base + ["--batch4", "--repeat", "2"], source)
+    assert repeated == expected  # the translation is printed once, the runs are counted twice
+    assert len(r["runs"]) == 2 and r["runs"][0]["output_ids"] == r["runs"][1]["output_ids"]

@@ -5,7 +5,9 @@ vocabulary with the original's shape (107,520 entries; controls with <|plamo:bos
 <|plamo:tag|> at 16; BYTE tokens <0x80>..<0xFF> at 128-255 and <0x00>..<0x7F> at 384-511,
 where the reference's own decode tests find them, CacheTests.swift:98-101).  Encodings are
 pinned by brute force over every segmentation of short inputs, by hand-computed ties and
-boundary cases, and the native library must agree with the oracle token for token.
+boundary cases, and the native library must agree with the oracle token for token,
+including CostTests.swift:50-86's lengths around the reference's search windows and its
+modified scores.
 """
 import json
 import os
@@ -249,3 +251,48 @@ def test_stream_buffer_too_small_leaves_stream_unchanged(tmp_path, oracle_vocab)
     out = b"".join(st2.push(i) for i in ids) + st2.finish()
     assert out == tok.decode_bytes(ids) == bytes([a3[0]]) + long_piece.encode() + a3[1:]
     assert tok.decode_bytes([len(recs) - 1]) == long_piece.encode()
+
+
+def test_window_boundary_lengths_match_full_costs(oracle_vocab, native):
+    # CostTests.swift:50-65: every length around the reference's search windows (31-33,
+    # 62-65, 95-97, 127-129, 255-257, 1025 scalars) of mixed scalars, spaces and "ab" runs,
+    # with and without BOS, against the full-length cost recurrence (the oracle's Viterbi)
+    unicode = list("\U0001F9EA\U00020BB7é日 a\t")
+    for n in (0, 1, 2, 31, 32, 33, 62, 63, 64, 65, 95, 96, 97, 127, 128, 129, 255, 256, 257, 1025):
+        text = "".join(unicode[i % len(unicode)] for i in range(n))
+        for value in (text, " " * n, "ab" * n):
+            assert native.encode(value) == T.encode(oracle_vocab, value), n
+            assert native.encode(value, bos=True) == T.encode(oracle_vocab, value, bos=True), n
+    marked = "<|plamo:tag|>input<|plamo:msg|>" + "日本語 ab " * 50 + "aaaaaa\n\n\n\n"
+    assert native.encode(marked) == T.encode(oracle_vocab, marked)
+
+
+def test_modified_scores_across_wraps(tmp_path):
+    # CostTests.swift:67-86: "a" and "b" at 300000, "ab" at 500000 / 600000 / 700000 and a
+    # 32-space piece at 100000, so the best split flips between "ab" and "a"+"b" and the
+    # space run's split moves across 95-97 spaces
+    import plamo_hip
+    recs = _records()
+    ids = {p: i for i, r in enumerate(recs) if r and (p := r[0]) in ("a", "b", "ab")}
+    spare = next(i for i, r in enumerate(recs) if r[2] == "NORMAL" and ord(r[0][0]) >= 0xF0000)
+    recs[ids["a"]] = ["a", 300000, "NORMAL"]
+    recs[ids["b"]] = ["b", 300000, "NORMAL"]
+    recs[spare] = [" " * 32, 100000, "NORMAL"]
+    texts = ["ab" * 129 + "a", " " * 95, " " * 96, " " * 97]
+    for score in (500000, 600000, 700000):
+        for i, r in enumerate(recs):
+            if r[0] == "ab":
+                recs[i] = ["ab", score, "NORMAL"]
+        path = tmp_path / f"tok{score}.jsonl"
+        _write(path, recs)
+        v = T.Vocab(str(path))
+        tok = plamo_hip.Tokenizer(str(path))
+        try:
+            for text in texts:
+                assert tok.encode(text) == T.encode(v, text), (score, len(text))
+            # the split flips: "a" + "b" (600000) beats "ab" at 500000; at the 600000 tie the
+            # longer piece wins, as above 600000
+            pair = T.encode(v, "ab")
+            assert (pair == [v.lookup["ab"]]) == (score >= 600000), score
+        finally:
+            tok.close()
