@@ -1,7 +1,8 @@
 """Kernel-level parity on the GPU through the C-ABI kernel entry points.
 
 Known answers from the reference's kernel tests (PackedDecodeTests, ArgmaxTests,
-SamplerTests, PlamoTests.testMetalLinearAndMatrix) plus packed == plain bit equality and
+SamplerTests, PlamoTests.testMetalLinearAndMatrix) plus packed == plain bit equality
+(PackedTests.swift:6-46: one- and multi-row products of .p12 and raw weights) and
 FP32 references for the GEMV/GEMM.  Device memory comes from torch (plumbing only).
 """
 import numpy as np

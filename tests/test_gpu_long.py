@@ -143,8 +143,12 @@ def test_long_context_runs_to_the_cap_bit_exact(long_runtime, oracle_weights):
             generated.append(t)
             rt.observe(t)
         assert rt.position == 32768
+        # MaximumTests.swift:69-72: past the cap a forward is refused, the position and the
+        # logits stay
+        last = rt.logit_bits().copy()
         with pytest.raises(plamo_hip.PlamoError, match="context exhausted"):
             rt.forward([t])
+        assert rt.position == 32768 and np.array_equal(rt.logit_bits(), last)
         for layer in range(16):
             k, v = rt.kv(layer)
             slots = [p % k.shape[0] for p in range(start, 32768)]
