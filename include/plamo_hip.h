@@ -98,9 +98,10 @@ int plamo_forward(plamo_runtime* rt, const int32_t* tokens, int32_t count, int32
 /* Runtime.forward(_:output:all:sequential:) (Runtime.swift:322-467).  `all`: every row's
  * logits (slots 0 .. count-1 of plamo_logits) and prediction (plamo_predictions);
  * `sequential`: each row takes the local RoPE coordinates of a scalar decode step
- * (Kernels.metal:288-298), so its outputs equal count single-token forwards.  Both need an
- * MTP runtime and count <= 2 (Runtime.verifyRows), else "Invalid tokens or context
- * exhausted". */
+ * (Kernels.metal:288-298), so its outputs equal count single-token forwards; with `all`,
+ * two rows and no sampling controls or QSA they run as one pass over the weights (the
+ * reference's linear_pair pass, Runtime.swift:370-371).  Both need an MTP runtime and
+ * count <= 2 (Runtime.verifyRows), else "Invalid tokens or context exhausted". */
 int plamo_forward_ex(plamo_runtime* rt, const int32_t* tokens, int32_t count, int32_t output, int32_t all,
                      int32_t sequential, int32_t* next, char* err, size_t errlen);
 
