@@ -10,6 +10,8 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(os.path.dirname(_HERE), "lib", "libplamo_hip.so")
 # the same library with the step timeline compiled in (make timeline)
 TIMELINE_LIB_PATH = os.path.join(os.path.dirname(_HERE), "lib", "libplamo_hip_timeline.so")
+# the host code built with AddressSanitizer (make asan; needs the sanitizer runtime preloaded)
+ASAN_LIB_PATH = os.path.join(os.path.dirname(_HERE), "lib", "libplamo_hip_asan.so")
 HEADER_PATH = os.path.join(os.path.dirname(os.path.dirname(_HERE)), "include", "plamo_hip.h")
 
 VOCAB, HIDDEN = 107520, 1536
