@@ -5,6 +5,8 @@
 
 #include <cstdint>
 
+#include "common.h"
+
 namespace plamo {
 
 enum GemmEpilogue { GEMM_F32 = 0, GEMM_BF16 = 1, GEMM_SWIGLU = 2, GEMM_RAW = 3 };
@@ -53,6 +55,26 @@ constexpr int FLASH_PARTS = 3;
 constexpr int FLASH_PART_TILES = 11;         // 64-key tiles a part aims at
 __host__ __device__ inline int flash_blocks(int tokens) { return (tokens + 7) / 8; }
 // workspace floats: per block and part, O^T [128 columns][128 dims] and (m, l) per column
+// Key tiles (64 keys) that query block qb of a call attends to, and the parts they are split
+// into (contiguous tile ranges, part q from q * tiles / parts).
+__host__ __device__ inline int flash_block_tiles(int tokens, uint32_t p0, int full, int qb) {
+    const int t0 = qb * 8, t1 = t0 + 8 < tokens ? t0 + 8 : tokens;
+    const uint32_t plo = p0 + uint32_t(t0), khi = p0 + uint32_t(t1 - 1);
+    const uint32_t klo = full ? 0u : (plo > uint32_t(WINDOW - 1) ? plo - uint32_t(WINDOW - 1) : 0u);
+    return int((khi + 1 - klo + 63) / 64);
+}
+__host__ __device__ inline int flash_block_parts(int tiles) {
+    const int parts = (tiles + FLASH_PART_TILES - 1) / FLASH_PART_TILES;
+    return parts < FLASH_PARTS ? parts : FLASH_PARTS;
+}
+// The order in which workgroups take the (query block, part) items of a call: item w of the
+// launch is item[w] (qb << 2 | part).  n = 0: workgroup w takes part w / blocks of block
+// blocks - 1 - w % blocks (and returns if the block has fewer parts).
+constexpr int FLASH_SCHEDULE_MAX = 768;  // the items of a 2048-token call, at most
+struct FlashSchedule {
+    uint32_t n;
+    uint16_t item[FLASH_SCHEDULE_MAX];
+};
 inline size_t flash_part_o_floats(int tokens) { return size_t(flash_blocks(tokens)) * FLASH_PARTS * 128 * 128; }
 inline size_t flash_part_ml_floats(int tokens) { return size_t(flash_blocks(tokens)) * FLASH_PARTS * 128 * 2; }
 
