@@ -544,6 +544,11 @@ __global__ __launch_bounds__(256) void qk_prep_kernel(const QkPrepParams p) {
 // from `exp2_det` and nothing is contracted, so every output is a fixed function of the
 // inputs that a CPU restatement reproduces bit for bit.
 //
+// Two kernels share that arithmetic: the staged one (K/V tiles through registers into K rows
+// and V^T in LDS; the only one that can rotate keys while staging) and the direct one (K/V
+// tiles loaded straight into LDS, V^T operands by transposing LDS reads), used when no block
+// of a call rotates its keys: global layers, and local layers inside the rotated-key cache.
+//
 // Keys of local layers are rotated while staged, with coordinate key_pos - base of the
 // workgroup's 16-token chunk (base = max(0, chunk_start - 2047)); where base is 0 and every
 // key of the block lies in the rotated-key cache, that coordinate is the key's position and
@@ -551,6 +556,11 @@ __global__ __launch_bounds__(256) void qk_prep_kernel(const QkPrepParams p) {
 constexpr int FT = 8;                 // tokens per query block (workgroup)
 constexpr int FK = 64;                // keys per tile
 static_assert(FT == 8 && FK == 64, "flash_block_tiles (prefill.h) assumes these sizes");
+// Direct path row strides (BF16 elements): key rows of 272 bytes (17 16-byte chunks, the
+// last one padding: consecutive rows start 4 banks apart), value rows of 320 bytes (20
+// chunks: 16 banks apart)
+constexpr int DK_ROW = 136, DV_ROW = 160;
+constexpr int DK_CHUNKS = DK_ROW / 8, DV_CHUNKS = DV_ROW / 8;
 constexpr int KST = HEAD_DIM + 8;     // K tile row stride (BF16), 16-byte aligned rows
 constexpr int VST = FK + 4;           // V^T tile row stride (BF16): 34 dwords, so 16 lanes reading
                                       // 8 bytes from 16 consecutive rows hit 32 distinct banks
@@ -654,11 +664,17 @@ __device__ __forceinline__ void split_bf16(float a, float b, uint32_t& hw, uint3
 
 // Part `part` of query block qb.  QSA: global layers with a selection bitmap (a separate
 // instance, so the dense kernel's edge tiles carry no bitmap test).
-template <bool QSA>
+template <bool QSA, bool DIRECT>
 __device__ __forceinline__ void flash_prefill(const FlashParams& p, const int qb, const int part) {
 #pragma clang fp contract(off)  // fixed rounding sequence, reproduced by the CPU oracle
-    __shared__ __align__(16) uint16_t Ks[2][FK * KST];
-    __shared__ __align__(16) uint16_t Vt[2][HEAD_DIM * VST];
+    // four distinct arrays (the compiler then tells the buffers apart and waits for the loads
+    // into one of them only before reading that one): K and V^T tiles of the staged path, or K
+    // and V tiles of the direct path, double-buffered
+    static_assert(FK * KST == FK * DK_ROW && HEAD_DIM * VST <= FK * DV_ROW, "tile buffers");
+    __shared__ __align__(1024) uint16_t L0[FK * DK_ROW];
+    __shared__ __align__(1024) uint16_t L1[FK * DK_ROW];
+    __shared__ __align__(1024) uint16_t L2[FK * DV_ROW];
+    __shared__ __align__(1024) uint16_t L3[FK * DV_ROW];
     __shared__ int s_last;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int col = lane & 31, half = lane >> 5;
@@ -700,33 +716,19 @@ __device__ __forceinline__ void flash_prefill(const FlashParams& p, const int qb
     const uint32_t qcomplete = (qpos + 1) / 4;
     const bool cached = !p.full && p.keys_rot != nullptr && base == 0 && khi < p.rot_rows;
     const KvSource src{cached ? p.keys_rot : p.keys, !p.full && !cached};
-    KvStage st;
-    flash_load(p, src, klo + uint32_t(j0 * FK), khi, base, st);
-    flash_store(src, st, Ks[0], Vt[0]);
-    __syncthreads();
-    for (int j = j0; j < j1; ++j) {
-        const int buf = (j - j0) & 1;
+
+    // Online softmax of tile j in the base-2 domain: x = score * scale * log2(e),
+    // p = 2^(x - max).  Element i of tile r is key k0 + 32r + 8(i/4) + 4*half + i%4.  Only
+    // tiles that cross a query's causal edge or window start need the mask.  QSA: every tile
+    // is masked by the query's selected blocks (its unfinished block is always seen).  Leaves
+    // the probabilities in sacc and rescales oacc.
+    // Online softmax of tile j in the base-2 domain: x = score * scale * log2(e),
+    // p = 2^(x - max).  Element i of tile r is key k0 + 32r + 8(i/4) + 4*half + i%4.  Only
+    // tiles that cross a query's causal edge or window start need the mask.  QSA: every tile
+    // is masked by the query's selected blocks (its unfinished block is always seen).  Leaves
+    // the probabilities in sacc and rescales oacc.
+    auto softmax = [&](int j, floatx16 (&sacc)[2]) {
         const uint32_t k0 = klo + uint32_t(j * FK);
-        if (j + 1 < j1) flash_load(p, src, k0 + FK, khi, base, st);
-        // S^T = K Q^T for 64 keys (two 32-row tiles)
-        floatx16 sacc[2];
-#pragma unroll
-        for (int r = 0; r < 2; ++r)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) sacc[r][i] = 0.f;
-#pragma unroll
-        for (int s = 0; s < 8; ++s) {
-#pragma unroll
-            for (int r = 0; r < 2; ++r) {
-                const bf16x8 a = as_bf16x8(*reinterpret_cast<const uint4*>(&Ks[buf][(r * 32 + col) * KST + 16 * s + 8 * half]));
-                sacc[r] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[s], sacc[r], 0, 0, 0);
-            }
-        }
-        // Online softmax in the base-2 domain: x = score * scale * log2(e), p = 2^(x - max).
-        // Element i of tile r is key k0 + 32r + 8(i/4) + 4*half + i%4.  Only tiles that cross
-        // a query's causal edge or window start need the mask.
-        // QSA: every tile is masked by the query's selected blocks (its unfinished block is
-        // always seen)
         const bool edge = QSA || !(k0 + uint32_t(FK - 1) <= plo && (p.full || k0 + uint32_t(WINDOW - 1) >= khi));
         float mt = NEG_INF;
         if (edge) {
@@ -782,7 +784,10 @@ __device__ __forceinline__ void flash_prefill(const FlashParams& p, const int qb
 #pragma unroll
                 for (int i = 0; i < 16; ++i) oacc[dt][i] *= alpha;
         }
-        // O^T += V^T P^T; k-step s takes keys 16s + 4*half + {0..3} and 16s + 8 + 4*half + {0..3}
+    };
+    // O^T += V^T P^T; k-step s takes keys 16s + 4*half + {0..3} and 16s + 8 + 4*half + {0..3};
+    // vt(dt, s) returns the V^T operand of d-tile dt at k-step s
+    auto pv = [&](const floatx16 (&sacc)[2], auto vt) {
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
             const int r = s >> 1, i0 = (s & 1) * 8;
@@ -793,16 +798,164 @@ __device__ __forceinline__ void flash_prefill(const FlashParams& p, const int qb
             const bf16x8 pl = as_bf16x8(make_uint4(lw[0], lw[1], lw[2], lw[3]));
 #pragma unroll
             for (int dt = 0; dt < 4; ++dt) {
-                const uint16_t* vrow = &Vt[buf][(dt * 32 + col) * VST + 16 * s + 4 * half];
-                const uint2 x0 = *reinterpret_cast<const uint2*>(vrow);
-                const uint2 x1 = *reinterpret_cast<const uint2*>(vrow + 8);
-                const bf16x8 a = as_bf16x8(make_uint4(x0.x, x0.y, x1.x, x1.y));
+                const bf16x8 a = vt(dt, s);
                 oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, ph, oacc[dt], 0, 0, 0);
                 oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pl, oacc[dt], 0, 0, 0);
             }
         }
-        if (j + 1 < j1) flash_store(src, st, Ks[buf ^ 1], Vt[buf ^ 1]);
+    };
+    // S^T = K Q^T for 64 keys (two 32-row tiles); kop(r, s) returns the K operand of row tile
+    // r at k-step s
+    auto qk = [&](floatx16 (&sacc)[2], auto kop) {
+#pragma unroll
+        for (int r = 0; r < 2; ++r)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) sacc[r][i] = 0.f;
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+#pragma unroll
+            for (int r = 0; r < 2; ++r) sacc[r] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kop(r, s), qf[s], sacc[r], 0, 0, 0);
+        }
+    };
+
+    if constexpr (!DIRECT) {
+        // staged through registers (keys rotated on the way where the block needs it): K rows
+        // and V^T in LDS
+        KvStage st;
+        flash_load(p, src, klo + uint32_t(j0 * FK), khi, base, st);
+        flash_store(src, st, L0, L2);
         __syncthreads();
+        for (int j = j0; j < j1; ++j) {
+            const bool odd = ((j - j0) & 1) != 0;
+            const uint16_t* Kc = odd ? L1 : L0;
+            const uint16_t* Vc = odd ? L3 : L2;
+            if (j + 1 < j1) flash_load(p, src, klo + uint32_t((j + 1) * FK), khi, base, st);
+            floatx16 sacc[2];
+            qk(sacc, [&](int r, int s) {
+                return as_bf16x8(*reinterpret_cast<const uint4*>(&Kc[(r * 32 + col) * KST + 16 * s + 8 * half]));
+            });
+            softmax(j, sacc);
+            pv(sacc, [&](int dt, int s) {
+                const uint16_t* vrow = &Vc[(dt * 32 + col) * VST + 16 * s + 4 * half];
+                const uint2 x0 = *reinterpret_cast<const uint2*>(vrow);
+                const uint2 x1 = *reinterpret_cast<const uint2*>(vrow + 8);
+                return as_bf16x8(make_uint4(x0.x, x0.y, x1.x, x1.y));
+            });
+            if (j + 1 < j1) flash_store(src, st, odd ? L0 : L1, odd ? L2 : L3);
+            __syncthreads();
+        }
+    } else {
+        // (DIRECT: the launch holds only blocks whose keys need no rotation)
+        // Keys (already rotated) and values loaded straight into LDS (buffer loads with the
+        // LDS destination, no staging registers), in padded rows: key row R at R * 272 bytes
+        // (the S^T operand reads of 16 consecutive rows hit every bank), value row R at
+        // R * 320 bytes (the transposing V^T operand reads, ds_read_b64_tr_b16, of four rows x
+        // 64 bytes per half wave hit every bank).  Every operand read is one base address plus
+        // an immediate offset.  Tile j's keys and values go to buffer (j - j0) % 2 (L0/L1
+        // keys, L2/L3 values) and are requested at the start of tile j - 1.  Same arithmetic
+        // as the staged path.
+        // A tile is loaded as 16-byte chunks: chunk L of the tile (row L / chunks per row,
+        // piece L % chunks per row, pieces past 15 being padding) is lane L % 64 of load L / 64;
+        // wave w issues loads w, w + 4, ...  Its lanes' offsets within the tile are fixed: a
+        // tile whose 64 keys are consecutive ring slots without a wrap adds the first slot as
+        // a scalar offset; the last tile of a block (keys past khi load key khi) and tiles
+        // across the ring's end take per-lane slots.
+        constexpr int KLOADS = FK * DK_CHUNKS / 64, VLOADS = FK * DV_CHUNKS / 64;  // 17, 20
+        constexpr int KPER = (KLOADS + 3) / 4, VPER = VLOADS / 4;                 // 5, 5
+        static_assert(VLOADS % 4 == 0 && FK * DK_CHUNKS % 64 == 0, "tile loads");
+        const uint32_t krows = cached ? p.rot_rows : p.capacity;
+        const __amdgpu_buffer_rsrc_t kview = buffer_view(src.keys, krows * uint32_t(HEAD_DIM * 2));
+        const __amdgpu_buffer_rsrc_t vview = buffer_view(p.values, p.capacity * uint32_t(HEAD_DIM * 2));
+        // per load t of this wave: row (bits 0..7) and piece (bits 8..15) of this lane's chunk
+        uint32_t kpiece[KPER], vpiece[VPER];
+#pragma unroll
+        for (int t = 0; t < KPER; ++t) {
+            const int L = 64 * (wave + 4 * t) + lane;
+            kpiece[t] = uint32_t(L / DK_CHUNKS) | (uint32_t(L % DK_CHUNKS) << 8);
+        }
+#pragma unroll
+        for (int t = 0; t < VPER; ++t) {
+            const int L = 64 * (wave + 4 * t) + lane;
+            vpiece[t] = uint32_t(L / DV_CHUNKS) | (uint32_t(L % DV_CHUNKS) << 8);
+        }
+        auto tile_load = [&](const __amdgpu_buffer_rsrc_t view, uint16_t* dst, const uint32_t* piece, auto nloads,
+                             auto row_elems, int j, bool by_position) {
+            constexpr int N = decltype(nloads)::value, RE = decltype(row_elems)::value;
+            const uint32_t k0 = klo + uint32_t(j * FK);
+            const uint32_t slot0 = by_position ? k0 : k0 % p.capacity;
+            const bool plain = k0 + uint32_t(FK - 1) <= khi && (by_position || slot0 + uint32_t(FK - 1) < p.capacity);
+#pragma unroll
+            for (int t = 0; t < N; ++t) {
+                const int li = wave + 4 * t;
+                if (li * 64 >= FK * (RE / 8)) break;
+                const uint32_t row = piece[t] & 255u, pc = piece[t] >> 8;
+                uint32_t off;
+                if (plain) {
+                    off = row * uint32_t(HEAD_DIM * 2) + pc * 16u;
+                } else {
+                    const uint32_t kp = min(k0 + row, khi);
+                    uint32_t slot = by_position ? kp : slot0 + (kp - k0);
+                    slot = slot >= p.capacity && !by_position ? slot - p.capacity : slot;
+                    off = slot * uint32_t(HEAD_DIM * 2) + pc * 16u;
+                }
+                off = pc < 16u ? off : OOB_OFFSET;  // padding: nothing to load
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(view, (lds_ptr_t)(dst + li * 512), 16, off,
+                                                         plain ? int(slot0 * uint32_t(HEAD_DIM * 2)) : 0, 0, 0);
+            }
+        };
+        using KN = std::integral_constant<int, KPER>;
+        using VN = std::integral_constant<int, VPER>;
+        using KR = std::integral_constant<int, DK_ROW>;
+        using VR = std::integral_constant<int, DV_ROW>;
+        auto dma_k = [&](uint16_t* dst, int j) { tile_load(kview, dst, kpiece, KN{}, KR{}, j, cached || p.full); };
+        auto dma_v = [&](uint16_t* dst, int j) { tile_load(vview, dst, vpiece, VN{}, VR{}, j, false); };
+        // S^T operand of row tile r, k-step s: key row 32r + col, dims 16s + 8 half .. + 8
+        auto kop_of = [&](const uint16_t* Kb) {
+            const uint16_t* base = Kb + col * DK_ROW + 8 * half;
+            return [=](int r, int s) {
+                return as_bf16x8(*reinterpret_cast<const uint4*>(base + 32 * r * DK_ROW + 16 * s));
+            };
+        };
+        // V^T operand of d-tile dt, k-step s: source lane sl = lane % 16 of 16-lane group g =
+        // lane / 16 addresses keys 16s + 4(g / 2) + sl / 4 (and + 8), dims 32dt + 16(g % 2) +
+        // 4(sl % 4) .. + 3; the transposing read hands lane j of the group element j % 4 of
+        // source lane 4t + j / 4 as its element t: dim 32dt + 16(g % 2) + j of keys 16s + 4(g / 2)
+        // + t (and + 8 + t), the rows of the P^T operand's k-step s
+        typedef short short4_t __attribute__((ext_vector_type(4)));
+        typedef __attribute__((address_space(3))) short4_t* tr_ptr_t;
+        const int sl = lane & 15, grp = lane >> 4;
+        const int vlane = (4 * (grp >> 1) + (sl >> 2)) * DV_ROW + 16 * (grp & 1) + 4 * (sl & 3);
+        auto vop_of = [&](const uint16_t* Vb) {
+            const uint16_t* base = Vb + vlane;
+            return [=](int dt, int s) {
+                const short4_t x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((tr_ptr_t)(base + 16 * s * DV_ROW + 32 * dt));
+                const short4_t x1 =
+                    __builtin_amdgcn_ds_read_tr16_b64_v4i16((tr_ptr_t)(base + (16 * s + 8) * DV_ROW + 32 * dt));
+                bf16x8 a;
+                __builtin_memcpy(&a, &x0, 8);
+                __builtin_memcpy(reinterpret_cast<char*>(&a) + 8, &x1, 8);
+                return a;
+            };
+        };
+        // tile j: its keys and values are in Kc / Vc; the next tile's go to Kn / Vn (free:
+        // read by tile j - 1 before this tile's barrier)
+        auto tile = [&](int j, const uint16_t* Kc, uint16_t* Kn, const uint16_t* Vc, uint16_t* Vn) {
+            __syncthreads();  // tile j is in; tile j - 1 is done with Kn and Vn
+            if (j + 1 < j1) {
+                dma_k(Kn, j + 1);
+                dma_v(Vn, j + 1);
+            }
+            floatx16 sacc[2];
+            qk(sacc, kop_of(Kc));
+            softmax(j, sacc);
+            pv(sacc, vop_of(Vc));
+        };
+        dma_k(L0, j0);
+        dma_v(L2, j0);
+        for (int j = j0; j < j1; j += 2) {
+            tile(j, L0, L1, L2, L3);
+            if (j + 1 < j1) tile(j + 1, L1, L0, L3, L2);
+        }
     }
     // O = O^T / l; element i of d-tile dt is dim 32dt + 8(i/4) + 4*half + i%4
     float lt = ls + xor_lane<32>(ls);
@@ -884,17 +1037,17 @@ __device__ __forceinline__ void flash_prefill(const FlashParams& p, const int qb
 // Workgroup w takes part w / blocks of query block blocks - 1 - w % blocks (consecutive
 // workgroups, dealt round-robin to the XCDs, take different blocks; a block's parts share an
 // XCD) and returns if the block has fewer parts.
-template <bool QSA>
+template <bool QSA, bool DIRECT>
 __global__ __launch_bounds__(256, 2) void flash_prefill_kernel(const FlashParams p) {
     const int nqb = flash_blocks(p.tokens);
-    flash_prefill<QSA>(p, nqb - 1 - int(blockIdx.x) % nqb, int(blockIdx.x) / nqb);
+    flash_prefill<QSA, DIRECT>(p, nqb - 1 - int(blockIdx.x) % nqb, int(blockIdx.x) / nqb);
 }
 
 // Workgroup w takes the item the host's schedule ranks for it (qb << 2 | part).
-template <bool QSA>
+template <bool QSA, bool DIRECT>
 __global__ __launch_bounds__(256, 2) void flash_prefill_ranked_kernel(const FlashParams p, const FlashSchedule sched) {
     const uint32_t item = sched.item[blockIdx.x];
-    flash_prefill<QSA>(p, int(item >> 2), int(item & 3u));
+    flash_prefill<QSA, DIRECT>(p, int(item >> 2), int(item & 3u));
 }
 
 template <int BT, int BW, int WT, int NT, int KD, int NS>
@@ -1038,16 +1191,27 @@ void launch_flash_prefill(const FlashParams& p, hipStream_t s) {
     FlashSchedule sched;
     sched.n = 0;
     if (flash_blocks(p.tokens) * FLASH_PARTS <= FLASH_SCHEDULE_MAX) flash_schedule(p, sched);
+    // keys straight into LDS when no block of the call rotates its keys: global layers, and
+    // local layers whose keys all sit in the rotated-key cache (window base 0)
+    const uint32_t last = p.p0 + uint32_t(p.tokens) - 1;
+    const bool direct = p.capacity >= uint32_t(FK) &&
+                        (p.full || (p.keys_rot != nullptr && last < p.rot_rows && last < uint32_t(WINDOW)));
     const dim3 block(256);
     if (sched.n) {
         // the schedule travels in the kernel arguments (1.5 KB): only the launches that use it
         const dim3 grid(sched.n);
-        if (qsa) hipLaunchKernelGGL(flash_prefill_ranked_kernel<true>, grid, block, 0, s, p, sched);
-        else hipLaunchKernelGGL(flash_prefill_ranked_kernel<false>, grid, block, 0, s, p, sched);
+#define PLAMO_FLASH(Q, D) hipLaunchKernelGGL((flash_prefill_ranked_kernel<Q, D>), grid, block, 0, s, p, sched)
+        if (qsa) PLAMO_FLASH(true, true);
+        else if (direct) PLAMO_FLASH(false, true);
+        else PLAMO_FLASH(false, false);
+#undef PLAMO_FLASH
     } else {
         const dim3 grid(uint32_t(flash_blocks(p.tokens) * FLASH_PARTS));
-        if (qsa) hipLaunchKernelGGL(flash_prefill_kernel<true>, grid, block, 0, s, p);
-        else hipLaunchKernelGGL(flash_prefill_kernel<false>, grid, block, 0, s, p);
+#define PLAMO_FLASH(Q, D) hipLaunchKernelGGL((flash_prefill_kernel<Q, D>), grid, block, 0, s, p)
+        if (qsa) PLAMO_FLASH(true, true);
+        else if (direct) PLAMO_FLASH(false, true);
+        else PLAMO_FLASH(false, false);
+#undef PLAMO_FLASH
     }
 }
 
