@@ -1,6 +1,7 @@
 """The host code under AddressSanitizer: the safetensors, .p12 and auxiliary readers, the .p12
 packer, the tokenizer and its stream, the document plan and the C ABI's argument checks
-(everything the no-GPU tests reach through the library) run in a child process against
+(everything the no-GPU tests reach through the library, and the seeded mutations of every
+file format in tests/test_host_fuzz.py) run in a child process against
 lib/libplamo_hip_asan.so (`make asan`: host units built with -fsanitize=address, device
 objects unchanged), with the sanitizer runtime preloaded.  Any report fails the child.
 """
@@ -41,7 +42,7 @@ def test_host_code_is_clean_under_asan():
             "assert any(native.ASAN_LIB_PATH in l for l in open('/proc/self/maps'))\n"
             "sys.exit(pytest.main(['-q', '-x', '-p', 'no:cacheprovider', '-m', 'not gpu',\n"
             "                      'tests/test_native_cpu.py', 'tests/test_tokenizer.py',\n"
-            "                      'tests/test_ordered.py', 'tests/test_cli.py']))\n")
+            "                      'tests/test_ordered.py', 'tests/test_cli.py', 'tests/test_host_fuzz.py']))\n")
     run = subprocess.run([sys.executable, "-c", code], cwd=ROOT, env=env, capture_output=True, text=True,
                          timeout=900)
     tail = run.stdout[-3000:] + run.stderr[-3000:]
