@@ -118,7 +118,7 @@ void write_outputs(const std::vector<LaneOutput>& res, int32_t* ids, int32_t str
     for (size_t i = 0; i < res.size(); ++i) {
         const int n = int(res[i].ids.size());
         if (n > stride) throw plamo::Error(plamo::E_INVAL, "output buffer too small");
-        if (ids) std::memcpy(ids + i * size_t(stride), res[i].ids.data(), size_t(n) * 4);
+        if (ids && n > 0) std::memcpy(ids + i * size_t(stride), res[i].ids.data(), size_t(n) * 4);
         if (lengths) lengths[i] = n;
         if (reasons) reasons[i] = res[i].reason;
     }
@@ -368,7 +368,7 @@ int plamo_batch_prefill(plamo_batch* b, const int32_t* tokens, const int32_t* le
     return guard(err, errlen, [&] {
         if (!b) throw plamo::Error(plamo::E_INVAL, "null argument");
         auto res = b->impl->prefill(split_prompts(tokens, lengths, count));
-        if (next) std::memcpy(next, res.data(), res.size() * 4);
+        if (next && !res.empty()) std::memcpy(next, res.data(), res.size() * 4);
     });
 }
 
@@ -376,7 +376,7 @@ int plamo_batch_step(plamo_batch* b, const int32_t* tokens, int32_t count, int32
     return guard(err, errlen, [&] {
         if (!b || !tokens || count < 0) throw plamo::Error(plamo::E_INVAL, "Invalid quad step or context exhausted");
         auto res = b->impl->step(std::vector<int32_t>(tokens, tokens + count));
-        if (next) std::memcpy(next, res.data(), res.size() * 4);
+        if (next && !res.empty()) std::memcpy(next, res.data(), res.size() * 4);
     });
 }
 

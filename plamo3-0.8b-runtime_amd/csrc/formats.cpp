@@ -461,7 +461,7 @@ PackReport pack_archive(const std::string& source, const std::string& output, co
                 const size_t count = view.bytes / 2;
                 if (count % 128) throw Error(E_FORMAT, "Tensor size is not a multiple of 128: " + name);
                 std::vector<uint16_t> values(count);
-                std::memcpy(values.data(), view.data, view.bytes);
+                if (count) std::memcpy(values.data(), view.data, view.bytes);
                 std::vector<uint32_t> entries;
                 int64_t compressed = 0;
                 auto data = pack_blocks(values.data(), count, entries, &compressed);

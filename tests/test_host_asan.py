@@ -1,9 +1,10 @@
-"""The host code under AddressSanitizer: the safetensors, .p12 and auxiliary readers, the .p12
-packer, the tokenizer and its stream, the document plan and the C ABI's argument checks
-(everything the no-GPU tests reach through the library, and the seeded mutations of every
-file format in tests/test_host_fuzz.py) run in a child process against
-lib/libplamo_hip_asan.so (`make asan`: host units built with -fsanitize=address, device
-objects unchanged), with the sanitizer runtime preloaded.  Any report fails the child.
+"""The host code under AddressSanitizer and UndefinedBehaviorSanitizer: the safetensors,
+.p12 and auxiliary readers, the .p12 packer, the tokenizer and its stream, the document plan
+and the C ABI's argument checks (everything the no-GPU tests reach through the library, and
+the seeded mutations of every file format in tests/test_host_fuzz.py) run in a child
+process against lib/libplamo_hip_asan.so (`make asan`: host units built with
+-fsanitize=address,undefined, device objects unchanged), with the sanitizer runtime
+preloaded.  Any report fails the child.
 """
 import os
 import shutil
@@ -34,6 +35,7 @@ def test_host_code_is_clean_under_asan():
     build = subprocess.run(["make", "-C", PKG, "-j8", "asan"], capture_output=True, text=True)
     assert build.returncode == 0, build.stdout[-2000:] + build.stderr[-2000:]
     env = dict(os.environ, LD_PRELOAD=runtime, ASAN_OPTIONS="detect_leaks=0:abort_on_error=1",
+               UBSAN_OPTIONS="print_stacktrace=1:halt_on_error=1",
                PYTHONPATH=os.pathsep.join([ROOT, PKG]))
     code = ("import sys, pytest\n"
             "from plamo_hip import native\n"
@@ -47,5 +49,5 @@ def test_host_code_is_clean_under_asan():
                          timeout=900)
     tail = run.stdout[-3000:] + run.stderr[-3000:]
     assert run.returncode == 0, tail
-    assert "AddressSanitizer" not in run.stderr, tail
+    assert "AddressSanitizer" not in run.stderr and "runtime error" not in run.stderr, tail
     print("  " + run.stdout.strip().splitlines()[-1])
