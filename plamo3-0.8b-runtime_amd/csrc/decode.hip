@@ -423,9 +423,6 @@ __device__ __forceinline__ uint4 stream_load16(const void* p) {
     const v4 v = __builtin_nontemporal_load(reinterpret_cast<const v4*>(p));
     return make_uint4(v[0], v[1], v[2], v[3]);
 }
-__device__ __forceinline__ uint32_t stream_load4(const void* p) {
-    return __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p));
-}
 __device__ __forceinline__ uint2 stream_load8(const void* p) {
     typedef uint32_t v2 __attribute__((ext_vector_type(2)));
     const v2 v = __builtin_nontemporal_load(reinterpret_cast<const v2*>(p));
