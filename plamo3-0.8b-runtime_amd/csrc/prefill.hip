@@ -395,6 +395,11 @@ __global__ __launch_bounds__(256) void rows_norm_kernel(const RowsNormParams p) 
     };
     float xv[C][8];
     const size_t row = size_t(t) * HIDDEN;
+    // the next norm's gains are requested with the row's inputs (off the reductions' path)
+    uint4 gnw[C];
+#pragma unroll
+    for (int c = 0; c < C; ++c)
+        gnw[c] = p.xn ? *reinterpret_cast<const uint4*>(p.g_next + 512 * c + 8 * lane) : make_uint4(0, 0, 0, 0);
     if (p.tokens_in) {
         int tok = p.tokens_in[t];
         tok = (tok < 0 || tok >= VOCAB) ? 0 : tok;
@@ -440,7 +445,7 @@ __global__ __launch_bounds__(256) void rows_norm_kernel(const RowsNormParams p) 
         const int i = 512 * c + 8 * lane;
         uint32_t xw[4], nw[4];
         float gn[8];
-        if (p.xn) unpack(*reinterpret_cast<const uint4*>(p.g_next + i), gn);
+        unpack(gnw[c], gn);
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             xw[k] = pack_bf16(xv[c][2 * k], xv[c][2 * k + 1]);  // BF16 values: exact
@@ -477,6 +482,20 @@ __global__ __launch_bounds__(256) void qk_prep_kernel(const QkPrepParams p) {
         const uint2 w = *reinterpret_cast<const uint2*>(s);
         return make_float4(lo(w.x), hi(w.x), lo(w.y), hi(w.y));
     };
+    // the key part's inputs (threads 0..15) are requested with the queries'
+    const bool kthread = tid < 16;
+    const bool krot = !p.full && p.keys_rot && pos < p.rot_rows;
+    float4 klo = make_float4(0.f, 0.f, 0.f, 0.f), khi = klo;
+    uint2 kgl = make_uint2(0, 0), kgh = kgl;
+    uint4 kr4 = make_uint4(0, 0, 0, 0);
+    if (kthread) {
+        klo = load4(x + ATTN + tid * 4);
+        khi = load4(x + ATTN + 64 + tid * 4);
+        kgl = *reinterpret_cast<const uint2*>(p.k_norm + tid * 4);
+        kgh = *reinterpret_cast<const uint2*>(p.k_norm + 64 + tid * 4);
+        if (p.full || krot)
+            kr4 = *reinterpret_cast<const uint4*>((p.full ? p.global_rope : p.local_rope) + size_t(pos) * 64 + tid * 4);
+    }
     {
         const float4 qlo = load4(x + hq * HEAD_DIM + sq * 4);
         const float4 qhi = load4(x + hq * HEAD_DIM + 64 + sq * 4);
@@ -494,22 +513,15 @@ __global__ __launch_bounds__(256) void qk_prep_kernel(const QkPrepParams p) {
         *reinterpret_cast<uint2*>(qo + 64 + sq * 4) = make_uint2(pack_bf16(z[4], z[5]), pack_bf16(z[6], z[7]));
     }
     const size_t slot = size_t(pos % p.capacity) * HEAD_DIM;
-    if (tid < 16) {
-        const float4 klo = load4(x + ATTN + tid * 4);
-        const float4 khi = load4(x + ATTN + 64 + tid * 4);
-        const uint2 gl = *reinterpret_cast<const uint2*>(p.k_norm + tid * 4);
-        const uint2 gh = *reinterpret_cast<const uint2*>(p.k_norm + 64 + tid * 4);
+    if (kthread) {
         float z[8];
-        head_norm8(klo, khi, gl, gh, z);
+        head_norm8(klo, khi, kgl, kgh, z);
+        const uint32_t c4[4] = {kr4.x, kr4.y, kr4.z, kr4.w};
         if (p.full) {
-            const uint4 gr = *reinterpret_cast<const uint4*>(p.global_rope + size_t(pos) * 64 + tid * 4);
-            const uint32_t c4[4] = {gr.x, gr.y, gr.z, gr.w};
 #pragma unroll
             for (int j = 0; j < 4; j += 2) rope_pair_x2f(z[j], z[4 + j], c4[j], z[j + 1], z[4 + j + 1], c4[j + 1]);
-        } else if (p.keys_rot && pos < p.rot_rows) {
+        } else if (krot) {
             // the copy rotated at the key's own position (decode inside the first window)
-            const uint4 lr = *reinterpret_cast<const uint4*>(p.local_rope + size_t(pos) * 64 + tid * 4);
-            const uint32_t c4[4] = {lr.x, lr.y, lr.z, lr.w};
             float zr[8] = {z[0], z[1], z[2], z[3], z[4], z[5], z[6], z[7]};
 #pragma unroll
             for (int j = 0; j < 4; j += 2) rope_pair_x2f(zr[j], zr[4 + j], c4[j], zr[j + 1], zr[4 + j + 1], c4[j + 1]);
@@ -517,11 +529,9 @@ __global__ __launch_bounds__(256) void qk_prep_kernel(const QkPrepParams p) {
             *reinterpret_cast<uint2*>(kr + tid * 4) = make_uint2(pack_bf16(zr[0], zr[1]), pack_bf16(zr[2], zr[3]));
             *reinterpret_cast<uint2*>(kr + 64 + tid * 4) = make_uint2(pack_bf16(zr[4], zr[5]), pack_bf16(zr[6], zr[7]));
         }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            p.keys[slot + tid * 4 + j] = uint16_t(bits(z[j]));
-            p.keys[slot + 64 + tid * 4 + j] = uint16_t(bits(z[4 + j]));
-        }
+        auto word = [](float a, float b) { return (bits(a) & 0xffffu) | (bits(b) << 16); };
+        *reinterpret_cast<uint2*>(p.keys + slot + tid * 4) = make_uint2(word(z[0], z[1]), word(z[2], z[3]));
+        *reinterpret_cast<uint2*>(p.keys + slot + 64 + tid * 4) = make_uint2(word(z[4], z[5]), word(z[6], z[7]));
     }
     if (tid >= 64 && tid < 64 + HEAD_DIM) {
         const int d = tid - 64;
