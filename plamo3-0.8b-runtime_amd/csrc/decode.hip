@@ -1363,36 +1363,55 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const AttnParams p) {
     const int q = blockIdx.z, h = blockIdx.y, d0 = blockIdx.x * 32;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    if (st->stopped || q >= int(st->rows)) return;
-    // keys 0 .. pos on global layers, the last WINDOW of them on local layers
-    const uint32_t count = p.window && st->pos[q] + 1 > p.window ? p.window : st->pos[q] + 1;
-    const uint32_t nparts = (count + KP - 1) / KP;
-    if (nparts <= p.defer || nparts > MAXP || nparts > p.parts) return;  // merged in the attention kernel
     const size_t row0 = size_t(q) * p.parts;
     const uint32_t pstats = uint32_t(ROWS) * p.parts * HEADS;
     const __amdgpu_buffer_rsrc_t mview = buffer_view(p.part_m, pstats * 4u);
     const __amdgpu_buffer_rsrc_t lview = buffer_view(p.part_l, pstats * 4u);
     const __amdgpu_buffer_rsrc_t oview = buffer_view(p.part_o, pstats * HEAD_DIM * 4u);
     // every load first: statistics of partitions tid and tid + 256, then the output slice
-    // (eight threads per partition, 16 bytes each)
+    // (eight threads per partition, 16 bytes each).  The first EARLY partitions of the buffer
+    // are requested before the step state arrives (their addresses do not depend on it; a
+    // local layer's partitions all fall there); entries past the row's partitions are never
+    // used.  The rest follow once the state gives the row's partition count.
+    constexpr uint32_t EARLY = 64;
+    const uint32_t early = p.parts < EARLY ? p.parts : EARLY;
+    constexpr int OPT = int(MAXP) / 32;  // output loads per thread
+    static_assert(EARLY <= 256 && EARLY % 32 == 0, "early statistics: one per thread of the first slot");
     float mv[2] = {NEG_INF, NEG_INF}, lv[2] = {0.f, 0.f};
+    uint4 ov[OPT];
+    const int sub4 = (tid & 7) * 4;
+    if (uint32_t(tid) < early) {
+        mv[0] = __uint_as_float(buffer_load4_sc1(mview, uint32_t((row0 + tid) * HEADS + h) * 4u));
+        lv[0] = __uint_as_float(buffer_load4_sc1(lview, uint32_t((row0 + tid) * HEADS + h) * 4u));
+    }
+#pragma unroll
+    for (int j = 0; j < int(EARLY / 32); ++j) {
+        const uint32_t k = uint32_t((tid >> 3) + 32 * j);
+        if (k < early)
+            ov[j] = buffer_load16_sc1(oview, uint32_t(((row0 + k) * HEADS + h) * HEAD_DIM + d0 + sub4) * 4u);
+    }
+    if (st->stopped || q >= int(st->rows)) return;
+    // keys 0 .. pos on global layers, the last WINDOW of them on local layers
+    const uint32_t count = p.window && st->pos[q] + 1 > p.window ? p.window : st->pos[q] + 1;
+    const uint32_t nparts = (count + KP - 1) / KP;
+    if (nparts <= p.defer || nparts > MAXP || nparts > p.parts) return;  // merged in the attention kernel
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
         const uint32_t k = uint32_t(tid + 256 * j);
-        if (k < nparts) {
+        if (k >= early && k < nparts) {
             mv[j] = __uint_as_float(buffer_load4_sc1(mview, uint32_t((row0 + k) * HEADS + h) * 4u));
             lv[j] = __uint_as_float(buffer_load4_sc1(lview, uint32_t((row0 + k) * HEADS + h) * 4u));
         }
     }
-    constexpr int OPT = int(MAXP) / 32;  // output loads per thread
-    uint4 ov[OPT];
-    const int sub4 = (tid & 7) * 4;
 #pragma unroll
     for (int j = 0; j < OPT; ++j) {
         const uint32_t k = uint32_t((tid >> 3) + 32 * j);
-        if (k < nparts)
+        if (k >= early && k < nparts)
             ov[j] = buffer_load16_sc1(oview, uint32_t(((row0 + k) * HEADS + h) * HEAD_DIM + d0 + sub4) * 4u);
     }
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+        if (uint32_t(tid + 256 * j) >= nparts) mv[j] = NEG_INF;  // early entries past the row's partitions
     // M: a maximum has no rounding, so any order gives the same value
     float M = fmaxf(mv[0], mv[1]);
     M = fmaxf(M, xor_lane<32>(M));
