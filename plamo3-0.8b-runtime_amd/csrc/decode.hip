@@ -1098,6 +1098,15 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
     //      (c0 + c1) + (c2 + c3).
     {
         const int j = lane, w = wave;
+        // validity first: with the QSA mask's branch and load after the score chains, the
+        // compiler holds every operand of the chains at once (135 instead of 75 VGPRs)
+        bool valid = k0 + j < count;
+        if (FULL && p.qsa_mask) {
+            // QSA: key k = position k; the blocks of four keys complete at this position must be
+            // selected, the unfinished block is always seen (Kernels.metal:618-700)
+            const uint32_t b = (k0 + uint32_t(j)) >> 2;
+            valid = valid && (b >= (pos + 1) / 4 || ((p.qsa_mask[size_t(q) * p.qsa_words + (b >> 5)] >> (b & 31)) & 1u));
+        }
         float sc[4] = {0.f, 0.f, 0.f, 0.f};
         const uint32_t* krow = ks + j * KS;
         const uint32_t* qrow = qs + w * (HEAD_DIM / 2);
@@ -1112,13 +1121,6 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
                 sc[c] = dot2bf(qd.z, kd.z, sc[c]);
                 sc[c] = dot2bf(qd.w, kd.w, sc[c]);
             }
-        }
-        bool valid = k0 + j < count;
-        if (FULL && p.qsa_mask) {
-            // QSA: key k = position k; the blocks of four keys complete at this position must be
-            // selected, the unfinished block is always seen (Kernels.metal:618-700)
-            const uint32_t b = (k0 + uint32_t(j)) >> 2;
-            valid = valid && (b >= (pos + 1) / 4 || ((p.qsa_mask[size_t(q) * p.qsa_words + (b >> 5)] >> (b & 31)) & 1u));
         }
         const float dot = (sc[0] + sc[1]) + (sc[2] + sc[3]);
         const float s = valid ? dot * SCALE : NEG_INF;
@@ -1241,13 +1243,17 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
 #pragma unroll
         for (uint32_t j = 0; j < PRE; ++j) load_one(c0 + j < nparts ? c0 + j : nparts - 1, dst[j]);
     };
-    if (nparts == np) {
+    // Global layers merge only rows of up to F partitions here (every caller hands longer
+    // rows to attn_merge_kernel); a longer one would take the memory path below, which has
+    // the same operations in the same order, so the chunked loop is left out of that kernel.
+    const bool staged = nparts == np && (!FULL || nparts <= F);
+    if (staged) {
 #pragma unroll
         for (uint32_t j = 0; j < F; ++j)
             if (j < nparts) load_one(j, ovf[j]);
     }
     __syncthreads();
-    if (nparts == np) {
+    if (staged) {
         // M per head; then every weight exp(m_p - M) in parallel (in place of m_p); then each
         // thread forms den for its own two heads (partition order) while summing o_p w_p
         // M per head: up to 16 partitions one thread per head; more: wave w takes local head w
@@ -1275,7 +1281,8 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
         __syncthreads();
         float num[2] = {0.f, 0.f}, den[2] = {0.f, 0.f};
         float ovp[PRE][2];
-        if (F < nparts) load_chunk(F, ovp);
+        if constexpr (!FULL)
+            if (F < nparts) load_chunk(F, ovp);
 #pragma unroll
         for (uint32_t k = 0; k < F; ++k) {
             if (k >= nparts) break;
@@ -1286,7 +1293,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
                 den[i] = den[i] + wl[k * HG + hb + 2 * i] * w;
             }
         }
-        for (uint32_t c0 = F; c0 < nparts; c0 += PRE) {
+        for (uint32_t c0 = F; !FULL && c0 < nparts; c0 += PRE) {
             const bool more = c0 + PRE < nparts;
             float nxt[PRE][2];
             if (more) load_chunk(c0 + PRE, nxt);
@@ -1312,7 +1319,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
 #pragma unroll
         for (int i = 0; i < 2; ++i)
             p.out16[size_t(q) * ATTN + (hg * HG + hb + 2 * i) * HEAD_DIM + d] = uint16_t(bits(num[i] / den[i]));
-    } else {  // more partitions than LDS holds: read them from memory
+    } else {  // more partitions than LDS holds (or a global row past F): read them from memory
         if (tid < HG) {
             const int h = hg * HG + tid;
             float M = NEG_INF, den = 0.f;
