@@ -376,6 +376,10 @@ __global__ __launch_bounds__(NT) void gemm_dma_kernel(const GemmParams p, int co
         constexpr int i = decltype(b)::value;
         if (kt + i < nk) step(stage_of(b), stage_of(std::integral_constant<int, (i + NS - 1) % NS>{}), kt + i);
     });
+    // The last steps issued loads for the stages past the end (out of range: they write zeros
+    // into LDS, and keep the per-step load counts uniform).  No wave ends with a load into LDS
+    // in flight: the workgroup's LDS may go to the next workgroup on this CU.
+    wait_vmcnt<0>();
     gemm_epilogue<EPI, TT, TW>(p, acc, t0 + wt * TT * 32, n0, ww, lane);
 }
 
