@@ -244,6 +244,12 @@ __device__ __forceinline__ void wait_vmcnt() {
     static_assert(N >= 0 && N < 64, "vmcnt range");
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
 }
+// The same, and every LDS operation of the wave done (lgkmcnt 0).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt_lds() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0070);
+}
 
 // Calls f(std::integral_constant<int, I>) for I = B .. E-1.
 template <int B, int E, class F>
@@ -265,8 +271,8 @@ __device__ __forceinline__ void load_to_lds(__amdgpu_buffer_rsrc_t v, void* lds,
 // rows of KD * 2 bytes; the 16-byte chunk c of row R sits in slot c ^ ((R >> SH) & (CPR - 1))
 // (SH = 1 for 128-byte rows, 2 for 64-byte rows), which spreads both the loads' row segments
 // and the operand reads' 16-row columns over all banks.  Each wave loads Q 1 KB blocks per
-// stage.  Waves synchronise with a bare s_barrier after waiting for their own stage loads, so
-// the later stages stay in flight across the barrier.
+// stage.  Waves synchronise with a bare s_barrier after waiting for their own stage loads and
+// LDS reads, so the later stages stay in flight across the barrier.
 template <int EPI, int BT, int BW, int WT, int NT, int KD, int NS>
 __global__ __launch_bounds__(NT) void gemm_dma_kernel(const GemmParams p, int col_tiles, int row_tiles) {
     constexpr int NW = NT / 64, WW = NW / WT, TT = BT / WT / 32, TW = BW / WW / 32;
@@ -356,10 +362,13 @@ __global__ __launch_bounds__(NT) void gemm_dma_kernel(const GemmParams p, int co
         }
     };
     // step kt: this wave's loads of stage kt are done once at most the loads of the NS - 2
-    // later stages are outstanding; after the barrier every wave's are, and the buffer of
-    // stage kt - 1 is free for stage kt + NS - 1
+    // later stages are outstanding, and its reads of stage kt - 1 once no LDS operation is
+    // (a read issued before the barrier may still be queued in the LDS, and a load into the
+    // freed buffer can return before it runs: from L2, or at once when out of range); after
+    // the barrier every wave's are, and the buffer of stage kt - 1 is free for stage kt + NS - 1
     auto step = [&](const uint8_t* cur, uint8_t* freed, int kt) {
-        wait_vmcnt<(NS - 2) * Q>();
+        __asm__ volatile("" ::: "memory");  // no LDS access of the previous step moves below
+        wait_vmcnt_lds<(NS - 2) * Q>();
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
         issue(freed, kt + NS - 1);
@@ -954,7 +963,11 @@ __device__ __forceinline__ void flash_prefill(const FlashParams& p, const int qb
         // tile j: its keys and values are in Kc / Vc; the next tile's go to Kn / Vn (free:
         // read by tile j - 1 before this tile's barrier)
         auto tile = [&](int j, const uint16_t* Kc, uint16_t* Kn, const uint16_t* Vc, uint16_t* Vn) {
-            __syncthreads();  // tile j is in; tile j - 1 is done with Kn and Vn
+            // tile j is in (each wave waits for its own loads into LDS: the barrier's fence
+            // covers LDS operations, not loads into LDS, and every wave reads rows that other
+            // waves loaded); tile j - 1 is done with Kn and Vn
+            wait_vmcnt<0>();
+            __syncthreads();
             if (j + 1 < j1) {
                 dma_k(Kn, j + 1);
                 dma_v(Vn, j + 1);
