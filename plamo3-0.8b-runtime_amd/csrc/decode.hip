@@ -1141,39 +1141,44 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const AttnParams p) {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    // ---- unnormalised P.V: thread -> dims 2e, 2e+1 (e = tid & 63) of local head tid >> 6;
-    //      keys 0..31 and 32..63 as two ordered chains of fused multiply-adds per dim, added
-    //      at the end
+    // ---- unnormalised P.V: wave w = local head w; lanes 0..31 take keys 0..31 and lanes
+    //      32..63 keys 32..63, lane l owning dims 4(l % 32) .. +3 (one 8-byte value read per
+    //      key).  Per dim: two ordered chains of fused multiply-adds (keys 0..31, keys 32..63),
+    //      added at the end (lanes 0..31 add the partner lane's chain to their own)
     {
-        const int e = tid & 63, hl = wave;
-        const uint32_t* v32 = reinterpret_cast<const uint32_t*>(vs);
-        float o[2][2] = {{0.f, 0.f}, {0.f, 0.f}};  // [dim][half]
+        const int hl = wave, hf = lane >> 5, d4 = (lane & 31) * 4;
+        const float* pr = ps + hl * KP + hf * (KP / 2);
+        const uint16_t* vb = vs + hf * (KP / 2) * HEAD_DIM + d4;
+        float o[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll 2
         for (int j = 0; j < KP / 2; j += 4) {
-            uint32_t vw[2][4];
+            uint2 vw[4];
 #pragma unroll
-            for (int hf = 0; hf < 2; ++hf)
+            for (int i = 0; i < 4; ++i) vw[i] = *reinterpret_cast<const uint2*>(vb + (j + i) * HEAD_DIM);
+            const float4 pp = *reinterpret_cast<const float4*>(pr + j);
+            const float pw[4] = {pp.x, pp.y, pp.z, pp.w};
 #pragma unroll
-                for (int i = 0; i < 4; ++i) vw[hf][i] = v32[(hf * (KP / 2) + j + i) * (HEAD_DIM / 2) + e];
-#pragma unroll
-            for (int hf = 0; hf < 2; ++hf) {
-                const float4 pp = *reinterpret_cast<const float4*>(ps + hl * KP + hf * (KP / 2) + j);
-                const float pw[4] = {pp.x, pp.y, pp.z, pp.w};
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    o[0][hf] = fmaf(pw[i], lo(vw[hf][i]), o[0][hf]);
-                    o[1][hf] = fmaf(pw[i], hi(vw[hf][i]), o[1][hf]);
-                }
+            for (int i = 0; i < 4; ++i) {
+                o[0] = fmaf(pw[i], lo(vw[i].x), o[0]);
+                o[1] = fmaf(pw[i], hi(vw[i].x), o[1]);
+                o[2] = fmaf(pw[i], lo(vw[i].y), o[2]);
+                o[3] = fmaf(pw[i], hi(vw[i].y), o[3]);
             }
         }
+        float of[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) of[k] = o[k] + xor_lane<32>(o[k]);  // lanes 0..31: first half + second
         const int h = hg * HG + hl;
-        const float of0 = o[0][0] + o[0][1], of1 = o[1][0] + o[1][1];
-        if (nparts == 1) {  // one partition: the merge reduces to o / l (exp(0) == 1 exactly)
-            p.out16[size_t(q) * ATTN + h * HEAD_DIM + 2 * e] = uint16_t(bits(of0 / l_s[hl]));
-            p.out16[size_t(q) * ATTN + h * HEAD_DIM + 2 * e + 1] = uint16_t(bits(of1 / l_s[hl]));
-        } else {
-            buffer_store8_sc1(oview, uint32_t((pslot * HEADS + h) * HEAD_DIM + 2 * e) * 4u,
-                              make_uint2(__float_as_uint(of0), __float_as_uint(of1)));
+        if (lane < 32) {
+            if (nparts == 1) {  // one partition: the merge reduces to o / l (exp(0) == 1 exactly)
+                const float l = l_s[hl];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) p.out16[size_t(q) * ATTN + h * HEAD_DIM + d4 + k] = uint16_t(bits(of[k] / l));
+            } else {
+                buffer_store16_sc1(oview, uint32_t((pslot * HEADS + h) * HEAD_DIM + d4) * 4u,
+                                   make_uint4(__float_as_uint(of[0]), __float_as_uint(of[1]), __float_as_uint(of[2]),
+                                              __float_as_uint(of[3])));
+            }
         }
     }
     if (nparts == 1) return;
